@@ -1,0 +1,368 @@
+"""ctypes binding of the oracle (CPU restatement of the zip engine's hot path).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, never by the product package ``mesh_amd``.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+f32p = C.POINTER(C.c_float)
+i32p = C.POINTER(C.c_int)
+u32p = C.POINTER(C.c_uint32)
+
+
+def build(force: bool = False) -> str:
+    """Compile liboracle.so with the committed Makefile."""
+    if force or not os.path.exists(_LIB_PATH):
+        subprocess.check_call(["make", "-s", "-B" if force else "-s", "-C", _HERE])
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = C.CDLL(_LIB_PATH)
+        L.or_last_error.restype = C.c_char_p
+        L.or_session_new.restype = C.c_void_p
+        L.or_session_new.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]
+        L.or_session_free.argtypes = [C.c_void_p]
+        for name in ("or_session_append_layer",):
+            getattr(L, name).argtypes = [C.c_void_p, C.c_int, f32p, f32p, C.c_int]
+        L.or_session_retain_suffix.argtypes = [C.c_void_p, C.c_int]
+        L.or_session_clear.argtypes = [C.c_void_p]
+        for name in ("or_session_seq_len", "or_session_allocated_pages"):
+            getattr(L, name).argtypes = [C.c_void_p, C.c_int]
+        for name in ("or_session_base_position", "or_session_position"):
+            getattr(L, name).argtypes = [C.c_void_p]
+        L.or_session_set_position.argtypes = [C.c_void_p, C.c_int]
+        L.or_session_block_table.argtypes = [C.c_void_p, C.c_int, u32p, i32p, i32p, C.c_int]
+        L.or_session_gather.argtypes = [C.c_void_p, C.c_int, f32p, f32p]
+        L.or_session_export.argtypes = [C.c_void_p, C.c_int, f32p, f32p, i32p, i32p]
+        L.or_session_import.argtypes = [C.c_void_p, f32p, f32p, C.c_int, C.c_int, C.c_int]
+        L.or_model_new.restype = C.c_void_p
+        L.or_model_free.argtypes = [C.c_void_p]
+        L.or_model_set_globals.argtypes = [C.c_void_p, f32p, f32p, f32p]
+        L.or_model_set_layer.argtypes = [C.c_void_p, C.c_int] + [f32p] * 9
+        L.or_decode_microbatch.argtypes = [C.c_void_p, C.POINTER(C.c_void_p), C.c_int, u32p, f32p, f32p]
+        L.or_prefill.argtypes = [C.c_void_p, C.c_void_p, u32p, C.c_int, f32p]
+        L.or_prefill_chunk.argtypes = [C.c_void_p, C.c_void_p, u32p, C.c_int, f32p, f32p]
+        L.or_matmul.argtypes = [f32p, f32p, f32p, C.c_int, C.c_int, C.c_int]
+        L.or_rms_norm.argtypes = [f32p, f32p, f32p, C.c_int, C.c_int, C.c_float]
+        L.or_silu.argtypes = [f32p, f32p, C.c_int64]
+        L.or_apply_rope.argtypes = [f32p, f32p, C.c_int, C.c_int, u32p, C.c_int, C.c_float]
+        L.or_rope_inv_freq.argtypes = [C.c_int, C.c_float, f32p]
+        L.or_sample_greedy.argtypes = [f32p, C.c_int]
+        L.or_sample_greedy.restype = C.c_uint32
+        L.or_sample_token.argtypes = [f32p, C.c_int, C.c_float, C.c_float, C.c_uint64]
+        L.or_sample_token.restype = C.c_uint32
+        L.or_sample_threshold.argtypes = [C.c_uint64]
+        L.or_sample_threshold.restype = C.c_float
+        L.or_causal_attention_with_prefix.argtypes = [f32p, f32p, f32p, f32p, C.c_int, C.c_int,
+                                                      C.c_int, C.c_float, C.c_int]
+        L.or_f32_to_bf16.argtypes = [C.c_float]
+        L.or_f32_to_bf16.restype = C.c_uint16
+        L.or_resolve_shard_layout.argtypes = [C.c_int] * 5 + [C.c_void_p, u32p]
+        L.or_partition_columns.argtypes = [C.c_int, C.c_int, C.c_int]
+        L.or_pack.argtypes = [C.c_int, i32p, i32p, i32p, i32p, i32p, C.c_int, C.c_int,
+                              i32p, i32p, i32p, i32p, i32p]
+        _lib = L
+    return _lib
+
+
+class OracleError(RuntimeError):
+    pass
+
+
+def _check(rc):
+    if rc < 0:
+        raise OracleError(lib().or_last_error().decode())
+    return rc
+
+
+def _f(a):
+    return a.ctypes.data_as(f32p)
+
+
+def _i(a):
+    return a.ctypes.data_as(i32p)
+
+
+def _u(a):
+    return a.ctypes.data_as(u32p)
+
+
+def f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+# ------------------------------------------------------------------- ops --
+def matmul(a, b):
+    a, b = f32(a), f32(b)
+    out = np.empty((a.shape[0], b.shape[1]), np.float32)
+    _check(lib().or_matmul(_f(a), _f(b), _f(out), a.shape[0], a.shape[1], b.shape[1]))
+    return out
+
+
+def rms_norm(x, gamma, eps):
+    x, gamma = f32(x), f32(gamma)
+    out = np.empty_like(x)
+    _check(lib().or_rms_norm(_f(x), _f(gamma), _f(out), x.shape[0], x.shape[1], eps))
+    return out
+
+
+def silu(x):
+    x = f32(x)
+    out = np.empty_like(x)
+    lib().or_silu(_f(x), _f(out), x.size)
+    return out
+
+
+def apply_rope(x, positions, head_dim, base):
+    x = f32(x)
+    pos = np.ascontiguousarray(positions, dtype=np.uint32)
+    out = np.empty_like(x)
+    _check(lib().or_apply_rope(_f(x), _f(out), x.shape[0], x.shape[1], _u(pos), head_dim, base))
+    return out
+
+
+def rope_inv_freq(head_dim, base):
+    out = np.empty(head_dim // 2, np.float32)
+    lib().or_rope_inv_freq(head_dim, base, _f(out))
+    return out
+
+
+def sample_greedy(logits):
+    x = f32(logits)
+    return int(lib().or_sample_greedy(_f(x), x.size))
+
+
+def sample_token(logits, temperature, top_p, seed):
+    x = f32(logits)
+    return int(lib().or_sample_token(_f(x), x.size, temperature, top_p, seed))
+
+
+def sample_threshold(seed):
+    return float(lib().or_sample_threshold(seed))
+
+
+def causal_attention_with_prefix(q, k, v, scale, prefix_len):
+    q, k, v = f32(q), f32(k), f32(v)
+    out = np.empty((q.shape[0], v.shape[1]), np.float32)
+    _check(lib().or_causal_attention_with_prefix(_f(q), _f(k), _f(v), _f(out), q.shape[0],
+                                                 k.shape[0], q.shape[1], scale, prefix_len))
+    return out
+
+
+def to_bf16_bits(x):
+    """Round-to-nearest-even f32 -> bf16 bit patterns (uint16)."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    if nan.any():
+        r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def bf16_bits_to_f32(h):
+    return (np.ascontiguousarray(h, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def round_bf16(x):
+    return bf16_bits_to_f32(to_bf16_bits(x))
+
+
+class ShardLayout(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("head_dim", "q_heads_per_kv_head", "q_cols", "q_head_start",
+                                       "local_q_heads", "kv_cols", "kv_head_start", "local_kv_heads")]
+
+
+def resolve_shard_layout(hidden, num_heads, num_kv_heads, shard_start, shard_end):
+    lay = ShardLayout()
+    idx = np.zeros(num_heads, np.uint32)
+    _check(lib().or_resolve_shard_layout(hidden, num_heads, num_kv_heads, shard_start, shard_end,
+                                         C.byref(lay), _u(idx)))
+    return lay, idx[:lay.local_q_heads].tolist()
+
+
+def partition_columns(total, position, workers):
+    return int(lib().or_partition_columns(total, position, workers))
+
+
+def pack(q_len, kv_before, first_pos, first_offset, block_tables, page_rows=16):
+    q_len = np.ascontiguousarray(q_len, np.int32)
+    kv_before = np.ascontiguousarray(kv_before, np.int32)
+    first_pos = np.ascontiguousarray(first_pos, np.int32)
+    first_offset = np.ascontiguousarray(first_offset, np.int32)
+    bt = np.ascontiguousarray(block_tables, np.int32)
+    n = q_len.size
+    total = int(q_len.sum())
+    cu_q = np.zeros(n + 1, np.int32)
+    cu_k = np.zeros(n + 1, np.int32)
+    pos = np.zeros(max(total, 1), np.int32)
+    slot = np.zeros(max(total, 1), np.int32)
+    seq = np.zeros(max(total, 1), np.int32)
+    _check(lib().or_pack(n, _i(q_len), _i(kv_before), _i(first_pos), _i(first_offset), _i(bt),
+                         bt.shape[1], page_rows, _i(cu_q), _i(cu_k), _i(pos), _i(slot), _i(seq)))
+    return cu_q, cu_k, pos[:total], slot[:total], seq[:total]
+
+
+# ---------------------------------------------------------------- session --
+class Session:
+    """One session's paged device KV cache (DeviceKVCache) + ForwardPass.position."""
+
+    def __init__(self, num_layers, kv_cols, page_rows=16, max_seq_len=4096, kv_round_bf16=False):
+        self.num_layers, self.kv_cols = num_layers, kv_cols
+        self.h = lib().or_session_new(num_layers, kv_cols, page_rows, max_seq_len, int(kv_round_bf16))
+        if not self.h:
+            raise OracleError(lib().or_last_error().decode())
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().or_session_free(self.h)
+            self.h = None
+
+    def append_layer(self, layer, k, v):
+        k, v = f32(k), f32(v)
+        _check(lib().or_session_append_layer(self.h, layer, _f(k), _f(v), k.shape[0]))
+
+    def append_all_layers(self, k, v):
+        for layer in range(self.num_layers):
+            self.append_layer(layer, k, v)
+
+    def retain_suffix(self, keep):
+        _check(lib().or_session_retain_suffix(self.h, keep))
+
+    def clear(self):
+        lib().or_session_clear(self.h)
+
+    def seq_len(self, layer=0):
+        return _check(lib().or_session_seq_len(self.h, layer))
+
+    @property
+    def base_position(self):
+        return lib().or_session_base_position(self.h)
+
+    @property
+    def position(self):
+        return lib().or_session_position(self.h)
+
+    @position.setter
+    def position(self, p):
+        lib().or_session_set_position(self.h, p)
+
+    def next_position(self):
+        return self.base_position + self.seq_len()
+
+    def allocated_pages(self, layer=0):
+        return _check(lib().or_session_allocated_pages(self.h, layer))
+
+    def block_table(self, layer=0):
+        n = _check(lib().or_session_block_table(self.h, layer, None, None, None, 0))
+        ids = np.zeros(max(n, 1), np.uint32)
+        st = np.zeros(max(n, 1), np.int32)
+        ct = np.zeros(max(n, 1), np.int32)
+        _check(lib().or_session_block_table(self.h, layer, _u(ids), _i(st), _i(ct), n))
+        return [(int(ids[i]), int(st[i]), int(ct[i])) for i in range(n)]
+
+    def gather(self, layer=0):
+        n = self.seq_len(layer)
+        k = np.zeros((n, self.kv_cols), np.float32)
+        v = np.zeros((n, self.kv_cols), np.float32)
+        _check(lib().or_session_gather(self.h, layer, _f(k), _f(v)))
+        return k, v
+
+    def export(self, max_cached_tokens=None):
+        n = self.seq_len()
+        k = np.zeros((self.num_layers, max(n, 1), self.kv_cols), np.float32)
+        v = np.zeros_like(k)
+        base = C.c_int()
+        nxt = C.c_int()
+        rows = _check(lib().or_session_export(self.h, -1 if max_cached_tokens is None else max_cached_tokens,
+                                              _f(k), _f(v), C.byref(base), C.byref(nxt)))
+        if rows == 0:
+            return None
+        flat_k = k.reshape(-1)[: self.num_layers * rows * self.kv_cols].reshape(self.num_layers, rows, self.kv_cols)
+        flat_v = v.reshape(-1)[: self.num_layers * rows * self.kv_cols].reshape(self.num_layers, rows, self.kv_cols)
+        return {"keys": flat_k.copy(), "values": flat_v.copy(), "base_position": base.value,
+                "next_position": nxt.value, "cached_tokens": rows}
+
+    def import_snapshot(self, snap):
+        k, v = f32(snap["keys"]), f32(snap["values"])
+        _check(lib().or_session_import(self.h, _f(k), _f(v), int(snap["cached_tokens"]),
+                                       int(snap["base_position"]), int(snap["next_position"])))
+
+
+class ModelConfig(C.Structure):
+    _fields_ = [("hidden", C.c_int), ("num_heads", C.c_int), ("num_kv_heads", C.c_int),
+                ("num_layers", C.c_int), ("vocab", C.c_int), ("ffn_cols", C.c_int),
+                ("shard_start", C.c_int), ("shard_end", C.c_int),
+                ("rms_norm_eps", C.c_float), ("rope_base", C.c_float)]
+
+
+class Model:
+    """Weights are f32 numpy arrays in the reference [in, out] layout (kept alive here)."""
+
+    def __init__(self, cfg: dict, weights: dict):
+        c = ModelConfig(cfg["hidden"], cfg["num_heads"], cfg["num_kv_heads"], cfg["num_layers"],
+                        cfg["vocab"], cfg["ffn_cols"], cfg.get("shard_start", 0),
+                        cfg.get("shard_end", cfg["hidden"]), cfg.get("rms_norm_eps", 1e-5),
+                        cfg.get("rope_base", 10000.0))
+        self.cfg = cfg
+        self.h = lib().or_model_new(C.byref(c))
+        if not self.h:
+            raise OracleError(lib().or_last_error().decode())
+        self._keep = []
+
+        def keep(a):
+            a = f32(a)
+            self._keep.append(a)
+            return _f(a)
+
+        _check(lib().or_model_set_globals(self.h, keep(weights["embedding"]), keep(weights["final_norm"]),
+                                          keep(weights["lm_head"])))
+        for l, lw in enumerate(weights["layers"]):
+            _check(lib().or_model_set_layer(self.h, l, keep(lw["w_q"]), keep(lw["w_k"]), keep(lw["w_v"]),
+                                            keep(lw["w_o"]), keep(lw["w_gate"]), keep(lw["w_up"]),
+                                            keep(lw["w_down"]), keep(lw["attn_norm"]), keep(lw["mlp_norm"])))
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().or_model_free(self.h)
+            self.h = None
+
+    def decode(self, sessions, tokens, want_partials=False):
+        B = len(sessions)
+        toks = np.ascontiguousarray(tokens, np.uint32)
+        logits = np.zeros((B, self.cfg["vocab"]), np.float32)
+        parts = (np.zeros((self.cfg["num_layers"], 2, B, self.cfg["hidden"]), np.float32)
+                 if want_partials else None)
+        arr = (C.c_void_p * B)(*[s.h for s in sessions])
+        _check(lib().or_decode_microbatch(self.h, arr, B, _u(toks), _f(logits),
+                                          _f(parts) if parts is not None else None))
+        return (logits, parts) if want_partials else logits
+
+    def prefill(self, session, tokens):
+        toks = np.ascontiguousarray(tokens, np.uint32)
+        logits = np.zeros(self.cfg["vocab"], np.float32)
+        _check(lib().or_prefill(self.h, session.h, _u(toks), toks.size, _f(logits)))
+        return logits
+
+    def prefill_chunk(self, session, tokens, want_partials=False):
+        toks = np.ascontiguousarray(tokens, np.uint32)
+        logits = np.zeros(self.cfg["vocab"], np.float32)
+        parts = (np.zeros((self.cfg["num_layers"], 2, toks.size, self.cfg["hidden"]), np.float32)
+                 if want_partials else None)
+        _check(lib().or_prefill_chunk(self.h, session.h, _u(toks), toks.size, _f(logits),
+                                      _f(parts) if parts is not None else None))
+        return (logits, parts) if want_partials else logits
