@@ -1,0 +1,222 @@
+/*
+ * zip_rocm.h -- C ABI of the MI355X (gfx950) execution provider for zip.
+ *
+ * This is the thin FFI a `rocm` arm of zip's provider abstraction binds
+ * (agent/src/inference/backend.rs:30-88 ExecutionBackend, provider/mod.rs:8-33
+ * ExecutionProviderKind).  The host keeps ownership of scheduling and of the
+ * paged-KV page tables; every call here executes one worker's share of the
+ * forward pass on one GPU with hand-written CDNA4 kernels.
+ *
+ * Conventions
+ *  - Every function returns zr_status (0 = ok).  Failures never abort: the
+ *    message is kept per context (zr_last_error) or per thread
+ *    (zr_global_last_error) -- the AgentError::Execution / Config split of
+ *    agent/src/errors.rs:19-36.
+ *  - Plain pointers and sizes only.  "host" arrays are ordinary CPU memory;
+ *    "device" pointers come from zr_device_alloc.  Weight uploads accept either.
+ *  - One context = one device + one HIP stream; calls on a context are
+ *    serialised by the caller (the reference drives a backend through &mut
+ *    self from one task, coordinator.rs:2291-2306).  Entry points are
+ *    synchronous at return unless named *_async.
+ *  - Weights are bf16 bit patterns in the reference's row-major [in, out]
+ *    layout (x @ W, forward_pass.rs:89-114); norms are f32.
+ *  - The KV pool is global pages of `page_tokens` (16) rows for K and V of
+ *    every layer; a page id in a block table indexes all layers
+ *    (page tables are per-layer identical, forward_pass.rs:1024-1047).
+ */
+#ifndef ZIP_ROCM_H
+#define ZIP_ROCM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int zr_status;
+#define ZR_OK 0
+#define ZR_E_INVALID (-1)     /* bad argument / shape (AgentError::Execution) */
+#define ZR_E_OOM (-2)         /* device or pool memory exhausted */
+#define ZR_E_HIP (-3)         /* HIP runtime failure */
+#define ZR_E_INVARIANT (-4)   /* page-table / position invariant violated */
+#define ZR_E_UNSUPPORTED (-5) /* geometry the kernels do not cover */
+#define ZR_E_NODEVICE (-6)    /* no gfx950 device */
+
+#define ZR_DTYPE_F32 0
+#define ZR_DTYPE_BF16 1
+
+/* zr_model_desc.flags */
+#define ZR_FLAG_SPLIT_ACTIVATIONS 1 /* GEMM A operands as bf16 hi+lo pairs (~fp32) */
+
+/* ------------------------------------------------------------- device --- */
+typedef struct {
+    int device_count;
+    int device;          /* the device described below */
+    int compute_units;
+    int clock_mhz;
+    uint64_t hbm_bytes;
+    char arch[64];       /* e.g. "gfx950:sramecc+:xnack-" */
+} zr_device_info;
+
+/* runtime.rs:335-385 probe_provider: reports the device, ZR_E_NODEVICE if the
+ * selected device is not gfx950. */
+zr_status zr_probe(int device, zr_device_info* out);
+const char* zr_global_last_error(void);
+
+/* ------------------------------------------------------------ context --- */
+typedef struct {
+    int hidden, num_heads, num_kv_heads, num_layers, vocab;
+    int ffn_cols;                 /* this shard's FFN columns (partition_columns) */
+    int shard_start, shard_end;   /* this shard's q-column range (forward_pass.rs:1257) */
+    float rms_norm_eps, rope_base;
+    int page_tokens;              /* 16 (kv_cache.rs:214) */
+    int kv_dtype;                 /* ZR_DTYPE_BF16 or ZR_DTYPE_F32 */
+    int max_tokens;               /* rows of one microbatch (sum of q_len) */
+    int max_seqs;                 /* sequences of one microbatch */
+    int max_pages_per_seq;        /* block-table width */
+    int flags;
+} zr_model_desc;
+
+typedef struct zr_context zr_context;
+
+/* ForwardPass::from_residency / SharedModelResidency::from_host
+ * (forward_pass.rs:1725-1824): validates the shard geometry with the rules of
+ * resolve_attention_shard_layout and allocates activations on `device`. */
+zr_status zr_context_create(const zr_model_desc* desc, int device, zr_context** out);
+void zr_context_destroy(zr_context* ctx);
+const char* zr_last_error(const zr_context* ctx);
+/* Local q-head -> local kv-head map (build_local_kv_head_indices 2951-2970). */
+zr_status zr_kv_head_map(const zr_context* ctx, uint32_t* out, int capacity, int* count);
+
+/* ------------------------------------------------------------ weights --- */
+typedef struct {
+    const uint16_t* w_q;     /* [hidden, q_cols]  bf16 */
+    const uint16_t* w_k;     /* [hidden, kv_cols] */
+    const uint16_t* w_v;     /* [hidden, kv_cols] */
+    const uint16_t* w_o;     /* [q_cols, hidden] */
+    const uint16_t* w_gate;  /* [hidden, ffn_cols] */
+    const uint16_t* w_up;    /* [hidden, ffn_cols] */
+    const uint16_t* w_down;  /* [ffn_cols, hidden] */
+    const float* attn_norm;  /* [hidden] */
+    const float* mlp_norm;   /* [hidden] */
+} zr_layer_weights;
+
+/* DeviceModelWeights::from_host (forward_pass.rs:1560-1591): w_qkv = [q|k|v]
+ * and w_gate_up = [gate|up] column concatenations, repacked into the MFMA
+ * fragment layout.  Pointers may be host or device memory. */
+zr_status zr_upload_layer(zr_context* ctx, int layer, const zr_layer_weights* w);
+zr_status zr_upload_globals(zr_context* ctx, const uint16_t* embedding /* [vocab, hidden] */,
+                            const float* final_norm /* [hidden] */,
+                            const uint16_t* lm_head /* [hidden, vocab] */);
+
+/* ------------------------------------------------------------ KV pool --- */
+/* Allocates n_pages global pages (zero-filled).  Page p of layer l holds K and
+ * V for 16 token rows of every local kv head. */
+zr_status zr_kv_pool_create(zr_context* ctx, int n_pages);
+int zr_kv_pool_pages(const zr_context* ctx);
+uint64_t zr_kv_pool_bytes(const zr_context* ctx);
+
+/* ------------------------------------------------------- microbatches --- */
+/* One ragged microbatch: decode rows (q_len 1) and prefill chunks (q_len > 1)
+ * packed into one varlen token tensor.  All arrays are host memory.
+ * Sequence s appends q_len[s] rows after kv_before[s] cached rows (the live
+ * window after the sliding-window trim); its first new token has absolute
+ * position first_pos[s].  block_tables[s] lists the global pages of the live
+ * window AFTER the append, oldest first; the window starts at row
+ * first_offset[s] of the first page (a span trimmed by retain_suffix). */
+typedef struct {
+    int num_seqs;
+    const int* q_len;
+    const int* kv_before;
+    const int* first_pos;
+    const int* first_offset;
+    const int* block_tables;   /* [num_seqs][block_table_stride] */
+    int block_table_stride;
+    const uint32_t* tokens;    /* [sum q_len]; may be NULL for staged runs fed on device */
+} zr_microbatch;
+
+/* Runs embed -> num_layers x (norm, QKV, RoPE+KV write, paged attention, O,
+ * residual, norm, gate_up+SwiGLU, down, residual) -> final norm -> LM head on
+ * the last row of every sequence -> greedy argmax
+ * (fast_path_decode_microbatch, forward_pass.rs:2143-2319).  Outputs are host
+ * arrays, each nullable: out_tokens [num_seqs] greedy ids (first index on
+ * ties), out_logits [num_seqs, vocab] f32, out_partials
+ * [num_layers][2][sum q_len][hidden] f32 = per-layer pre-all-reduce
+ * (o_partial, down_partial) (forward_pass.rs:2265, 2290). */
+zr_status zr_forward(zr_context* ctx, const zr_microbatch* mb, uint32_t* out_tokens,
+                     float* out_logits, float* out_partials);
+
+/* Device-resident variant: metadata staged once into device memory. */
+typedef struct zr_staged zr_staged;
+zr_status zr_stage(zr_context* ctx, const zr_microbatch* mb, zr_staged** out);
+void zr_staged_destroy(zr_staged* st);
+/* Enqueues the forward pass on the context stream without synchronising.
+ * d_tokens: device [sum q_len] input ids, or NULL to use the staged ids.
+ * d_out_tokens: device [num_seqs] greedy ids (may be d_tokens of a later
+ * decode step); d_out_logits nullable device [num_seqs, vocab]. */
+zr_status zr_forward_staged_async(zr_context* ctx, zr_staged* st, const uint32_t* d_tokens,
+                                  uint32_t* d_out_tokens, float* d_out_logits);
+zr_status zr_synchronize(zr_context* ctx);
+
+/* ------------------------------------------------------ op-level entries --- */
+/* Ragged packing on the GPU: device outputs cu_q/cu_k [num_seqs+1],
+ * positions/slot_mapping/seq_ids [sum q_len] (host arrays, copied back). */
+zr_status zr_pack(zr_context* ctx, const zr_microbatch* mb, int* cu_q, int* cu_k, int* positions,
+                  int* slot_mapping, int* seq_ids);
+/* RoPE on q and k + KV append (the RopeKvWrite stage): d_qkv device
+ * [sum q_len, q_cols + 2*kv_cols] f32 projection output; writes RoPE'd q to
+ * d_q_out [sum q_len, q_cols] and RoPE'd k / v into the pool at the staged
+ * slot mapping for `layer`.  rope=0 skips the rotation (append only). */
+zr_status zr_rope_kv_write(zr_context* ctx, zr_staged* st, int layer, const float* d_qkv,
+                           float* d_q_out, int rope);
+/* GQA paged attention (decode rows and causal chunked prefill) over the
+ * staged microbatch for `layer`: d_q device [sum q_len, q_cols] f32 (RoPE'd),
+ * d_out device [sum q_len, q_cols] f32. */
+zr_status zr_attention(zr_context* ctx, zr_staged* st, int layer, const float* d_q, float* d_out);
+/* Checkpoint KV handoff gather (build_active_tensors + retain_suffix window,
+ * forward_pass.rs:633-680, 1169-1204): rows [first_row, first_row + n_rows)
+ * of one sequence's live window, all layers, into dst_k/dst_v
+ * [num_layers][n_rows][kv_cols] f32 (host or device memory). */
+zr_status zr_kv_gather(zr_context* ctx, const int* block_table, int n_pages, int first_offset,
+                       int first_row, int n_rows, float* dst_k, float* dst_v);
+/* Snapshot import scatter (import_snapshot, forward_pass.rs:1206-1242):
+ * writes rows [0, n_rows) of src_k/src_v [num_layers][n_rows][kv_cols] f32 at
+ * logical rows first_row.. of the window described by block_table. */
+zr_status zr_kv_scatter(zr_context* ctx, const int* block_table, int n_pages, int first_offset,
+                        int first_row, int n_rows, const float* src_k, const float* src_v);
+/* Raw page access for bit-exact checks: copies `n_pages` pages of `layer`
+ * (K then V, pool dtype, pool layout) into host memory. */
+zr_status zr_kv_read_pages(zr_context* ctx, int layer, const int* pages, int n_pages, void* dst);
+/* Greedy argmax over rows of a device [rows, cols] f32 matrix (first index on
+ * ties; runtime.rs:561-570). */
+zr_status zr_argmax(zr_context* ctx, const float* d_x, int rows, int cols, uint32_t* d_out);
+/* y = rms_norm(x) * gamma (tensor_ops.rs:285-304), device f32 [rows, cols]. */
+zr_status zr_rms_norm(zr_context* ctx, const float* d_x, const float* d_gamma, float* d_y, int rows,
+                      int cols);
+/* C[M,N] = A[M,K] @ W[K,N] with W bf16 [K,N] (host or device, reference
+ * layout), A/C device f32 -- the shard projection GEMM on MFMA. */
+zr_status zr_gemm(zr_context* ctx, const float* d_a, const uint16_t* w, float* d_c, int m, int n,
+                  int k);
+
+/* --------------------------------------------------------- device memory --- */
+zr_status zr_device_alloc(zr_context* ctx, size_t bytes, void** out);
+zr_status zr_device_free(zr_context* ctx, void* p);
+zr_status zr_memcpy_h2d(zr_context* ctx, void* dst, const void* src, size_t bytes);
+zr_status zr_memcpy_d2h(zr_context* ctx, void* dst, const void* src, size_t bytes);
+/* Fills device bf16 [n] with N(0, std) draws (Box-Muller over a counter-based
+ * SplitMix64 stream keyed by seed) -- synthetic random-init weights. */
+zr_status zr_fill_normal_bf16(zr_context* ctx, uint16_t* d_dst, size_t n, uint64_t seed, float std);
+/* Fills every page of the KV pool with N(0, std) values in the pool dtype. */
+zr_status zr_kv_pool_fill_normal(zr_context* ctx, uint64_t seed, float std);
+
+/* ---------------------------------------------------------- profiling --- */
+/* Per-kernel-class timing with HIP events on the context stream (enabled
+ * between begin/end).  Classes: 0 attention, 1 gemm, 2 norm/rope/kv, 3 other. */
+zr_status zr_timing_begin(zr_context* ctx);
+zr_status zr_timing_end(zr_context* ctx, double* ms_by_class /* [4] */, int* launches_by_class /* [4] */);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,99 @@
+/*
+ * zip_rocm_host.h -- host-side `rocm` execution backend over zip_rocm.h.
+ *
+ * The reference's provider host is Rust (agent/src/inference/backend.rs,
+ * forward_pass.rs); this image has no Rust toolchain, so the same host logic
+ * is C++ here with a C ABI: one zrh_backend is one session's
+ * ProviderExecutionBackend (backend.rs:400-662) = ForwardPass position +
+ * DeviceKVCache page tables (forward_pass.rs:899-1243).  The host owns the
+ * page tables and positions; the GPU executes through zr_forward.
+ *
+ * Page tables reproduce the reference bit for bit: session-local page ids
+ * with a LIFO free list, span block tables with a first-span start row after
+ * retain_suffix, a sliding window of max_seq_len tokens.  Each local page is
+ * bound to one global page of the KV pool when it is first allocated.
+ */
+#ifndef ZIP_ROCM_HOST_H
+#define ZIP_ROCM_HOST_H
+
+#include "zip_rocm.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Global page allocator of a context's KV pool (LIFO).  initial_order
+ * (nullable, n entries) is the initial free list; pages are popped from its
+ * end.  NULL means pages come out 0, 1, 2, ...  With ctx == NULL the pool is
+ * bookkeeping-only (n pages, no device): page tables, reserve and trim work,
+ * compute and KV transfer calls fail with ZR_E_INVALID. */
+typedef struct zrh_pool zrh_pool;
+zr_status zrh_pool_create(zr_context* ctx, const int* initial_order, int n, zrh_pool** out);
+void zrh_pool_destroy(zrh_pool* pool);
+int zrh_pool_free_pages(const zrh_pool* pool);
+
+typedef struct zrh_backend zrh_backend;
+/* ForwardPass::from_residency (forward_pass.rs:1781-1824); the reference
+ * hard-codes max_seq_len 4096 (1795), configs with longer contexts pass 8192. */
+zr_status zrh_backend_create(zrh_pool* pool, int max_seq_len, zrh_backend** out);
+void zrh_backend_destroy(zrh_backend* b); /* returns its global pages to the pool */
+
+/* ForwardPass::prefill (2089-2112): clears the cache, keeps the last window.
+ * logits [vocab] (nullable), greedy (nullable). */
+zr_status zrh_prefill(zrh_backend* b, const uint32_t* tokens, int n, float* logits, uint32_t* greedy);
+/* ForwardPass::decode_step (2115-2139). */
+zr_status zrh_decode_step(zrh_backend* b, uint32_t token, float* logits, uint32_t* greedy);
+/* BackendMicrobatchExecutor::decode_step_batch (backend.rs:110-151) on the
+ * fast path: one fused microbatch over n sessions of one context.
+ * out_tokens [n] greedy, out_logits [n, vocab], out_partials
+ * [layers][2][n][hidden] -- each nullable. */
+zr_status zrh_decode_step_batch(zrh_backend* const* backends, int n, const uint32_t* tokens, uint32_t* out_tokens,
+                                float* out_logits, float* out_partials);
+/* Mixed chunked-prefill + decode microbatch: session i appends q_len[i]
+ * tokens at its current position (tokens packed back to back); logits come
+ * from the last row of every session. */
+zr_status zrh_forward_mixed(zrh_backend* const* backends, int n, const int* q_len, const uint32_t* tokens,
+                            uint32_t* out_tokens, float* out_logits, float* out_partials);
+/* Same bookkeeping as zrh_forward_mixed but only stages the microbatch for
+ * device-resident replay (zr_forward_staged_async); positions advance. */
+zr_status zrh_stage_mixed(zrh_backend* const* backends, int n, const int* q_len, const uint32_t* tokens,
+                          zr_staged** out);
+
+int zrh_cache_seq_len(const zrh_backend* b);
+int zrh_sequence_position(const zrh_backend* b);
+int zrh_logical_kv_tokens(const zrh_backend* b);
+int zrh_base_position(const zrh_backend* b);
+uint64_t zrh_live_kv_cache_bytes(const zrh_backend* b);
+int zrh_allocated_pages(const zrh_backend* b);
+/* LiveKVBlockTable of the session (kv_cache.rs:325-438): spans in
+ * session-local page ids, plus the global pool page of each span.  Returns
+ * the span count (or <0); arrays may be NULL to query the count. */
+int zrh_block_table(const zrh_backend* b, uint32_t* page_ids, int* start_tokens, int* token_counts,
+                    int* global_pages, int capacity);
+
+/* export_kv_cache (forward_pass.rs:2442-2448 -> 1169-1204) with the segmented
+ * retention window: the newest min(seq_len, max(max_cached_tokens, 1)) rows
+ * (all rows if max_cached_tokens < 0) gathered from the pool, f32
+ * [layers][rows][kv_cols].  *rows = 0 means no snapshot (empty cache). */
+zr_status zrh_export_kv(const zrh_backend* b, int max_cached_tokens, float* k, float* v, int* rows,
+                        int* base_position, int* next_position);
+/* import_kv_cache (2450-2454 -> 1206-1242): clears, scatters the rows into
+ * fresh pages, validates cached_tokens and base_position. */
+zr_status zrh_import_kv(zrh_backend* b, const float* k, const float* v, int rows, int base_position,
+                        int next_position);
+/* ForwardPass::clear_cache (2423-2426). */
+void zrh_clear(zrh_backend* b);
+/* Eviction under KV pressure: every global page bound to the session goes
+ * back to the pool; the session restarts empty at position 0. */
+zr_status zrh_release_pages(zrh_backend* b);
+
+/* Page-table state machine without compute, for allocator checks:
+ * DeviceKVCache::append_layer over all layers (rows appended, window trim
+ * included) and DeviceKVCache::retain_suffix. */
+zr_status zrh_kv_reserve(zrh_backend* b, int rows);
+zr_status zrh_retain_suffix(zrh_backend* b, int keep_rows);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,13 @@
+"""mesh_amd -- MI355X (gfx950) `rocm` execution provider for the zip engine.
+
+The compute path is libzip_rocm.so (hand-written HIP kernels + C ABI,
+include/zip_rocm.h); this package is its Python mirror of zip's provider
+interface (mesh_amd.provider).
+"""
+from .provider import (BackendMicrobatchExecutor, DecodeMicrobatchOutput, DecodeMicrobatchRequest,
+                       DeviceBuffer, DeviceContext, ExecutionProviderKind, KVCacheSnapshot, ModelGeometry,
+                       RocmExecutionBackend, bf16_bits, device_info, probe_provider)
+
+__all__ = ["BackendMicrobatchExecutor", "DecodeMicrobatchOutput", "DecodeMicrobatchRequest", "DeviceBuffer",
+           "DeviceContext", "ExecutionProviderKind", "KVCacheSnapshot", "ModelGeometry", "RocmExecutionBackend",
+           "bf16_bits", "device_info", "probe_provider"]

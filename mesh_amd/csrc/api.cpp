@@ -1,0 +1,858 @@
+// C ABI entry points of the zip MI355X provider (include/zip_rocm.h):
+// context and weight residency, KV pool, microbatch staging and the decode /
+// prefill forward pass (ForwardPass::fast_path_decode_microbatch,
+// agent/src/inference/forward_pass.rs:2143-2319).
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <cstdlib>
+
+#include "zr_internal.h"
+
+namespace zr {
+
+zr_status pack_weight_gate_up(zr_context* ctx, const uint16_t* gate, const uint16_t* up, int k, int f,
+                              uint16_t** out);
+
+static thread_local std::string g_err;
+
+zr_status set_err(zr_context* ctx, zr_status code, const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (ctx) ctx->err = buf;
+    g_err = buf;
+    return code;
+}
+
+zr_status set_global_err(zr_status code, const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+// ------------------------------------------------------------- timing
+void timing_mark_begin(zr_context* ctx, int, hipEvent_t* out) {
+    *out = nullptr;
+    TimingState& t = ctx->timing;
+    if (!t.enabled) return;
+    if (t.next_event + 2 > t.pool.size()) {
+        for (int i = 0; i < 64; ++i) {
+            hipEvent_t e;
+            if (hipEventCreate(&e) != hipSuccess) return;
+            t.pool.push_back(e);
+        }
+    }
+    *out = t.pool[t.next_event++];
+    hipEventRecord(*out, ctx->stream);
+}
+
+void timing_mark_end(zr_context* ctx, int cls, hipEvent_t begin) {
+    TimingState& t = ctx->timing;
+    if (!t.enabled || !begin) return;
+    hipEvent_t e = t.pool[t.next_event++];
+    hipEventRecord(e, ctx->stream);
+    t.spans.push_back({cls, {begin, e}});
+}
+
+// ------------------------------------------------------------- geometry
+// resolve_attention_shard_layout (forward_pass.rs:1257-1315) and
+// build_local_kv_head_indices (2951-2970).
+static zr_status resolve_geometry(zr_context* ctx) {
+    const zr_model_desc& d = ctx->desc;
+    if (d.num_heads <= 0 || d.hidden % d.num_heads != 0)
+        return set_err(ctx, ZR_E_INVALID, "Unsupported attention geometry: hidden_dim %d num_heads %d", d.hidden,
+                       d.num_heads);
+    if (d.num_kv_heads <= 0 || d.num_heads % d.num_kv_heads != 0)
+        return set_err(ctx, ZR_E_INVALID,
+                       "Unsupported grouped-query attention geometry: num_heads %d num_kv_heads %d", d.num_heads,
+                       d.num_kv_heads);
+    if (d.shard_start >= d.shard_end || d.shard_end > d.hidden || d.shard_start < 0)
+        return set_err(ctx, ZR_E_INVALID, "Invalid shard range %d..%d for hidden_dim %d", d.shard_start,
+                       d.shard_end, d.hidden);
+    const int head_dim = d.hidden / d.num_heads;
+    const int qpk = d.num_heads / d.num_kv_heads;
+    const int group = qpk * head_dim;
+    if (d.hidden % group != 0)
+        return set_err(ctx, ZR_E_INVALID, "Hidden dim %d is not divisible by grouped-query shard width %d",
+                       d.hidden, group);
+    if (d.shard_start % group != 0 || d.shard_end % group != 0)
+        return set_err(ctx, ZR_E_INVALID, "Shard range %d..%d is not aligned to grouped-query shard width %d",
+                       d.shard_start, d.shard_end, group);
+    ctx->head_dim = head_dim;
+    ctx->q_per_kv = qpk;
+    ctx->q_cols = d.shard_end - d.shard_start;
+    const int groups = ctx->q_cols / group;
+    ctx->local_q_heads = groups * qpk;
+    ctx->local_kv_heads = groups;
+    ctx->kv_cols = groups * head_dim;
+    ctx->q_head_start = d.shard_start / head_dim;
+    ctx->kv_head_start = d.shard_start / group;
+    ctx->kv_head_map.clear();
+    for (int i = 0; i < ctx->local_q_heads; ++i) {
+        const int gq = ctx->q_head_start + i, gk = gq / qpk;
+        if (gk < ctx->kv_head_start || gk >= ctx->kv_head_start + ctx->local_kv_heads)
+            return set_err(ctx, ZR_E_INVARIANT, "Local KV head ownership mismatch: q_head %d maps to kv_head %d", gq,
+                           gk);
+        ctx->kv_head_map.push_back((uint32_t)(gk - ctx->kv_head_start));
+    }
+    if (head_dim != 64 && head_dim != 128)
+        return set_err(ctx, ZR_E_UNSUPPORTED, "head_dim %d not supported (64 or 128)", head_dim);
+    if (qpk > 16) return set_err(ctx, ZR_E_UNSUPPORTED, "more than 16 q heads per kv head (%d)", qpk);
+    if (16 % qpk != 0) return set_err(ctx, ZR_E_UNSUPPORTED, "q heads per kv head (%d) must divide 16", qpk);
+    return ZR_OK;
+}
+
+// Split-K plan shared by launch_gemm and the workspace sizing.
+static size_t gemm_ws_floats(int m, int n, int k, int epilogue) {
+    const int KT = (k + 31) / 32, NT = (n + 15) / 16;
+    const int wm = m <= 16 ? 1 : m <= 32 ? 2 : m <= 64 ? 4 : m <= 128 ? 8 : 16;
+    const int row_blocks = (m + wm * 16 - 1) / (wm * 16);
+    const int col_blocks = (NT + 7) / 8;
+    int splits = 1;
+    while (col_blocks * row_blocks * splits < 512 && KT / (splits * 2) >= 8) splits *= 2;
+    const int kps = (KT + splits - 1) / splits;
+    splits = (KT + kps - 1) / kps;
+    if (splits == 1 && epilogue == kEpiStore) return 0;
+    return (size_t)splits * m * n;
+}
+
+static void free_ctx_buffers(zr_context* ctx) {
+    void* bufs[] = {ctx->hidden, ctx->xn, ctx->qkv, ctx->q_rope, ctx->attn, ctx->proj, ctx->ffn,
+                    ctx->logits, ctx->final_x, ctx->tokens_out, ctx->splitk_ws, ctx->attn_part,
+                    ctx->argmax_ws, ctx->inv_freq, ctx->kv_pool, ctx->embedding, ctx->lm_head,
+                    ctx->final_norm};
+    for (void* b : bufs)
+        if (b) hipFree(b);
+    for (auto& L : ctx->layers) {
+        void* lb[] = {L.w_qkv, L.w_o, L.w_gate_up, L.w_down, L.attn_norm, L.mlp_norm};
+        for (void* b : lb)
+            if (b) hipFree(b);
+    }
+}
+
+// ----------------------------------------------------------------- staging
+static inline size_t align16(size_t x) { return (x + 15) & ~(size_t)15; }
+
+zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta* st) {
+    if (!mb) return set_err(ctx, ZR_E_INVALID, "null microbatch");
+    const int S = mb->num_seqs;
+    if (S <= 0 || S > ctx->desc.max_seqs)
+        return set_err(ctx, ZR_E_INVALID, "microbatch has %d sequences (capacity %d)", S, ctx->desc.max_seqs);
+    if (!mb->q_len || !mb->kv_before || !mb->first_pos || !mb->first_offset || !mb->block_tables)
+        return set_err(ctx, ZR_E_INVALID, "microbatch arrays must not be null");
+    const int stride = mb->block_table_stride;
+    if (stride <= 0 || stride > ctx->desc.max_pages_per_seq)
+        return set_err(ctx, ZR_E_INVALID, "block table stride %d outside 1..%d", stride, ctx->desc.max_pages_per_seq);
+    if (!ctx->kv_pool) return set_err(ctx, ZR_E_INVALID, "KV pool not created");
+    int total_q = 0, max_kv = 0;
+    for (int s = 0; s < S; ++s) {
+        const int ql = mb->q_len[s], kb = mb->kv_before[s], fo = mb->first_offset[s];
+        if (ql <= 0) return set_err(ctx, ZR_E_INVALID, "sequence %d has q_len %d", s, ql);
+        if (kb < 0 || fo < 0 || fo >= kPageRows || mb->first_pos[s] < 0)
+            return set_err(ctx, ZR_E_INVALID, "sequence %d has kv_before %d first_offset %d first_pos %d", s, kb, fo,
+                           mb->first_pos[s]);
+        if (mb->first_pos[s] < kb)
+            return set_err(ctx, ZR_E_INVARIANT, "sequence %d: first_pos %d precedes %d cached rows", s,
+                           mb->first_pos[s], kb);
+        const long need = ((long)fo + kb + ql + kPageRows - 1) / kPageRows;
+        if (need > stride)
+            return set_err(ctx, ZR_E_INVALID, "sequence %d needs %ld pages, block table holds %d", s, need, stride);
+        for (long p = 0; p < need; ++p) {
+            const int id = mb->block_tables[(size_t)s * stride + p];
+            if (id < 0 || id >= ctx->n_pages)
+                return set_err(ctx, ZR_E_INVARIANT, "sequence %d page slot %ld holds page %d outside pool of %d", s, p,
+                               id, ctx->n_pages);
+        }
+        total_q += ql;
+        max_kv = std::max(max_kv, kb + ql);
+    }
+    if (total_q > ctx->desc.max_tokens)
+        return set_err(ctx, ZR_E_INVALID, "microbatch has %d tokens (capacity %d)", total_q, ctx->desc.max_tokens);
+    if (mb->tokens)
+        for (int t = 0; t < total_q; ++t)
+            if (mb->tokens[t] >= (uint32_t)ctx->desc.vocab)
+                return set_err(ctx, ZR_E_INVALID, "Token %u out of vocabulary bounds %d", mb->tokens[t],
+                               ctx->desc.vocab);
+
+    st->ctx = ctx;
+    st->num_seqs = S;
+    st->total_q = total_q;
+    st->stride = stride;
+    st->max_kv = max_kv;
+
+    // attention tiles / split items
+    const int G = ctx->q_per_kv, qpt = 16 / G;
+    st->h_tiles.clear();
+    st->h_items.clear();
+    std::vector<int> tile_pages;
+    long total_pages = 0;
+    for (int s = 0; s < S; ++s) {
+        const int ql = mb->q_len[s], kb = mb->kv_before[s], fo = mb->first_offset[s];
+        for (int q0 = 0; q0 < ql; q0 += qpt) {
+            const int nq = std::min(qpt, ql - q0);
+            const int last_visible = kb + q0 + nq - 1;  // logical index of the tile's last key
+            const int pages = (fo + last_visible + 1 + kPageRows - 1) / kPageRows;
+            st->h_tiles.push_back(make_int4(s, q0, nq, 0));
+            tile_pages.push_back(pages);
+            total_pages += pages;
+        }
+    }
+    const long target_wgs = 8192;
+    int pps = (int)std::min<long>(4096, std::max<long>(4, (total_pages * ctx->local_kv_heads + target_wgs - 1) / target_wgs));
+    if (const char* env = getenv("ZR_ATTN_PAGES_PER_SPLIT")) pps = std::max(1, atoi(env));
+    for (size_t t = 0; t < st->h_tiles.size(); ++t) {
+        st->h_tiles[t].w = (int)st->h_items.size();
+        for (int pb = 0; pb < tile_pages[t]; pb += pps)
+            st->h_items.push_back(make_int4((int)t, pb, std::min(tile_pages[t], pb + pps), 0));
+    }
+    st->h_tiles.push_back(make_int4(0, 0, 0, (int)st->h_items.size()));  // sentinel
+    st->n_tiles = (int)st->h_tiles.size() - 1;
+    st->n_attn_items = (int)st->h_items.size();
+
+    const size_t need_part = (size_t)st->n_attn_items * ctx->local_kv_heads * 16 * (ctx->head_dim + 2);
+    if (need_part > ctx->attn_part_floats) {
+        hipStreamSynchronize(ctx->stream);
+        if (ctx->attn_part) hipFree(ctx->attn_part);
+        ctx->attn_part = nullptr;
+        ctx->attn_part_floats = 0;
+        ZR_HIP(ctx, hipMalloc(&ctx->attn_part, need_part * sizeof(float)));
+        ctx->attn_part_floats = need_part;
+    }
+
+    // one blob: inputs, derived arrays, attention items
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off = align16(off + bytes);
+        return o;
+    };
+    const size_t o_qlen = take(4 * S), o_kvb = take(4 * S), o_fpos = take(4 * S), o_foff = take(4 * S);
+    const size_t o_bt = take(4 * (size_t)S * stride), o_tok = take(4 * (size_t)std::max(total_q, 1));
+    const size_t o_items = take(16 * (size_t)st->n_attn_items), o_tiles = take(16 * st->h_tiles.size());
+    const size_t host_bytes = off;
+    const size_t o_cuq = take(4 * (S + 1)), o_cuk = take(4 * (S + 1)), o_pos = take(4 * (size_t)total_q);
+    const size_t o_slot = take(4 * (size_t)total_q), o_seq = take(4 * (size_t)total_q), o_last = take(4 * S);
+    const size_t total_bytes = off;
+    if (total_bytes > st->cap_bytes) {
+        hipStreamSynchronize(ctx->stream);
+        if (st->dev) hipFree(st->dev);
+        st->dev = nullptr;
+        st->cap_bytes = 0;
+        ZR_HIP(ctx, hipMalloc(&st->dev, total_bytes));
+        st->cap_bytes = total_bytes;
+    }
+    st->dev_bytes = total_bytes;
+    st->h_blob.assign(host_bytes, 0);
+    unsigned char* hb = st->h_blob.data();
+    memcpy(hb + o_qlen, mb->q_len, 4 * S);
+    memcpy(hb + o_kvb, mb->kv_before, 4 * S);
+    memcpy(hb + o_fpos, mb->first_pos, 4 * S);
+    memcpy(hb + o_foff, mb->first_offset, 4 * S);
+    memcpy(hb + o_bt, mb->block_tables, 4 * (size_t)S * stride);
+    if (mb->tokens) memcpy(hb + o_tok, mb->tokens, 4 * (size_t)total_q);
+    memcpy(hb + o_items, st->h_items.data(), 16 * (size_t)st->n_attn_items);
+    memcpy(hb + o_tiles, st->h_tiles.data(), 16 * st->h_tiles.size());
+    unsigned char* db = (unsigned char*)st->dev;
+    st->q_len = (int*)(db + o_qlen);
+    st->kv_before = (int*)(db + o_kvb);
+    st->first_pos = (int*)(db + o_fpos);
+    st->first_offset = (int*)(db + o_foff);
+    st->block_tables = (int*)(db + o_bt);
+    st->tokens = (uint32_t*)(db + o_tok);
+    st->attn_items = (int4*)(db + o_items);
+    st->attn_tiles = (int4*)(db + o_tiles);
+    st->cu_q = (int*)(db + o_cuq);
+    st->cu_k = (int*)(db + o_cuk);
+    st->positions = (int*)(db + o_pos);
+    st->slot_mapping = (int*)(db + o_slot);
+    st->seq_ids = (int*)(db + o_seq);
+    st->last_rows = (int*)(db + o_last);
+    st->h_q_len.assign(mb->q_len, mb->q_len + S);
+    st->h_kv_before.assign(mb->kv_before, mb->kv_before + S);
+    ZR_HIP(ctx, hipMemcpyAsync(st->dev, hb, host_bytes, hipMemcpyHostToDevice, ctx->stream));
+    return launch_pack(ctx, st);
+}
+
+// ----------------------------------------------------------- forward pass
+static zr_status check_ready(zr_context* ctx) {
+    if (!ctx->embedding || !ctx->lm_head || !ctx->final_norm)
+        return set_err(ctx, ZR_E_INVALID, "global weights not uploaded");
+    for (int l = 0; l < ctx->desc.num_layers; ++l)
+        if (!ctx->layers[l].w_qkv) return set_err(ctx, ZR_E_INVALID, "layer %d weights not uploaded", l);
+    if (!ctx->kv_pool) return set_err(ctx, ZR_E_INVALID, "KV pool not created");
+    return ZR_OK;
+}
+
+static zr_status run_forward(zr_context* ctx, StagedMeta* st, const uint32_t* d_tokens, uint32_t* d_out_tokens,
+                             float* d_out_logits, float* h_partials) {
+    zr_status rc = check_ready(ctx);
+    if (rc) return rc;
+    const zr_model_desc& d = ctx->desc;
+    const int T = st->total_q, S = st->num_seqs, H = d.hidden, F = d.ffn_cols;
+    const int QKV = ctx->q_cols + 2 * ctx->kv_cols;
+    if ((rc = launch_embed(ctx, st, d_tokens ? d_tokens : st->tokens))) return rc;
+    for (int l = 0; l < d.num_layers; ++l) {
+        const LayerDev& L = ctx->layers[l];
+        // hidden += previous down partial; xn = rms_norm(hidden) * attn_norm
+        if ((rc = launch_rms_norm(ctx, ctx->hidden, l > 0 ? ctx->proj : nullptr, ctx->hidden, L.attn_norm, ctx->xn,
+                                  nullptr, T, H)))
+            return rc;
+        if ((rc = launch_gemm(ctx, ctx->xn, L.w_qkv, ctx->qkv, T, QKV, H, kEpiStore))) return rc;
+        if ((rc = launch_rope_kv_write(ctx, st, l, ctx->qkv, ctx->q_rope, 1))) return rc;
+        if ((rc = launch_attention(ctx, st, l, ctx->q_rope, ctx->attn))) return rc;
+        if ((rc = launch_gemm(ctx, ctx->attn, L.w_o, ctx->proj, T, H, ctx->q_cols, kEpiStore))) return rc;
+        if (h_partials)
+            ZR_HIP(ctx, hipMemcpyAsync(h_partials + ((size_t)l * 2 + 0) * T * H, ctx->proj, sizeof(float) * T * H,
+                                       hipMemcpyDeviceToHost, ctx->stream));
+        // post_attn = hidden + o_partial (identity all-reduce at one worker)
+        if ((rc = launch_rms_norm(ctx, ctx->hidden, ctx->proj, ctx->hidden, L.mlp_norm, ctx->xn, nullptr, T, H)))
+            return rc;
+        if ((rc = launch_gemm(ctx, ctx->xn, L.w_gate_up, ctx->ffn, T, 2 * F, H, kEpiSwiGLU))) return rc;
+        if ((rc = launch_gemm(ctx, ctx->ffn, L.w_down, ctx->proj, T, H, F, kEpiStore))) return rc;
+        if (h_partials)
+            ZR_HIP(ctx, hipMemcpyAsync(h_partials + ((size_t)l * 2 + 1) * T * H, ctx->proj, sizeof(float) * T * H,
+                                       hipMemcpyDeviceToHost, ctx->stream));
+    }
+    // final residual + norm on the last row of every sequence, LM head, argmax
+    if ((rc = launch_rms_norm(ctx, ctx->hidden, ctx->proj, ctx->hidden, ctx->final_norm, ctx->final_x, st->last_rows,
+                              S, H)))
+        return rc;
+    float* logits = ctx->logits;
+    if ((rc = launch_gemm(ctx, ctx->final_x, ctx->lm_head, logits, S, d.vocab, H, kEpiStore))) return rc;
+    if ((rc = launch_argmax(ctx, logits, S, d.vocab, d_out_tokens ? d_out_tokens : ctx->tokens_out))) return rc;
+    if (d_out_logits)
+        ZR_HIP(ctx, hipMemcpyAsync(d_out_logits, logits, sizeof(float) * S * d.vocab, hipMemcpyDeviceToDevice,
+                                   ctx->stream));
+    return ZR_OK;
+}
+
+}  // namespace zr
+
+using namespace zr;
+
+// ============================================================ C ABI ======
+extern "C" {
+
+const char* zr_global_last_error(void) { return g_err.c_str(); }
+const char* zr_last_error(const zr_context* ctx) { return ctx ? ctx->err.c_str() : g_err.c_str(); }
+
+zr_status zr_probe(int device, zr_device_info* out) {
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count == 0)
+        return set_global_err(ZR_E_NODEVICE, "no HIP device available (%s)", hipGetErrorString(e));
+    if (device < 0 || device >= count) return set_global_err(ZR_E_INVALID, "device %d outside 0..%d", device, count - 1);
+    hipDeviceProp_t p;
+    e = hipGetDeviceProperties(&p, device);
+    if (e != hipSuccess) return set_global_err(ZR_E_HIP, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+    if (out) {
+        memset(out, 0, sizeof *out);
+        out->device_count = count;
+        out->device = device;
+        out->compute_units = p.multiProcessorCount;
+        out->clock_mhz = p.clockRate / 1000;
+        out->hbm_bytes = p.totalGlobalMem;
+        snprintf(out->arch, sizeof out->arch, "%s", p.gcnArchName);
+    }
+    if (strncmp(p.gcnArchName, "gfx950", 6) != 0)
+        return set_global_err(ZR_E_NODEVICE, "device %d is %s, this provider is built for gfx950", device,
+                              p.gcnArchName);
+    return ZR_OK;
+}
+
+zr_status zr_context_create(const zr_model_desc* desc, int device, zr_context** out) {
+    if (!desc || !out) return set_global_err(ZR_E_INVALID, "null argument");
+    *out = nullptr;
+    zr_status rc = ZR_OK;
+    zr_context* ctx = new zr_context();
+    ctx->desc = *desc;
+    ctx->device = device;
+    const zr_model_desc& d = ctx->desc;
+    if (d.page_tokens != kPageRows) rc = set_err(ctx, ZR_E_UNSUPPORTED, "page_tokens must be 16, got %d", d.page_tokens);
+    else if (d.kv_dtype != ZR_DTYPE_BF16 && d.kv_dtype != ZR_DTYPE_F32) rc = set_err(ctx, ZR_E_INVALID, "kv_dtype %d", d.kv_dtype);
+    else if (d.num_layers <= 0 || d.vocab <= 0 || d.ffn_cols <= 0 || d.max_tokens <= 0 || d.max_seqs <= 0 ||
+             d.max_pages_per_seq <= 0)
+        rc = set_err(ctx, ZR_E_INVALID, "model descriptor has a non-positive size");
+    else if (d.hidden % 32 != 0 || d.ffn_cols % 32 != 0)
+        rc = set_err(ctx, ZR_E_UNSUPPORTED, "hidden %d / ffn %d must be multiples of 32", d.hidden, d.ffn_cols);
+    if (!rc) rc = resolve_geometry(ctx);
+    if (!rc) {
+        rc = zr_probe(device, nullptr);  // geometry errors are reported before device errors
+        if (rc) ctx->err = g_err;
+    }
+    if (rc) {
+        set_global_err(rc, "%s", ctx->err.c_str());
+        delete ctx;
+        return rc;
+    }
+    auto fail = [&](hipError_t e, const char* what) {
+        set_global_err(ZR_E_HIP, "%s: %s", what, hipGetErrorString(e));
+        free_ctx_buffers(ctx);
+        if (ctx->stream) hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return e == hipErrorOutOfMemory ? ZR_E_OOM : ZR_E_HIP;
+    };
+    hipError_t e = hipSetDevice(device);
+    if (e != hipSuccess) return fail(e, "hipSetDevice");
+    e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) return fail(e, "hipStreamCreate");
+    const size_t T = d.max_tokens, S = d.max_seqs, H = d.hidden, Q = ctx->q_cols, KV = ctx->kv_cols, F = d.ffn_cols;
+    struct {
+        void** p;
+        size_t bytes;
+    } allocs[] = {
+        {(void**)&ctx->hidden, 4 * T * H},           {(void**)&ctx->xn, 4 * T * H},
+        {(void**)&ctx->qkv, 4 * T * (Q + 2 * KV)},   {(void**)&ctx->q_rope, 4 * T * Q},
+        {(void**)&ctx->attn, 4 * T * Q},             {(void**)&ctx->proj, 4 * T * H},
+        {(void**)&ctx->ffn, 4 * T * 2 * F},          {(void**)&ctx->logits, 4 * S * d.vocab},
+        {(void**)&ctx->final_x, 4 * S * H},          {(void**)&ctx->tokens_out, 4 * S},
+        {(void**)&ctx->inv_freq, 4 * (size_t)ctx->head_dim / 2},
+    };
+    for (auto& a : allocs) {
+        e = hipMalloc(a.p, a.bytes);
+        if (e != hipSuccess) return fail(e, "hipMalloc activations");
+    }
+    // split-K workspace: max over microbatch row counts of every GEMM shape
+    size_t ws = 0;
+    for (size_t m = 1; m <= T + 15; m += (m < 16 ? 15 : 16)) {
+        const int mm = (int)std::min(m, T);
+        ws = std::max(ws, gemm_ws_floats(mm, (int)(Q + 2 * KV), (int)H, kEpiStore));
+        ws = std::max(ws, gemm_ws_floats(mm, (int)H, (int)Q, kEpiStore));
+        ws = std::max(ws, gemm_ws_floats(mm, (int)(2 * F), (int)H, kEpiSwiGLU));
+        ws = std::max(ws, gemm_ws_floats(mm, (int)H, (int)F, kEpiStore));
+        if (m <= S) ws = std::max(ws, gemm_ws_floats(mm, d.vocab, (int)H, kEpiStore));
+    }
+    ws = std::max<size_t>(ws, 1);
+    e = hipMalloc(&ctx->splitk_ws, ws * 4);
+    if (e != hipSuccess) return fail(e, "hipMalloc split-K workspace");
+    ctx->splitk_ws_floats = ws;
+    ctx->argmax_ws_floats = S * ((d.vocab + 4095) / 4096) * 2;
+    e = hipMalloc(&ctx->argmax_ws, ctx->argmax_ws_floats * 4);
+    if (e != hipSuccess) return fail(e, "hipMalloc argmax workspace");
+    // RoPE inverse frequencies with the host powf, exactly as the reference
+    // builds them (runtime.rs:282-301): 1 / base^(2i / d) in f32.
+    std::vector<float> inv(ctx->head_dim / 2);
+    for (int i = 0; i < ctx->head_dim / 2; ++i)
+        inv[i] = 1.0f / powf(d.rope_base, (float)i * 2.0f / (float)ctx->head_dim);
+    e = hipMemcpy(ctx->inv_freq, inv.data(), inv.size() * 4, hipMemcpyHostToDevice);
+    if (e != hipSuccess) return fail(e, "hipMemcpy inv_freq");
+    ctx->layers.resize(d.num_layers);
+    ctx->scratch_stage = new StagedMeta();
+    *out = ctx;
+    return ZR_OK;
+}
+
+void zr_context_destroy(zr_context* ctx) {
+    if (!ctx) return;
+    hipSetDevice(ctx->device);
+    if (ctx->stream) hipStreamSynchronize(ctx->stream);
+    if (ctx->scratch_stage) {
+        if (ctx->scratch_stage->dev) hipFree(ctx->scratch_stage->dev);
+        delete ctx->scratch_stage;
+    }
+    for (hipEvent_t e : ctx->timing.pool) hipEventDestroy(e);
+    free_ctx_buffers(ctx);
+    if (ctx->stream) hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+zr_status zr_kv_head_map(const zr_context* ctx, uint32_t* out, int capacity, int* count) {
+    if (!ctx) return set_global_err(ZR_E_INVALID, "null context");
+    if (count) *count = (int)ctx->kv_head_map.size();
+    if (out) {
+        if (capacity < (int)ctx->kv_head_map.size()) return set_global_err(ZR_E_INVALID, "capacity too small");
+        std::copy(ctx->kv_head_map.begin(), ctx->kv_head_map.end(), out);
+    }
+    return ZR_OK;
+}
+
+zr_status zr_upload_layer(zr_context* ctx, int layer, const zr_layer_weights* w) {
+    if (!ctx || !w) return set_global_err(ZR_E_INVALID, "null argument");
+    if (layer < 0 || layer >= ctx->desc.num_layers) return set_err(ctx, ZR_E_INVALID, "Invalid layer index: %d", layer);
+    if (!w->w_q || !w->w_k || !w->w_v || !w->w_o || !w->w_gate || !w->w_up || !w->w_down || !w->attn_norm ||
+        !w->mlp_norm)
+        return set_err(ctx, ZR_E_INVALID, "layer %d: null weight pointer", layer);
+    ZR_HIP(ctx, hipSetDevice(ctx->device));
+    LayerDev& L = ctx->layers[layer];
+    LayerDev fresh;
+    const int H = ctx->desc.hidden, F = ctx->desc.ffn_cols;
+    const uint16_t* qkv[3] = {w->w_q, w->w_k, w->w_v};
+    const int widths[3] = {ctx->q_cols, ctx->kv_cols, ctx->kv_cols};
+    zr_status rc = pack_weight_concat(ctx, qkv, widths, 3, H, &fresh.w_qkv);
+    if (!rc) rc = pack_weight(ctx, w->w_o, ctx->q_cols, H, &fresh.w_o);
+    if (!rc) rc = pack_weight_gate_up(ctx, w->w_gate, w->w_up, H, F, &fresh.w_gate_up);
+    if (!rc) rc = pack_weight(ctx, w->w_down, F, H, &fresh.w_down);
+    if (!rc) {
+        hipError_t e = hipMalloc(&fresh.attn_norm, 4 * (size_t)H);
+        if (e == hipSuccess) e = hipMalloc(&fresh.mlp_norm, 4 * (size_t)H);
+        if (e == hipSuccess) e = hipMemcpy(fresh.attn_norm, w->attn_norm, 4 * (size_t)H, hipMemcpyDefault);
+        if (e == hipSuccess) e = hipMemcpy(fresh.mlp_norm, w->mlp_norm, 4 * (size_t)H, hipMemcpyDefault);
+        if (e != hipSuccess) rc = set_err(ctx, ZR_E_HIP, "norm upload: %s", hipGetErrorString(e));
+    }
+    if (rc) {
+        void* lb[] = {fresh.w_qkv, fresh.w_o, fresh.w_gate_up, fresh.w_down, fresh.attn_norm, fresh.mlp_norm};
+        for (void* b : lb)
+            if (b) hipFree(b);
+        return rc;
+    }
+    void* old[] = {L.w_qkv, L.w_o, L.w_gate_up, L.w_down, L.attn_norm, L.mlp_norm};
+    for (void* b : old)
+        if (b) hipFree(b);
+    L = fresh;
+    return ZR_OK;
+}
+
+zr_status zr_upload_globals(zr_context* ctx, const uint16_t* embedding, const float* final_norm,
+                            const uint16_t* lm_head) {
+    if (!ctx || !embedding || !final_norm || !lm_head) return set_global_err(ZR_E_INVALID, "null argument");
+    ZR_HIP(ctx, hipSetDevice(ctx->device));
+    const size_t H = ctx->desc.hidden, V = ctx->desc.vocab;
+    uint16_t* emb = nullptr;
+    float* fn = nullptr;
+    uint16_t* head = nullptr;
+    hipError_t e = hipMalloc(&emb, 2 * V * H);
+    if (e == hipSuccess) e = hipMemcpy(emb, embedding, 2 * V * H, hipMemcpyDefault);
+    if (e == hipSuccess) e = hipMalloc(&fn, 4 * H);
+    if (e == hipSuccess) e = hipMemcpy(fn, final_norm, 4 * H, hipMemcpyDefault);
+    zr_status rc = e == hipSuccess ? ZR_OK : set_err(ctx, ZR_E_HIP, "global upload: %s", hipGetErrorString(e));
+    if (!rc) rc = pack_weight(ctx, lm_head, (int)H, (int)V, &head);
+    if (rc) {
+        if (emb) hipFree(emb);
+        if (fn) hipFree(fn);
+        if (head) hipFree(head);
+        return rc;
+    }
+    if (ctx->embedding) hipFree(ctx->embedding);
+    if (ctx->final_norm) hipFree(ctx->final_norm);
+    if (ctx->lm_head) hipFree(ctx->lm_head);
+    ctx->embedding = emb;
+    ctx->final_norm = fn;
+    ctx->lm_head = head;
+    return ZR_OK;
+}
+
+zr_status zr_kv_pool_create(zr_context* ctx, int n_pages) {
+    if (!ctx) return set_global_err(ZR_E_INVALID, "null context");
+    if (n_pages <= 0) return set_err(ctx, ZR_E_INVALID, "n_pages %d", n_pages);
+    ZR_HIP(ctx, hipSetDevice(ctx->device));
+    const size_t esz = ctx->desc.kv_dtype == ZR_DTYPE_BF16 ? 2 : 4;
+    const size_t page_bytes = (size_t)2 * ctx->kv_cols * kPageRows * esz;
+    const size_t total = page_bytes * n_pages * ctx->desc.num_layers;
+    if (ctx->kv_pool) {
+        hipStreamSynchronize(ctx->stream);
+        hipFree(ctx->kv_pool);
+        ctx->kv_pool = nullptr;
+        ctx->n_pages = 0;
+    }
+    hipError_t e = hipMalloc(&ctx->kv_pool, total);
+    if (e != hipSuccess)
+        return set_err(ctx, e == hipErrorOutOfMemory ? ZR_E_OOM : ZR_E_HIP, "KV pool of %zu bytes: %s", total,
+                       hipGetErrorString(e));
+    ZR_HIP(ctx, hipMemsetAsync(ctx->kv_pool, 0, total, ctx->stream));
+    ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    ctx->n_pages = n_pages;
+    ctx->page_bytes = page_bytes;
+    return ZR_OK;
+}
+
+int zr_kv_pool_pages(const zr_context* ctx) { return ctx ? ctx->n_pages : 0; }
+uint64_t zr_kv_pool_bytes(const zr_context* ctx) {
+    return ctx ? (uint64_t)ctx->page_bytes * ctx->n_pages * ctx->desc.num_layers : 0;
+}
+
+zr_status zr_stage(zr_context* ctx, const zr_microbatch* mb, zr_staged** out) {
+    if (!ctx || !out) return set_global_err(ZR_E_INVALID, "null argument");
+    ZR_HIP(ctx, hipSetDevice(ctx->device));
+    StagedMeta* st = new StagedMeta();
+    zr_status rc = stage_microbatch(ctx, mb, st);
+    if (rc) {
+        if (st->dev) hipFree(st->dev);
+        delete st;
+        return rc;
+    }
+    *out = (zr_staged*)st;
+    return ZR_OK;
+}
+
+void zr_staged_destroy(zr_staged* s) {
+    StagedMeta* st = (StagedMeta*)s;
+    if (!st) return;
+    if (st->ctx) hipStreamSynchronize(st->ctx->stream);
+    if (st->dev) hipFree(st->dev);
+    delete st;
+}
+
+zr_status zr_forward_staged_async(zr_context* ctx, zr_staged* s, const uint32_t* d_tokens, uint32_t* d_out_tokens,
+                                  float* d_out_logits) {
+    StagedMeta* st = (StagedMeta*)s;
+    if (!ctx || !st || st->ctx != ctx) return set_global_err(ZR_E_INVALID, "staged microbatch of another context");
+    return run_forward(ctx, st, d_tokens, d_out_tokens, d_out_logits, nullptr);
+}
+
+zr_status zr_synchronize(zr_context* ctx) {
+    if (!ctx) return set_global_err(ZR_E_INVALID, "null context");
+    ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return ZR_OK;
+}
+
+zr_status zr_forward(zr_context* ctx, const zr_microbatch* mb, uint32_t* out_tokens, float* out_logits,
+                     float* out_partials) {
+    if (!ctx || !mb) return set_global_err(ZR_E_INVALID, "null argument");
+    if (!mb->tokens) return set_err(ctx, ZR_E_INVALID, "zr_forward needs host token ids");
+    ZR_HIP(ctx, hipSetDevice(ctx->device));
+    StagedMeta* st = ctx->scratch_stage;
+    zr_status rc = stage_microbatch(ctx, mb, st);
+    if (!rc) rc = run_forward(ctx, st, nullptr, ctx->tokens_out, nullptr, out_partials);
+    if (!rc && out_tokens)
+        ZR_HIP(ctx, hipMemcpyAsync(out_tokens, ctx->tokens_out, 4 * (size_t)mb->num_seqs, hipMemcpyDeviceToHost,
+                                   ctx->stream));
+    if (!rc && out_logits)
+        ZR_HIP(ctx, hipMemcpyAsync(out_logits, ctx->logits, 4 * (size_t)mb->num_seqs * ctx->desc.vocab,
+                                   hipMemcpyDeviceToHost, ctx->stream));
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (!rc && e != hipSuccess) rc = set_err(ctx, ZR_E_HIP, "forward: %s", hipGetErrorString(e));
+    return rc;
+}
+
+// ------------------------------------------------------- op-level entries
+zr_status zr_pack(zr_context* ctx, const zr_microbatch* mb, int* cu_q, int* cu_k, int* positions, int* slot_mapping,
+                  int* seq_ids) {
+    if (!ctx) return set_global_err(ZR_E_INVALID, "null context");
+    ZR_HIP(ctx, hipSetDevice(ctx->device));
+    StagedMeta* st = ctx->scratch_stage;
+    zr_status rc = stage_microbatch(ctx, mb, st);
+    if (rc) return rc;
+    const int S = st->num_seqs, T = st->total_q;
+    if (cu_q) ZR_HIP(ctx, hipMemcpyAsync(cu_q, st->cu_q, 4 * (S + 1), hipMemcpyDeviceToHost, ctx->stream));
+    if (cu_k) ZR_HIP(ctx, hipMemcpyAsync(cu_k, st->cu_k, 4 * (S + 1), hipMemcpyDeviceToHost, ctx->stream));
+    if (positions) ZR_HIP(ctx, hipMemcpyAsync(positions, st->positions, 4 * (size_t)T, hipMemcpyDeviceToHost, ctx->stream));
+    if (slot_mapping)
+        ZR_HIP(ctx, hipMemcpyAsync(slot_mapping, st->slot_mapping, 4 * (size_t)T, hipMemcpyDeviceToHost, ctx->stream));
+    if (seq_ids) ZR_HIP(ctx, hipMemcpyAsync(seq_ids, st->seq_ids, 4 * (size_t)T, hipMemcpyDeviceToHost, ctx->stream));
+    ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return ZR_OK;
+}
+
+zr_status zr_rope_kv_write(zr_context* ctx, zr_staged* s, int layer, const float* d_qkv, float* d_q_out, int rope) {
+    StagedMeta* st = (StagedMeta*)s;
+    if (!ctx || !st || !d_qkv || !d_q_out) return set_global_err(ZR_E_INVALID, "null argument");
+    if (layer < 0 || layer >= ctx->desc.num_layers) return set_err(ctx, ZR_E_INVALID, "Invalid layer index: %d", layer);
+    zr_status rc = launch_rope_kv_write(ctx, st, layer, d_qkv, d_q_out, rope);
+    if (!rc) ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return rc;
+}
+
+zr_status zr_attention(zr_context* ctx, zr_staged* s, int layer, const float* d_q, float* d_out) {
+    StagedMeta* st = (StagedMeta*)s;
+    if (!ctx || !st || !d_q || !d_out) return set_global_err(ZR_E_INVALID, "null argument");
+    if (layer < 0 || layer >= ctx->desc.num_layers) return set_err(ctx, ZR_E_INVALID, "Invalid layer index: %d", layer);
+    zr_status rc = launch_attention(ctx, st, layer, d_q, d_out);
+    if (!rc) ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return rc;
+}
+
+static zr_status kv_copy_entry(zr_context* ctx, const int* block_table, int n_pages, int first_offset, int first_row,
+                               int n_rows, float* k, float* v, int to_pool) {
+    if (!ctx || !block_table || !k || !v) return set_global_err(ZR_E_INVALID, "null argument");
+    if (!ctx->kv_pool) return set_err(ctx, ZR_E_INVALID, "KV pool not created");
+    if (n_rows <= 0) return ZR_OK;
+    if (first_offset < 0 || first_offset >= kPageRows || first_row < 0)
+        return set_err(ctx, ZR_E_INVALID, "first_offset %d first_row %d", first_offset, first_row);
+    const long last = (long)first_offset + first_row + n_rows - 1;
+    if (last / kPageRows >= n_pages)
+        return set_err(ctx, ZR_E_INVALID, "rows up to %ld exceed %d pages", last, n_pages);
+    for (long p = (first_offset + first_row) / kPageRows; p <= last / kPageRows; ++p)
+        if (block_table[p] < 0 || block_table[p] >= ctx->n_pages)
+            return set_err(ctx, ZR_E_INVARIANT, "page slot %ld holds page %d outside pool of %d", p, block_table[p],
+                           ctx->n_pages);
+    ZR_HIP(ctx, hipSetDevice(ctx->device));
+    const int L = ctx->desc.num_layers;
+    const size_t elems = (size_t)L * n_rows * ctx->kv_cols;
+    int* d_table = nullptr;
+    float* d_k = nullptr;
+    float* d_v = nullptr;
+    hipError_t e = hipMalloc(&d_table, 4 * (size_t)n_pages);
+    if (e == hipSuccess) e = hipMalloc(&d_k, 4 * elems);
+    if (e == hipSuccess) e = hipMalloc(&d_v, 4 * elems);
+    if (e == hipSuccess) e = hipMemcpyAsync(d_table, block_table, 4 * (size_t)n_pages, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess && to_pool) e = hipMemcpyAsync(d_k, k, 4 * elems, hipMemcpyDefault, ctx->stream);
+    if (e == hipSuccess && to_pool) e = hipMemcpyAsync(d_v, v, 4 * elems, hipMemcpyDefault, ctx->stream);
+    zr_status rc = e == hipSuccess ? ZR_OK : set_err(ctx, ZR_E_HIP, "kv copy staging: %s", hipGetErrorString(e));
+    if (!rc) rc = launch_kv_copy(ctx, 0, L, d_table, first_offset, first_row, n_rows, d_k, d_v, to_pool);
+    if (!rc && !to_pool) {
+        e = hipMemcpyAsync(k, d_k, 4 * elems, hipMemcpyDefault, ctx->stream);
+        if (e == hipSuccess) e = hipMemcpyAsync(v, d_v, 4 * elems, hipMemcpyDefault, ctx->stream);
+        if (e != hipSuccess) rc = set_err(ctx, ZR_E_HIP, "kv gather copy-out: %s", hipGetErrorString(e));
+    }
+    e = hipStreamSynchronize(ctx->stream);
+    if (!rc && e != hipSuccess) rc = set_err(ctx, ZR_E_HIP, "kv copy: %s", hipGetErrorString(e));
+    hipFree(d_table);
+    hipFree(d_k);
+    hipFree(d_v);
+    return rc;
+}
+
+zr_status zr_kv_gather(zr_context* ctx, const int* block_table, int n_pages, int first_offset, int first_row,
+                       int n_rows, float* dst_k, float* dst_v) {
+    return kv_copy_entry(ctx, block_table, n_pages, first_offset, first_row, n_rows, dst_k, dst_v, 0);
+}
+
+zr_status zr_kv_scatter(zr_context* ctx, const int* block_table, int n_pages, int first_offset, int first_row,
+                        int n_rows, const float* src_k, const float* src_v) {
+    return kv_copy_entry(ctx, block_table, n_pages, first_offset, first_row, n_rows, (float*)src_k, (float*)src_v, 1);
+}
+
+zr_status zr_kv_read_pages(zr_context* ctx, int layer, const int* pages, int n_pages, void* dst) {
+    if (!ctx || !pages || !dst) return set_global_err(ZR_E_INVALID, "null argument");
+    if (layer < 0 || layer >= ctx->desc.num_layers) return set_err(ctx, ZR_E_INVALID, "Invalid layer index: %d", layer);
+    ZR_HIP(ctx, hipSetDevice(ctx->device));
+    for (int i = 0; i < n_pages; ++i) {
+        if (pages[i] < 0 || pages[i] >= ctx->n_pages) return set_err(ctx, ZR_E_INVALID, "page %d outside pool", pages[i]);
+        const char* src = (const char*)ctx->kv_pool + ((size_t)layer * ctx->n_pages + pages[i]) * ctx->page_bytes;
+        ZR_HIP(ctx, hipMemcpyAsync((char*)dst + (size_t)i * ctx->page_bytes, src, ctx->page_bytes,
+                                   hipMemcpyDeviceToHost, ctx->stream));
+    }
+    ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return ZR_OK;
+}
+
+zr_status zr_argmax(zr_context* ctx, const float* d_x, int rows, int cols, uint32_t* d_out) {
+    if (!ctx || !d_x || !d_out) return set_global_err(ZR_E_INVALID, "null argument");
+    if (rows <= 0 || cols <= 0) return set_err(ctx, ZR_E_INVALID, "Device sampling received an empty logits tensor");
+    const size_t need = (size_t)rows * ((cols + 4095) / 4096) * 2;
+    if (need > ctx->argmax_ws_floats) {
+        hipStreamSynchronize(ctx->stream);
+        hipFree(ctx->argmax_ws);
+        ctx->argmax_ws = nullptr;
+        ctx->argmax_ws_floats = 0;
+        ZR_HIP(ctx, hipMalloc(&ctx->argmax_ws, need * 4));
+        ctx->argmax_ws_floats = need;
+    }
+    zr_status rc = launch_argmax(ctx, d_x, rows, cols, d_out);
+    if (!rc) ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return rc;
+}
+
+zr_status zr_rms_norm(zr_context* ctx, const float* d_x, const float* d_gamma, float* d_y, int rows, int cols) {
+    if (!ctx || !d_x || !d_gamma || !d_y) return set_global_err(ZR_E_INVALID, "null argument");
+    zr_status rc = launch_rms_norm(ctx, d_x, nullptr, nullptr, d_gamma, d_y, nullptr, rows, cols);
+    if (!rc) ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return rc;
+}
+
+zr_status zr_gemm(zr_context* ctx, const float* d_a, const uint16_t* w, float* d_c, int m, int n, int k) {
+    if (!ctx || !d_a || !w || !d_c) return set_global_err(ZR_E_INVALID, "null argument");
+    if (m <= 0 || n <= 0 || k <= 0) return set_err(ctx, ZR_E_INVALID, "Matmul shape mismatch: %dx%d @ %dx%d", m, k, k, n);
+    uint16_t* packed = nullptr;
+    zr_status rc = pack_weight(ctx, w, k, n, &packed);
+    if (rc) return rc;
+    const size_t need = gemm_ws_floats(m, n, k, kEpiStore);
+    float* saved_ws = ctx->splitk_ws;
+    size_t saved_n = ctx->splitk_ws_floats;
+    float* tmp_ws = nullptr;
+    if (need > saved_n) {
+        hipError_t e = hipMalloc(&tmp_ws, need * 4);
+        if (e != hipSuccess) {
+            hipFree(packed);
+            return set_err(ctx, ZR_E_OOM, "gemm workspace: %s", hipGetErrorString(e));
+        }
+        ctx->splitk_ws = tmp_ws;
+        ctx->splitk_ws_floats = need;
+    }
+    rc = launch_gemm(ctx, d_a, packed, d_c, m, n, k, kEpiStore);
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (!rc && e != hipSuccess) rc = set_err(ctx, ZR_E_HIP, "gemm: %s", hipGetErrorString(e));
+    ctx->splitk_ws = saved_ws;
+    ctx->splitk_ws_floats = saved_n;
+    if (tmp_ws) hipFree(tmp_ws);
+    hipFree(packed);
+    return rc;
+}
+
+zr_status zr_device_alloc(zr_context* ctx, size_t bytes, void** out) {
+    if (!ctx || !out) return set_global_err(ZR_E_INVALID, "null argument");
+    ZR_HIP(ctx, hipSetDevice(ctx->device));
+    hipError_t e = hipMalloc(out, bytes ? bytes : 1);
+    if (e != hipSuccess) return set_err(ctx, e == hipErrorOutOfMemory ? ZR_E_OOM : ZR_E_HIP, "hipMalloc(%zu): %s",
+                                        bytes, hipGetErrorString(e));
+    return ZR_OK;
+}
+
+zr_status zr_device_free(zr_context* ctx, void* p) {
+    if (!ctx) return set_global_err(ZR_E_INVALID, "null context");
+    if (p) {
+        hipStreamSynchronize(ctx->stream);
+        ZR_HIP(ctx, hipFree(p));
+    }
+    return ZR_OK;
+}
+
+zr_status zr_memcpy_h2d(zr_context* ctx, void* dst, const void* src, size_t bytes) {
+    if (!ctx) return set_global_err(ZR_E_INVALID, "null context");
+    ZR_HIP(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return ZR_OK;
+}
+
+zr_status zr_memcpy_d2h(zr_context* ctx, void* dst, const void* src, size_t bytes) {
+    if (!ctx) return set_global_err(ZR_E_INVALID, "null context");
+    ZR_HIP(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return ZR_OK;
+}
+
+zr_status zr_fill_normal_bf16(zr_context* ctx, uint16_t* d_dst, size_t n, uint64_t seed, float std) {
+    if (!ctx || !d_dst) return set_global_err(ZR_E_INVALID, "null argument");
+    zr_status rc = launch_fill_normal_bf16(ctx, d_dst, n, seed, std);
+    if (!rc) ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return rc;
+}
+
+zr_status zr_kv_pool_fill_normal(zr_context* ctx, uint64_t seed, float std) {
+    if (!ctx) return set_global_err(ZR_E_INVALID, "null context");
+    if (!ctx->kv_pool) return set_err(ctx, ZR_E_INVALID, "KV pool not created");
+    zr_status rc = launch_fill_pool_normal(ctx, seed, std);
+    if (!rc) ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return rc;
+}
+
+zr_status zr_timing_begin(zr_context* ctx) {
+    if (!ctx) return set_global_err(ZR_E_INVALID, "null context");
+    ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    ctx->timing.enabled = true;
+    ctx->timing.spans.clear();
+    ctx->timing.next_event = 0;
+    return ZR_OK;
+}
+
+zr_status zr_timing_end(zr_context* ctx, double* ms_by_class, int* launches_by_class) {
+    if (!ctx) return set_global_err(ZR_E_INVALID, "null context");
+    ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    double ms[4] = {0, 0, 0, 0};
+    int n[4] = {0, 0, 0, 0};
+    for (auto& sp : ctx->timing.spans) {
+        float t = 0.0f;
+        if (hipEventElapsedTime(&t, sp.second.first, sp.second.second) == hipSuccess) {
+            ms[sp.first] += t;
+            n[sp.first] += 1;
+        }
+    }
+    ctx->timing.enabled = false;
+    ctx->timing.spans.clear();
+    ctx->timing.next_event = 0;
+    if (ms_by_class) memcpy(ms_by_class, ms, sizeof ms);
+    if (launches_by_class) memcpy(launches_by_class, n, sizeof n);
+    return ZR_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,152 @@
+// Embedding gather, RMSNorm with a fused residual add, and greedy argmax.
+#include "zr_internal.h"
+
+namespace zr {
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Row gather of the bf16 embedding table into the f32 residual stream
+// (forward_pass.rs:2230-2237; embed_tokens tensor_ops.rs:482-500).
+__global__ __launch_bounds__(256) void embed_kernel(const uint32_t* __restrict__ tokens,
+                                                    const uint16_t* __restrict__ table, int H, int V,
+                                                    float* __restrict__ hidden) {
+    const int t = blockIdx.x;
+    uint32_t id = tokens[t];
+    if (id >= (uint32_t)V) id = 0;  // validated on the host; never read out of bounds
+    const uint16_t* src = table + (size_t)id * H;
+    float* dst = hidden + (size_t)t * H;
+    for (int i = threadIdx.x; i < H; i += blockDim.x) dst[i] = bf16_bits_to_f32(src[i]);
+}
+
+zr_status launch_embed(zr_context* ctx, StagedMeta* st, const uint32_t* d_tokens) {
+    if (st->total_q == 0) return ZR_OK;
+    hipLaunchKernelGGL(embed_kernel, dim3(st->total_q), dim3(256), 0, ctx->stream, d_tokens,
+                       ctx->embedding, ctx->desc.hidden, ctx->desc.vocab, ctx->hidden);
+    ZR_LAUNCH_CHECK(ctx);
+    return ZR_OK;
+}
+
+// y = rms_norm(x (+ residual)) * gamma (tensor_ops.rs:285-304,
+// runtime.rs:919-925).  With residual_in, x_out = x + residual_in is written
+// first (the broadcast_add of forward_pass.rs:2279 / 2304).  row_index
+// selects source rows (e.g. the last token of every sequence for the LM head).
+__global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__ x,
+                                                       const float* __restrict__ residual_in,
+                                                       float* __restrict__ x_out,
+                                                       const float* __restrict__ gamma,
+                                                       float* __restrict__ y,
+                                                       const int* __restrict__ row_index, int cols,
+                                                       float eps) {
+    __shared__ float red[4];
+    const int r = blockIdx.x;
+    const int src = row_index ? row_index[r] : r;
+    const float* xr = x + (size_t)src * cols;
+    const float* rr = residual_in ? residual_in + (size_t)src * cols : nullptr;
+    float* xo = x_out ? x_out + (size_t)src * cols : nullptr;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < cols; i += blockDim.x) {
+        float v = xr[i];
+        if (rr) {
+            v = v + rr[i];
+            xo[i] = v;
+        }
+        ss += v * v;
+    }
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float total = red[0] + red[1] + red[2] + red[3];
+    const float inv_rms = 1.0f / sqrtf(total / (float)cols + eps);
+    const float* xs = rr ? xo : xr;
+    float* yr = y + (size_t)r * cols;
+    for (int i = threadIdx.x; i < cols; i += blockDim.x) yr[i] = xs[i] * inv_rms * gamma[i];
+}
+
+zr_status launch_rms_norm(zr_context* ctx, const float* x, const float* residual_in, float* x_out,
+                          const float* gamma, float* y, const int* row_index, int rows, int cols) {
+    if (rows <= 0) return ZR_OK;
+    hipEvent_t ev;
+    timing_mark_begin(ctx, kClassNormRopeKv, &ev);
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(rows), dim3(256), 0, ctx->stream, x, residual_in, x_out, gamma,
+                       y, row_index, cols, ctx->desc.rms_norm_eps);
+    ZR_LAUNCH_CHECK(ctx);
+    timing_mark_end(ctx, kClassNormRopeKv, ev);
+    return ZR_OK;
+}
+
+// Greedy argmax, two stages; ties keep the lowest index
+// (sample_greedy tensor_ops.rs:461-473; device argmax runtime.rs:561-570).
+__device__ inline void better(float& bv, int& bi, float v, int i) {
+    if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+
+constexpr int kArgmaxChunk = 4096;
+
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __restrict__ x, int cols,
+                                                             int chunks, float* __restrict__ ws) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const int r = blockIdx.y, ch = blockIdx.x;
+    const int c0 = ch * kArgmaxChunk, c1 = min(cols, c0 + kArgmaxChunk);
+    const float* xr = x + (size_t)r * cols;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = c0 + threadIdx.x; i < c1; i += blockDim.x) better(bv, bi, xr[i], i);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        better(bv, bi, ov, oi);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        sv[threadIdx.x >> 6] = bv;
+        si[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        bv = sv[0];
+        bi = si[0];
+        for (int w = 1; w < 4; ++w) better(bv, bi, sv[w], si[w]);
+        ws[((size_t)r * chunks + ch) * 2] = bv;
+        ws[((size_t)r * chunks + ch) * 2 + 1] = __int_as_float(bi);
+    }
+}
+
+__global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restrict__ ws, int chunks,
+                                                          uint32_t* __restrict__ out) {
+    const int r = blockIdx.x;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int ch = threadIdx.x; ch < chunks; ch += 64)
+        better(bv, bi, ws[((size_t)r * chunks + ch) * 2], __float_as_int(ws[((size_t)r * chunks + ch) * 2 + 1]));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        better(bv, bi, ov, oi);
+    }
+    // a row of all -inf/NaN keeps index 0, as the reference's initial max_idx
+    if (threadIdx.x == 0) out[r] = bi == 0x7fffffff ? 0u : (uint32_t)bi;
+}
+
+zr_status launch_argmax(zr_context* ctx, const float* x, int rows, int cols, uint32_t* out) {
+    if (rows <= 0) return ZR_OK;
+    const int chunks = (cols + kArgmaxChunk - 1) / kArgmaxChunk;
+    if ((size_t)rows * chunks * 2 > ctx->argmax_ws_floats)
+        return set_err(ctx, ZR_E_OOM, "argmax workspace too small");
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(chunks, rows), dim3(256), 0, ctx->stream, x, cols, chunks,
+                       ctx->argmax_ws);
+    ZR_LAUNCH_CHECK(ctx);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(rows), dim3(64), 0, ctx->stream, ctx->argmax_ws, chunks, out);
+    ZR_LAUNCH_CHECK(ctx);
+    return ZR_OK;
+}
+
+}  // namespace zr

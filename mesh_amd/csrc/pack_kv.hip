@@ -1,0 +1,274 @@
+// Ragged-batch packing, fused RoPE + paged-KV append, and the KV handoff
+// gather/scatter kernels.
+//
+// KV pool layout (per layer, per global page, K block then V block, one
+// [16 x head_dim] tile per local kv head, element type = pool dtype):
+//   K tile: element (t, d) at ((d / 8) * 16 + t) * 8 + d % 8
+//           -> one 1 KiB row of 64 lanes x 16 B is exactly the MFMA A-operand
+//              fragment (token = lane % 16, 8 dims per lane) for 32 dims.
+//   V tile: element (t, d) at ((t / 4) * head_dim + d) * 4 + t % 4
+//           -> a lane's 4 consecutive tokens of one dim form the 16x16x16
+//              MFMA operand of the P.V product.
+#include "zr_internal.h"
+
+namespace zr {
+
+__device__ inline size_t k_off(int t, int d) { return ((size_t)(d >> 3) * kPageRows + t) * 8 + (d & 7); }
+__device__ inline size_t v_off(int t, int d, int D) { return ((size_t)(t >> 2) * D + d) * 4 + (t & 3); }
+
+template <typename T> __device__ inline void store_elem(T* p, float x);
+template <> __device__ inline void store_elem<float>(float* p, float x) { *p = x; }
+template <> __device__ inline void store_elem<uint16_t>(uint16_t* p, float x) { *p = f32_to_bf16_bits(x); }
+template <typename T> __device__ inline float load_elem(const T* p);
+template <> __device__ inline float load_elem<float>(const float* p) { return *p; }
+template <> __device__ inline float load_elem<uint16_t>(const uint16_t* p) { return bf16_bits_to_f32(*p); }
+
+// ------------------------------------------------------------------ pack
+// One workgroup: exclusive scans of q_len and kv_after, then per-token
+// positions / slot mapping / sequence ids
+// (DecodeWorkspaceLease::stage_with_slot_reader, fast_path.rs:263-338;
+// PrefillWorkspaceLease::stage_positions, fast_path.rs:409-445).
+__global__ __launch_bounds__(1024) void pack_kernel(int S, const int* __restrict__ q_len,
+                                                    const int* __restrict__ kv_before,
+                                                    const int* __restrict__ first_pos,
+                                                    const int* __restrict__ first_offset,
+                                                    const int* __restrict__ bt, int stride,
+                                                    int* __restrict__ cu_q, int* __restrict__ cu_k,
+                                                    int* __restrict__ positions, int* __restrict__ slot,
+                                                    int* __restrict__ seq_ids, int* __restrict__ last_rows) {
+    __shared__ int sq[1024], sk[1024];
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const int per = (S + nt - 1) / nt;
+    const int s0 = tid * per, s1 = min(S, s0 + per);
+    int lq = 0, lk = 0;
+    for (int s = s0; s < s1; ++s) {
+        lq += q_len[s];
+        lk += kv_before[s] + q_len[s];
+    }
+    sq[tid] = lq;
+    sk[tid] = lk;
+    __syncthreads();
+    // Hillis-Steele inclusive scan over the per-thread sums
+    for (int off = 1; off < nt; off <<= 1) {
+        int aq = tid >= off ? sq[tid - off] : 0;
+        int ak = tid >= off ? sk[tid - off] : 0;
+        __syncthreads();
+        sq[tid] += aq;
+        sk[tid] += ak;
+        __syncthreads();
+    }
+    int bq = sq[tid] - lq, bk = sk[tid] - lk;
+    if (tid == 0) {
+        cu_q[0] = 0;
+        cu_k[0] = 0;
+    }
+    for (int s = s0; s < s1; ++s) {
+        bq += q_len[s];
+        bk += kv_before[s] + q_len[s];
+        cu_q[s + 1] = bq;
+        cu_k[s + 1] = bk;
+        last_rows[s] = bq - 1;
+    }
+    __syncthreads();
+    __threadfence_block();
+    const int total = sq[nt - 1];
+    for (int t = tid; t < total; t += nt) {
+        // binary search: largest s with cu_q[s] <= t
+        int lo = 0, hi = S - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (cu_q[mid] <= t) lo = mid; else hi = mid - 1;
+        }
+        const int s = lo, i = t - cu_q[s];
+        const int row = first_offset[s] + kv_before[s] + i;
+        positions[t] = first_pos[s] + i;
+        slot[t] = bt[(size_t)s * stride + row / kPageRows] * kPageRows + row % kPageRows;
+        seq_ids[t] = s;
+    }
+}
+
+zr_status launch_pack(zr_context* ctx, StagedMeta* st) {
+    hipLaunchKernelGGL(pack_kernel, dim3(1), dim3(1024), 0, ctx->stream, st->num_seqs, st->q_len,
+                       st->kv_before, st->first_pos, st->first_offset, st->block_tables, st->stride,
+                       st->cu_q, st->cu_k, st->positions, st->slot_mapping, st->seq_ids, st->last_rows);
+    ZR_LAUNCH_CHECK(ctx);
+    return ZR_OK;
+}
+
+// ---------------------------------------------------------- RoPE + append
+// One workgroup per token row.  RoPE follows tensor_ops.rs:509-560 /
+// runtime.rs:935-1005 (rotate-half, theta = position * inv_freq in f32) and
+// the KV append is DeviceLayerKVCache::append (forward_pass.rs:462-521) at the
+// slot the host reserved.
+template <typename KV>
+__global__ __launch_bounds__(256) void rope_kv_write_kernel(
+    const float* __restrict__ qkv, int qkv_stride, float* __restrict__ q_out, int q_cols, int kv_cols,
+    int D, const int* __restrict__ positions, const int* __restrict__ slot,
+    const float* __restrict__ inv_freq, KV* __restrict__ layer_pool, size_t page_elems, int rope) {
+#pragma clang fp contract(off)
+    const int t = blockIdx.x;
+    const int half = D / 2;
+    const float pos = (float)positions[t];
+    const float* row = qkv + (size_t)t * qkv_stride;
+    const int s = slot[t];
+    const int page = s / kPageRows, r = s % kPageRows;
+    KV* kpage = layer_pool + (size_t)page * page_elems;
+    const int kv_heads = kv_cols / D;
+    KV* vpage = kpage + (size_t)kv_heads * kPageRows * D;
+    // q: q_cols / 2 rotation pairs, k: kv_cols / 2 pairs, v: kv_cols copies
+    const int nq = q_cols / 2, nk = kv_cols / 2;
+    for (int j = threadIdx.x; j < nq + nk + kv_cols; j += blockDim.x) {
+        if (j < nq + nk) {
+            const bool is_q = j < nq;
+            const int jj = is_q ? j : j - nq;
+            const int head = jj / half, i = jj % half;
+            const float* src = row + (is_q ? 0 : q_cols) + head * D;
+            float a = src[i], b = src[i + half];
+            if (rope) {
+                const float theta = pos * inv_freq[i];
+                const float c = cosf(theta), sn = sinf(theta);
+                const float na = a * c - b * sn;
+                const float nb = a * sn + b * c;
+                a = na;
+                b = nb;
+            }
+            if (is_q) {
+                q_out[(size_t)t * q_cols + head * D + i] = a;
+                q_out[(size_t)t * q_cols + head * D + i + half] = b;
+            } else {
+                KV* kt = kpage + (size_t)head * kPageRows * D;
+                store_elem(kt + k_off(r, i), a);
+                store_elem(kt + k_off(r, i + half), b);
+            }
+        } else {
+            const int c = j - nq - nk;
+            const int head = c / D, d = c % D;
+            KV* vt = vpage + (size_t)head * kPageRows * D;
+            store_elem(vt + v_off(r, d, D), row[q_cols + kv_cols + c]);
+        }
+    }
+}
+
+static inline size_t page_elems_of(const zr_context* ctx) {
+    return (size_t)2 * ctx->kv_cols * kPageRows;
+}
+
+zr_status launch_rope_kv_write(zr_context* ctx, StagedMeta* st, int layer, const float* qkv,
+                               float* q_out, int rope) {
+    if (st->total_q == 0) return ZR_OK;
+    const size_t pe = page_elems_of(ctx);
+    const int stride = ctx->q_cols + 2 * ctx->kv_cols;
+    hipEvent_t ev;
+    timing_mark_begin(ctx, kClassNormRopeKv, &ev);
+    if (ctx->desc.kv_dtype == ZR_DTYPE_BF16) {
+        uint16_t* pool = (uint16_t*)ctx->kv_pool + (size_t)layer * ctx->n_pages * pe;
+        hipLaunchKernelGGL(rope_kv_write_kernel<uint16_t>, dim3(st->total_q), dim3(256), 0, ctx->stream,
+                           qkv, stride, q_out, ctx->q_cols, ctx->kv_cols, ctx->head_dim, st->positions,
+                           st->slot_mapping, ctx->inv_freq, pool, pe, rope);
+    } else {
+        float* pool = (float*)ctx->kv_pool + (size_t)layer * ctx->n_pages * pe;
+        hipLaunchKernelGGL(rope_kv_write_kernel<float>, dim3(st->total_q), dim3(256), 0, ctx->stream,
+                           qkv, stride, q_out, ctx->q_cols, ctx->kv_cols, ctx->head_dim, st->positions,
+                           st->slot_mapping, ctx->inv_freq, pool, pe, rope);
+    }
+    ZR_LAUNCH_CHECK(ctx);
+    timing_mark_end(ctx, kClassNormRopeKv, ev);
+    return ZR_OK;
+}
+
+// ------------------------------------------------------ gather / scatter
+// Logical window row j of a sequence lives at physical row first_offset + j of
+// its page list (interior spans are full pages; only the first span may start
+// mid-page after retain_suffix).  grid = (n_rows, layers).
+template <typename KV>
+__global__ __launch_bounds__(256) void kv_copy_kernel(KV* __restrict__ pool, size_t page_elems,
+                                                      int n_pages_pool, int layer_begin,
+                                                      const int* __restrict__ table, int first_offset,
+                                                      int first_row, int n_rows, int kv_cols, int D,
+                                                      float* __restrict__ k, float* __restrict__ v,
+                                                      int to_pool) {
+    const int i = blockIdx.x;
+    const int l = blockIdx.y;
+    const int layer = layer_begin + l;
+    const int prow = first_offset + first_row + i;
+    const int page = table[prow / kPageRows], r = prow % kPageRows;
+    KV* kpage = pool + ((size_t)layer * n_pages_pool + page) * page_elems;
+    KV* vpage = kpage + (size_t)kv_cols * kPageRows;
+    float* kd = k + ((size_t)l * n_rows + i) * kv_cols;
+    float* vd = v + ((size_t)l * n_rows + i) * kv_cols;
+    for (int c = threadIdx.x; c < kv_cols; c += blockDim.x) {
+        const int head = c / D, d = c % D;
+        KV* kp = kpage + (size_t)head * kPageRows * D + k_off(r, d);
+        KV* vp = vpage + (size_t)head * kPageRows * D + v_off(r, d, D);
+        if (to_pool) {
+            store_elem(kp, kd[c]);
+            store_elem(vp, vd[c]);
+        } else {
+            kd[c] = load_elem(kp);
+            vd[c] = load_elem(vp);
+        }
+    }
+}
+
+zr_status launch_kv_copy(zr_context* ctx, int layer_begin, int layer_end, const int* d_table,
+                         int first_offset, int first_row, int n_rows, float* k, float* v, int to_pool) {
+    if (n_rows <= 0 || layer_end <= layer_begin) return ZR_OK;
+    const size_t pe = page_elems_of(ctx);
+    dim3 grid(n_rows, layer_end - layer_begin);
+    if (ctx->desc.kv_dtype == ZR_DTYPE_BF16)
+        hipLaunchKernelGGL(kv_copy_kernel<uint16_t>, grid, dim3(256), 0, ctx->stream,
+                           (uint16_t*)ctx->kv_pool, pe, ctx->n_pages, layer_begin, d_table, first_offset,
+                           first_row, n_rows, ctx->kv_cols, ctx->head_dim, k, v, to_pool);
+    else
+        hipLaunchKernelGGL(kv_copy_kernel<float>, grid, dim3(256), 0, ctx->stream, (float*)ctx->kv_pool,
+                           pe, ctx->n_pages, layer_begin, d_table, first_offset, first_row, n_rows,
+                           ctx->kv_cols, ctx->head_dim, k, v, to_pool);
+    ZR_LAUNCH_CHECK(ctx);
+    return ZR_OK;
+}
+
+// --------------------------------------------------------- synthetic fill
+// Counter-based SplitMix64 -> two uniforms -> Box-Muller normal.
+__device__ inline uint64_t splitmix64(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
+__device__ inline float normal_at(uint64_t seed, uint64_t i) {
+    const uint64_t r = splitmix64(seed * 0x100000001B3ull + i);
+    const float u1 = ((float)(uint32_t)(r >> 40) + 1.0f) * (1.0f / 16777217.0f);
+    const float u2 = (float)(uint32_t)(r & 0xFFFFFF) * (1.0f / 16777216.0f);
+    return sqrtf(-2.0f * logf(u1)) * cosf(6.28318530718f * u2);
+}
+
+__global__ void fill_normal_bf16_kernel(uint16_t* dst, size_t n, uint64_t seed, float std) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        dst[i] = f32_to_bf16_bits(normal_at(seed, i) * std);
+}
+
+__global__ void fill_normal_f32_kernel(float* dst, size_t n, uint64_t seed, float std) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        dst[i] = normal_at(seed, i) * std;
+}
+
+zr_status launch_fill_normal_bf16(zr_context* ctx, uint16_t* dst, size_t n, uint64_t seed, float std) {
+    hipLaunchKernelGGL(fill_normal_bf16_kernel, dim3(4096), dim3(256), 0, ctx->stream, dst, n, seed, std);
+    ZR_LAUNCH_CHECK(ctx);
+    return ZR_OK;
+}
+
+zr_status launch_fill_pool_normal(zr_context* ctx, uint64_t seed, float std) {
+    const size_t n = (size_t)ctx->desc.num_layers * ctx->n_pages * page_elems_of(ctx);
+    if (ctx->desc.kv_dtype == ZR_DTYPE_BF16)
+        hipLaunchKernelGGL(fill_normal_bf16_kernel, dim3(8192), dim3(256), 0, ctx->stream,
+                           (uint16_t*)ctx->kv_pool, n, seed, std);
+    else
+        hipLaunchKernelGGL(fill_normal_f32_kernel, dim3(8192), dim3(256), 0, ctx->stream,
+                           (float*)ctx->kv_pool, n, seed, std);
+    ZR_LAUNCH_CHECK(ctx);
+    return ZR_OK;
+}
+
+}  // namespace zr

@@ -1,0 +1,580 @@
+// Host-side rocm execution backend (include/zip_rocm_host.h): the session page
+// tables, positions and microbatch assembly that the reference keeps in its
+// Rust provider host (forward_pass.rs:303-1243, 2089-2319; backend.rs:110-151).
+#include <string.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "../../include/zip_rocm_host.h"
+#include "zr_internal.h"
+
+using zr::kPageRows;
+using zr::set_err;
+using zr::set_global_err;
+
+struct zrh_pool {
+    zr_context* ctx = nullptr;
+    std::vector<int> free_list;  // LIFO: pop_back
+};
+
+namespace {
+
+struct PageEntry {
+    int global = -1;
+    int used_rows = 0;
+    bool active = false;
+};
+
+struct Span {
+    int page_index, start_row, row_count;
+};
+
+// One session's DeviceKVCache with a single canonical block table: the
+// reference keeps one allocator per layer, but every layer evolves
+// identically (checked by DeviceKVCache::live_block_table, 1024-1048), so the
+// device pool stores all layers of a page at one page id.
+struct SessionKV {
+    std::vector<PageEntry> pages;
+    std::vector<int> free_pages;  // LIFO of local page indices
+    std::vector<Span> spans;
+    int seq_len = 0;
+    int base_position = 0;
+};
+
+}  // namespace
+
+struct zrh_backend {
+    zrh_pool* pool = nullptr;
+    zr_context* ctx = nullptr;
+    int max_seq_len = 4096;
+    int position = 0;  // ForwardPass.position (forward_pass.rs:1774)
+    SessionKV kv;
+};
+
+namespace {
+
+zr_status fail(zrh_backend* b, zr_status code, const char* msg, int a = 0, int c = 0, int d = 0) {
+    return set_err(b ? b->ctx : nullptr, code, msg, a, c, d);
+}
+
+// allocate_page (forward_pass.rs:396-424): LIFO reuse, else a new local page
+// bound to a fresh global page of the pool.
+zr_status allocate_page(zrh_backend* b, int* out) {
+    SessionKV& kv = b->kv;
+    if (!kv.free_pages.empty()) {
+        const int idx = kv.free_pages.back();
+        kv.free_pages.pop_back();
+        if (kv.pages[idx].active)
+            return fail(b, ZR_E_INVARIANT, "Device KV allocator attempted to reuse page %d while it was Active", idx);
+        kv.pages[idx].used_rows = 0;
+        kv.pages[idx].active = true;
+        *out = idx;
+        return ZR_OK;
+    }
+    if (b->pool->free_list.empty())
+        return fail(b, ZR_E_OOM, "KV pool exhausted: no free global page for local page %d", (int)kv.pages.size());
+    PageEntry pe;
+    pe.global = b->pool->free_list.back();
+    b->pool->free_list.pop_back();
+    pe.active = true;
+    kv.pages.push_back(pe);
+    *out = (int)kv.pages.size() - 1;
+    return ZR_OK;
+}
+
+// release_page (426-446)
+zr_status release_page(zrh_backend* b, int idx) {
+    SessionKV& kv = b->kv;
+    if (idx < 0 || idx >= (int)kv.pages.size()) return fail(b, ZR_E_INVARIANT, "Invalid device KV page index %d", idx);
+    if (!kv.pages[idx].active) return fail(b, ZR_E_INVARIANT, "Device KV allocator double-freed page %d", idx);
+    kv.pages[idx].used_rows = 0;
+    kv.pages[idx].active = false;
+    kv.free_pages.push_back(idx);
+    return ZR_OK;
+}
+
+// reclaim_unused_pages (448-460)
+zr_status reclaim_unused(zrh_backend* b) {
+    SessionKV& kv = b->kv;
+    std::vector<char> referenced(kv.pages.size(), 0);
+    for (const Span& s : kv.spans) referenced[s.page_index] = 1;
+    for (int p = 0; p < (int)kv.pages.size(); ++p)
+        if (!referenced[p] && kv.pages[p].used_rows != 0) {
+            zr_status rc = release_page(b, p);
+            if (rc) return rc;
+        }
+    return ZR_OK;
+}
+
+// DeviceLayerKVCache::clear (840-850): free list re-seeded 0..n
+void clear_kv(SessionKV& kv) {
+    for (PageEntry& p : kv.pages) {
+        p.used_rows = 0;
+        p.active = false;
+    }
+    kv.free_pages.clear();
+    for (int p = 0; p < (int)kv.pages.size(); ++p) kv.free_pages.push_back(p);
+    kv.spans.clear();
+    kv.seq_len = 0;
+    kv.base_position = 0;
+}
+
+// DeviceKVCache::retain_suffix (1084-1094) over DeviceLayerKVCache::retain_suffix (852-881)
+zr_status retain_suffix(zrh_backend* b, int keep) {
+    SessionKV& kv = b->kv;
+    if (keep < 0) keep = 0;
+    const int seq = kv.seq_len;
+    if (seq <= keep) return ZR_OK;
+    if (keep == 0) {
+        const int base = kv.base_position;
+        clear_kv(kv);
+        kv.base_position = base + seq;
+        return ZR_OK;
+    }
+    int drop = seq - keep;
+    while (drop > 0) {
+        if (kv.spans.empty()) return fail(b, ZR_E_INVARIANT, "Device KV block table unexpectedly empty");
+        Span& front = kv.spans.front();
+        if (drop >= front.row_count) {
+            drop -= front.row_count;
+            const int idx = front.page_index;
+            kv.spans.erase(kv.spans.begin());
+            zr_status rc = release_page(b, idx);
+            if (rc) return rc;
+            continue;
+        }
+        front.start_row += drop;
+        front.row_count -= drop;
+        drop = 0;
+    }
+    kv.seq_len = keep;
+    kv.base_position += seq - keep;
+    return reclaim_unused(b);
+}
+
+// ensure_writable_tail (353-394) + the row bookkeeping of append (462-521)
+zr_status reserve_rows(zrh_backend* b, int rows) {
+    SessionKV& kv = b->kv;
+    int done = 0;
+    while (done < rows) {
+        int idx;
+        if (kv.spans.empty()) {
+            zr_status rc = allocate_page(b, &idx);
+            if (rc) return rc;
+            kv.spans.push_back({idx, 0, 0});
+        } else {
+            const Span tail = kv.spans.back();
+            const PageEntry& tp = kv.pages[tail.page_index];
+            if (tail.start_row + tail.row_count != tp.used_rows)
+                return fail(b, ZR_E_INVARIANT, "Device KV tail span for page %d is inconsistent: span end %d vs used_rows %d",
+                            tail.page_index, tail.start_row + tail.row_count, tp.used_rows);
+            if (kPageRows - tp.used_rows > 0) {
+                idx = tail.page_index;
+            } else {
+                zr_status rc = allocate_page(b, &idx);
+                if (rc) return rc;
+                kv.spans.push_back({idx, 0, 0});
+            }
+        }
+        PageEntry& pg = kv.pages[idx];
+        const int n = std::min(kPageRows - pg.used_rows, rows - done);
+        pg.used_rows += n;
+        kv.spans.back().row_count += n;
+        kv.seq_len += n;
+        done += n;
+    }
+    return ZR_OK;
+}
+
+// DeviceKVCache::append_layer (920-957) applied to every layer at once.
+zr_status append_rows(zrh_backend* b, int rows) {
+    const int max_seq = std::max(b->max_seq_len, 1);
+    if (rows > max_seq) rows = max_seq;
+    if (b->kv.seq_len + rows > max_seq) {
+        const int drop = b->kv.seq_len + rows - max_seq;
+        zr_status rc = retain_suffix(b, std::max(0, b->kv.seq_len - drop));
+        if (rc) return rc;
+    }
+    return reserve_rows(b, rows);
+}
+
+// Canonical device table of the live window: global pages oldest first,
+// first-span start row.  Interior spans must be full pages from row 0 (the
+// invariant the kernels' row = first_offset + logical index relies on).
+zr_status device_table(zrh_backend* b, std::vector<int>& table, int* first_offset) {
+    const SessionKV& kv = b->kv;
+    table.clear();
+    *first_offset = kv.spans.empty() ? 0 : kv.spans.front().start_row;
+    for (size_t i = 0; i < kv.spans.size(); ++i) {
+        const Span& s = kv.spans[i];
+        if (i > 0 && s.start_row != 0)
+            return fail(b, ZR_E_INVARIANT, "span %d starts at row %d", (int)i, s.start_row);
+        if (i + 1 < kv.spans.size() && s.start_row + s.row_count != kPageRows)
+            return fail(b, ZR_E_INVARIANT, "interior span %d ends at row %d", (int)i, s.start_row + s.row_count);
+        table.push_back(kv.pages[s.page_index].global);
+    }
+    return ZR_OK;
+}
+
+struct Assembled {
+    std::vector<int> q_len, kv_before, first_pos, first_offset, tables;
+    int stride = 0;
+};
+
+// One microbatch row per session: trim the window for the incoming rows, then
+// reserve them (attention_output 1446-1452 / the batched decode 2703-2723).
+zr_status assemble(zrh_backend* const* backends, int n, const int* q_len, bool decode_only, Assembled& out,
+                   std::vector<SessionKV>& saved, std::vector<int>& saved_pos) {
+    if (n <= 0 || !backends) return set_global_err(ZR_E_INVALID, "Decode microbatch requires at least one backend and token");
+    zr_context* ctx = backends[0]->ctx;
+    std::vector<std::vector<int>> tables(n);
+    saved.clear();
+    saved_pos.clear();
+    for (int i = 0; i < n; ++i) {
+        zrh_backend* b = backends[i];
+        if (!b || b->ctx != ctx) return set_err(ctx, ZR_E_INVALID, "microbatch mixes contexts");
+        for (int j = 0; j < i; ++j)
+            if (backends[j] == b) return set_err(ctx, ZR_E_INVALID, "session %d appears twice in one microbatch", i);
+        saved.push_back(b->kv);
+        saved_pos.push_back(b->position);
+    }
+    out = Assembled();
+    zr_status rc = ZR_OK;
+    for (int i = 0; i < n && !rc; ++i) {
+        zrh_backend* b = backends[i];
+        const int ql = q_len[i];
+        if (ql <= 0) rc = set_err(ctx, ZR_E_INVALID, "session %d has q_len %d", i, ql);
+        else if (ql > std::max(b->max_seq_len, 1))
+            rc = set_err(ctx, ZR_E_INVALID, "chunk of %d tokens exceeds the %d-token window", ql, b->max_seq_len);
+        else if (decode_only && b->position == 0)
+            rc = set_err(ctx, ZR_E_INVALID, "Decode microbatch requested before prompt prefill");
+        else if (b->kv.base_position + b->kv.seq_len != b->position)
+            rc = set_err(ctx, ZR_E_INVARIANT, "Forward pass position %d diverged from KV cache next position %d",
+                         b->position, b->kv.base_position + b->kv.seq_len);
+        if (rc) break;
+        const int max_seq = std::max(b->max_seq_len, 1);
+        if (b->kv.seq_len + ql > max_seq) {
+            const int drop = b->kv.seq_len + ql - max_seq;
+            rc = retain_suffix(b, std::max(0, b->kv.seq_len - drop));
+            if (rc) break;
+        }
+        const int prefix = b->kv.seq_len;
+        if (b->position != b->kv.base_position + prefix) {
+            rc = set_err(ctx, ZR_E_INVARIANT, "Non-contiguous attention positions: expected %d, got %d",
+                         b->kv.base_position + prefix, b->position);
+            break;
+        }
+        rc = reserve_rows(b, ql);
+        if (rc) break;
+        int foff = 0;
+        rc = device_table(b, tables[i], &foff);
+        if (rc) break;
+        out.q_len.push_back(ql);
+        out.kv_before.push_back(prefix);
+        out.first_pos.push_back(b->position);
+        out.first_offset.push_back(foff);
+        out.stride = std::max(out.stride, (int)tables[i].size());
+    }
+    if (rc) {
+        for (int i = 0; i < n; ++i) {
+            backends[i]->kv = saved[i];
+            backends[i]->position = saved_pos[i];
+        }
+        return rc;
+    }
+    out.tables.assign((size_t)n * out.stride, 0);
+    for (int i = 0; i < n; ++i) std::copy(tables[i].begin(), tables[i].end(), out.tables.begin() + (size_t)i * out.stride);
+    return ZR_OK;
+}
+
+zr_microbatch as_microbatch(const Assembled& a, const uint32_t* tokens) {
+    zr_microbatch mb;
+    mb.num_seqs = (int)a.q_len.size();
+    mb.q_len = a.q_len.data();
+    mb.kv_before = a.kv_before.data();
+    mb.first_pos = a.first_pos.data();
+    mb.first_offset = a.first_offset.data();
+    mb.block_tables = a.tables.data();
+    mb.block_table_stride = a.stride;
+    mb.tokens = tokens;
+    return mb;
+}
+
+zr_status run_mixed(zrh_backend* const* backends, int n, const int* q_len, const uint32_t* tokens, bool decode_only,
+                    uint32_t* out_tokens, float* out_logits, float* out_partials) {
+    if (!backends[0]->ctx) return set_global_err(ZR_E_INVALID, "bookkeeping-only pool has no device context");
+    Assembled a;
+    std::vector<SessionKV> saved;
+    std::vector<int> saved_pos;
+    zr_status rc = assemble(backends, n, q_len, decode_only, a, saved, saved_pos);
+    if (rc) return rc;
+    zr_microbatch mb = as_microbatch(a, tokens);
+    rc = zr_forward(backends[0]->ctx, &mb, out_tokens, out_logits, out_partials);
+    if (rc) {
+        for (int i = 0; i < n; ++i) {
+            backends[i]->kv = saved[i];
+            backends[i]->position = saved_pos[i];
+        }
+        return rc;
+    }
+    for (int i = 0; i < n; ++i) backends[i]->position += q_len[i];
+    return ZR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+zr_status zrh_pool_create(zr_context* ctx, const int* initial_order, int n, zrh_pool** out) {
+    if (!out) return set_global_err(ZR_E_INVALID, "null argument");
+    // ctx == NULL: a bookkeeping-only pool of n pages (page tables without a device)
+    const int pages = ctx ? zr_kv_pool_pages(ctx) : n;
+    if (pages <= 0) return set_err(ctx, ZR_E_INVALID, ctx ? "KV pool not created" : "pool of %d pages", n);
+    zrh_pool* p = new zrh_pool();
+    p->ctx = ctx;
+    if (initial_order) {
+        if (n != pages) {
+            delete p;
+            return set_err(ctx, ZR_E_INVALID, "initial order has %d pages, pool has %d", n, pages);
+        }
+        std::vector<char> seen(pages, 0);
+        for (int i = 0; i < n; ++i) {
+            if (initial_order[i] < 0 || initial_order[i] >= pages || seen[initial_order[i]]) {
+                delete p;
+                return set_err(ctx, ZR_E_INVALID, "initial order is not a permutation of the pool pages");
+            }
+            seen[initial_order[i]] = 1;
+        }
+        p->free_list.assign(initial_order, initial_order + n);
+    } else {
+        for (int i = pages - 1; i >= 0; --i) p->free_list.push_back(i);
+    }
+    *out = p;
+    return ZR_OK;
+}
+
+void zrh_pool_destroy(zrh_pool* pool) { delete pool; }
+int zrh_pool_free_pages(const zrh_pool* pool) { return pool ? (int)pool->free_list.size() : 0; }
+
+zr_status zrh_backend_create(zrh_pool* pool, int max_seq_len, zrh_backend** out) {
+    if (!pool || !out) return set_global_err(ZR_E_INVALID, "null argument");
+    zrh_backend* b = new zrh_backend();
+    b->pool = pool;
+    b->ctx = pool->ctx;
+    b->max_seq_len = max_seq_len;
+    *out = b;
+    return ZR_OK;
+}
+
+void zrh_backend_destroy(zrh_backend* b) {
+    if (!b) return;
+    zrh_release_pages(b);
+    delete b;
+}
+
+zr_status zrh_prefill(zrh_backend* b, const uint32_t* tokens, int n, float* logits, uint32_t* greedy) {
+    if (!b || !tokens) return set_global_err(ZR_E_INVALID, "null argument");
+    if (n <= 0) return set_err(b->ctx, ZR_E_INVALID, "Cannot prefill an empty prompt without an explicit BOS policy");
+    const SessionKV saved = b->kv;
+    const int saved_pos = b->position;
+    // clear_cache + keep the last window (forward_pass.rs:2101-2105)
+    clear_kv(b->kv);
+    b->position = 0;
+    const int window = std::max(b->max_seq_len, 1);
+    const int start = n > window ? n - window : 0;
+    b->kv.base_position = start;
+    b->position = start;
+    const int ql = n - start;
+    uint32_t tok;
+    zr_status rc = run_mixed(&b, 1, &ql, tokens + start, false, greedy ? greedy : &tok, logits, nullptr);
+    if (rc) {
+        b->kv = saved;
+        b->position = saved_pos;
+    }
+    return rc;
+}
+
+zr_status zrh_decode_step(zrh_backend* b, uint32_t token, float* logits, uint32_t* greedy) {
+    if (!b) return set_global_err(ZR_E_INVALID, "null argument");
+    if (b->position == 0) return set_err(b->ctx, ZR_E_INVALID, "Decode step requested before prompt prefill");
+    const int one = 1;
+    uint32_t tok;
+    return run_mixed(&b, 1, &one, &token, true, greedy ? greedy : &tok, logits, nullptr);
+}
+
+zr_status zrh_decode_step_batch(zrh_backend* const* backends, int n, const uint32_t* tokens, uint32_t* out_tokens,
+                                float* out_logits, float* out_partials) {
+    if (!backends || !tokens || n <= 0) return set_global_err(ZR_E_INVALID, "Decode microbatch requires at least one backend and token");
+    std::vector<int> ones(n, 1);
+    return run_mixed(backends, n, ones.data(), tokens, true, out_tokens, out_logits, out_partials);
+}
+
+zr_status zrh_forward_mixed(zrh_backend* const* backends, int n, const int* q_len, const uint32_t* tokens,
+                            uint32_t* out_tokens, float* out_logits, float* out_partials) {
+    if (!backends || !tokens || !q_len || n <= 0) return set_global_err(ZR_E_INVALID, "null argument");
+    return run_mixed(backends, n, q_len, tokens, false, out_tokens, out_logits, out_partials);
+}
+
+zr_status zrh_stage_mixed(zrh_backend* const* backends, int n, const int* q_len, const uint32_t* tokens,
+                          zr_staged** out) {
+    if (!backends || !q_len || !out || n <= 0) return set_global_err(ZR_E_INVALID, "null argument");
+    if (!backends[0]->ctx) return set_global_err(ZR_E_INVALID, "bookkeeping-only pool has no device context");
+    Assembled a;
+    std::vector<SessionKV> saved;
+    std::vector<int> saved_pos;
+    zr_status rc = assemble(backends, n, q_len, false, a, saved, saved_pos);
+    if (rc) return rc;
+    zr_microbatch mb = as_microbatch(a, tokens);
+    rc = zr_stage(backends[0]->ctx, &mb, out);
+    if (rc) {
+        for (int i = 0; i < n; ++i) {
+            backends[i]->kv = saved[i];
+            backends[i]->position = saved_pos[i];
+        }
+        return rc;
+    }
+    for (int i = 0; i < n; ++i) backends[i]->position += q_len[i];
+    return ZR_OK;
+}
+
+int zrh_cache_seq_len(const zrh_backend* b) { return b ? b->kv.seq_len : 0; }
+int zrh_sequence_position(const zrh_backend* b) { return b ? b->position : 0; }
+int zrh_logical_kv_tokens(const zrh_backend* b) { return b ? b->position - b->kv.base_position : 0; }
+int zrh_base_position(const zrh_backend* b) { return b ? b->kv.base_position : 0; }
+int zrh_allocated_pages(const zrh_backend* b) { return b ? (int)b->kv.pages.size() : 0; }
+
+uint64_t zrh_live_kv_cache_bytes(const zrh_backend* b) {
+    // DeviceLayerKVCache::memory_usage (883-891) summed over layers, at the
+    // pool's element size.
+    if (!b || !b->ctx) return 0;
+    const zr_context* ctx = b->ctx;
+    const uint64_t esz = ctx->desc.kv_dtype == ZR_DTYPE_BF16 ? 2 : 4;
+    return (uint64_t)b->kv.pages.size() * kPageRows * ctx->kv_cols * esz * 2 * ctx->desc.num_layers;
+}
+
+int zrh_block_table(const zrh_backend* b, uint32_t* page_ids, int* start_tokens, int* token_counts, int* global_pages,
+                    int capacity) {
+    if (!b) return set_global_err(ZR_E_INVALID, "null backend");
+    const SessionKV& kv = b->kv;
+    const int n = (int)kv.spans.size();
+    if (page_ids || start_tokens || token_counts || global_pages) {
+        if (capacity < n) return set_err(b->ctx, ZR_E_INVALID, "block table has %d spans > capacity %d", n, capacity);
+        for (int i = 0; i < n; ++i) {
+            const Span& s = kv.spans[i];
+            if (page_ids) page_ids[i] = (uint32_t)s.page_index;
+            if (start_tokens) start_tokens[i] = s.start_row;
+            if (token_counts) token_counts[i] = s.row_count;
+            if (global_pages) global_pages[i] = kv.pages[s.page_index].global;
+        }
+    }
+    return n;
+}
+
+zr_status zrh_export_kv(const zrh_backend* cb, int max_cached_tokens, float* k, float* v, int* rows,
+                        int* base_position, int* next_position) {
+    zrh_backend* b = (zrh_backend*)cb;
+    if (!b || !rows) return set_global_err(ZR_E_INVALID, "null argument");
+    const SessionKV& kv = b->kv;
+    if (kv.base_position + kv.seq_len != b->position)
+        return set_err(b->ctx, ZR_E_INVARIANT, "Device KV export next_position %d does not match cache next position %d",
+                       b->position, kv.base_position + kv.seq_len);
+    if (next_position) *next_position = b->position;
+    *rows = 0;
+    if (base_position) *base_position = kv.base_position;
+    if (kv.seq_len == 0) return ZR_OK;
+    int keep = kv.seq_len;
+    if (max_cached_tokens >= 0) keep = std::min(keep, std::max(max_cached_tokens, 1));
+    if (!k || !v) return set_err(b->ctx, ZR_E_INVALID, "null export buffers");
+    if (!b->ctx) return set_global_err(ZR_E_INVALID, "bookkeeping-only pool has no device context");
+    std::vector<int> table;
+    int foff = 0;
+    zr_status rc = device_table(b, table, &foff);
+    if (!rc) rc = zr_kv_gather(b->ctx, table.data(), (int)table.size(), foff, kv.seq_len - keep, keep, k, v);
+    if (rc) return rc;
+    *rows = keep;
+    if (base_position) *base_position = kv.base_position + (kv.seq_len - keep);
+    return ZR_OK;
+}
+
+zr_status zrh_import_kv(zrh_backend* b, const float* k, const float* v, int rows, int base_position,
+                        int next_position) {
+    if (!b) return set_global_err(ZR_E_INVALID, "null argument");
+    if (rows < 0 || rows > next_position)
+        return set_err(b->ctx, ZR_E_INVALID, "KV sequence state is invalid: cached_tokens %d exceeds next_position %d",
+                       rows, next_position);
+    if (base_position != next_position - rows)
+        return set_err(b->ctx, ZR_E_INVALID, "KV snapshot base position mismatch: payload starts at %d, sequence metadata says %d",
+                       base_position, next_position - rows);
+    const SessionKV saved = b->kv;
+    const int saved_pos = b->position;
+    clear_kv(b->kv);
+    b->kv.base_position = base_position;
+    zr_status rc = ZR_OK;
+    if (rows > 0) {
+        if (!k || !v) rc = set_err(b->ctx, ZR_E_INVALID, "null import buffers");
+        if (!b->ctx) rc = set_global_err(ZR_E_INVALID, "bookkeeping-only pool has no device context");
+        const int max_seq = std::max(b->max_seq_len, 1);
+        const int keep = std::min(rows, max_seq);
+        if (!rc) rc = append_rows(b, keep);
+        if (!rc && b->kv.seq_len != rows)
+            rc = set_err(b->ctx, ZR_E_INVARIANT, "Recovered device KV cache length %d does not match snapshot cached token count %d",
+                         b->kv.seq_len, rows);
+        std::vector<int> table;
+        int foff = 0;
+        if (!rc) rc = device_table(b, table, &foff);
+        if (!rc) rc = zr_kv_scatter(b->ctx, table.data(), (int)table.size(), foff, 0, rows, k, v);
+    }
+    if (!rc && b->kv.base_position != next_position - rows)
+        rc = set_err(b->ctx, ZR_E_INVARIANT, "Recovered device KV cache base position %d does not match snapshot first cached position %d",
+                     b->kv.base_position, next_position - rows);
+    if (rc) {
+        b->kv = saved;
+        b->position = saved_pos;
+        return rc;
+    }
+    b->position = next_position;
+    return ZR_OK;
+}
+
+void zrh_clear(zrh_backend* b) {
+    if (!b) return;
+    clear_kv(b->kv);
+    b->position = 0;
+}
+
+zr_status zrh_release_pages(zrh_backend* b) {
+    if (!b) return set_global_err(ZR_E_INVALID, "null backend");
+    for (const PageEntry& p : b->kv.pages)
+        if (p.global >= 0) b->pool->free_list.push_back(p.global);
+    b->kv = SessionKV();
+    b->position = 0;
+    return ZR_OK;
+}
+
+zr_status zrh_kv_reserve(zrh_backend* b, int rows) {
+    if (!b) return set_global_err(ZR_E_INVALID, "null backend");
+    if (rows <= 0) return set_err(b->ctx, ZR_E_INVALID, "Device KV append received an empty key shape");
+    const SessionKV saved = b->kv;
+    zr_status rc = append_rows(b, rows);
+    if (rc) {
+        b->kv = saved;
+        return rc;
+    }
+    b->position = b->kv.base_position + b->kv.seq_len;
+    return ZR_OK;
+}
+
+zr_status zrh_retain_suffix(zrh_backend* b, int keep_rows) {
+    if (!b) return set_global_err(ZR_E_INVALID, "null backend");
+    const SessionKV saved = b->kv;
+    zr_status rc = retain_suffix(b, keep_rows);
+    if (rc) {
+        b->kv = saved;
+        return rc;
+    }
+    b->position = b->kv.base_position + b->kv.seq_len;
+    return ZR_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,198 @@
+// Internal declarations of the zip MI355X provider: context layout, kernel
+// launchers and small device helpers shared by the .hip translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/zip_rocm.h"
+
+namespace zr {
+
+constexpr int kPageRows = 16;   // DEFAULT_LIVE_KV_PAGE_TOKENS (kv_cache.rs:214)
+constexpr int kWave = 64;       // CDNA wavefront
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+
+// ---------------------------------------------------------------- helpers
+__host__ __device__ inline uint16_t f32_to_bf16_bits(float x) {
+    uint32_t u = __builtin_bit_cast(uint32_t, x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+__host__ __device__ inline float bf16_bits_to_f32(uint16_t h) {
+    return __builtin_bit_cast(float, (uint32_t)h << 16);
+}
+
+// Split x into bf16 hi + lo with x ~= hi + lo to ~2^-16 relative.
+__device__ inline void split_bf16(float x, uint16_t& hi, uint16_t& lo) {
+    hi = f32_to_bf16_bits(x);
+    lo = f32_to_bf16_bits(x - bf16_bits_to_f32(hi));
+}
+
+// --------------------------------------------------------------- context
+struct StagedMeta;  // device copy of one microbatch's metadata
+
+struct LayerDev {
+    uint16_t* w_qkv = nullptr;     // packed [K=H, N=Q+2Kc]
+    uint16_t* w_o = nullptr;       // packed [K=Q, N=H]
+    uint16_t* w_gate_up = nullptr; // packed [K=H, N=2F] ([gate|up])
+    uint16_t* w_down = nullptr;    // packed [K=F, N=H]
+    float* attn_norm = nullptr;
+    float* mlp_norm = nullptr;
+};
+
+struct TimingState {
+    bool enabled = false;
+    std::vector<hipEvent_t> pool;    // recycled events
+    std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> spans;
+    size_t next_event = 0;
+};
+
+}  // namespace zr
+
+struct zr_context {
+    zr_model_desc desc{};
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+
+    // shard geometry (resolve_attention_shard_layout)
+    int head_dim = 0, q_cols = 0, kv_cols = 0, local_q_heads = 0, local_kv_heads = 0;
+    int q_per_kv = 0, q_head_start = 0, kv_head_start = 0;
+    std::vector<uint32_t> kv_head_map;
+
+    // weights
+    std::vector<zr::LayerDev> layers;
+    uint16_t* embedding = nullptr;  // [V, H] bf16 (row gather)
+    uint16_t* lm_head = nullptr;    // packed [K=H, N=V]
+    float* final_norm = nullptr;
+    float* inv_freq = nullptr;      // [head_dim/2] host powf table
+
+    // KV pool: layer l, page p at kv_pool + (l * n_pages + p) * page_bytes;
+    // K block then V block, each [kv_heads][page layout] in kv dtype.
+    void* kv_pool = nullptr;
+    int n_pages = 0;
+    size_t page_bytes = 0;   // bytes of one page of one layer (K and V)
+
+    // activations (max_tokens rows)
+    float* hidden = nullptr;  // [T, H] residual stream
+    float* xn = nullptr;      // [T, H] normed GEMM input
+    float* qkv = nullptr;     // [T, Q + 2Kc]
+    float* q_rope = nullptr;  // [T, Q]
+    float* attn = nullptr;    // [T, Q]
+    float* proj = nullptr;    // [T, H] O / down projection output
+    float* ffn = nullptr;     // [T, 2F] gate|up, then SwiGLU output [T, F]
+    float* logits = nullptr;  // [S, V]
+    float* final_x = nullptr; // [S, H] normed last rows
+    uint32_t* tokens_out = nullptr; // [S]
+    float* splitk_ws = nullptr;     // split-K partial workspace
+    size_t splitk_ws_floats = 0;
+    float* attn_part = nullptr;     // attention split partials
+    size_t attn_part_floats = 0;
+    float* argmax_ws = nullptr;     // argmax partials
+    size_t argmax_ws_floats = 0;
+
+    zr::StagedMeta* scratch_stage = nullptr;  // reused by zr_forward
+    zr::TimingState timing;
+};
+
+namespace zr {
+
+// Error helpers --------------------------------------------------------
+zr_status set_err(zr_context* ctx, zr_status code, const char* fmt, ...);
+zr_status set_global_err(zr_status code, const char* fmt, ...);
+
+#define ZR_HIP(ctx, expr)                                                            \
+    do {                                                                            \
+        hipError_t e__ = (expr);                                                    \
+        if (e__ != hipSuccess)                                                      \
+            return ::zr::set_err((ctx), ZR_E_HIP, "%s failed: %s (%s:%d)", #expr,   \
+                                 hipGetErrorString(e__), __FILE__, __LINE__);       \
+    } while (0)
+
+#define ZR_LAUNCH_CHECK(ctx)                                                         \
+    do {                                                                            \
+        hipError_t e__ = hipGetLastError();                                         \
+        if (e__ != hipSuccess)                                                      \
+            return ::zr::set_err((ctx), ZR_E_HIP, "kernel launch failed: %s (%s:%d)", \
+                                 hipGetErrorString(e__), __FILE__, __LINE__);       \
+    } while (0)
+
+// Timing of kernel classes (HIP events on the context stream).
+enum { kClassAttention = 0, kClassGemm = 1, kClassNormRopeKv = 2, kClassOther = 3 };
+void timing_mark_begin(zr_context* ctx, int cls, hipEvent_t* out);
+void timing_mark_end(zr_context* ctx, int cls, hipEvent_t begin);
+
+// Staged microbatch metadata (device) ------------------------------------
+struct StagedMeta {
+    zr_context* ctx = nullptr;
+    int num_seqs = 0, total_q = 0, stride = 0;
+    int max_kv = 0;           // max kv_after over sequences
+    int n_attn_items = 0;     // attention work items (per kv head)
+    int n_tiles = 0;          // attention query tiles (per kv head)
+    bool owns = true;
+    // one device allocation holding every array below
+    void* dev = nullptr;
+    size_t dev_bytes = 0, cap_bytes = 0;
+    // device arrays
+    int* q_len = nullptr;
+    int* kv_before = nullptr;
+    int* first_pos = nullptr;
+    int* first_offset = nullptr;
+    int* block_tables = nullptr;
+    uint32_t* tokens = nullptr;
+    int* cu_q = nullptr;        // [S+1]   (pack kernel output)
+    int* cu_k = nullptr;        // [S+1]
+    int* positions = nullptr;   // [T]
+    int* slot_mapping = nullptr;// [T]
+    int* seq_ids = nullptr;     // [T]
+    int* last_rows = nullptr;   // [S] row index of each sequence's last token
+    int4* attn_items = nullptr; // [n_attn_items] {tile, page_begin, page_end, part_index}
+    int4* attn_tiles = nullptr; // [n_tiles] {seq, q0, nq, first_part}
+    int* tile_nparts = nullptr; // [n_tiles]
+    // host copies
+    std::vector<int> h_q_len, h_kv_before, h_first_pos, h_first_offset, h_block_tables;
+    std::vector<int4> h_items, h_tiles;
+    std::vector<int> h_tile_nparts;
+    std::vector<uint32_t> h_tokens;
+    std::vector<unsigned char> h_blob;
+};
+
+zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta* st);
+
+// Kernel launchers (one per .hip file) ------------------------------------
+zr_status launch_pack(zr_context* ctx, StagedMeta* st);
+zr_status launch_embed(zr_context* ctx, StagedMeta* st, const uint32_t* d_tokens);
+zr_status launch_rms_norm(zr_context* ctx, const float* x, const float* residual_in,
+                          float* x_out, const float* gamma, float* y, const int* row_index,
+                          int rows, int cols);
+zr_status launch_rope_kv_write(zr_context* ctx, StagedMeta* st, int layer, const float* qkv,
+                               float* q_out, int rope);
+zr_status launch_attention(zr_context* ctx, StagedMeta* st, int layer, const float* q, float* out);
+zr_status launch_kv_copy(zr_context* ctx, int layer_begin, int layer_end, const int* d_table,
+                         int first_offset, int first_row, int n_rows, float* k, float* v,
+                         int to_pool);
+zr_status launch_argmax(zr_context* ctx, const float* x, int rows, int cols, uint32_t* out);
+
+enum GemmEpilogue { kEpiStore = 0, kEpiSwiGLU = 1 };
+// C = A @ W (W packed), epilogue applied after the split-K reduction.
+zr_status launch_gemm(zr_context* ctx, const float* a, const uint16_t* w_packed, float* c, int m,
+                      int n, int k, int epilogue);
+zr_status pack_weight(zr_context* ctx, const uint16_t* src /* [K,N] host or device */,
+                      int k, int n, uint16_t** out_packed);
+// Packs [K, n1] | [K, n2] | ... (column concatenation) into one packed matrix.
+zr_status pack_weight_concat(zr_context* ctx, const uint16_t* const* srcs, const int* widths,
+                             int count, int k, uint16_t** out_packed);
+size_t packed_weight_elems(int k, int n);
+
+zr_status launch_fill_normal_bf16(zr_context* ctx, uint16_t* dst, size_t n, uint64_t seed, float std);
+zr_status launch_fill_pool_normal(zr_context* ctx, uint64_t seed, float std);
+
+}  // namespace zr

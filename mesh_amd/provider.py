@@ -1,0 +1,455 @@
+"""The `rocm` execution provider, mirroring zip's provider interface.
+
+Names, argument meaning and error behaviour follow the reference:
+  ExecutionProviderKind           agent/src/provider/mod.rs:8-33 (+ "rocm")
+  ExecutionBackend / ProviderExecutionBackend
+                                  agent/src/inference/backend.rs:30-88, 400-662
+  BackendMicrobatchExecutor.decode_step_batch
+                                  agent/src/inference/backend.rs:107-151
+  DecodeMicrobatchRequest / Output  backend.rs:90-105
+  KVCacheSnapshot                 agent/src/inference/kv_cache.rs:102-187
+Every compute call goes through libzip_rocm.so (HIP kernels on gfx950); a
+missing library raises instead of falling back to the CPU.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import time
+import weakref
+from dataclasses import dataclass, field
+from enum import Enum
+from typing import List, Optional, Sequence
+
+import numpy as np
+
+from . import _lib
+from ._lib import ZrError, check
+
+
+class ExecutionProviderKind(str, Enum):
+    CPU = "cpu"
+    METAL = "metal"
+    CUDA = "cuda"
+    ROCM = "rocm"
+
+    @classmethod
+    def from_str(cls, value: str) -> Optional["ExecutionProviderKind"]:
+        try:
+            return cls(value.strip().lower())
+        except ValueError:
+            return None
+
+
+# FusedKernelStage (engine.rs:124-132) -> the kernels that implement it here.
+FUSED_KERNEL_STAGES = {
+    "norm_qkv": ["rms_norm_kernel", "gemm_kernel"],
+    "rope_kv_write": ["rope_kv_write_kernel"],
+    "paged_attention": ["paged_attention_kernel", "attention_reduce_kernel"],
+    "residual_mlp": ["rms_norm_kernel", "gemm_kernel", "splitk_reduce_kernel"],
+    "device_sampling": ["argmax_partial_kernel", "argmax_final_kernel"],
+}
+
+
+def probe_provider(device: int = 0):
+    """runtime.rs:335-385: (available, error message)."""
+    try:
+        lib = _lib.load()
+    except ImportError as exc:
+        return False, str(exc)
+    info = _lib.DeviceInfo()
+    rc = lib.zr_probe(device, C.byref(info))
+    if rc != 0:
+        return False, lib.zr_global_last_error().decode()
+    return True, None
+
+
+def device_info(device: int = 0) -> dict:
+    lib = _lib.load()
+    info = _lib.DeviceInfo()
+    check(lib.zr_probe(device, C.byref(info)))
+    return {"device_count": info.device_count, "compute_units": info.compute_units,
+            "clock_mhz": info.clock_mhz, "hbm_bytes": info.hbm_bytes, "arch": info.arch.decode()}
+
+
+def _ptr(a: np.ndarray, ctype):
+    return a.ctypes.data_as(C.POINTER(ctype))
+
+
+def bf16_bits(x: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even f32 -> bf16 bit patterns (uint16)."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+class DeviceBuffer:
+    """Device memory owned by a context (zr_device_alloc)."""
+
+    def __init__(self, ctx: "DeviceContext", nbytes: int):
+        self.ctx = ctx
+        self.nbytes = int(nbytes)
+        p = C.c_void_p()
+        check(ctx.lib.zr_device_alloc(ctx.h, self.nbytes, C.byref(p)), ctx.h)
+        self.ptr = p.value
+
+    @classmethod
+    def from_numpy(cls, ctx, arr: np.ndarray) -> "DeviceBuffer":
+        arr = np.ascontiguousarray(arr)
+        buf = cls(ctx, arr.nbytes)
+        buf.upload(arr)
+        return buf
+
+    def upload(self, arr: np.ndarray):
+        arr = np.ascontiguousarray(arr)
+        assert arr.nbytes <= self.nbytes
+        check(self.ctx.lib.zr_memcpy_h2d(self.ctx.h, self.ptr, arr.ctypes.data, arr.nbytes), self.ctx.h)
+
+    def download(self, dtype, shape) -> np.ndarray:
+        out = np.empty(shape, dtype)
+        assert out.nbytes <= self.nbytes
+        check(self.ctx.lib.zr_memcpy_d2h(self.ctx.h, out.ctypes.data, self.ptr, out.nbytes), self.ctx.h)
+        return out
+
+    def free(self):
+        if self.ptr:
+            self.ctx.lib.zr_device_free(self.ctx.h, self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+@dataclass
+class ModelGeometry:
+    """ModelConfig (forward_pass.rs:156-174) plus this worker's shard range."""
+    hidden: int
+    num_heads: int
+    num_kv_heads: int
+    num_layers: int
+    vocab: int
+    ffn: int
+    rms_norm_eps: float = 1e-5
+    rope_base: float = 10000.0
+    shard_start: int = 0
+    shard_end: Optional[int] = None
+    ffn_cols: Optional[int] = None
+
+    def __post_init__(self):
+        if self.shard_end is None:
+            self.shard_end = self.hidden
+        if self.ffn_cols is None:
+            self.ffn_cols = self.ffn
+
+    @property
+    def head_dim(self):
+        return self.hidden // self.num_heads
+
+    @property
+    def q_cols(self):
+        return self.shard_end - self.shard_start
+
+    @property
+    def kv_cols(self):
+        qpk = self.num_heads // self.num_kv_heads
+        return (self.q_cols // (qpk * self.head_dim)) * self.head_dim
+
+
+class DeviceContext:
+    """SharedModelResidency + KV pool of one worker on one GPU (zr_context)."""
+
+    def __init__(self, geo: ModelGeometry, *, kv_dtype: str = "bf16", max_tokens: int = 256,
+                 max_seqs: int = 256, max_pages_per_seq: int = 512, split_activations: bool = False,
+                 device: int = 0):
+        self.lib = _lib.load()
+        self.geo = geo
+        d = _lib.ModelDesc()
+        d.hidden, d.num_heads, d.num_kv_heads = geo.hidden, geo.num_heads, geo.num_kv_heads
+        d.num_layers, d.vocab, d.ffn_cols = geo.num_layers, geo.vocab, geo.ffn_cols
+        d.shard_start, d.shard_end = geo.shard_start, geo.shard_end
+        d.rms_norm_eps, d.rope_base = geo.rms_norm_eps, geo.rope_base
+        d.page_tokens = 16
+        d.kv_dtype = _lib.ZR_DTYPE_BF16 if kv_dtype == "bf16" else _lib.ZR_DTYPE_F32
+        d.max_tokens, d.max_seqs, d.max_pages_per_seq = max_tokens, max_seqs, max_pages_per_seq
+        d.flags = _lib.ZR_FLAG_SPLIT_ACTIVATIONS if split_activations else 0
+        self.desc = d
+        self.kv_dtype = kv_dtype
+        h = C.c_void_p()
+        check(self.lib.zr_context_create(C.byref(d), device, C.byref(h)))
+        self.h = h.value
+        self.pool = None
+        self._backends = weakref.WeakSet()
+
+    def close(self):
+        for b in list(getattr(self, "_backends", ())):
+            b.close()
+        if getattr(self, "pool", None) is not None:
+            self.lib.zrh_pool_destroy(self.pool)
+            self.pool = None
+        if getattr(self, "h", None):
+            self.lib.zr_context_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def check(self, rc):
+        return check(rc, self.h)
+
+    # -- weights (bf16 bits, reference [in, out] layout) -------------------------------
+    def upload_layer(self, layer: int, w: dict):
+        keep = {k: np.ascontiguousarray(v, np.float32 if k.endswith("norm") else np.uint16) for k, v in w.items()}
+        lw = _lib.LayerWeights()
+        for name in ("w_q", "w_k", "w_v", "w_o", "w_gate", "w_up", "w_down"):
+            setattr(lw, name, _ptr(keep[name], C.c_uint16))
+        lw.attn_norm = _ptr(keep["attn_norm"], C.c_float)
+        lw.mlp_norm = _ptr(keep["mlp_norm"], C.c_float)
+        self.check(self.lib.zr_upload_layer(self.h, layer, C.byref(lw)))
+
+    def upload_globals(self, embedding: np.ndarray, final_norm: np.ndarray, lm_head: np.ndarray):
+        e = np.ascontiguousarray(embedding, np.uint16)
+        f = np.ascontiguousarray(final_norm, np.float32)
+        l = np.ascontiguousarray(lm_head, np.uint16)
+        self.check(self.lib.zr_upload_globals(self.h, _ptr(e, C.c_uint16), _ptr(f, C.c_float), _ptr(l, C.c_uint16)))
+
+    def upload_f32_model(self, weights: dict):
+        """Upload a model given as f32 arrays holding bf16-exact values."""
+        for l, lw in enumerate(weights["layers"]):
+            w = {k: bf16_bits(lw[k]) for k in ("w_q", "w_k", "w_v", "w_o", "w_gate", "w_up", "w_down")}
+            w["attn_norm"], w["mlp_norm"] = lw["attn_norm"], lw["mlp_norm"]
+            self.upload_layer(l, w)
+        self.upload_globals(bf16_bits(weights["embedding"]), weights["final_norm"], bf16_bits(weights["lm_head"]))
+
+    # -- KV pool -----------------------------------------------------------------------
+    def create_kv_pool(self, n_pages: int, initial_order: Optional[Sequence[int]] = None):
+        self.check(self.lib.zr_kv_pool_create(self.h, n_pages))
+        if self.pool is not None:
+            self.lib.zrh_pool_destroy(self.pool)
+        p = C.c_void_p()
+        if initial_order is None:
+            self.check(self.lib.zrh_pool_create(self.h, None, 0, C.byref(p)))
+        else:
+            order = np.ascontiguousarray(initial_order, np.int32)
+            self.check(self.lib.zrh_pool_create(self.h, _ptr(order, C.c_int), order.size, C.byref(p)))
+        self.pool = p.value
+
+    @property
+    def free_pages(self) -> int:
+        return self.lib.zrh_pool_free_pages(self.pool)
+
+    def kv_pool_bytes(self) -> int:
+        return int(self.lib.zr_kv_pool_bytes(self.h))
+
+    def kv_head_map(self) -> List[int]:
+        n = C.c_int()
+        out = np.zeros(max(self.geo.num_heads, 1), np.uint32)
+        self.check(self.lib.zr_kv_head_map(self.h, _ptr(out, C.c_uint32), out.size, C.byref(n)))
+        return out[: n.value].tolist()
+
+    def new_backend(self, max_seq_len: int = 4096) -> "RocmExecutionBackend":
+        b = RocmExecutionBackend(self, max_seq_len)
+        self._backends.add(b)
+        return b
+
+
+@dataclass
+class KVCacheSnapshot:
+    """Sequence state + per-layer KV rows (KVCacheSnapshot, kv_cache.rs:102-187)."""
+    next_position: int
+    cached_tokens: int
+    keys: np.ndarray    # [layers, cached_tokens, kv_cols] f32
+    values: np.ndarray
+
+    def first_cached_position(self) -> int:
+        return self.next_position - self.cached_tokens
+
+
+class RocmExecutionBackend:
+    """One session's ExecutionBackend on the rocm provider (zrh_backend)."""
+
+    provider_kind = ExecutionProviderKind.ROCM
+    optimization_profile = "rocm_fused"
+
+    def __init__(self, ctx: DeviceContext, max_seq_len: int = 4096):
+        self.ctx = ctx
+        self.lib = ctx.lib
+        p = C.c_void_p()
+        ctx.check(self.lib.zrh_backend_create(ctx.pool, max_seq_len, C.byref(p)))
+        self.h = p.value
+        self.max_seq_len = max_seq_len
+
+    def close(self):
+        if getattr(self, "h", None) and self.ctx.pool is not None:
+            self.lib.zrh_backend_destroy(self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- ExecutionBackend ---------------------------------------------------------------
+    def prefill(self, tokens: Sequence[int]) -> np.ndarray:
+        toks = np.ascontiguousarray(tokens, np.uint32)
+        logits = np.zeros(self.ctx.geo.vocab, np.float32)
+        greedy = C.c_uint32()
+        self.ctx.check(self.lib.zrh_prefill(self.h, _ptr(toks, C.c_uint32), toks.size, _ptr(logits, C.c_float),
+                                            C.byref(greedy)))
+        self.last_greedy = int(greedy.value)
+        return logits
+
+    def decode_step(self, token: int) -> np.ndarray:
+        logits = np.zeros(self.ctx.geo.vocab, np.float32)
+        greedy = C.c_uint32()
+        self.ctx.check(self.lib.zrh_decode_step(self.h, int(token), _ptr(logits, C.c_float), C.byref(greedy)))
+        self.last_greedy = int(greedy.value)
+        return logits
+
+    def sample(self, logits: np.ndarray, temperature: float, top_p: float, seed: int) -> int:
+        """ForwardPass::sample (forward_pass.rs:2046-2086): greedy when temperature <= 0
+        or (temperature == 1 and top_p >= 1).  The greedy id was computed on the GPU
+        with the logits; stochastic sampling is not provided by this provider yet."""
+        if temperature <= 0.0 or (temperature == 1.0 and top_p >= 1.0):
+            return self.last_greedy
+        raise ZrError(-5, "Device stochastic sampling failed: temperature/top-p sampling is not "
+                          "implemented by the rocm provider")
+
+    def cache_seq_len(self) -> int:
+        return self.lib.zrh_cache_seq_len(self.h)
+
+    def live_kv_cache_bytes(self) -> int:
+        return int(self.lib.zrh_live_kv_cache_bytes(self.h))
+
+    def logical_kv_tokens(self) -> int:
+        return self.lib.zrh_logical_kv_tokens(self.h)
+
+    def sequence_position(self) -> int:
+        return self.lib.zrh_sequence_position(self.h)
+
+    def base_position(self) -> int:
+        return self.lib.zrh_base_position(self.h)
+
+    def allocated_pages(self) -> int:
+        return self.lib.zrh_allocated_pages(self.h)
+
+    def export_kv_cache(self, max_cached_tokens: Optional[int] = None) -> Optional[KVCacheSnapshot]:
+        geo = self.ctx.geo
+        n = self.cache_seq_len()
+        k = np.zeros((geo.num_layers, max(n, 1), geo.kv_cols), np.float32)
+        v = np.zeros_like(k)
+        rows, base, nxt = C.c_int(), C.c_int(), C.c_int()
+        self.ctx.check(self.lib.zrh_export_kv(self.h, -1 if max_cached_tokens is None else int(max_cached_tokens),
+                                              _ptr(k, C.c_float), _ptr(v, C.c_float), C.byref(rows),
+                                              C.byref(base), C.byref(nxt)))
+        r = rows.value
+        if r == 0:
+            return None
+        flat = geo.num_layers * r * geo.kv_cols
+        return KVCacheSnapshot(nxt.value, r, k.reshape(-1)[:flat].reshape(geo.num_layers, r, geo.kv_cols).copy(),
+                               v.reshape(-1)[:flat].reshape(geo.num_layers, r, geo.kv_cols).copy())
+
+    def import_kv_cache(self, snap: KVCacheSnapshot):
+        k = np.ascontiguousarray(snap.keys, np.float32)
+        v = np.ascontiguousarray(snap.values, np.float32)
+        self.ctx.check(self.lib.zrh_import_kv(self.h, _ptr(k, C.c_float), _ptr(v, C.c_float), snap.cached_tokens,
+                                              snap.first_cached_position(), snap.next_position))
+
+    def clear(self):
+        self.lib.zrh_clear(self.h)
+
+    def release_pages(self):
+        self.ctx.check(self.lib.zrh_release_pages(self.h))
+
+    # -- page-table introspection --------------------------------------------------------
+    def block_table(self):
+        n = self.lib.zrh_block_table(self.h, None, None, None, None, 0)
+        if n < 0:
+            self.ctx.check(n)
+        ids = np.zeros(max(n, 1), np.uint32)
+        st = np.zeros(max(n, 1), np.int32)
+        ct = np.zeros(max(n, 1), np.int32)
+        gl = np.zeros(max(n, 1), np.int32)
+        self.ctx.check(min(0, self.lib.zrh_block_table(self.h, _ptr(ids, C.c_uint32), _ptr(st, C.c_int),
+                                                       _ptr(ct, C.c_int), _ptr(gl, C.c_int), n)))
+        return [(int(ids[i]), int(st[i]), int(ct[i]), int(gl[i])) for i in range(n)]
+
+    def kv_reserve(self, rows: int):
+        self.ctx.check(self.lib.zrh_kv_reserve(self.h, rows))
+
+    def retain_suffix(self, keep: int):
+        self.ctx.check(self.lib.zrh_retain_suffix(self.h, keep))
+
+
+@dataclass
+class DecodeMicrobatchRequest:
+    session_id: str
+    token: int
+    backend: RocmExecutionBackend
+    job_id: str = ""
+    temperature: float = 0.0
+    top_p: float = 1.0
+    sampling_seed: int = 0
+
+
+@dataclass
+class DecodeMicrobatchOutput:
+    session_id: str
+    logits: Optional[np.ndarray]
+    sampled_token: Optional[int]
+    execution_time_ms: int
+
+
+def _backend_array(backends):
+    arr = (C.c_void_p * len(backends))(*[b.h for b in backends])
+    return C.cast(arr, C.POINTER(C.c_void_p)), arr
+
+
+class BackendMicrobatchExecutor:
+    @staticmethod
+    def decode_step_batch(requests: List[DecodeMicrobatchRequest], want_logits: bool = False,
+                          partials: Optional[np.ndarray] = None) -> List[DecodeMicrobatchOutput]:
+        """backend.rs:110-151 fast path: one fused microbatch over every session.
+        Greedy requests get `sampled_token` from the device argmax (backend.rs:537-553)."""
+        if not requests:
+            raise ZrError(-1, "Decode microbatch requires at least one backend and token")
+        ctx = requests[0].backend.ctx
+        for r in requests:
+            if r.backend.ctx is not ctx:
+                raise ZrError(-1, "Fast-path decode batch requires one shared model residency")
+            if not (r.temperature <= 0.0 or r.top_p <= 0.0):
+                raise ZrError(-5, "Device stochastic sampling failed: temperature/top-p sampling is not "
+                                  "implemented by the rocm provider")
+        n = len(requests)
+        toks = np.ascontiguousarray([r.token for r in requests], np.uint32)
+        out_tokens = np.zeros(n, np.uint32)
+        logits = np.zeros((n, ctx.geo.vocab), np.float32) if want_logits else None
+        ptrs, _keep = _backend_array([r.backend for r in requests])
+        t0 = time.perf_counter()
+        ctx.check(ctx.lib.zrh_decode_step_batch(ptrs, n, _ptr(toks, C.c_uint32), _ptr(out_tokens, C.c_uint32),
+                                                _ptr(logits, C.c_float) if logits is not None else None,
+                                                _ptr(partials, C.c_float) if partials is not None else None))
+        ms = int((time.perf_counter() - t0) * 1000)
+        return [DecodeMicrobatchOutput(r.session_id, logits[i] if logits is not None else None, int(out_tokens[i]), ms)
+                for i, r in enumerate(requests)]
+
+    @staticmethod
+    def forward_mixed(backends: List[RocmExecutionBackend], chunks: List[Sequence[int]], want_logits: bool = True,
+                      partials: Optional[np.ndarray] = None):
+        """Mixed chunked-prefill + decode microbatch packed into one varlen tensor."""
+        ctx = backends[0].ctx
+        q_len = np.ascontiguousarray([len(c) for c in chunks], np.int32)
+        toks = np.ascontiguousarray(np.concatenate([np.asarray(c, np.uint32) for c in chunks]), np.uint32)
+        n = len(backends)
+        out_tokens = np.zeros(n, np.uint32)
+        logits = np.zeros((n, ctx.geo.vocab), np.float32) if want_logits else None
+        ptrs, _keep = _backend_array(backends)
+        ctx.check(ctx.lib.zrh_forward_mixed(ptrs, n, _ptr(q_len, C.c_int), _ptr(toks, C.c_uint32),
+                                            _ptr(out_tokens, C.c_uint32),
+                                            _ptr(logits, C.c_float) if logits is not None else None,
+                                            _ptr(partials, C.c_float) if partials is not None else None))
+        return out_tokens, logits

@@ -1,0 +1,289 @@
+"""Op-level parity of the HIP kernels against the oracle, through the C-ABI.
+
+Tolerances (from the provider's contract): packing, page tables, KV appends
+and gathers, greedy ids are bit-exact; attention outputs within 2e-3 relative
+(per head: max|got - want| <= 2e-3 * max|want|); GEMM / norm within the stated
+float bounds below.
+"""
+import ctypes as C
+import math
+
+import numpy as np
+import pytest
+
+import oracle as O
+from mesh_amd import DeviceBuffer, DeviceContext, ModelGeometry, _lib
+from tests.gpu_util import f32p, i32p, max_rel_err_rows, stage_mixed, u32p
+
+pytestmark = pytest.mark.gpu
+
+ATTN_RTOL = 2e-3
+
+
+def tiny_llama_attn_ctx(kv_dtype, n_pages=512, order=None, layers=1):
+    # TinyLlama-1.1B attention shape: 32 q heads, 4 kv heads, head_dim 64
+    geo = ModelGeometry(hidden=2048, num_heads=32, num_kv_heads=4, num_layers=layers, vocab=64, ffn=64)
+    ctx = DeviceContext(geo, kv_dtype=kv_dtype, max_tokens=256, max_seqs=64, max_pages_per_seq=128)
+    ctx.create_kv_pool(n_pages, order)
+    return ctx, geo
+
+
+# --------------------------------------------------------------- packing --
+def test_pack_matches_oracle_bit_exact():
+    ctx, geo = tiny_llama_attn_ctx("f32", n_pages=10000)
+    rng = np.random.default_rng(5)
+    n = 37
+    q_len = rng.integers(1, 4, n).astype(np.int32)
+    kv_before = rng.integers(0, 300, n).astype(np.int32)
+    first_off = rng.integers(0, 16, n).astype(np.int32)
+    first_pos = (kv_before + rng.integers(0, 1000, n)).astype(np.int32)
+    pages = (first_off + kv_before + q_len + 15) // 16
+    stride = int(pages.max())
+    bt = np.zeros((n, stride), np.int32)
+    perm = rng.permutation(10000)
+    used = 0
+    for s in range(n):
+        bt[s, :pages[s]] = perm[used:used + pages[s]]
+        used += pages[s]
+    total = int(q_len.sum())
+    mb = _lib.Microbatch(n, i32p(q_len), i32p(kv_before), i32p(first_pos), i32p(first_off), i32p(bt), stride, None)
+    cu_q = np.zeros(n + 1, np.int32)
+    cu_k = np.zeros(n + 1, np.int32)
+    pos = np.zeros(total, np.int32)
+    slot = np.zeros(total, np.int32)
+    seq = np.zeros(total, np.int32)
+    ctx.check(ctx.lib.zr_pack(ctx.h, C.byref(mb), i32p(cu_q), i32p(cu_k), i32p(pos), i32p(slot), i32p(seq)))
+    w = O.pack(q_len, kv_before, first_pos, first_off, bt)
+    for got, want in zip((cu_q, cu_k, pos, slot, seq), w):
+        np.testing.assert_array_equal(got, want)
+    ctx.close()
+
+
+def test_stage_rejects_pages_outside_pool():
+    ctx, geo = tiny_llama_attn_ctx("f32", n_pages=8)
+    one = np.ones(1, np.int32)
+    zero = np.zeros(1, np.int32)
+    bt = np.array([[9]], np.int32)
+    mb = _lib.Microbatch(1, i32p(one), i32p(zero), i32p(zero), i32p(zero), i32p(bt), 1, None)
+    st = C.c_void_p()
+    rc = ctx.lib.zr_stage(ctx.h, C.byref(mb), C.byref(st))
+    assert rc == -4 and b"outside pool" in ctx.lib.zr_last_error(ctx.h)
+    ctx.close()
+
+
+# ------------------------------------------------ C1: attention + append --
+def c1_inputs(seed=0xC1):
+    rng = np.random.default_rng(seed)
+    B = 8
+    ctxlens = rng.integers(16, 513, B)
+    order = rng.permutation(512)
+    Q = rng.standard_normal((B, 32 * 64), dtype=np.float32)
+    K = [rng.standard_normal((L, 256), dtype=np.float32) for L in ctxlens]
+    V = [rng.standard_normal((L, 256), dtype=np.float32) for L in ctxlens]
+    return B, ctxlens, order, Q, K, V
+
+
+def run_c1(kv_dtype):
+    B, ctxlens, order, Q, K, V = c1_inputs()
+    ctx, geo = tiny_llama_attn_ctx(kv_dtype, 512, order)
+    backends = [ctx.new_backend() for _ in range(B)]
+    # prefix rows (L - 1) scattered into the permuted pool
+    for b, L, k, v in zip(backends, ctxlens, K, V):
+        if L > 1:
+            b.import_kv_cache(_snapshot(k[:-1], v[:-1]))
+    st = stage_mixed(ctx, backends, [1] * B)
+    qkv = np.concatenate([Q, np.stack([k[-1] for k in K]), np.stack([v[-1] for v in V])], 1)
+    d_qkv = DeviceBuffer.from_numpy(ctx, qkv)
+    d_q = DeviceBuffer(ctx, Q.nbytes)
+    d_o = DeviceBuffer(ctx, Q.nbytes)
+    ctx.check(ctx.lib.zr_rope_kv_write(ctx.h, st, 0, d_qkv.ptr, d_q.ptr, 0))
+    ctx.check(ctx.lib.zr_attention(ctx.h, st, 0, d_q.ptr, d_o.ptr))
+    out = d_o.download(np.float32, Q.shape)
+    ctx.lib.zr_staged_destroy(st)
+    return ctx, backends, (B, ctxlens, order, Q, K, V), out
+
+
+def _snapshot(k, v):
+    from mesh_amd import KVCacheSnapshot
+
+    return KVCacheSnapshot(next_position=k.shape[0], cached_tokens=k.shape[0], keys=k[None], values=v[None])
+
+
+@pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
+def test_c1_paged_gqa_decode_attention_and_append(kv_dtype):
+    ctx, backends, (B, ctxlens, order, Q, K, V), out = run_c1(kv_dtype)
+    bf = kv_dtype == "bf16"
+    for s in range(B):
+        o = O.Session(1, 256, 16, 4096, kv_round_bf16=bf)
+        o.append_layer(0, K[s], V[s])
+        ok, ov = o.gather(0)
+        # the appended row and every page: bit-exact against the oracle's cache
+        snap = backends[s].export_kv_cache()
+        assert snap.cached_tokens == ctxlens[s]
+        np.testing.assert_array_equal(snap.keys[0], ok)
+        np.testing.assert_array_equal(snap.values[0], ov)
+        # attention per q head (GQA: q head h reads kv head h // 8)
+        want = np.zeros(32 * 64, np.float32)
+        for h in range(32):
+            kvh = h // 8
+            want[h * 64:(h + 1) * 64] = O.causal_attention_with_prefix(
+                Q[s, h * 64:(h + 1) * 64][None], ok[:, kvh * 64:(kvh + 1) * 64], ov[:, kvh * 64:(kvh + 1) * 64],
+                1 / math.sqrt(64), ctxlens[s] - 1)[0]
+        err = max_rel_err_rows(out[s], want, 64)
+        assert err <= ATTN_RTOL, (s, err)
+    # page tables: session-local ids are the reference's sequential ids; the
+    # global pages are exactly the first pops of the seeded permutation (LIFO)
+    used = []
+    for b in backends:
+        table = b.block_table()
+        assert [p for p, _, _, _ in table] == list(range(len(table)))
+        used += [g for _, _, _, g in table]
+    assert sorted(used) == sorted(int(x) for x in order[::-1][:len(used)])
+    ctx.close()
+
+
+def test_c1_raw_page_row_holds_appended_kv_in_pool_layout():
+    ctx, backends, (B, ctxlens, order, Q, K, V), out = run_c1("f32")
+    s = 3
+    table = backends[s].block_table()
+    last = table[-1]
+    row = (last[1] + last[2] - 1)  # row of the newest token inside its page
+    page = np.zeros(2 * 256 * 16, np.float32)
+    pages = np.array([last[3]], np.int32)
+    ctx.check(ctx.lib.zr_kv_read_pages(ctx.h, 0, i32p(pages), 1, page.ctypes.data))
+    kblk, vblk = page[:4096].reshape(4, 16 * 64), page[4096:].reshape(4, 16 * 64)
+    for h in range(4):
+        for d in range(64):
+            assert kblk[h][((d // 8) * 16 + row) * 8 + d % 8] == K[s][-1][h * 64 + d]
+            assert vblk[h][((row // 4) * 64 + d) * 4 + row % 4] == V[s][-1][h * 64 + d]
+    ctx.close()
+
+
+@pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
+def test_chunked_prefill_attention_causal_with_prefix(kv_dtype):
+    """Masked multi-query attention with a cached prefix (forward_pass.rs:2764-2836):
+    chunk rows see keys [0, prefix + r]; a page-unaligned prefix is included."""
+    ctx, geo = tiny_llama_attn_ctx(kv_dtype, 4096)
+    rng = np.random.default_rng(11)
+    prefixes, chunks = [0, 37, 512, 1000], [5, 40, 33, 16]
+    backends = [ctx.new_backend() for _ in prefixes]
+    Ks, Vs = [], []
+    for b, p, c in zip(backends, prefixes, chunks):
+        k = rng.standard_normal((p + c, 256), dtype=np.float32)
+        v = rng.standard_normal((p + c, 256), dtype=np.float32)
+        Ks.append(k)
+        Vs.append(v)
+        if p:
+            b.import_kv_cache(_snapshot(k[:p], v[:p]))
+    T = sum(chunks)
+    Q = rng.standard_normal((T, 2048), dtype=np.float32)
+    newk = np.concatenate([k[p:] for k, p in zip(Ks, prefixes)])
+    newv = np.concatenate([v[p:] for v, p in zip(Vs, prefixes)])
+    st = stage_mixed(ctx, backends, chunks)
+    d_qkv = DeviceBuffer.from_numpy(ctx, np.concatenate([Q, newk, newv], 1))
+    d_q = DeviceBuffer(ctx, Q.nbytes)
+    d_o = DeviceBuffer(ctx, Q.nbytes)
+    ctx.check(ctx.lib.zr_rope_kv_write(ctx.h, st, 0, d_qkv.ptr, d_q.ptr, 0))
+    ctx.check(ctx.lib.zr_attention(ctx.h, st, 0, d_q.ptr, d_o.ptr))
+    out = d_o.download(np.float32, Q.shape)
+    ctx.lib.zr_staged_destroy(st)
+    row = 0
+    for s, (p, c) in enumerate(zip(prefixes, chunks)):
+        k, v = Ks[s], Vs[s]
+        if kv_dtype == "bf16":
+            k, v = O.round_bf16(k), O.round_bf16(v)
+        for h in range(32):
+            kvh = h // 8
+            want = O.causal_attention_with_prefix(Q[row:row + c, h * 64:(h + 1) * 64], k[:, kvh * 64:(kvh + 1) * 64],
+                                                  v[:, kvh * 64:(kvh + 1) * 64], 1 / math.sqrt(64), p)
+            err = max_rel_err_rows(out[row:row + c, h * 64:(h + 1) * 64], want, 64)
+            assert err <= ATTN_RTOL, (s, h, err)
+        row += c
+    ctx.close()
+
+
+# ------------------------------------------------------- gather / scatter --
+@pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
+def test_kv_gather_scatter_round_trip_with_partial_first_page(kv_dtype):
+    ctx, geo = tiny_llama_attn_ctx(kv_dtype, 256, layers=3)
+    rng = np.random.default_rng(2)
+    b = ctx.new_backend(max_seq_len=4096)
+    k = rng.standard_normal((3, 50, 256), dtype=np.float32)
+    v = rng.standard_normal((3, 50, 256), dtype=np.float32)
+    if kv_dtype == "bf16":
+        k, v = O.round_bf16(k), O.round_bf16(v)
+    from mesh_amd import KVCacheSnapshot
+
+    b.import_kv_cache(KVCacheSnapshot(50, 50, k, v))
+    b.retain_suffix(37)  # first span now starts at row 13
+    assert b.block_table()[0][1] == 13
+    full = b.export_kv_cache()
+    np.testing.assert_array_equal(full.keys, k[:, 13:])
+    np.testing.assert_array_equal(full.values, v[:, 13:])
+    seg = b.export_kv_cache(max_cached_tokens=20)  # segmented retention window
+    assert seg.cached_tokens == 20 and seg.next_position == 50 and seg.first_cached_position() == 30
+    np.testing.assert_array_equal(seg.keys, k[:, 30:])
+    # import into a fresh session on other pages: identical bytes back
+    b2 = ctx.new_backend(max_seq_len=4096)
+    b2.import_kv_cache(seg)
+    back = b2.export_kv_cache()
+    np.testing.assert_array_equal(back.keys, seg.keys)
+    np.testing.assert_array_equal(back.values, seg.values)
+    assert b2.sequence_position() == 50 and b2.base_position() == 30
+    ctx.close()
+
+
+# -------------------------------------------------------------- GEMM etc --
+@pytest.mark.parametrize("split", [True, False])
+@pytest.mark.parametrize("m,k,n", [(1, 64, 100), (7, 256, 4112), (32, 2048, 2048), (100, 512, 1000),
+                                   (256, 4096, 1024), (300, 128, 64)])
+def test_gemm_matches_fp64(split, m, k, n):
+    geo = ModelGeometry(hidden=256, num_heads=4, num_kv_heads=4, num_layers=1, vocab=64, ffn=256)
+    ctx = DeviceContext(geo, kv_dtype="f32", max_tokens=16, max_seqs=4, max_pages_per_seq=4, split_activations=split)
+    rng = np.random.default_rng(m + k + n)
+    a = rng.standard_normal((m, k), dtype=np.float32)
+    w = O.round_bf16(rng.standard_normal((k, n), dtype=np.float32) * 0.02)
+    d_a = DeviceBuffer.from_numpy(ctx, a)
+    d_c = DeviceBuffer(ctx, m * n * 4)
+    from mesh_amd import bf16_bits
+
+    wb = bf16_bits(w)
+    ctx.check(ctx.lib.zr_gemm(ctx.h, d_a.ptr, wb.ctypes.data, d_c.ptr, m, n, k))
+    got = d_c.download(np.float32, (m, n))
+    ref = a.astype(np.float64) @ w.astype(np.float64)
+    scale = np.sqrt(k) * 0.02  # typical |c| magnitude
+    # hi+lo activations: ~2^-16 relative per product; bf16 activations: ~2^-8
+    tol = 2e-5 * scale if split else 1.5e-2 * scale
+    assert np.max(np.abs(got - ref)) <= tol, np.max(np.abs(got - ref)) / scale
+    ctx.close()
+
+
+def test_rms_norm_matches_oracle():
+    geo = ModelGeometry(hidden=256, num_heads=4, num_kv_heads=4, num_layers=1, vocab=64, ffn=256)
+    ctx = DeviceContext(geo, kv_dtype="f32", max_tokens=16, max_seqs=4, max_pages_per_seq=4)
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((37, 4096), dtype=np.float32) * 3
+    g = rng.standard_normal(4096, dtype=np.float32)
+    d_x, d_g, d_y = DeviceBuffer.from_numpy(ctx, x), DeviceBuffer.from_numpy(ctx, g), DeviceBuffer(ctx, x.nbytes)
+    ctx.check(ctx.lib.zr_rms_norm(ctx.h, d_x.ptr, d_g.ptr, d_y.ptr, 37, 4096))
+    np.testing.assert_allclose(d_y.download(np.float32, x.shape), O.rms_norm(x, g, 1e-5), rtol=2e-6, atol=2e-6)
+    ctx.close()
+
+
+def test_argmax_first_index_on_ties_and_large_vocab():
+    geo = ModelGeometry(hidden=256, num_heads=4, num_kv_heads=4, num_layers=1, vocab=64, ffn=256)
+    ctx = DeviceContext(geo, kv_dtype="f32", max_tokens=16, max_seqs=4, max_pages_per_seq=4)
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((6, 128256), dtype=np.float32)
+    x[0, :4] = [1.0, 5.0, 2.0, 3.0]  # tensor_ops.rs:633-639 -> 1
+    x[0, 4:] = -10
+    x[1, 70000] = x[1, 3] = x[1, 100000] = 99.0  # ties -> lowest index
+    x[2] = -np.inf
+    x[3, 128255] = 50.0
+    d_x, d_o = DeviceBuffer.from_numpy(ctx, x), DeviceBuffer(ctx, 6 * 4)
+    ctx.check(ctx.lib.zr_argmax(ctx.h, d_x.ptr, 6, 128256, d_o.ptr))
+    got = d_o.download(np.uint32, 6)
+    want = [O.sample_greedy(r) for r in x]
+    assert got.tolist() == want
+    assert got[:4].tolist() == [1, 3, 0, 128255]
+    ctx.close()
