@@ -1,0 +1,306 @@
+"""Decode-step benchmark of the rocm provider on one MI355X.
+
+Headline workload: one ragged decode step of a Llama-3-8B-shape model
+(32 layers, hidden 4096, 32 q / 8 kv heads, head_dim 128, FFN 14336, vocab
+128256, bf16 weights and bf16 paged KV) over 256 sessions whose contexts are
+lognormal (median 1024, sigma 1, clipped to [64, 8192]), page 16.  The bs-32
+TinyLlama-shape step (22 layers, contexts U[128, 2048]) is measured in the same
+run and reported under "bs32".
+
+Inputs are resident in HBM before the timed region: weights are random-init
+bf16 N(0, 0.02) generated on the device, the KV pages of every session's
+context are filled with N(0, 1) bf16 (standing in for prefill output), and the
+per-step metadata (page tables after each step's append) is staged on the
+device ahead of time.  Each step feeds its greedy tokens to the next step on
+the device.  The attention kernel's duration comes from HIP events recorded on
+the provider's stream around every attention launch in the timed region.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--skip-bs32]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+METRIC = "decode tokens/sec @1 MI355X (bs 32/256); paged-attn HBM GB/s as % of peak"
+
+
+def contexts_lognormal(seed, n, median, sigma, lo, hi):
+    rng = np.random.default_rng(seed)
+    return np.clip(np.round(rng.lognormal(math.log(median), sigma, n)), lo, hi).astype(np.int64)
+
+
+def contexts_uniform(seed, n, lo, hi):
+    return np.random.default_rng(seed).integers(lo, hi + 1, n).astype(np.int64)
+
+
+WORKLOADS = {
+    "llama3_8b_b256": dict(
+        geo=dict(hidden=4096, num_heads=32, num_kv_heads=8, num_layers=32, vocab=128256, ffn=14336,
+                 rope_base=500000.0),
+        batch=256, max_seq_len=8192,
+        contexts=lambda: contexts_lognormal(0xC5, 256, 1024, 1.0, 64, 8192),
+        desc="Llama-3-8B-shape decode step, 256 sessions, lognormal contexts (median 1024, sigma 1, "
+             "clip [64, 8192]), page 16, bf16 weights + bf16 KV, 32 layers, greedy"),
+    "tinyllama_b32": dict(
+        geo=dict(hidden=2048, num_heads=32, num_kv_heads=4, num_layers=22, vocab=32000, ffn=5632,
+                 rope_base=10000.0),
+        batch=32, max_seq_len=4096,
+        contexts=lambda: contexts_uniform(0xC2, 32, 128, 2048),
+        desc="TinyLlama-1.1B-shape decode step, 32 sessions, contexts U[128, 2048], page 16, "
+             "bf16 weights + bf16 KV, 22 layers, greedy"),
+}
+
+
+def step_bytes(geo, batch, kv_rows_total):
+    """Algorithmic HBM bytes of one decode step: every weight once (bf16), the
+    embedding rows, every cached K/V row of every layer once (bf16), the new
+    K/V rows written, and the per-row activations in and out of each kernel."""
+    H, Q, KV, F, V, L = geo.hidden, geo.q_cols, geo.kv_cols, geo.ffn_cols, geo.vocab, geo.num_layers
+    weights = 2 * (L * (H * (Q + 2 * KV) + Q * H + H * 2 * F + F * H) + H * V) + 4 * (2 * L + 1) * H
+    kv = L * kv_rows_total * KV * 2 * 2 + L * batch * KV * 2 * 2
+    act = 4 * batch * (L * (3 * H + 2 * (Q + 2 * KV) + 2 * Q + 2 * H + 3 * F + 2 * H) + V)
+    return weights + 2 * batch * H + kv + act
+
+
+class GpuDecodeBench:
+    """One workload resident on the GPU with `steps_total` decode steps staged."""
+
+    def __init__(self, name, steps_total):
+        from mesh_amd import DeviceContext, ModelGeometry, _lib
+
+        self._lib = _lib
+        w = WORKLOADS[name]
+        self.name, self.w = name, w
+        self.geo = g = ModelGeometry(**w["geo"])
+        self.B = w["batch"]
+        self.ctxlens = w["contexts"]()
+        self.max_seq = w["max_seq_len"]
+        self.ctx = DeviceContext(g, kv_dtype="bf16", max_tokens=self.B, max_seqs=self.B,
+                                 max_pages_per_seq=self.max_seq // 16 + 2)
+        ctx, lib = self.ctx, self.ctx.lib
+        H, Q, KV, F, V = g.hidden, g.q_cols, g.kv_cols, g.ffn_cols, g.vocab
+        shapes = dict(w_q=(H, Q), w_k=(H, KV), w_v=(H, KV), w_o=(Q, H), w_gate=(H, F), w_up=(H, F), w_down=(F, H))
+        bufs = {k: self._dev(2 * a * b) for k, (a, b) in shapes.items()}
+        ones = np.ones(H, np.float32)
+        for layer in range(g.num_layers):
+            for i, (k, (a, b)) in enumerate(shapes.items()):
+                ctx.check(lib.zr_fill_normal_bf16(ctx.h, bufs[k], a * b, 1000 * layer + i + 1, 0.02))
+            lw = _lib.LayerWeights()
+            for k in shapes:
+                setattr(lw, k, C.cast(bufs[k], _lib.c_u16_p))
+            lw.attn_norm = ones.ctypes.data_as(_lib.c_f32_p)
+            lw.mlp_norm = ones.ctypes.data_as(_lib.c_f32_p)
+            ctx.check(lib.zr_upload_layer(ctx.h, layer, C.byref(lw)))
+        for b in bufs.values():
+            lib.zr_device_free(ctx.h, b)
+        emb, head = self._dev(2 * V * H), self._dev(2 * H * V)
+        ctx.check(lib.zr_fill_normal_bf16(ctx.h, emb, V * H, 777, 0.02))
+        ctx.check(lib.zr_fill_normal_bf16(ctx.h, head, H * V, 778, 0.02))
+        ctx.check(lib.zr_upload_globals(ctx.h, C.cast(emb, _lib.c_u16_p), ones.ctypes.data_as(_lib.c_f32_p),
+                                        C.cast(head, _lib.c_u16_p)))
+        lib.zr_device_free(ctx.h, emb)
+        lib.zr_device_free(ctx.h, head)
+        # KV pool: every session's context plus the benchmarked steps
+        pages = int(sum((min(int(L) + steps_total, self.max_seq) + 15) // 16 + 1 for L in self.ctxlens))
+        ctx.create_kv_pool(pages)
+        ctx.check(lib.zr_kv_pool_fill_normal(ctx.h, 4242, 1.0))
+        self.backends = [ctx.new_backend(self.max_seq) for _ in range(self.B)]
+        for b, L in zip(self.backends, self.ctxlens):
+            b.kv_reserve(int(L))  # the pages hold the synthetic prefix KV
+        # stage every step's metadata on the device ahead of the timed region
+        arr = (C.c_void_p * self.B)(*[b.h for b in self.backends])
+        ptrs = C.cast(arr, C.POINTER(C.c_void_p))
+        q_len = np.ones(self.B, np.int32)
+        self.staged, self.kv_rows = [], []
+        for _ in range(steps_total):
+            st = C.c_void_p()
+            ctx.check(lib.zrh_stage_mixed(ptrs, self.B, q_len.ctypes.data_as(_lib.c_int_p), None, C.byref(st)))
+            self.staged.append(st.value)
+            self.kv_rows.append(sum(b.cache_seq_len() for b in self.backends))
+        self.tok = [self._dev(4 * self.B), self._dev(4 * self.B)]
+        first = np.random.default_rng(1).integers(0, V, self.B).astype(np.uint32)
+        ctx.check(lib.zr_memcpy_h2d(ctx.h, self.tok[0], first.ctypes.data, first.nbytes))
+
+    def _dev(self, nbytes):
+        p = C.c_void_p()
+        self.ctx.check(self.ctx.lib.zr_device_alloc(self.ctx.h, int(nbytes), C.byref(p)))
+        return p.value
+
+    def run(self, first, count, timed):
+        ctx, lib = self.ctx, self.ctx.lib
+        if timed:
+            ctx.check(lib.zr_timing_begin(ctx.h))
+        ctx.check(lib.zr_synchronize(ctx.h))
+        t0 = time.perf_counter()
+        for i in range(first, first + count):
+            ctx.check(lib.zr_forward_staged_async(ctx.h, self.staged[i], self.tok[i % 2], self.tok[(i + 1) % 2], None))
+        ctx.check(lib.zr_synchronize(ctx.h))
+        dt = time.perf_counter() - t0
+        ms = (C.c_double * 4)()
+        n = (C.c_int * 4)()
+        if timed:
+            ctx.check(lib.zr_timing_end(ctx.h, ms, n))
+        return dt, list(ms), list(n)
+
+    def tokens(self, i):
+        out = np.zeros(self.B, np.uint32)
+        self.ctx.check(self.ctx.lib.zr_memcpy_d2h(self.ctx.h, out.ctypes.data, self.tok[i % 2], out.nbytes))
+        return out
+
+    def close(self):
+        for st in self.staged:
+            self.ctx.lib.zr_staged_destroy(st)
+        self.staged = []
+        self.ctx.close()
+
+
+def measure(name, steps, warmup):
+    bench = GpuDecodeBench(name, steps + warmup)
+    g, B = bench.geo, bench.B
+    bench.run(0, warmup, timed=False)
+    dt, ms, n = bench.run(warmup, steps, timed=True)
+    toks = bench.tokens(warmup + steps)
+    assert toks.max() < g.vocab
+    ms_per_step = dt / steps * 1000.0
+    # attention: algorithmic bytes per launch (K+V of every attended row, bf16;
+    # Q in and the output out, f32), averaged over the timed launches
+    timed_rows = bench.kv_rows[warmup:warmup + steps]
+    kv_bytes = sum(timed_rows) * g.num_layers * g.kv_cols * 2 * 2
+    qo_bytes = steps * g.num_layers * B * g.q_cols * 4 * 2
+    attn_launches = n[0]
+    attn_bytes_per_launch = (kv_bytes + qo_bytes) / max(attn_launches, 1)
+    attn_ms_per_launch = ms[0] / max(attn_launches, 1)
+    attn_gbs = attn_bytes_per_launch / (attn_ms_per_launch * 1e-3) / 1e9
+    sb = np.mean([step_bytes(g, B, r) for r in timed_rows])
+    roof_tps = B / (sb / (HBM_PEAK_GBS * 1e9))
+    result = dict(
+        workload=WORKLOADS[name]["desc"], batch=B, layers=g.num_layers,
+        context_tokens=int(np.sum(bench.ctxlens)), context_max=int(np.max(bench.ctxlens)),
+        tokens_per_s=B / (ms_per_step / 1e3), ms_per_step=ms_per_step,
+        step_bytes=float(sb), step_roofline_tokens_per_s=roof_tps,
+        step_roofline_frac=(B / (ms_per_step / 1e3)) / roof_tps,
+        kernel_ms_per_step={"attention": ms[0] / steps, "gemm": ms[1] / steps, "norm_rope_kv": ms[2] / steps,
+                            "other": ms[3] / steps},
+        attention=dict(launches=attn_launches, bytes_per_launch=attn_bytes_per_launch,
+                       avg_ms=attn_ms_per_launch, achieved_gbs=attn_gbs, frac=attn_gbs / HBM_PEAK_GBS),
+    )
+    bench.close()
+    return result
+
+
+# ------------------------------------------------------------- CPU baseline --
+def cpu_baseline(name):
+    """The oracle (C restatement of the CPU provider) on this host's cores: one
+    decode microbatch of the same sessions and contexts with 1 and with 2
+    layers; per-step time = T1 + (L - 1) * (T2 - T1)."""
+    import oracle as O
+
+    w = WORKLOADS[name]
+    geo = w["geo"]
+    B, ctxlens, max_seq = w["batch"], w["contexts"](), w["max_seq_len"]
+    H, V, F = geo["hidden"], geo["vocab"], geo["ffn"]
+    d = H // geo["num_heads"]
+    KV = geo["num_kv_heads"] * d
+    rng = np.random.default_rng(0)
+    block = (rng.standard_normal(1 << 20, dtype=np.float32) * 0.02)
+
+    def fill(shape):
+        return np.resize(block, shape).astype(np.float32)
+
+    def model(layers):
+        cfg = dict(hidden=H, num_heads=geo["num_heads"], num_kv_heads=geo["num_kv_heads"], num_layers=layers,
+                   vocab=V, ffn_cols=F, rms_norm_eps=1e-5, rope_base=geo["rope_base"])
+        lw = [dict(w_q=fill((H, H)), w_k=fill((H, KV)), w_v=fill((H, KV)), w_o=fill((H, H)), w_gate=fill((H, F)),
+                   w_up=fill((H, F)), w_down=fill((F, H)), attn_norm=np.ones(H, np.float32),
+                   mlp_norm=np.ones(H, np.float32)) for _ in range(layers)]
+        return O.Model(cfg, dict(embedding=fill((V, H)), final_norm=np.ones(H, np.float32), lm_head=fill((H, V)),
+                                 layers=lw))
+
+    kv_rows = np.resize(rng.standard_normal(1 << 20, dtype=np.float32), (int(ctxlens.max()), KV))
+    times = {}
+    for layers in (1, 2):
+        m = model(layers)
+        sess = []
+        for L in ctxlens:
+            s = O.Session(layers, KV, 16, max_seq)
+            s.append_all_layers(kv_rows[:L], kv_rows[:L])
+            s.position = int(L)
+            sess.append(s)
+        toks = rng.integers(0, V, B).astype(np.uint32)
+        t0 = time.perf_counter()
+        m.decode(sess, toks)
+        times[layers] = time.perf_counter() - t0
+        del sess, m
+    per_layer = max(times[2] - times[1], 1e-9)
+    step_s = times[1] + (geo["num_layers"] - 1) * per_layer
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return dict(value=B / step_s, unit="tokens/s", cores=threads, kind="port",
+                sample=f"oracle decode microbatch of the same {B} sessions and contexts with 1 and 2 layers of "
+                       f"the model ({times[1]:.2f} s, {times[2]:.2f} s); step = T1 + {geo['num_layers'] - 1} x "
+                       f"(T2 - T1) = {step_s:.2f} s; f32 weights/KV as the reference CPU provider")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--skip-bs32", action="store_true")
+    ap.add_argument("--workload", default="llama3_8b_b256", choices=sorted(WORKLOADS))
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(json.dumps({"error": "this provider runs one worker's shard on one GPU; --gpus must be 1 "
+                                   "(multi-GPU sharding is a design note, not part of this build)"}))
+        sys.exit(2)
+    from mesh_amd import probe_provider
+
+    ok, err = probe_provider(0)
+    if not ok:
+        raise SystemExit(f"rocm provider unavailable: {err}")
+    main_r = measure(a.workload, a.steps, a.warmup)
+    bs32 = None
+    if not a.skip_bs32 and a.workload != "tinyllama_b32":
+        r = measure("tinyllama_b32", a.steps, a.warmup)
+        bs32 = dict(value=r["tokens_per_s"], unit="tokens/s", ms_per_step=r["ms_per_step"],
+                    workload=r["workload"], step_roofline_frac=r["step_roofline_frac"],
+                    attention_gbs=r["attention"]["achieved_gbs"], kernel_ms_per_step=r["kernel_ms_per_step"])
+    cpu = None if a.skip_cpu else cpu_baseline(a.workload)
+    att = main_r["attention"]
+    line = {
+        "metric": METRIC, "value": main_r["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": main_r["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: random-init bf16 N(0,0.02) weights, KV pages filled with N(0,1) bf16 as prefill "
+                "output, greedy tokens fed back on the device",
+        "config": {"workload": main_r["workload"], "sessions": main_r["batch"], "layers": main_r["layers"],
+                   "context_tokens": main_r["context_tokens"], "context_max": main_r["context_max"],
+                   "parallelism": "one worker shard (1 of 1) on one GPU"},
+        "roofline": {"bound": "hbm", "kernel": "paged_attention_kernel", "achieved": att["achieved_gbs"],
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": att["frac"], "traffic": None,
+                     "bytes_per_launch": att["bytes_per_launch"], "avg_ms": att["avg_ms"],
+                     "launches": att["launches"]},
+        "step_roofline": {"tokens_per_s": main_r["step_roofline_tokens_per_s"], "frac": main_r["step_roofline_frac"],
+                          "bytes_per_step": main_r["step_bytes"]},
+        "kernel_ms_per_step": main_r["kernel_ms_per_step"],
+        "bs32": bs32,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -14,11 +14,12 @@
 #include <stdlib.h>
 #include <string.h>
 
-static __thread char g_err[512];
+static char g_err[512];
 
 static int fail(const char* fmt, ...) {
     va_list ap;
     va_start(ap, fmt);
+#pragma omp critical(oracle_err)
     vsnprintf(g_err, sizeof g_err, fmt, ap);
     va_end(ap);
     return -1;
@@ -30,22 +31,25 @@ const char* or_last_error(void) { return g_err; }
 
 /* tensor_ops.rs:219-240.  The reference loops i, k, j with out[i][j] +=
  * a[i][k] * b[k][j]: every output element accumulates over k in order, which
- * this keeps exactly; rows (or column blocks when m is small) run in parallel. */
+ * this keeps exactly.  Tiles of 16 rows x 256 columns run in parallel and
+ * reuse each weight block from cache; no accumulation is reordered. */
 int or_matmul(const float* a, const float* b, float* c, int m, int k, int n) {
     if (m < 0 || k < 0 || n < 0) return fail("Matmul shape mismatch: %dx%d @ %dx%d", m, k, k, n);
     memset(c, 0, sizeof(float) * (size_t)m * (size_t)n);
-    const int jb = 512;
-    const int nblk = (n + jb - 1) / jb;
+    const int ib = 16, jb = 256;
+    const int nib = (m + ib - 1) / ib, njb = (n + jb - 1) / jb;
 #pragma omp parallel for collapse(2) schedule(static)
-    for (int i = 0; i < m; ++i) {
-        for (int blk = 0; blk < nblk; ++blk) {
+    for (int it = 0; it < nib; ++it) {
+        for (int blk = 0; blk < njb; ++blk) {
+            const int i0 = it * ib, i1 = i0 + ib < m ? i0 + ib : m;
             const int j0 = blk * jb, j1 = j0 + jb < n ? j0 + jb : n;
-            float* out_row = c + (size_t)i * n;
-            const float* a_row = a + (size_t)i * k;
             for (int kk = 0; kk < k; ++kk) {
-                const float a_ik = a_row[kk];
                 const float* b_row = b + (size_t)kk * n;
-                for (int j = j0; j < j1; ++j) out_row[j] += a_ik * b_row[j];
+                for (int i = i0; i < i1; ++i) {
+                    const float a_ik = a[(size_t)i * k + kk];
+                    float* out_row = c + (size_t)i * n;
+                    for (int j = j0; j < j1; ++j) out_row[j] += a_ik * b_row[j];
+                }
             }
         }
     }
@@ -888,26 +892,33 @@ int or_decode_microbatch(const or_model* m, or_session** sessions, int batch,
         if (rc >= 0) rc = or_matmul(w.normed, Lw->w_v, w.v, batch, H, KV);
         if (rc >= 0) rc = or_apply_rope(w.q, w.qr, batch, Q, positions, d, m->cfg.rope_base);
         if (rc >= 0) rc = or_apply_rope(w.k, w.kr, batch, KV, positions, d, m->cfg.rope_base);
-        for (int b = 0; rc >= 0 && b < batch; ++b) {
-            or_session* s = sessions[b];
-            const int cur = s->layers[l].seq_len;
-            const int max_seq = s->max_seq_len > 1 ? s->max_seq_len : 1;
-            if (cur + 1 > max_seq) {
-                const int drop = cur + 1 - max_seq;
-                rc = or_session_retain_suffix(s, cur - drop > 0 ? cur - drop : 0);
-                if (rc < 0) break;
+        /* sessions are independent: each one's trim / append / attention
+         * runs in the reference's order, sessions in parallel */
+        int bad = 0;
+        if (rc >= 0) {
+#pragma omp parallel for schedule(dynamic, 1) reduction(| : bad)
+            for (int b = 0; b < batch; ++b) {
+                or_session* s = sessions[b];
+                int src = 0;
+                const int cur = s->layers[l].seq_len;
+                const int max_seq = s->max_seq_len > 1 ? s->max_seq_len : 1;
+                if (cur + 1 > max_seq) {
+                    const int drop = cur + 1 - max_seq;
+                    src = or_session_retain_suffix(s, cur - drop > 0 ? cur - drop : 0);
+                }
+                const int prefix = s->layers[l].seq_len;
+                if (src >= 0 && (int)positions[b] != s->base_position + prefix)
+                    src = fail("Non-contiguous attention positions: expected %d, got %u",
+                               s->base_position + prefix, positions[b]);
+                if (src >= 0)
+                    src = or_session_append_layer(s, l, w.kr + (size_t)b * KV, w.v + (size_t)b * KV, 1);
+                if (src >= 0)
+                    src = session_attention(m, s, l, w.qr + (size_t)b * Q, Q, 1, prefix,
+                                            w.attn + (size_t)b * Q);
+                if (src < 0) bad |= 1;
             }
-            const int prefix = s->layers[l].seq_len;
-            if ((int)positions[b] != s->base_position + prefix) {
-                rc = fail("Non-contiguous attention positions: expected %d, got %u",
-                          s->base_position + prefix, positions[b]);
-                break;
-            }
-            rc = or_session_append_layer(s, l, w.kr + (size_t)b * KV, w.v + (size_t)b * KV, 1);
-            if (rc >= 0)
-                rc = session_attention(m, s, l, w.qr + (size_t)b * Q, Q, 1, prefix,
-                                       w.attn + (size_t)b * Q);
         }
+        if (bad) rc = -1;
         if (rc >= 0) rc = or_matmul(w.attn, Lw->w_o, w.o, batch, Q, H);
         if (rc >= 0) {
             float* po = partials ? partials + ((size_t)l * 2 + 0) * (size_t)batch * H : NULL;
