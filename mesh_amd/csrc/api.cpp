@@ -112,23 +112,12 @@ static zr_status resolve_geometry(zr_context* ctx) {
     return ZR_OK;
 }
 
-// Split-K plan shared by launch_gemm and the workspace sizing.
-static size_t gemm_ws_floats(int m, int n, int k, int epilogue) {
-    const int KT = (k + 31) / 32, NT = (n + 15) / 16;
-    const int wm = m <= 16 ? 1 : m <= 32 ? 2 : m <= 64 ? 4 : m <= 128 ? 8 : 16;
-    const int row_blocks = (m + wm * 16 - 1) / (wm * 16);
-    const int col_blocks = (NT + 7) / 8;
-    int splits = 1;
-    while (col_blocks * row_blocks * splits < 512 && KT / (splits * 2) >= 8) splits *= 2;
-    const int kps = (KT + splits - 1) / splits;
-    splits = (KT + kps - 1) / kps;
-    if (splits == 1 && epilogue == kEpiStore) return 0;
-    return (size_t)splits * m * n;
-}
+// Split-K workspace of one GEMM shape (same plan as launch_gemm).
+static size_t gemm_ws_floats(int m, int n, int k, int epilogue) { return gemm_plan(m, n, k, epilogue).ws_floats; }
 
 static void free_ctx_buffers(zr_context* ctx) {
-    void* bufs[] = {ctx->hidden, ctx->xn, ctx->qkv, ctx->q_rope, ctx->attn, ctx->proj, ctx->ffn,
-                    ctx->logits, ctx->final_x, ctx->tokens_out, ctx->splitk_ws, ctx->attn_part,
+    void* bufs[] = {ctx->hidden, ctx->xa, ctx->qkv, ctx->q_rope, ctx->attn_a, ctx->proj, ctx->ffn_a,
+                    ctx->logits, ctx->final_a, ctx->tokens_out, ctx->splitk_ws, ctx->attn_part,
                     ctx->argmax_ws, ctx->inv_freq, ctx->kv_pool, ctx->embedding, ctx->lm_head,
                     ctx->final_norm};
     for (void* b : bufs)
@@ -207,7 +196,7 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
             total_pages += pages;
         }
     }
-    const long target_wgs = 8192;
+    const long target_wgs = 4096;  // ~48 pages per split at 256 x 8 kv heads x ~1.5k tokens
     int pps = (int)std::min<long>(4096, std::max<long>(4, (total_pages * ctx->local_kv_heads + target_wgs - 1) / target_wgs));
     if (const char* env = getenv("ZR_ATTN_PAGES_PER_SPLIT")) pps = std::max(1, atoi(env));
     for (size_t t = 0; t < st->h_tiles.size(); ++t) {
@@ -299,36 +288,39 @@ static zr_status run_forward(zr_context* ctx, StagedMeta* st, const uint32_t* d_
     if (rc) return rc;
     const zr_model_desc& d = ctx->desc;
     const int T = st->total_q, S = st->num_seqs, H = d.hidden, F = d.ffn_cols;
+    (void)S;
     const int QKV = ctx->q_cols + 2 * ctx->kv_cols;
     if ((rc = launch_embed(ctx, st, d_tokens ? d_tokens : st->tokens))) return rc;
+    const int lo = (d.flags & ZR_FLAG_SPLIT_ACTIVATIONS) ? 1 : 0;
     for (int l = 0; l < d.num_layers; ++l) {
         const LayerDev& L = ctx->layers[l];
-        // hidden += previous down partial; xn = rms_norm(hidden) * attn_norm
-        if ((rc = launch_rms_norm(ctx, ctx->hidden, l > 0 ? ctx->proj : nullptr, ctx->hidden, L.attn_norm, ctx->xn,
-                                  nullptr, T, H)))
+        // hidden += previous down partial; xa = rms_norm(hidden) * attn_norm
+        if ((rc = launch_rms_norm(ctx, ctx->hidden, l > 0 ? ctx->proj : nullptr, ctx->hidden, L.attn_norm, nullptr,
+                                  ctx->xa, lo, nullptr, T, H)))
             return rc;
-        if ((rc = launch_gemm(ctx, ctx->xn, L.w_qkv, ctx->qkv, T, QKV, H, kEpiStore))) return rc;
+        if ((rc = launch_gemm(ctx, ctx->xa, L.w_qkv, ctx->qkv, nullptr, T, QKV, H, kEpiStore))) return rc;
         if ((rc = launch_rope_kv_write(ctx, st, l, ctx->qkv, ctx->q_rope, 1))) return rc;
-        if ((rc = launch_attention(ctx, st, l, ctx->q_rope, ctx->attn))) return rc;
-        if ((rc = launch_gemm(ctx, ctx->attn, L.w_o, ctx->proj, T, H, ctx->q_cols, kEpiStore))) return rc;
+        if ((rc = launch_attention(ctx, st, l, ctx->q_rope, nullptr, ctx->attn_a))) return rc;
+        if ((rc = launch_gemm(ctx, ctx->attn_a, L.w_o, ctx->proj, nullptr, T, H, ctx->q_cols, kEpiStore))) return rc;
         if (h_partials)
             ZR_HIP(ctx, hipMemcpyAsync(h_partials + ((size_t)l * 2 + 0) * T * H, ctx->proj, sizeof(float) * T * H,
                                        hipMemcpyDeviceToHost, ctx->stream));
         // post_attn = hidden + o_partial (identity all-reduce at one worker)
-        if ((rc = launch_rms_norm(ctx, ctx->hidden, ctx->proj, ctx->hidden, L.mlp_norm, ctx->xn, nullptr, T, H)))
+        if ((rc = launch_rms_norm(ctx, ctx->hidden, ctx->proj, ctx->hidden, L.mlp_norm, nullptr, ctx->xa, lo, nullptr,
+                                  T, H)))
             return rc;
-        if ((rc = launch_gemm(ctx, ctx->xn, L.w_gate_up, ctx->ffn, T, 2 * F, H, kEpiSwiGLU))) return rc;
-        if ((rc = launch_gemm(ctx, ctx->ffn, L.w_down, ctx->proj, T, H, F, kEpiStore))) return rc;
+        if ((rc = launch_gemm(ctx, ctx->xa, L.w_gate_up, nullptr, ctx->ffn_a, T, 2 * F, H, kEpiSwiGLU))) return rc;
+        if ((rc = launch_gemm(ctx, ctx->ffn_a, L.w_down, ctx->proj, nullptr, T, H, F, kEpiStore))) return rc;
         if (h_partials)
             ZR_HIP(ctx, hipMemcpyAsync(h_partials + ((size_t)l * 2 + 1) * T * H, ctx->proj, sizeof(float) * T * H,
                                        hipMemcpyDeviceToHost, ctx->stream));
     }
     // final residual + norm on the last row of every sequence, LM head, argmax
-    if ((rc = launch_rms_norm(ctx, ctx->hidden, ctx->proj, ctx->hidden, ctx->final_norm, ctx->final_x, st->last_rows,
-                              S, H)))
+    if ((rc = launch_rms_norm(ctx, ctx->hidden, ctx->proj, ctx->hidden, ctx->final_norm, nullptr, ctx->final_a, lo,
+                              st->last_rows, S, H)))
         return rc;
     float* logits = ctx->logits;
-    if ((rc = launch_gemm(ctx, ctx->final_x, ctx->lm_head, logits, S, d.vocab, H, kEpiStore))) return rc;
+    if ((rc = launch_gemm(ctx, ctx->final_a, ctx->lm_head, logits, nullptr, S, d.vocab, H, kEpiStore))) return rc;
     if ((rc = launch_argmax(ctx, logits, S, d.vocab, d_out_tokens ? d_out_tokens : ctx->tokens_out))) return rc;
     if (d_out_logits)
         ZR_HIP(ctx, hipMemcpyAsync(d_out_logits, logits, sizeof(float) * S * d.vocab, hipMemcpyDeviceToDevice,
@@ -411,11 +403,11 @@ zr_status zr_context_create(const zr_model_desc* desc, int device, zr_context** 
         void** p;
         size_t bytes;
     } allocs[] = {
-        {(void**)&ctx->hidden, 4 * T * H},           {(void**)&ctx->xn, 4 * T * H},
+        {(void**)&ctx->hidden, 4 * T * H},           {(void**)&ctx->xa, 2 * 2 * T * H},
         {(void**)&ctx->qkv, 4 * T * (Q + 2 * KV)},   {(void**)&ctx->q_rope, 4 * T * Q},
-        {(void**)&ctx->attn, 4 * T * Q},             {(void**)&ctx->proj, 4 * T * H},
-        {(void**)&ctx->ffn, 4 * T * 2 * F},          {(void**)&ctx->logits, 4 * S * d.vocab},
-        {(void**)&ctx->final_x, 4 * S * H},          {(void**)&ctx->tokens_out, 4 * S},
+        {(void**)&ctx->attn_a, 2 * 2 * T * Q},       {(void**)&ctx->proj, 4 * T * H},
+        {(void**)&ctx->ffn_a, 2 * 2 * T * F},        {(void**)&ctx->logits, 4 * S * d.vocab},
+        {(void**)&ctx->final_a, 2 * 2 * S * H},      {(void**)&ctx->tokens_out, 4 * S},
         {(void**)&ctx->inv_freq, 4 * (size_t)ctx->head_dim / 2},
     };
     for (auto& a : allocs) {
@@ -656,7 +648,7 @@ zr_status zr_attention(zr_context* ctx, zr_staged* s, int layer, const float* d_
     StagedMeta* st = (StagedMeta*)s;
     if (!ctx || !st || !d_q || !d_out) return set_global_err(ZR_E_INVALID, "null argument");
     if (layer < 0 || layer >= ctx->desc.num_layers) return set_err(ctx, ZR_E_INVALID, "Invalid layer index: %d", layer);
-    zr_status rc = launch_attention(ctx, st, layer, d_q, d_out);
+    zr_status rc = launch_attention(ctx, st, layer, d_q, d_out, nullptr);
     if (!rc) ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
     return rc;
 }
@@ -745,7 +737,7 @@ zr_status zr_argmax(zr_context* ctx, const float* d_x, int rows, int cols, uint3
 
 zr_status zr_rms_norm(zr_context* ctx, const float* d_x, const float* d_gamma, float* d_y, int rows, int cols) {
     if (!ctx || !d_x || !d_gamma || !d_y) return set_global_err(ZR_E_INVALID, "null argument");
-    zr_status rc = launch_rms_norm(ctx, d_x, nullptr, nullptr, d_gamma, d_y, nullptr, rows, cols);
+    zr_status rc = launch_rms_norm(ctx, d_x, nullptr, nullptr, d_gamma, d_y, nullptr, 0, nullptr, rows, cols);
     if (!rc) ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
     return rc;
 }
@@ -753,28 +745,33 @@ zr_status zr_rms_norm(zr_context* ctx, const float* d_x, const float* d_gamma, f
 zr_status zr_gemm(zr_context* ctx, const float* d_a, const uint16_t* w, float* d_c, int m, int n, int k) {
     if (!ctx || !d_a || !w || !d_c) return set_global_err(ZR_E_INVALID, "null argument");
     if (m <= 0 || n <= 0 || k <= 0) return set_err(ctx, ZR_E_INVALID, "Matmul shape mismatch: %dx%d @ %dx%d", m, k, k, n);
+    ZR_HIP(ctx, hipSetDevice(ctx->device));
     uint16_t* packed = nullptr;
     zr_status rc = pack_weight(ctx, w, k, n, &packed);
     if (rc) return rc;
+    const int lo = (ctx->desc.flags & ZR_FLAG_SPLIT_ACTIVATIONS) ? 1 : 0;
     const size_t need = gemm_ws_floats(m, n, k, kEpiStore);
     float* saved_ws = ctx->splitk_ws;
     size_t saved_n = ctx->splitk_ws_floats;
     float* tmp_ws = nullptr;
-    if (need > saved_n) {
-        hipError_t e = hipMalloc(&tmp_ws, need * 4);
-        if (e != hipSuccess) {
-            hipFree(packed);
-            return set_err(ctx, ZR_E_OOM, "gemm workspace: %s", hipGetErrorString(e));
+    uint16_t* a16 = nullptr;
+    hipError_t e = hipMalloc(&a16, (size_t)2 * 2 * m * k);
+    if (e == hipSuccess && need > saved_n) {
+        e = hipMalloc(&tmp_ws, need * 4);
+        if (e == hipSuccess) {
+            ctx->splitk_ws = tmp_ws;
+            ctx->splitk_ws_floats = need;
         }
-        ctx->splitk_ws = tmp_ws;
-        ctx->splitk_ws_floats = need;
     }
-    rc = launch_gemm(ctx, d_a, packed, d_c, m, n, k, kEpiStore);
-    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) rc = set_err(ctx, ZR_E_OOM, "gemm workspace: %s", hipGetErrorString(e));
+    if (!rc) rc = launch_to_bf16_pair(ctx, d_a, (size_t)m * k, a16, lo);
+    if (!rc) rc = launch_gemm(ctx, a16, packed, d_c, nullptr, m, n, k, kEpiStore);
+    e = hipStreamSynchronize(ctx->stream);
     if (!rc && e != hipSuccess) rc = set_err(ctx, ZR_E_HIP, "gemm: %s", hipGetErrorString(e));
     ctx->splitk_ws = saved_ws;
     ctx->splitk_ws_floats = saved_n;
     if (tmp_ws) hipFree(tmp_ws);
+    if (a16) hipFree(a16);
     hipFree(packed);
     return rc;
 }

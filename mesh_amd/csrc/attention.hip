@@ -85,19 +85,20 @@ __device__ inline bf16x4 to_bf16x4(const float* x, bool lo_part) {
     return r;
 }
 
+// qhi / qlo point at [D / 32][64] fragment arrays (LDS); lane selects its slot.
 template <int D>
-__device__ inline f32x4 qk_mfma(const PageRegs<uint16_t, D>& pg, const bf16x8* qhi, const bf16x8* qlo) {
+__device__ inline f32x4 qk_mfma(const PageRegs<uint16_t, D>& pg, const bf16x8* qhi, const bf16x8* qlo, int lane) {
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kb = 0; kb < D / 32; ++kb) {
-        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pg.k[kb], qhi[kb], s, 0, 0, 0);
-        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pg.k[kb], qlo[kb], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pg.k[kb], qhi[kb * 64 + lane], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pg.k[kb], qlo[kb * 64 + lane], s, 0, 0, 0);
     }
     return s;
 }
 
 template <int D>
-__device__ inline f32x4 qk_mfma(const PageRegs<float, D>& pg, const bf16x8* qhi, const bf16x8* qlo) {
+__device__ inline f32x4 qk_mfma(const PageRegs<float, D>& pg, const bf16x8* qhi, const bf16x8* qlo, int lane) {
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kb = 0; kb < D / 32; ++kb) {
@@ -108,32 +109,54 @@ __device__ inline f32x4 qk_mfma(const PageRegs<float, D>& pg, const bf16x8* qhi,
             kf[4 + j] = pg.k[kb][1][j];
         }
         const bf16x8 khi = to_bf16x8(kf, false), klo = to_bf16x8(kf, true);
-        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, qhi[kb], s, 0, 0, 0);
-        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, qlo[kb], s, 0, 0, 0);
-        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(klo, qhi[kb], s, 0, 0, 0);
+        const bf16x8 qh = qhi[kb * 64 + lane];
+        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, qh, s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, qlo[kb * 64 + lane], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(klo, qh, s, 0, 0, 0);
     }
     return s;
 }
 
+// O^T += V^T P^T over a page pair (32 tokens) on the 16x16x32 MFMA: lane l
+// supplies tokens 4*q4 .. 4*q4+3 of page A then of page B for both operands,
+// which is exactly its own score registers for P^T and the concatenation of
+// its two V fragments for V^T.
+__device__ inline bf16x8 cat4(bf16x4 a, bf16x4 b) {
+    return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
 template <int D>
-__device__ inline void pv_mfma(const PageRegs<uint16_t, D>& pg, bf16x4 phi, bf16x4 plo, f32x4* o) {
+__device__ inline void pv_mfma2(const PageRegs<uint16_t, D>& pa, const PageRegs<uint16_t, D>& pb, bf16x8 phi,
+                                bf16x8 plo, f32x4* o) {
 #pragma unroll
     for (int db = 0; db < D / 16; ++db) {
-        o[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pg.v[db], phi, o[db], 0, 0, 0);
-        o[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pg.v[db], plo, o[db], 0, 0, 0);
+        const bf16x8 v = cat4(pa.v[db], pb.v[db]);
+        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v, phi, o[db], 0, 0, 0);
+        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v, plo, o[db], 0, 0, 0);
     }
 }
 
 template <int D>
-__device__ inline void pv_mfma(const PageRegs<float, D>& pg, bf16x4 phi, bf16x4 plo, f32x4* o) {
+__device__ inline void pv_mfma2(const PageRegs<float, D>& pa, const PageRegs<float, D>& pb, bf16x8 phi, bf16x8 plo,
+                                f32x4* o) {
 #pragma unroll
     for (int db = 0; db < D / 16; ++db) {
-        float vf[4] = {pg.v[db][0], pg.v[db][1], pg.v[db][2], pg.v[db][3]};
-        const bf16x4 vhi = to_bf16x4(vf, false), vlo = to_bf16x4(vf, true);
-        o[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vhi, phi, o[db], 0, 0, 0);
-        o[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vhi, plo, o[db], 0, 0, 0);
-        o[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vlo, phi, o[db], 0, 0, 0);
+        float vf[8] = {pa.v[db][0], pa.v[db][1], pa.v[db][2], pa.v[db][3],
+                       pb.v[db][0], pb.v[db][1], pb.v[db][2], pb.v[db][3]};
+        const bf16x8 vhi = to_bf16x8(vf, false), vlo = to_bf16x8(vf, true);
+        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vhi, phi, o[db], 0, 0, 0);
+        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vhi, plo, o[db], 0, 0, 0);
+        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vlo, phi, o[db], 0, 0, 0);
     }
+}
+
+// max over the lanes {l, l^16, l^32, l^48} (the four quads holding one column),
+// with gfx950's VALU lane swaps.
+__device__ inline float quad_max(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 struct AttnArgs {
@@ -152,6 +175,9 @@ struct AttnArgs {
     int kv_heads;
     float scale_log2;        // log2(e) / sqrt(d)
     float* part;             // [items][kv_heads][16][D + 2]
+    float* out_f32;          // final output of single-split tiles ([T, q_cols]) ...
+    uint16_t* out_bf16;      // ... or as the bf16 A operand (lo half at out_lo_offset)
+    size_t out_lo_offset;
 };
 
 template <typename KV, int D>
@@ -169,8 +195,9 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
     // last visible logical key index of this column (causal: prefix + row)
     const int jmax = kvb + q0 + (col_valid ? qi : 0);
 
-    // Q^T as the MFMA B operand: lane holds Q[c][32*kb + 8*q4 + j]
-    bf16x8 qhi[D / 32], qlo[D / 32];
+    // Q^T as the MFMA B operand (lane holds Q[c][32*kb + 8*q4 + j]) as bf16
+    // hi + lo fragments, parked in LDS to keep registers for the page ring.
+    __shared__ bf16x8 qs[2][D / 32][64];
     {
         const int row = a.cu_q[seq] + q0 + (col_valid ? qi : 0);
         const float* qp = a.q + (size_t)row * a.q_cols + (size_t)(kvh * a.G + g) * D;
@@ -179,10 +206,12 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
             float x[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) x[j] = col_valid ? qp[kb * 32 + q4 * 8 + j] : 0.0f;
-            qhi[kb] = to_bf16x8(x, false);
-            qlo[kb] = to_bf16x8(x, true);
+            qs[0][kb][lane] = to_bf16x8(x, false);
+            qs[1][kb][lane] = to_bf16x8(x, true);
         }
     }
+    const bf16x8* qhi = qs[0][0];
+    const bf16x8* qlo = qs[1][0];
 
     const KV* pool = (const KV*)a.pool;
     const int* bt = a.block_tables + (size_t)seq * a.stride;
@@ -194,38 +223,30 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
     for (int db = 0; db < D / 16; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m = -INFINITY, lsum = 0.0f;
 
-    PageRegs<KV, D> cur, nxt;
-    int p = it.y;
-    const int pend = it.z;
-    {
-        const KV* base = pool + (size_t)bt[p] * a.page_elems + (size_t)kvh * kv_tile;
-        cur.load(base, base + v_block, lane);
-    }
-    for (; p < pend; ++p) {
-        if (p + 1 < pend) {
-            const KV* base = pool + (size_t)bt[p + 1] * a.page_elems + (size_t)kvh * kv_tile;
-            nxt.load(base, base + v_block, lane);
-        }
-        const f32x4 s = qk_mfma<D>(cur, qhi, qlo);
-        float sc[4];
+    // a page pair (p, p + 1): S^T = K Q^T for both, one online-softmax step
+    // over 32 tokens, O^T += V^T P^T.  has_b == false masks page B (odd tail).
+    auto process2 = [&](const PageRegs<KV, D>& pa, const PageRegs<KV, D>& pb, int p, bool has_b) {
+        const f32x4 sa = qk_mfma<D>(pa, qhi, qlo, lane);
+        const f32x4 sb = qk_mfma<D>(pb, qhi, qlo, lane);
+        float sc[8];
         float pmax = -INFINITY;
         const int jbase = p * kPageRows + q4 * 4 - foff;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int j = jbase + i;
-            const bool ok = j >= 0 && j <= jmax;
-            sc[i] = ok ? s[i] * a.scale_log2 : -INFINITY;
-            pmax = fmaxf(pmax, sc[i]);
+            const int ja = jbase + i, jb = jbase + kPageRows + i;
+            sc[i] = (ja >= 0 && ja <= jmax) ? sa[i] * a.scale_log2 : -INFINITY;
+            sc[4 + i] = (has_b && jb <= jmax) ? sb[i] * a.scale_log2 : -INFINITY;
         }
-        pmax = fmaxf(pmax, shfl_xor(pmax, 16));
-        pmax = fmaxf(pmax, shfl_xor(pmax, 32));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pmax = fmaxf(pmax, sc[i]);
+        pmax = quad_max(pmax);
         const float m_new = fmaxf(m, pmax);
         const float m_use = m_new == -INFINITY ? 0.0f : m_new;
         const float alpha = exp2f(m - m_use);
-        float pr[4];
+        float pr[8];
         float psum = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 8; ++i) {
             pr[i] = exp2f(sc[i] - m_use);
             psum += pr[i];
         }
@@ -235,12 +256,58 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
         for (int db = 0; db < D / 16; ++db)
 #pragma unroll
             for (int i = 0; i < 4; ++i) o[db][i] *= alpha;
-        pv_mfma<D>(cur, to_bf16x4(pr, false), to_bf16x4(pr, true), o);
-        if (p + 1 < pend) cur = nxt;
+        pv_mfma2<D>(pa, pb, to_bf16x8(pr, false), to_bf16x8(pr, true), o);
+    };
+
+    // Register ring of RING page sets, consumed in pairs: RING - 2 pages are
+    // in flight while a pair is computed.
+    constexpr int RING = sizeof(KV) == 4 ? 4 : 6;
+    PageRegs<KV, D> ring[RING];
+    auto load = [&](PageRegs<KV, D>& r, int p) {
+        const KV* base = pool + (size_t)bt[p] * a.page_elems + (size_t)kvh * kv_tile;
+        r.load(base, base + v_block, lane);
+    };
+    const int pend = it.z;
+#pragma unroll
+    for (int r = 0; r < RING - 2; ++r)
+        if (it.y + r < pend) load(ring[r], it.y + r);
+    for (int p = it.y; p < pend; p += RING) {
+#pragma unroll
+        for (int r = 0; r < RING; r += 2) {
+            const int pp = p + r;
+            if (pp >= pend) break;
+            if (pp + RING - 2 < pend) load(ring[(r + RING - 2) % RING], pp + RING - 2);
+            if (pp + RING - 1 < pend) load(ring[(r + RING - 1) % RING], pp + RING - 1);
+            const bool has_b = pp + 1 < pend;
+            process2(ring[r], has_b ? ring[r + 1] : ring[r], pp, has_b);
+        }
     }
     lsum += shfl_xor(lsum, 16);
     lsum += shfl_xor(lsum, 32);
 
+    if (!col_valid) return;
+    if (a.tiles[it.x + 1].w - tl.w == 1) {
+        // the tile has one split: normalise and write the final output here
+        const int row = a.cu_q[seq] + q0 + qi;
+        const size_t ob = (size_t)row * a.q_cols + (size_t)(kvh * a.G + g) * D;
+        const float inv = 1.0f / lsum;
+#pragma unroll
+        for (int db = 0; db < D / 16; ++db)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const size_t o_idx = ob + db * 16 + q4 * 4 + i;
+                const float v = o[db][i] * inv;
+                if (a.out_bf16) {
+                    uint16_t hi, lo;
+                    split_bf16(v, hi, lo);
+                    a.out_bf16[o_idx] = hi;
+                    if (a.out_lo_offset) a.out_bf16[a.out_lo_offset + o_idx] = lo;
+                } else {
+                    a.out_f32[o_idx] = v;
+                }
+            }
+        return;
+    }
     float* out = a.part + (((size_t)item * a.kv_heads + kvh) * 16 + c) * (D + 2);
     if (q4 == 0) {
         out[0] = m;
@@ -252,39 +319,65 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
         for (int i = 0; i < 4; ++i) out[2 + db * 16 + q4 * 4 + i] = o[db][i];
 }
 
-// Merge the splits of one (tile, kv head): o = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
+// Merge the splits of one (tile, kv head) with more than one split:
+// o = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
 template <int D>
 __global__ __launch_bounds__(256) void attention_reduce_kernel(const float* __restrict__ part,
                                                                const int4* __restrict__ tiles,
                                                                const int* __restrict__ cu_q, int G,
                                                                int kv_heads, int q_cols,
-                                                               float* __restrict__ out) {
+                                                               float* __restrict__ out,
+                                                               uint16_t* __restrict__ out_bf16,
+                                                               size_t lo_offset) {
+    __shared__ float sM[16], sLinv[16];
     const int tile = blockIdx.x, kvh = blockIdx.y;
     const int4 tl = tiles[tile];
     const int seq = tl.x, q0 = tl.y, nq = tl.z, first = tl.w;
     const int nparts = tiles[tile + 1].w - first;
-    const int qpt = 16 / G;
-    for (int e = threadIdx.x; e < 16 * D; e += blockDim.x) {
-        const int c = e / D, d = e % D;
-        const int qi = c / G, g = c - qi * G;
-        if (qi >= nq || qi >= qpt) continue;
+    if (nparts <= 1) return;  // written by the attention kernel
+    const int ncols = min(nq, 16 / G) * G;
+    const size_t pstride = (size_t)kv_heads * 16 * (D + 2);
+    const float* base = part + ((size_t)first * kv_heads + kvh) * 16 * (D + 2);
+    if (threadIdx.x < ncols) {
+        const int c = threadIdx.x;
         float M = -INFINITY;
-        for (int s = 0; s < nparts; ++s)
-            M = fmaxf(M, part[(((size_t)(first + s) * kv_heads + kvh) * 16 + c) * (D + 2)]);
-        float L = 0.0f, acc = 0.0f;
+        for (int s = 0; s < nparts; ++s) M = fmaxf(M, base[s * pstride + (size_t)c * (D + 2)]);
+        float L = 0.0f;
         for (int s = 0; s < nparts; ++s) {
-            const float* ps = part + (((size_t)(first + s) * kv_heads + kvh) * 16 + c) * (D + 2);
-            const float w = ps[0] == -INFINITY ? 0.0f : exp2f(ps[0] - M);
-            L += ps[1] * w;
-            acc += ps[2 + d] * w;
+            const float* ps = base + s * pstride + (size_t)c * (D + 2);
+            if (ps[0] != -INFINITY) L += ps[1] * exp2f(ps[0] - M);
         }
+        sM[c] = M;
+        sLinv[c] = 1.0f / L;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < ncols * D; e += blockDim.x) {
+        const int c = e / D, d = e - c * D;
+        const float M = sM[c];
+        float acc = 0.0f;
+        for (int s = 0; s < nparts; ++s) {
+            const float* ps = base + s * pstride + (size_t)c * (D + 2);
+            const float mv = ps[0];
+            if (mv != -INFINITY) acc += ps[2 + d] * exp2f(mv - M);
+        }
+        const int qi = c / G, g = c - qi * G;
         const int row = cu_q[seq] + q0 + qi;
-        out[(size_t)row * q_cols + (size_t)(kvh * G + g) * D + d] = acc / L;
+        const size_t o = (size_t)row * q_cols + (size_t)(kvh * G + g) * D + d;
+        const float v = acc * sLinv[c];
+        if (out_bf16) {
+            uint16_t hi, lo;
+            split_bf16(v, hi, lo);
+            out_bf16[o] = hi;
+            if (lo_offset) out_bf16[lo_offset + o] = lo;
+        } else {
+            out[o] = v;
+        }
     }
 }
 
 template <typename KV, int D>
-static zr_status launch_attn_t(zr_context* ctx, StagedMeta* st, int layer, const float* q, float* out) {
+static zr_status launch_attn_t(zr_context* ctx, StagedMeta* st, int layer, const float* q, float* out,
+                               uint16_t* out_bf16) {
     AttnArgs a;
     a.q = q;
     a.q_cols = ctx->q_cols;
@@ -301,6 +394,9 @@ static zr_status launch_attn_t(zr_context* ctx, StagedMeta* st, int layer, const
     a.kv_heads = ctx->local_kv_heads;
     a.scale_log2 = 1.4426950408889634f / sqrtf((float)D);
     a.part = ctx->attn_part;
+    a.out_f32 = out;
+    a.out_bf16 = out_bf16;
+    a.out_lo_offset = (ctx->desc.flags & ZR_FLAG_SPLIT_ACTIVATIONS) ? (size_t)st->total_q * ctx->q_cols : 0;
     hipEvent_t ev;
     timing_mark_begin(ctx, kClassAttention, &ev);
     hipLaunchKernelGGL((paged_attention_kernel<KV, D>), dim3(st->n_attn_items, ctx->local_kv_heads),
@@ -310,13 +406,15 @@ static zr_status launch_attn_t(zr_context* ctx, StagedMeta* st, int layer, const
     timing_mark_begin(ctx, kClassOther, &ev);
     hipLaunchKernelGGL((attention_reduce_kernel<D>), dim3(st->n_tiles, ctx->local_kv_heads), dim3(256), 0,
                        ctx->stream, ctx->attn_part, st->attn_tiles, st->cu_q, ctx->q_per_kv,
-                       ctx->local_kv_heads, ctx->q_cols, out);
+                       ctx->local_kv_heads, ctx->q_cols, out, out_bf16,
+                       (ctx->desc.flags & ZR_FLAG_SPLIT_ACTIVATIONS) ? (size_t)st->total_q * ctx->q_cols : 0);
     ZR_LAUNCH_CHECK(ctx);
     timing_mark_end(ctx, kClassOther, ev);
     return ZR_OK;
 }
 
-zr_status launch_attention(zr_context* ctx, StagedMeta* st, int layer, const float* q, float* out) {
+zr_status launch_attention(zr_context* ctx, StagedMeta* st, int layer, const float* q, float* out,
+                           uint16_t* out_bf16) {
     if (st->n_attn_items == 0) return ZR_OK;
     const size_t need = (size_t)st->n_attn_items * ctx->local_kv_heads * 16 * (ctx->head_dim + 2);
     if (need > ctx->attn_part_floats)
@@ -325,8 +423,8 @@ zr_status launch_attention(zr_context* ctx, StagedMeta* st, int layer, const flo
     zr_status rc;
     const bool bf = ctx->desc.kv_dtype == ZR_DTYPE_BF16;
     switch (ctx->head_dim) {
-        case 64: rc = bf ? launch_attn_t<uint16_t, 64>(ctx, st, layer, q, out) : launch_attn_t<float, 64>(ctx, st, layer, q, out); break;
-        case 128: rc = bf ? launch_attn_t<uint16_t, 128>(ctx, st, layer, q, out) : launch_attn_t<float, 128>(ctx, st, layer, q, out); break;
+        case 64: rc = bf ? launch_attn_t<uint16_t, 64>(ctx, st, layer, q, out, out_bf16) : launch_attn_t<float, 64>(ctx, st, layer, q, out, out_bf16); break;
+        case 128: rc = bf ? launch_attn_t<uint16_t, 128>(ctx, st, layer, q, out, out_bf16) : launch_attn_t<float, 128>(ctx, st, layer, q, out, out_bf16); break;
         default: return set_err(ctx, ZR_E_UNSUPPORTED, "head_dim %d not supported (64, 128)", ctx->head_dim);
     }
     return rc;

@@ -4,9 +4,12 @@
 // MFMA B-operand fragments: fragment (nt, kt) is 64 lanes x 8 bf16 where lane l
 // holds W[32*kt + 8*(l/16) + j][16*nt + l%16], j < 8, stored contiguously and
 // fragments of one 16-column tile consecutive along K.  A wavefront streams
-// its weights as perfectly coalesced 1 KiB loads, each element read once.
-// A (f32 activations, L2-resident) is converted to bf16 -- or to a hi + lo
-// pair under ZR_FLAG_SPLIT_ACTIVATIONS -- while it is staged through LDS.
+// its weights as perfectly coalesced 1 KiB loads, each element read once per
+// row block, through a register ring PF k-steps deep.
+// A (activations) arrives as bf16 [M, K] -- or a hi + lo bf16 pair under
+// ZR_FLAG_SPLIT_ACTIVATIONS -- written by the producing kernel; a block
+// stages its A rows through a double-buffered LDS tile shared by the waves
+// that own different column slices.
 // Matmul semantics: forward_pass.rs:1696-1714 (w_qkv / w_gate_up column
 // concatenations), 2265 (O), 2290 (down), 2311 (LM head); f32 accumulation.
 // The gate|up concatenation is interleaved per 16 columns so one 32-column
@@ -15,6 +18,7 @@
 #include "zr_internal.h"
 
 #include <algorithm>
+#include <cstdlib>
 
 namespace zr {
 
@@ -23,13 +27,13 @@ size_t packed_weight_elems(int k, int n) {
     return kt * nt * 512;
 }
 
-// dst n-tile `nt_dst + i` takes source columns [16 * i, 16 * i + 16) of src
-// [K, n_src] (zero outside); tile_stride lets gate/up interleave.
+// dst n-tile `nt_dst0 + i * tile_step` takes source columns [16 i, 16 i + 16)
+// of src [K, n_src] (zero outside).
 __global__ __launch_bounds__(256) void pack_weight_kernel(const uint16_t* __restrict__ src, int K,
                                                           int n_src, int KT, int nt_dst0,
                                                           int tile_step, int n_tiles,
                                                           uint16_t* __restrict__ dst) {
-    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;  // one lane of one fragment
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     const size_t total = (size_t)n_tiles * KT * 64;
     if (gid >= total) return;
     const int lane = (int)(gid % 64);
@@ -113,21 +117,66 @@ zr_status pack_weight_gate_up(zr_context* ctx, const uint16_t* gate, const uint1
 }
 
 // ------------------------------------------------------------------ GEMM
-// Block = 4 wavefronts; block tile = (16*WM) rows x (4*WN*16) columns; each
-// wave owns WN 16-column tiles and every row tile.  grid = (column blocks,
-// K splits, row blocks).  HL = 2 feeds activations as hi + lo bf16 pairs.
-template <int WM, int WN, int HL, int KCH>
-__global__ __launch_bounds__(256) void gemm_kernel(const float* __restrict__ A, int M, int K,
-                                                   const bf16x8* __restrict__ Wp, int KT, int NT,
-                                                   float* __restrict__ C, int N, int kt_per_split,
-                                                   size_t split_stride) {
-    __shared__ bf16x8 lds[WM * KCH * HL * 64];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int nt0 = (blockIdx.x * 4 + wave) * WN;
-    const int m0 = blockIdx.z * WM * 16;
-    const int z = blockIdx.y;
-    const int kt_begin = z * kt_per_split;
+// Block = WAVES_M x WAVES_N wavefronts; wave tile = (16 WM) rows x (16 WN)
+// columns; block tile BM x BN.  grid = (column blocks, K splits, row blocks).
+// Per k-step of 32: one barrier; the next A slice is loaded to registers
+// before the MFMAs and written to the other LDS buffer after them; the
+// weight fragments of k-step kt + PF are requested as soon as step kt's are
+// consumed.
+template <int WM, int WN, int WAVES_M, int WAVES_N, int PF, int HL>
+__global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_kernel(
+    const uint16_t* __restrict__ A, int M, int K, const bf16x8* __restrict__ Wp, int KT, int NT,
+    float* __restrict__ C, int N, int kt_per_split, size_t split_stride) {
+    constexpr int BM = WAVES_M * WM * 16;
+    constexpr int NTHR = WAVES_M * WAVES_N * 64;
+    constexpr int A_CHUNKS = BM * 4 * HL;  // 16-byte chunks of one k-step of A
+    constexpr int A_PER_T = (A_CHUNKS + NTHR - 1) / NTHR;
+    __shared__ bf16x8 lds[2][HL][BM / 16][64];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wm_idx = wave / WAVES_N, wn_idx = wave % WAVES_N;
+    const int m0 = blockIdx.z * BM;
+    const int nt0 = blockIdx.x * (WAVES_N * WN) + wn_idx * WN;
+    const int kt_begin = blockIdx.y * kt_per_split;
     const int kt_end = min(KT, kt_begin + kt_per_split);
+    const size_t MK = (size_t)M * K;
+
+    bf16x8 areg[A_PER_T];
+    auto load_a = [&](int kt) {
+#pragma unroll
+        for (int j = 0; j < A_PER_T; ++j) {
+            const int c = tid + j * NTHR;
+            bf16x8 v = bf16x8{};
+            if (c < A_CHUNKS) {
+                const int hl = c / (BM * 4), r = c - hl * (BM * 4);
+                const int m = r >> 2, q = r & 3;
+                const int k = kt * 32 + q * 8;
+                if (m0 + m < M && kt < kt_end && k < K)
+                    v = *(const bf16x8*)(A + hl * MK + (size_t)(m0 + m) * K + k);
+            }
+            areg[j] = v;
+        }
+    };
+    auto store_a = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < A_PER_T; ++j) {
+            const int c = tid + j * NTHR;
+            if (c < A_CHUNKS) {
+                const int hl = c / (BM * 4), r = c - hl * (BM * 4);
+                const int m = r >> 2, q = r & 3;
+                lds[buf][hl][m >> 4][q * 16 + (m & 15)] = areg[j];
+            }
+        }
+    };
+
+    bf16x8 bring[PF][WN];
+    auto load_b = [&](bf16x8* dst, int kt) {
+#pragma unroll
+        for (int wn = 0; wn < WN; ++wn) {
+            const int nt = nt0 + wn;
+            dst[wn] = (nt < NT && kt < kt_end) ? Wp[((size_t)nt * KT + kt) * 64 + lane] : bf16x8{};
+        }
+    };
 
     f32x4 acc[WM][WN];
 #pragma unroll
@@ -135,68 +184,41 @@ __global__ __launch_bounds__(256) void gemm_kernel(const float* __restrict__ A, 
 #pragma unroll
         for (int wn = 0; wn < WN; ++wn) acc[mt][wn] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    for (int kc = kt_begin; kc < kt_end; kc += KCH) {
-        // weights of this chunk first: they are the HBM stream
-        bf16x8 b[KCH][WN];
+    load_a(kt_begin);
+    store_a(0);
 #pragma unroll
-        for (int ktl = 0; ktl < KCH; ++ktl)
+    for (int s = 0; s < PF; ++s) load_b(bring[s], kt_begin + s);
+
+    int buf = 0;
+    for (int kb = kt_begin; kb < kt_end; kb += PF) {
 #pragma unroll
-            for (int wn = 0; wn < WN; ++wn) {
-                const int nt = nt0 + wn, kt = kc + ktl;
-                if (nt < NT && kt < kt_end)
-                    b[ktl][wn] = Wp[((size_t)nt * KT + kt) * 64 + lane];
-                else
-                    b[ktl][wn] = bf16x8{};
-            }
-        __syncthreads();  // previous chunk finished reading LDS
-        for (int gidx = threadIdx.x; gidx < WM * 16 * KCH * 4; gidx += 256) {
-            const int row = gidx / (KCH * 4), rem = gidx - row * (KCH * 4);
-            const int ktl = rem >> 2, q4 = rem & 3;
-            const int m = m0 + row, k = (kc + ktl) * 32 + q4 * 8;
-            float x[8];
-            if (m < M && kc + ktl < kt_end && k < K) {
-                const f32x4* src = (const f32x4*)(A + (size_t)m * K + k);
-                const f32x4 lo4 = src[0], hi4 = src[1];
+        for (int s = 0; s < PF; ++s) {
+            const int kt = kb + s;
+            if (kt < kt_end) {  // uniform across the block
+                load_a(kt + 1);
+                __syncthreads();
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    x[j] = lo4[j];
-                    x[4 + j] = hi4[j];
-                }
-            } else {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) x[j] = 0.0f;
-            }
-            bf16x8 vh, vl;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                uint16_t h, l;
-                split_bf16(x[j], h, l);
-                vh[j] = __builtin_bit_cast(__bf16, h);
-                vl[j] = __builtin_bit_cast(__bf16, l);
-            }
-            const int base = (((row >> 4) * KCH + ktl) * HL) * 64 + q4 * 16 + (row & 15);
-            lds[base] = vh;
-            if (HL == 2) lds[base + 64] = vl;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int ktl = 0; ktl < KCH; ++ktl) {
-#pragma unroll
-            for (int mt = 0; mt < WM; ++mt) {
-                const bf16x8 ah = lds[((mt * KCH + ktl) * HL) * 64 + lane];
-#pragma unroll
-                for (int wn = 0; wn < WN; ++wn)
-                    acc[mt][wn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b[ktl][wn], acc[mt][wn], 0, 0, 0);
-                if (HL == 2) {
-                    const bf16x8 al = lds[((mt * KCH + ktl) * HL) * 64 + 64 + lane];
+                for (int mt = 0; mt < WM; ++mt) {
+                    const bf16x8 ah = lds[buf][0][wm_idx * WM + mt][lane];
 #pragma unroll
                     for (int wn = 0; wn < WN; ++wn)
-                        acc[mt][wn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b[ktl][wn], acc[mt][wn], 0, 0, 0);
+                        acc[mt][wn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bring[s][wn], acc[mt][wn], 0, 0, 0);
+                    if (HL == 2) {
+                        const bf16x8 al = lds[buf][HL - 1][wm_idx * WM + mt][lane];
+#pragma unroll
+                        for (int wn = 0; wn < WN; ++wn)
+                            acc[mt][wn] =
+                                __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bring[s][wn], acc[mt][wn], 0, 0, 0);
+                    }
                 }
+                load_b(bring[s], kt + PF);
+                buf ^= 1;
+                store_a(buf);
             }
         }
     }
-    float* out = C + (size_t)z * split_stride;
+
+    float* out = C + (size_t)blockIdx.y * split_stride;
 #pragma unroll
     for (int mt = 0; mt < WM; ++mt)
 #pragma unroll
@@ -204,24 +226,27 @@ __global__ __launch_bounds__(256) void gemm_kernel(const float* __restrict__ A, 
             const int n = (nt0 + wn) * 16 + (lane & 15);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int m = m0 + mt * 16 + (lane >> 4) * 4 + i;
+                const int m = m0 + (wm_idx * WM + mt) * 16 + (lane >> 4) * 4 + i;
                 if (m < M && n < N) out[(size_t)m * N + n] = acc[mt][wn][i];
             }
         }
 }
 
 // Sum of split-K slabs [S][M][N] with the epilogue.
-// kEpiStore:  out[m][n] = sum
-// kEpiSwiGLU: N = 2F interleaved per 16 columns; out[m][j] = silu(g) * u, out [M, F]
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, int S, int M,
-                                                            int N, size_t split_stride, int epilogue,
-                                                            float* __restrict__ out) {
+// kEpiStore:  out_f32[m][n] = sum
+// kEpiSwiGLU: N = 2F interleaved per 16 columns; h = silu(g) * u written as
+//             bf16 hi (+ lo) [M, F] (the next GEMM's A operand) or f32.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, int S, int M, int N,
+                                                            size_t split_stride, int epilogue,
+                                                            float* __restrict__ out_f32,
+                                                            uint16_t* __restrict__ out_bf16, int out_lo) {
 #pragma clang fp contract(off)
     const int n_out = epilogue == kEpiSwiGLU ? N / 2 : N;
     const size_t total = (size_t)M * n_out;
     for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
          idx += (size_t)gridDim.x * blockDim.x) {
         const int m = (int)(idx / n_out), j = (int)(idx % n_out);
+        float v;
         if (epilogue == kEpiSwiGLU) {
             const int gc = (j >> 4) * 32 + (j & 15);
             float g = 0.0f, u = 0.0f;
@@ -229,74 +254,123 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
                 g += ws[s * split_stride + (size_t)m * N + gc];
                 u += ws[s * split_stride + (size_t)m * N + gc + 16];
             }
-            out[idx] = g / (1.0f + expf(-g)) * u;
+            v = g / (1.0f + expf(-g)) * u;
         } else {
-            float v = 0.0f;
+            v = 0.0f;
             for (int s = 0; s < S; ++s) v += ws[s * split_stride + (size_t)m * N + j];
-            out[idx] = v;
+        }
+        if (out_bf16) {
+            uint16_t hi, lo;
+            split_bf16(v, hi, lo);
+            out_bf16[idx] = hi;
+            if (out_lo) out_bf16[total + idx] = lo;
+        } else {
+            out_f32[idx] = v;
         }
     }
 }
 
-template <int WM, int WN, int HL>
-static void gemm_launch(dim3 grid, hipStream_t stream, const float* a, int m, int k, const uint16_t* w,
-                        int KT, int NT, float* c, int n, int kt_per_split, size_t split_stride) {
-    constexpr int KCH = std::min(8, std::max(1, 64 / (WM * HL)));
-    hipLaunchKernelGGL((gemm_kernel<WM, WN, HL, KCH>), grid, dim3(256), 0, stream, a, m, k, (const bf16x8*)w, KT,
-                       NT, c, n, kt_per_split, split_stride);
+// f32 [M, K] -> bf16 hi (+ lo) [M, K] (A operand of zr_gemm)
+__global__ __launch_bounds__(256) void to_bf16_pair_kernel(const float* __restrict__ x, size_t n,
+                                                           uint16_t* __restrict__ out, int with_lo) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        uint16_t hi, lo;
+        split_bf16(x[i], hi, lo);
+        out[i] = hi;
+        if (with_lo) out[n + i] = lo;
+    }
 }
 
-zr_status launch_gemm(zr_context* ctx, const float* a, const uint16_t* w_packed, float* c, int m, int n,
-                      int k, int epilogue) {
+zr_status launch_to_bf16_pair(zr_context* ctx, const float* x, size_t n, uint16_t* out, int with_lo) {
+    const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 16384);
+    hipLaunchKernelGGL(to_bf16_pair_kernel, dim3(blocks), dim3(256), 0, ctx->stream, x, n, out, with_lo);
+    ZR_LAUNCH_CHECK(ctx);
+    return ZR_OK;
+}
+
+// Tile configurations by row count (wave tile WM x WN 16x16 tiles).
+struct GemmCfg {
+    int wm, wn, waves_m, waves_n;
+    int bm() const { return waves_m * wm * 16; }
+    int bn() const { return waves_n * wn * 16; }
+};
+
+static GemmCfg pick_cfg(int m) {
+    if (m <= 16) return {1, 4, 1, 8};
+    if (m <= 32) return {2, 4, 1, 8};
+    if (m <= 64) return {4, 4, 1, 8};
+    if (m <= 128) return {4, 4, 2, 4};
+    return {8, 4, 2, 4};
+}
+
+GemmPlan gemm_plan(int m, int n, int k, int epilogue) {
+    GemmPlan p;
+    const GemmCfg c = pick_cfg(m);
+    p.KT = (k + 31) / 32;
+    p.NT = (n + 15) / 16;
+    p.row_blocks = (m + c.bm() - 1) / c.bm();
+    p.col_blocks = (p.NT + c.bn() / 16 - 1) / (c.bn() / 16);
+    // split K until the grid covers every CU, keeping >= 8 k-steps per split
+    int splits = 1;
+    static const int target = getenv("ZR_GEMM_TARGET_BLOCKS") ? atoi(getenv("ZR_GEMM_TARGET_BLOCKS")) : 256;
+    while (p.col_blocks * p.row_blocks * splits * 2 <= target && p.KT / (splits * 2) >= 8) splits *= 2;
+    p.kt_per_split = (p.KT + splits - 1) / splits;
+    p.splits = (p.KT + p.kt_per_split - 1) / p.kt_per_split;
+    p.direct = p.splits == 1 && epilogue == kEpiStore;
+    p.ws_floats = p.direct ? 0 : (size_t)p.splits * m * n;
+    return p;
+}
+
+template <int WM, int WN, int WAVES_M, int WAVES_N, int HL>
+static void gemm_launch(dim3 grid, hipStream_t stream, const uint16_t* a, int m, int k, const uint16_t* w,
+                        int KT, int NT, float* c, int n, int kt_per_split, size_t split_stride) {
+    constexpr int PF = WM >= 8 ? 2 : 4;
+    hipLaunchKernelGGL((gemm_kernel<WM, WN, WAVES_M, WAVES_N, PF, HL>), grid, dim3(WAVES_M * WAVES_N * 64), 0,
+                       stream, a, m, k, (const bf16x8*)w, KT, NT, c, n, kt_per_split, split_stride);
+}
+
+zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_packed, float* c_f32,
+                      uint16_t* c_bf16, int m, int n, int k, int epilogue) {
     if (m <= 0) return ZR_OK;
     if (k % 8 != 0) return set_err(ctx, ZR_E_UNSUPPORTED, "GEMM K=%d must be a multiple of 8", k);
-    const int KT = (k + 31) / 32, NT = (n + 15) / 16;
-    constexpr int WN = 2;
-    const int wm = m <= 16 ? 1 : m <= 32 ? 2 : m <= 64 ? 4 : m <= 128 ? 8 : 16;
-    const int row_blocks = (m + wm * 16 - 1) / (wm * 16);
-    const int col_blocks = (NT + 4 * WN - 1) / (4 * WN);
-    // split K until the grid covers the chip ~2x, keeping >= 8 k-tiles per split
-    int splits = 1;
-    const int target = 2 * 256;
-    while (col_blocks * row_blocks * splits < target && KT / (splits * 2) >= 8) splits *= 2;
-    const int kt_per_split = (KT + splits - 1) / splits;
-    splits = (KT + kt_per_split - 1) / kt_per_split;
-    const bool direct = splits == 1 && epilogue == kEpiStore;
+    const GemmPlan p = gemm_plan(m, n, k, epilogue);
+    const GemmCfg cfg = pick_cfg(m);
+    const bool direct = p.direct && c_f32 && !c_bf16;
     const size_t split_stride = (size_t)m * n;
-    if (!direct && (size_t)splits * split_stride > ctx->splitk_ws_floats)
-        return set_err(ctx, ZR_E_OOM, "split-K workspace too small (%d x %d x %d)", splits, m, n);
-    float* dst = direct ? c : ctx->splitk_ws;
+    if (!direct && (size_t)p.splits * split_stride > ctx->splitk_ws_floats)
+        return set_err(ctx, ZR_E_OOM, "split-K workspace too small (%d x %d x %d)", p.splits, m, n);
+    float* dst = direct ? c_f32 : ctx->splitk_ws;
     const bool split_act = (ctx->desc.flags & ZR_FLAG_SPLIT_ACTIVATIONS) != 0;
-    dim3 grid(col_blocks, splits, row_blocks);
+    dim3 grid(p.col_blocks, p.splits, p.row_blocks);
     hipEvent_t ev;
     timing_mark_begin(ctx, kClassGemm, &ev);
-#define ZR_GEMM_CASE(WMV)                                                                                    \
-    case WMV:                                                                                                \
-        if (split_act)                                                                                       \
-            gemm_launch<WMV, WN, 2>(grid, ctx->stream, a, m, k, w_packed, KT, NT, dst, n, kt_per_split,     \
-                                    split_stride);                                                          \
-        else                                                                                                 \
-            gemm_launch<WMV, WN, 1>(grid, ctx->stream, a, m, k, w_packed, KT, NT, dst, n, kt_per_split,     \
-                                    split_stride);                                                          \
-        break;
-    switch (wm) {
-        ZR_GEMM_CASE(1)
-        ZR_GEMM_CASE(2)
-        ZR_GEMM_CASE(4)
-        ZR_GEMM_CASE(8)
-        ZR_GEMM_CASE(16)
+#define ZR_GEMM_CASE(WMV, WNV, WAM, WAN)                                                                       \
+    if (cfg.wm == WMV && cfg.wn == WNV && cfg.waves_m == WAM && cfg.waves_n == WAN) {                          \
+        if (split_act)                                                                                         \
+            gemm_launch<WMV, WNV, WAM, WAN, 2>(grid, ctx->stream, a, m, k, w_packed, p.KT, p.NT, dst, n,      \
+                                               p.kt_per_split, split_stride);                                  \
+        else                                                                                                   \
+            gemm_launch<WMV, WNV, WAM, WAN, 1>(grid, ctx->stream, a, m, k, w_packed, p.KT, p.NT, dst, n,      \
+                                               p.kt_per_split, split_stride);                                  \
     }
+    ZR_GEMM_CASE(1, 4, 1, 8)
+    ZR_GEMM_CASE(2, 4, 1, 8)
+    ZR_GEMM_CASE(4, 4, 1, 8)
+    ZR_GEMM_CASE(4, 4, 2, 4)
+    ZR_GEMM_CASE(8, 4, 2, 4)
 #undef ZR_GEMM_CASE
     ZR_LAUNCH_CHECK(ctx);
+    timing_mark_end(ctx, kClassGemm, ev);
     if (!direct) {
+        timing_mark_begin(ctx, kClassOther, &ev);
         const size_t n_out = epilogue == kEpiSwiGLU ? (size_t)n / 2 : (size_t)n;
         const size_t total = (size_t)m * n_out;
         const unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, 65535);
-        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, ctx->stream, ctx->splitk_ws, splits,
-                           m, n, split_stride, epilogue, c);
+        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, ctx->stream, ctx->splitk_ws, p.splits,
+                           m, n, split_stride, epilogue, c_f32, c_bf16, split_act ? 1 : 0);
         ZR_LAUNCH_CHECK(ctx);
+        timing_mark_end(ctx, kClassOther, ev);
     }
-    timing_mark_end(ctx, kClassGemm, ev);
     return ZR_OK;
 }
 

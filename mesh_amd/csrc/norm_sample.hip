@@ -38,7 +38,9 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__
                                                        const float* __restrict__ residual_in,
                                                        float* __restrict__ x_out,
                                                        const float* __restrict__ gamma,
-                                                       float* __restrict__ y,
+                                                       float* __restrict__ y_f32,
+                                                       uint16_t* __restrict__ y_bf16, int split_lo,
+                                                       size_t lo_offset,
                                                        const int* __restrict__ row_index, int cols,
                                                        float eps) {
     __shared__ float red[4];
@@ -62,17 +64,27 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__
     const float total = red[0] + red[1] + red[2] + red[3];
     const float inv_rms = 1.0f / sqrtf(total / (float)cols + eps);
     const float* xs = rr ? xo : xr;
-    float* yr = y + (size_t)r * cols;
-    for (int i = threadIdx.x; i < cols; i += blockDim.x) yr[i] = xs[i] * inv_rms * gamma[i];
+    for (int i = threadIdx.x; i < cols; i += blockDim.x) {
+        const float v = xs[i] * inv_rms * gamma[i];
+        if (y_bf16) {
+            uint16_t hi, lo;
+            split_bf16(v, hi, lo);
+            y_bf16[(size_t)r * cols + i] = hi;
+            if (split_lo) y_bf16[lo_offset + (size_t)r * cols + i] = lo;
+        } else {
+            y_f32[(size_t)r * cols + i] = v;
+        }
+    }
 }
 
 zr_status launch_rms_norm(zr_context* ctx, const float* x, const float* residual_in, float* x_out,
-                          const float* gamma, float* y, const int* row_index, int rows, int cols) {
+                          const float* gamma, float* y_f32, uint16_t* y_bf16, int split_lo,
+                          const int* row_index, int rows, int cols) {
     if (rows <= 0) return ZR_OK;
     hipEvent_t ev;
     timing_mark_begin(ctx, kClassNormRopeKv, &ev);
     hipLaunchKernelGGL(rms_norm_kernel, dim3(rows), dim3(256), 0, ctx->stream, x, residual_in, x_out, gamma,
-                       y, row_index, cols, ctx->desc.rms_norm_eps);
+                       y_f32, y_bf16, split_lo, (size_t)rows * cols, row_index, cols, ctx->desc.rms_norm_eps);
     ZR_LAUNCH_CHECK(ctx);
     timing_mark_end(ctx, kClassNormRopeKv, ev);
     return ZR_OK;

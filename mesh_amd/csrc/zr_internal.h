@@ -81,16 +81,17 @@ struct zr_context {
     int n_pages = 0;
     size_t page_bytes = 0;   // bytes of one page of one layer (K and V)
 
-    // activations (max_tokens rows)
-    float* hidden = nullptr;  // [T, H] residual stream
-    float* xn = nullptr;      // [T, H] normed GEMM input
-    float* qkv = nullptr;     // [T, Q + 2Kc]
-    float* q_rope = nullptr;  // [T, Q]
-    float* attn = nullptr;    // [T, Q]
-    float* proj = nullptr;    // [T, H] O / down projection output
-    float* ffn = nullptr;     // [T, 2F] gate|up, then SwiGLU output [T, F]
-    float* logits = nullptr;  // [S, V]
-    float* final_x = nullptr; // [S, H] normed last rows
+    // activations (max_tokens rows).  GEMM A operands are bf16 [M, K], followed
+    // by the lo half [M, K] under ZR_FLAG_SPLIT_ACTIVATIONS.
+    float* hidden = nullptr;     // [T, H] residual stream (f32)
+    uint16_t* xa = nullptr;      // normed hidden, A of QKV / gate_up
+    float* qkv = nullptr;        // [T, Q + 2Kc]
+    float* q_rope = nullptr;     // [T, Q]
+    uint16_t* attn_a = nullptr;  // attention output, A of O
+    float* proj = nullptr;       // [T, H] O / down projection output (pre-all-reduce partial)
+    uint16_t* ffn_a = nullptr;   // SwiGLU output, A of down
+    uint16_t* final_a = nullptr; // [S, H] normed last rows, A of the LM head
+    float* logits = nullptr;     // [S, V]
     uint32_t* tokens_out = nullptr; // [S]
     float* splitk_ws = nullptr;     // split-K partial workspace
     size_t splitk_ws_floats = 0;
@@ -170,21 +171,34 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
 // Kernel launchers (one per .hip file) ------------------------------------
 zr_status launch_pack(zr_context* ctx, StagedMeta* st);
 zr_status launch_embed(zr_context* ctx, StagedMeta* st, const uint32_t* d_tokens);
-zr_status launch_rms_norm(zr_context* ctx, const float* x, const float* residual_in,
-                          float* x_out, const float* gamma, float* y, const int* row_index,
-                          int rows, int cols);
+// y = rms_norm(x (+ residual_in)) * gamma.  With residual_in, x_out = x +
+// residual_in is written first.  Output as f32 (y_f32) or as the bf16 A operand
+// of the next GEMM (y_bf16: hi [rows, cols] then lo when split_lo).
+zr_status launch_rms_norm(zr_context* ctx, const float* x, const float* residual_in, float* x_out,
+                          const float* gamma, float* y_f32, uint16_t* y_bf16, int split_lo,
+                          const int* row_index, int rows, int cols);
 zr_status launch_rope_kv_write(zr_context* ctx, StagedMeta* st, int layer, const float* qkv,
                                float* q_out, int rope);
-zr_status launch_attention(zr_context* ctx, StagedMeta* st, int layer, const float* q, float* out);
+// out_f32 [T, q_cols] or out_bf16 (A operand of the O projection).
+zr_status launch_attention(zr_context* ctx, StagedMeta* st, int layer, const float* q, float* out_f32,
+                           uint16_t* out_bf16);
 zr_status launch_kv_copy(zr_context* ctx, int layer_begin, int layer_end, const int* d_table,
                          int first_offset, int first_row, int n_rows, float* k, float* v,
                          int to_pool);
 zr_status launch_argmax(zr_context* ctx, const float* x, int rows, int cols, uint32_t* out);
 
 enum GemmEpilogue { kEpiStore = 0, kEpiSwiGLU = 1 };
-// C = A @ W (W packed), epilogue applied after the split-K reduction.
-zr_status launch_gemm(zr_context* ctx, const float* a, const uint16_t* w_packed, float* c, int m,
-                      int n, int k, int epilogue);
+struct GemmPlan {
+    int KT = 0, NT = 0, row_blocks = 0, col_blocks = 0, splits = 1, kt_per_split = 0;
+    bool direct = true;
+    size_t ws_floats = 0;
+};
+GemmPlan gemm_plan(int m, int n, int k, int epilogue);
+// C = A @ W (W packed, A bf16 operand).  kEpiStore writes c_f32; kEpiSwiGLU
+// writes silu(gate) * up as the bf16 operand c_bf16 (or f32 c_f32).
+zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_packed, float* c_f32,
+                      uint16_t* c_bf16, int m, int n, int k, int epilogue);
+zr_status launch_to_bf16_pair(zr_context* ctx, const float* x, size_t n, uint16_t* out, int with_lo);
 zr_status pack_weight(zr_context* ctx, const uint16_t* src /* [K,N] host or device */,
                       int k, int n, uint16_t** out_packed);
 // Packs [K, n1] | [K, n2] | ... (column concatenation) into one packed matrix.
