@@ -16,6 +16,8 @@ the device.  The attention kernel's duration comes from HIP events recorded on
 the provider's stream around every attention launch in the timed region.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--skip-bs32]
+       python bench.py --calibrate-copy   (a plain 1 GiB device copy, for scaling
+                                           rocprofv3 FETCH_SIZE / WRITE_SIZE)
 """
 from __future__ import annotations
 
@@ -34,6 +36,8 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "paged_attention_llama3_8b_b256_traffic.md")
 METRIC = "decode tokens/sec @1 MI355X (bs 32/256); paged-attn HBM GB/s as % of peak"
 
 
@@ -64,6 +68,24 @@ WORKLOADS = {
 }
 
 
+def gemm_flops(geo, batch):
+    """MFMA work of one decode step's projections (2 flops per multiply-add)."""
+    H, Q, KV, F, V, L = geo.hidden, geo.q_cols, geo.kv_cols, geo.ffn_cols, geo.vocab, geo.num_layers
+    return 2.0 * batch * (L * (H * (Q + 2 * KV) + Q * H + H * 2 * F + F * H) + H * V)
+
+
+def measured_traffic():
+    """HBM bytes per paged-attention launch from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (already scaled by the copy calibration)."""
+    try:
+        for line in open(TRAFFIC_SUMMARY):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def step_bytes(geo, batch, kv_rows_total):
     """Algorithmic HBM bytes of one decode step: every weight once (bf16), the
     embedding rows, every cached K/V row of every layer once (bf16), the new
@@ -78,7 +100,7 @@ def step_bytes(geo, batch, kv_rows_total):
 class GpuDecodeBench:
     """One workload resident on the GPU with `steps_total` decode steps staged."""
 
-    def __init__(self, name, steps_total):
+    def __init__(self, name, steps_total, split=True):
         from mesh_amd import DeviceContext, ModelGeometry, _lib
 
         self._lib = _lib
@@ -89,7 +111,7 @@ class GpuDecodeBench:
         self.ctxlens = w["contexts"]()
         self.max_seq = w["max_seq_len"]
         self.ctx = DeviceContext(g, kv_dtype="bf16", max_tokens=self.B, max_seqs=self.B,
-                                 max_pages_per_seq=self.max_seq // 16 + 2)
+                                 max_pages_per_seq=self.max_seq // 16 + 2, split_activations=split)
         ctx, lib = self.ctx, self.ctx.lib
         H, Q, KV, F, V = g.hidden, g.q_cols, g.kv_cols, g.ffn_cols, g.vocab
         shapes = dict(w_q=(H, Q), w_k=(H, KV), w_v=(H, KV), w_o=(Q, H), w_gate=(H, F), w_up=(H, F), w_down=(F, H))
@@ -185,6 +207,7 @@ def measure(name, steps, warmup):
     attn_ms_per_launch = ms[0] / max(attn_launches, 1)
     attn_gbs = attn_bytes_per_launch / (attn_ms_per_launch * 1e-3) / 1e9
     sb = np.mean([step_bytes(g, B, r) for r in timed_rows])
+    gemm_tflops = gemm_flops(g, B) * steps / (ms[1] * 1e-3) / 1e12 if ms[1] > 0 else 0.0
     roof_tps = B / (sb / (HBM_PEAK_GBS * 1e9))
     result = dict(
         workload=WORKLOADS[name]["desc"], batch=B, layers=g.num_layers,
@@ -196,6 +219,9 @@ def measure(name, steps, warmup):
                             "other": ms[3] / steps},
         attention=dict(launches=attn_launches, bytes_per_launch=attn_bytes_per_launch,
                        avg_ms=attn_ms_per_launch, achieved_gbs=attn_gbs, frac=attn_gbs / HBM_PEAK_GBS),
+        gemm=dict(launches=n[1] // steps, ms_per_step=ms[1] / steps, achieved_tflops=gemm_tflops,
+                  frac=gemm_tflops / MFMA_BF16_PEAK_TFLOPS,
+                  weight_gbs=(2 * gemm_flops(g, B) / (2 * B)) * steps / (ms[1] * 1e-3) / 1e9 if ms[1] > 0 else 0.0),
     )
     bench.close()
     return result
@@ -253,6 +279,20 @@ def cpu_baseline(name):
                        f"(T2 - T1) = {step_s:.2f} s; f32 weights/KV as the reference CPU provider")
 
 
+def calibrate_copy():
+    """One plain device-to-device copy of 1 GiB (torch), the reference point
+    for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+
+    n = 1 << 28
+    a = torch.ones(n, device="cuda", dtype=torch.float32)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": n * 4}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -261,7 +301,11 @@ def main():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-bs32", action="store_true")
     ap.add_argument("--workload", default="llama3_8b_b256", choices=sorted(WORKLOADS))
+    ap.add_argument("--calibrate-copy", action="store_true")
     a = ap.parse_args()
+    if a.calibrate_copy:
+        calibrate_copy()
+        return
     if a.gpus != 1:
         print(json.dumps({"error": "this provider runs one worker's shard on one GPU; --gpus must be 1 "
                                    "(multi-GPU sharding is a design note, not part of this build)"}))
@@ -277,7 +321,8 @@ def main():
         r = measure("tinyllama_b32", a.steps, a.warmup)
         bs32 = dict(value=r["tokens_per_s"], unit="tokens/s", ms_per_step=r["ms_per_step"],
                     workload=r["workload"], step_roofline_frac=r["step_roofline_frac"],
-                    attention_gbs=r["attention"]["achieved_gbs"], kernel_ms_per_step=r["kernel_ms_per_step"])
+                    attention_gbs=r["attention"]["achieved_gbs"], kernel_ms_per_step=r["kernel_ms_per_step"],
+                    gemm_tflops=r["gemm"]["achieved_tflops"], gemm_weight_gbs=r["gemm"]["weight_gbs"])
     cpu = None if a.skip_cpu else cpu_baseline(a.workload)
     att = main_r["attention"]
     line = {
@@ -288,14 +333,18 @@ def main():
                 "output, greedy tokens fed back on the device",
         "config": {"workload": main_r["workload"], "sessions": main_r["batch"], "layers": main_r["layers"],
                    "context_tokens": main_r["context_tokens"], "context_max": main_r["context_max"],
-                   "parallelism": "one worker shard (1 of 1) on one GPU"},
+                   "parallelism": "one worker shard (1 of 1) on one GPU",
+                   "gemm_a_operand": "bf16 hi + lo pair (activation = hi + lo to 2^-16), fp32 accumulation"},
         "roofline": {"bound": "hbm", "kernel": "paged_attention_kernel", "achieved": att["achieved_gbs"],
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": att["frac"], "traffic": None,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": att["frac"], "traffic": measured_traffic(),
                      "bytes_per_launch": att["bytes_per_launch"], "avg_ms": att["avg_ms"],
                      "launches": att["launches"]},
         "step_roofline": {"tokens_per_s": main_r["step_roofline_tokens_per_s"], "frac": main_r["step_roofline_frac"],
                           "bytes_per_step": main_r["step_bytes"]},
         "kernel_ms_per_step": main_r["kernel_ms_per_step"],
+        "gemm_mfma": {"achieved": main_r["gemm"]["achieved_tflops"], "peak": MFMA_BF16_PEAK_TFLOPS,
+                      "unit": "TFLOP/s", "frac": main_r["gemm"]["frac"], "mfma_ops_per_flop": 2,
+                      "weight_stream_gbs": main_r["gemm"]["weight_gbs"]},
         "bs32": bs32,
         "cpu_baseline": cpu,
     }

@@ -295,25 +295,31 @@ struct GemmCfg {
     int bn() const { return waves_n * wn * 16; }
 };
 
-static GemmCfg pick_cfg(int m) {
-    if (m <= 16) return {1, 4, 1, 8};
-    if (m <= 32) return {2, 4, 1, 8};
-    if (m <= 64) return {4, 4, 1, 8};
+// Measured on MI355X over the decode shapes: 2x2 wave tiles with 8 waves
+// suit M <= 64; above 128 rows one 256-row block tile reads each weight
+// tile from HBM once (two 128-row tiles read it twice when the weights do
+// not stay in cache).
+static GemmCfg pick_cfg(int m, int n) {
+    (void)n;
+    if (m <= 16) return {1, 2, 1, 8};
+    if (m <= 32) return {2, 2, 1, 8};
+    if (m <= 64) return {4, 2, 1, 8};
     if (m <= 128) return {4, 4, 2, 4};
     return {8, 4, 2, 4};
 }
 
 GemmPlan gemm_plan(int m, int n, int k, int epilogue) {
     GemmPlan p;
-    const GemmCfg c = pick_cfg(m);
+    const GemmCfg c = pick_cfg(m, n);
     p.KT = (k + 31) / 32;
     p.NT = (n + 15) / 16;
     p.row_blocks = (m + c.bm() - 1) / c.bm();
     p.col_blocks = (p.NT + c.bn() / 16 - 1) / (c.bn() / 16);
-    // split K until the grid covers every CU, keeping >= 8 k-steps per split
+    // split K while the grid has fewer than ~1.5 blocks per CU, keeping at
+    // least 4 k-steps per split
+    static const int target = getenv("ZR_GEMM_TARGET_BLOCKS") ? atoi(getenv("ZR_GEMM_TARGET_BLOCKS")) : 384;
     int splits = 1;
-    static const int target = getenv("ZR_GEMM_TARGET_BLOCKS") ? atoi(getenv("ZR_GEMM_TARGET_BLOCKS")) : 256;
-    while (p.col_blocks * p.row_blocks * splits * 2 <= target && p.KT / (splits * 2) >= 8) splits *= 2;
+    while (p.col_blocks * p.row_blocks * splits * 2 <= target && p.KT / (splits * 2) >= 4) splits *= 2;
     p.kt_per_split = (p.KT + splits - 1) / splits;
     p.splits = (p.KT + p.kt_per_split - 1) / p.kt_per_split;
     p.direct = p.splits == 1 && epilogue == kEpiStore;
@@ -324,7 +330,7 @@ GemmPlan gemm_plan(int m, int n, int k, int epilogue) {
 template <int WM, int WN, int WAVES_M, int WAVES_N, int HL>
 static void gemm_launch(dim3 grid, hipStream_t stream, const uint16_t* a, int m, int k, const uint16_t* w,
                         int KT, int NT, float* c, int n, int kt_per_split, size_t split_stride) {
-    constexpr int PF = WM >= 8 ? 2 : 4;
+    constexpr int PF = 4;
     hipLaunchKernelGGL((gemm_kernel<WM, WN, WAVES_M, WAVES_N, PF, HL>), grid, dim3(WAVES_M * WAVES_N * 64), 0,
                        stream, a, m, k, (const bf16x8*)w, KT, NT, c, n, kt_per_split, split_stride);
 }
@@ -334,7 +340,7 @@ zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_pack
     if (m <= 0) return ZR_OK;
     if (k % 8 != 0) return set_err(ctx, ZR_E_UNSUPPORTED, "GEMM K=%d must be a multiple of 8", k);
     const GemmPlan p = gemm_plan(m, n, k, epilogue);
-    const GemmCfg cfg = pick_cfg(m);
+    const GemmCfg cfg = pick_cfg(m, n);
     const bool direct = p.direct && c_f32 && !c_bf16;
     const size_t split_stride = (size_t)m * n;
     if (!direct && (size_t)p.splits * split_stride > ctx->splitk_ws_floats)
@@ -353,9 +359,9 @@ zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_pack
             gemm_launch<WMV, WNV, WAM, WAN, 1>(grid, ctx->stream, a, m, k, w_packed, p.KT, p.NT, dst, n,      \
                                                p.kt_per_split, split_stride);                                  \
     }
-    ZR_GEMM_CASE(1, 4, 1, 8)
-    ZR_GEMM_CASE(2, 4, 1, 8)
-    ZR_GEMM_CASE(4, 4, 1, 8)
+    ZR_GEMM_CASE(1, 2, 1, 8)
+    ZR_GEMM_CASE(2, 2, 1, 8)
+    ZR_GEMM_CASE(4, 2, 1, 8)
     ZR_GEMM_CASE(4, 4, 2, 4)
     ZR_GEMM_CASE(8, 4, 2, 4)
 #undef ZR_GEMM_CASE
