@@ -232,6 +232,133 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_kernel(
         }
 }
 
+// ------------------------------------------------- GEMM, LDS-DMA pipeline
+// `s_waitcnt vmcnt(n)` with expcnt / lgkmcnt left unconstrained (gfx9
+// encoding: vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Both operands go global -> LDS with `global_load_lds_dwordx4` (no
+// registers, no per-lane address math beyond one pointer): every 1 KiB MFMA
+// fragment of a k-step -- A rows (hi, then lo) and packed weight tiles -- is
+// one wave instruction, spread evenly over the block's waves.  STAGES-deep
+// LDS ring: at step i a wave waits (vmcnt) for its own copies of stage i,
+// the block barrier publishes the stage to every wave and retires the slot
+// read at step i-1, which then takes stage i + STAGES - 1.  The compiler
+// does not order LDS reads after these copies, hence the explicit waits.
+// Block tile BM x BN = (16 WAVES_M WM) x (16 WAVES_N WN); wave tile
+// (16 WM) x (16 WN).  Grid: 1-D, decoded so that the row blocks of one
+// (column block, split) pair are dispatched 8 apart -- on the same XCD, one
+// after the other -- and share that weight tile through its L2.
+template <int WM, int WN, int WAVES_M, int WAVES_N, int HL, int STAGES>
+__global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_dma_kernel(
+    const uint16_t* __restrict__ A, int M, int K, const bf16x8* __restrict__ Wp, int KT, int NT,
+    float* __restrict__ C, int N, int kt_per_split, int splits, int row_blocks, int col_blocks,
+    size_t split_stride) {
+    constexpr int NW = WAVES_M * WAVES_N;
+    constexpr int BMT = WAVES_M * WM, BNT = WAVES_N * WN;
+    constexpr int FA = HL * BMT, FB = BNT, FS = FA + FB;
+    constexpr int PW = (FS + NW - 1) / NW;  // copies per wave per stage
+    constexpr int FSP = PW * NW;            // fragments per stage incl. padding
+    static_assert(STAGES >= 2 && STAGES <= 4, "stages");
+    static_assert(PW * (STAGES - 2) < 64, "vmcnt range");
+    __shared__ bf16x8 lds[STAGES][FSP][64];
+
+    const int b = blockIdx.x;
+    const int j = b >> 3;
+    const int rb = j % row_blocks;
+    const int g = (j / row_blocks) * 8 + (b & 7);
+    if (g >= col_blocks * splits) return;  // padding block of the XCD mapping
+    const int cb = g / splits, split = g - cb * splits;
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wm_idx = wave / WAVES_N, wn_idx = wave - wm_idx * WAVES_N;
+    const int m0 = rb * BMT * 16;
+    const int nt_blk = cb * BNT;
+    const int kt_begin = split * kt_per_split;
+    const int nsteps = min(KT, kt_begin + kt_per_split) - kt_begin;
+    const size_t MK = (size_t)M * K;
+
+    auto issue = [&](int slot, int kt) {
+#pragma unroll
+        for (int i = 0; i < PW; ++i) {
+            int f = i * NW + wave;
+            const int fs = f < FS ? f : f - FS;  // padding rows repeat a real fragment
+            const void* src;
+            if (fs < FA) {
+                const int hl = fs / BMT, mt = fs - hl * BMT;
+                const int row = min(m0 + mt * 16 + (lane & 15), M - 1);
+                const int kc = min(kt * 32 + (lane >> 4) * 8, K - 8);
+                src = A + (size_t)hl * MK + (size_t)row * K + kc;
+            } else {
+                const int nt = min(nt_blk + (fs - FA), NT - 1);
+                src = Wp + ((size_t)nt * KT + kt) * 64 + lane;
+            }
+            __builtin_amdgcn_global_load_lds(src, (lds_void*)&lds[slot][f][0], 16, 0, 0);
+        }
+    };
+
+    f32x4 acc[WM][WN];
+#pragma unroll
+    for (int mt = 0; mt < WM; ++mt)
+#pragma unroll
+        for (int wn = 0; wn < WN; ++wn) acc[mt][wn] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s)
+        if (s < nsteps) issue(s, kt_begin + s);
+
+    int slot = 0;
+    for (int i = 0; i < nsteps; ++i) {
+        const int ahead = min(STAGES - 2, nsteps - 1 - i);  // stages issued after stage i
+        if (STAGES >= 4 && ahead >= 2)
+            wait_vmcnt<PW * (STAGES >= 4 ? 2 : 0)>();
+        else if (STAGES >= 3 && ahead == 1)
+            wait_vmcnt<PW * (STAGES >= 3 ? 1 : 0)>();
+        else
+            wait_vmcnt<0>();
+        __syncthreads();
+        if (i + STAGES - 1 < nsteps) {
+            int ns = slot + STAGES - 1;
+            if (ns >= STAGES) ns -= STAGES;
+            issue(ns, kt_begin + i + STAGES - 1);
+        }
+        const bf16x8* sa = &lds[slot][0][0];
+        const bf16x8* sb = &lds[slot][FA][0];
+        bf16x8 bf[WN];
+#pragma unroll
+        for (int wn = 0; wn < WN; ++wn) bf[wn] = sb[(wn_idx * WN + wn) * 64 + lane];
+#pragma unroll
+        for (int mt = 0; mt < WM; ++mt)
+#pragma unroll
+            for (int hl = 0; hl < HL; ++hl) {
+                const bf16x8 af = sa[(hl * BMT + wm_idx * WM + mt) * 64 + lane];
+#pragma unroll
+                for (int wn = 0; wn < WN; ++wn)
+                    acc[mt][wn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bf[wn], acc[mt][wn], 0, 0, 0);
+            }
+        if (++slot == STAGES) slot = 0;
+    }
+
+    float* out = C + (size_t)split * split_stride;
+#pragma unroll
+    for (int mt = 0; mt < WM; ++mt)
+#pragma unroll
+        for (int wn = 0; wn < WN; ++wn) {
+            const int n = (nt_blk + wn_idx * WN + wn) * 16 + (lane & 15);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = m0 + (wm_idx * WM + mt) * 16 + (lane >> 4) * 4 + i;
+                if (m < M && n < N) out[(size_t)m * N + n] = acc[mt][wn][i];
+            }
+        }
+}
+
 // Sum of split-K slabs [S][M][N] with the epilogue.
 // kEpiStore:  out_f32[m][n] = sum
 // kEpiSwiGLU: N = 2F interleaved per 16 columns; h = silu(g) * u written as
@@ -288,24 +415,32 @@ zr_status launch_to_bf16_pair(zr_context* ctx, const float* x, size_t n, uint16_
     return ZR_OK;
 }
 
-// Tile configurations by row count (wave tile WM x WN 16x16 tiles).
+// Tile configurations (wave tile WM x WN 16x16 tiles; WAVES_M x WAVES_N waves).
+// family 0: register-ring kernel (gemm_kernel), for M <= 64 where the step
+//           streams weights; family 1: LDS-DMA kernel (gemm_dma_kernel), for
+//           M >= 128 where the hi + lo MFMA work dominates.
 struct GemmCfg {
-    int wm, wn, waves_m, waves_n;
+    int family, wm, wn, waves_m, waves_n, stages;
     int bm() const { return waves_m * wm * 16; }
     int bn() const { return waves_n * wn * 16; }
 };
 
-// Measured on MI355X over the decode shapes: 2x2 wave tiles with 8 waves
-// suit M <= 64; above 128 rows one 256-row block tile reads each weight
-// tile from HBM once (two 128-row tiles read it twice when the weights do
-// not stay in cache).
+static bool dma_enabled() {
+    static const bool on = !(getenv("ZR_GEMM_DMA") && atoi(getenv("ZR_GEMM_DMA")) == 0);
+    return on;
+}
+
+// Measured on MI355X over the decode shapes with weights streamed from HBM:
+// 2x2 wave tiles with 8 waves suit M <= 64; from 128 rows the LDS-DMA kernel
+// with 128 x 256 block tiles (8 waves, 3 stages) wins, and for very wide N
+// (the LM head) 4 waves with 2 stages, two blocks per CU.
 static GemmCfg pick_cfg(int m, int n) {
-    (void)n;
-    if (m <= 16) return {1, 2, 1, 8};
-    if (m <= 32) return {2, 2, 1, 8};
-    if (m <= 64) return {4, 2, 1, 8};
-    if (m <= 128) return {4, 4, 2, 4};
-    return {8, 4, 2, 4};
+    if (m <= 16) return {0, 1, 2, 1, 8, 0};
+    if (m <= 32) return {0, 2, 2, 1, 8, 0};
+    if (m <= 64) return {0, 4, 2, 1, 8, 0};
+    if (!dma_enabled()) return m <= 128 ? GemmCfg{0, 4, 4, 2, 4, 0} : GemmCfg{0, 8, 4, 2, 4, 0};
+    if (n >= 65536) return {1, 4, 8, 2, 2, 2};
+    return {1, 4, 4, 2, 4, 3};
 }
 
 GemmPlan gemm_plan(int m, int n, int k, int epilogue) {
@@ -315,11 +450,25 @@ GemmPlan gemm_plan(int m, int n, int k, int epilogue) {
     p.NT = (n + 15) / 16;
     p.row_blocks = (m + c.bm() - 1) / c.bm();
     p.col_blocks = (p.NT + c.bn() / 16 - 1) / (c.bn() / 16);
-    // split K while the grid has fewer than ~1.5 blocks per CU, keeping at
-    // least 4 k-steps per split
-    static const int target = getenv("ZR_GEMM_TARGET_BLOCKS") ? atoi(getenv("ZR_GEMM_TARGET_BLOCKS")) : 384;
     int splits = 1;
-    while (p.col_blocks * p.row_blocks * splits * 2 <= target && p.KT / (splits * 2) >= 4) splits *= 2;
+    if (c.family == 0) {
+        // split K while the grid has fewer than ~1.5 blocks per CU, keeping at
+        // least 4 k-steps per split
+        static const int target =
+            getenv("ZR_GEMM_TARGET_BLOCKS") ? atoi(getenv("ZR_GEMM_TARGET_BLOCKS")) : 384;
+        while (p.col_blocks * p.row_blocks * splits * 2 <= target && p.KT / (splits * 2) >= 4) splits *= 2;
+    } else {
+        // one resident block per CU (LDS-bound): split K while the grid still
+        // fits one pass over the CUs, keeping at least 4 k-steps per split
+        static const int cus = [] {
+            int v = 256;
+            int dev = 0;
+            if (hipGetDevice(&dev) == hipSuccess)
+                (void)hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev);
+            return v > 0 ? v : 256;
+        }();
+        while (p.col_blocks * p.row_blocks * splits * 2 <= cus && p.KT / (splits * 2) >= 4) splits *= 2;
+    }
     p.kt_per_split = (p.KT + splits - 1) / splits;
     p.splits = (p.KT + p.kt_per_split - 1) / p.kt_per_split;
     p.direct = p.splits == 1 && epilogue == kEpiStore;
@@ -328,17 +477,28 @@ GemmPlan gemm_plan(int m, int n, int k, int epilogue) {
 }
 
 template <int WM, int WN, int WAVES_M, int WAVES_N, int HL>
-static void gemm_launch(dim3 grid, hipStream_t stream, const uint16_t* a, int m, int k, const uint16_t* w,
-                        int KT, int NT, float* c, int n, int kt_per_split, size_t split_stride) {
+static void gemm_launch(const GemmPlan& p, hipStream_t stream, const uint16_t* a, int m, int k,
+                        const uint16_t* w, float* c, int n, size_t split_stride) {
     constexpr int PF = 4;
+    dim3 grid(p.col_blocks, p.splits, p.row_blocks);
     hipLaunchKernelGGL((gemm_kernel<WM, WN, WAVES_M, WAVES_N, PF, HL>), grid, dim3(WAVES_M * WAVES_N * 64), 0,
-                       stream, a, m, k, (const bf16x8*)w, KT, NT, c, n, kt_per_split, split_stride);
+                       stream, a, m, k, (const bf16x8*)w, p.KT, p.NT, c, n, p.kt_per_split, split_stride);
+}
+
+template <int WM, int WN, int WAVES_M, int WAVES_N, int STAGES, int HL>
+static void gemm_dma_launch(const GemmPlan& p, hipStream_t stream, const uint16_t* a, int m, int k,
+                            const uint16_t* w, float* c, int n, size_t split_stride) {
+    const int groups = p.col_blocks * p.splits;
+    const unsigned blocks = 8u * (unsigned)p.row_blocks * (unsigned)((groups + 7) / 8);
+    hipLaunchKernelGGL((gemm_dma_kernel<WM, WN, WAVES_M, WAVES_N, HL, STAGES>), dim3(blocks),
+                       dim3(WAVES_M * WAVES_N * 64), 0, stream, a, m, k, (const bf16x8*)w, p.KT, p.NT, c, n,
+                       p.kt_per_split, p.splits, p.row_blocks, p.col_blocks, split_stride);
 }
 
 zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_packed, float* c_f32,
                       uint16_t* c_bf16, int m, int n, int k, int epilogue) {
     if (m <= 0) return ZR_OK;
-    if (k % 8 != 0) return set_err(ctx, ZR_E_UNSUPPORTED, "GEMM K=%d must be a multiple of 8", k);
+    if (k % 8 != 0 || k < 8) return set_err(ctx, ZR_E_UNSUPPORTED, "GEMM K=%d must be a multiple of 8", k);
     const GemmPlan p = gemm_plan(m, n, k, epilogue);
     const GemmCfg cfg = pick_cfg(m, n);
     const bool direct = p.direct && c_f32 && !c_bf16;
@@ -347,24 +507,39 @@ zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_pack
         return set_err(ctx, ZR_E_OOM, "split-K workspace too small (%d x %d x %d)", p.splits, m, n);
     float* dst = direct ? c_f32 : ctx->splitk_ws;
     const bool split_act = (ctx->desc.flags & ZR_FLAG_SPLIT_ACTIVATIONS) != 0;
-    dim3 grid(p.col_blocks, p.splits, p.row_blocks);
     hipEvent_t ev;
     timing_mark_begin(ctx, kClassGemm, &ev);
-#define ZR_GEMM_CASE(WMV, WNV, WAM, WAN)                                                                       \
-    if (cfg.wm == WMV && cfg.wn == WNV && cfg.waves_m == WAM && cfg.waves_n == WAN) {                          \
-        if (split_act)                                                                                         \
-            gemm_launch<WMV, WNV, WAM, WAN, 2>(grid, ctx->stream, a, m, k, w_packed, p.KT, p.NT, dst, n,      \
-                                               p.kt_per_split, split_stride);                                  \
-        else                                                                                                   \
-            gemm_launch<WMV, WNV, WAM, WAN, 1>(grid, ctx->stream, a, m, k, w_packed, p.KT, p.NT, dst, n,      \
-                                               p.kt_per_split, split_stride);                                  \
+    bool launched = false;
+#define ZR_GEMM_CASE(WMV, WNV, WAM, WAN)                                                              \
+    if (!launched && cfg.family == 0 && cfg.wm == WMV && cfg.wn == WNV && cfg.waves_m == WAM &&        \
+        cfg.waves_n == WAN) {                                                                         \
+        if (split_act)                                                                                \
+            gemm_launch<WMV, WNV, WAM, WAN, 2>(p, ctx->stream, a, m, k, w_packed, dst, n, split_stride); \
+        else                                                                                          \
+            gemm_launch<WMV, WNV, WAM, WAN, 1>(p, ctx->stream, a, m, k, w_packed, dst, n, split_stride); \
+        launched = true;                                                                              \
+    }
+#define ZR_GEMM_DMA_CASE(WMV, WNV, WAM, WAN, ST)                                                      \
+    if (!launched && cfg.family == 1 && cfg.wm == WMV && cfg.wn == WNV && cfg.waves_m == WAM &&        \
+        cfg.waves_n == WAN && cfg.stages == ST) {                                                     \
+        if (split_act)                                                                                \
+            gemm_dma_launch<WMV, WNV, WAM, WAN, ST, 2>(p, ctx->stream, a, m, k, w_packed, dst, n,      \
+                                                       split_stride);                                 \
+        else                                                                                          \
+            gemm_dma_launch<WMV, WNV, WAM, WAN, ST, 1>(p, ctx->stream, a, m, k, w_packed, dst, n,      \
+                                                       split_stride);                                 \
+        launched = true;                                                                              \
     }
     ZR_GEMM_CASE(1, 2, 1, 8)
     ZR_GEMM_CASE(2, 2, 1, 8)
     ZR_GEMM_CASE(4, 2, 1, 8)
     ZR_GEMM_CASE(4, 4, 2, 4)
     ZR_GEMM_CASE(8, 4, 2, 4)
+    ZR_GEMM_DMA_CASE(4, 4, 2, 4, 3)
+    ZR_GEMM_DMA_CASE(4, 8, 2, 2, 2)
 #undef ZR_GEMM_CASE
+#undef ZR_GEMM_DMA_CASE
+    if (!launched) return set_err(ctx, ZR_E_INVARIANT, "no GEMM kernel for the selected tile configuration");
     ZR_LAUNCH_CHECK(ctx);
     timing_mark_end(ctx, kClassGemm, ev);
     if (!direct) {
