@@ -207,6 +207,11 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     st->h_tiles.push_back(make_int4(0, 0, 0, (int)st->h_items.size()));  // sentinel
     st->n_tiles = (int)st->h_tiles.size() - 1;
     st->n_attn_items = (int)st->h_items.size();
+    // tiles whose splits need the merge kernel
+    st->h_merge.clear();
+    for (int t = 0; t < st->n_tiles; ++t)
+        if (st->h_tiles[t + 1].w - st->h_tiles[t].w > 1) st->h_merge.push_back(t);
+    st->n_merge = (int)st->h_merge.size();
 
     const size_t need_part = (size_t)st->n_attn_items * ctx->local_kv_heads * 16 * (ctx->head_dim + 2);
     if (need_part > ctx->attn_part_floats) {
@@ -228,6 +233,7 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     const size_t o_qlen = take(4 * S), o_kvb = take(4 * S), o_fpos = take(4 * S), o_foff = take(4 * S);
     const size_t o_bt = take(4 * (size_t)S * stride), o_tok = take(4 * (size_t)std::max(total_q, 1));
     const size_t o_items = take(16 * (size_t)st->n_attn_items), o_tiles = take(16 * st->h_tiles.size());
+    const size_t o_merge = take(4 * (size_t)std::max(st->n_merge, 1));
     const size_t host_bytes = off;
     const size_t o_cuq = take(4 * (S + 1)), o_cuk = take(4 * (S + 1)), o_pos = take(4 * (size_t)total_q);
     const size_t o_slot = take(4 * (size_t)total_q), o_seq = take(4 * (size_t)total_q), o_last = take(4 * S);
@@ -251,6 +257,7 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     if (mb->tokens) memcpy(hb + o_tok, mb->tokens, 4 * (size_t)total_q);
     memcpy(hb + o_items, st->h_items.data(), 16 * (size_t)st->n_attn_items);
     memcpy(hb + o_tiles, st->h_tiles.data(), 16 * st->h_tiles.size());
+    if (st->n_merge) memcpy(hb + o_merge, st->h_merge.data(), 4 * (size_t)st->n_merge);
     unsigned char* db = (unsigned char*)st->dev;
     st->q_len = (int*)(db + o_qlen);
     st->kv_before = (int*)(db + o_kvb);
@@ -260,6 +267,7 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     st->tokens = (uint32_t*)(db + o_tok);
     st->attn_items = (int4*)(db + o_items);
     st->attn_tiles = (int4*)(db + o_tiles);
+    st->merge_tiles = (int*)(db + o_merge);
     st->cu_q = (int*)(db + o_cuq);
     st->cu_k = (int*)(db + o_cuk);
     st->positions = (int*)(db + o_pos);
@@ -292,31 +300,40 @@ static zr_status run_forward(zr_context* ctx, StagedMeta* st, const uint32_t* d_
     const int QKV = ctx->q_cols + 2 * ctx->kv_cols;
     if ((rc = launch_embed(ctx, st, d_tokens ? d_tokens : st->tokens))) return rc;
     const int lo = (d.flags & ZR_FLAG_SPLIT_ACTIVATIONS) ? 1 : 0;
+    // split-K products are left as slabs for the next kernel to sum, except
+    // where the caller asked for the per-layer partials (those are copied out)
+    Slabs down(nullptr);
     for (int l = 0; l < d.num_layers; ++l) {
         const LayerDev& L = ctx->layers[l];
+        Slabs* defer = h_partials ? nullptr : &down;
         // hidden += previous down partial; xa = rms_norm(hidden) * attn_norm
-        if ((rc = launch_rms_norm(ctx, ctx->hidden, l > 0 ? ctx->proj : nullptr, ctx->hidden, L.attn_norm, nullptr,
+        if ((rc = launch_rms_norm(ctx, ctx->hidden, l > 0 ? down : Slabs(nullptr), ctx->hidden, L.attn_norm, nullptr,
                                   ctx->xa, lo, nullptr, T, H)))
             return rc;
-        if ((rc = launch_gemm(ctx, ctx->xa, L.w_qkv, ctx->qkv, nullptr, T, QKV, H, kEpiStore))) return rc;
-        if ((rc = launch_rope_kv_write(ctx, st, l, ctx->qkv, ctx->q_rope, 1))) return rc;
+        Slabs qkv(ctx->qkv);
+        if ((rc = launch_gemm(ctx, ctx->xa, L.w_qkv, ctx->qkv, nullptr, T, QKV, H, kEpiStore, &qkv))) return rc;
+        if ((rc = launch_rope_kv_write(ctx, st, l, qkv, ctx->q_rope, 1))) return rc;
         if ((rc = launch_attention(ctx, st, l, ctx->q_rope, nullptr, ctx->attn_a))) return rc;
-        if ((rc = launch_gemm(ctx, ctx->attn_a, L.w_o, ctx->proj, nullptr, T, H, ctx->q_cols, kEpiStore))) return rc;
+        Slabs o(ctx->proj);
+        if ((rc = launch_gemm(ctx, ctx->attn_a, L.w_o, ctx->proj, nullptr, T, H, ctx->q_cols, kEpiStore,
+                              h_partials ? nullptr : &o)))
+            return rc;
         if (h_partials)
             ZR_HIP(ctx, hipMemcpyAsync(h_partials + ((size_t)l * 2 + 0) * T * H, ctx->proj, sizeof(float) * T * H,
                                        hipMemcpyDeviceToHost, ctx->stream));
         // post_attn = hidden + o_partial (identity all-reduce at one worker)
-        if ((rc = launch_rms_norm(ctx, ctx->hidden, ctx->proj, ctx->hidden, L.mlp_norm, nullptr, ctx->xa, lo, nullptr,
+        if ((rc = launch_rms_norm(ctx, ctx->hidden, o, ctx->hidden, L.mlp_norm, nullptr, ctx->xa, lo, nullptr,
                                   T, H)))
             return rc;
         if ((rc = launch_gemm(ctx, ctx->xa, L.w_gate_up, nullptr, ctx->ffn_a, T, 2 * F, H, kEpiSwiGLU))) return rc;
-        if ((rc = launch_gemm(ctx, ctx->ffn_a, L.w_down, ctx->proj, nullptr, T, H, F, kEpiStore))) return rc;
+        down = Slabs(ctx->proj);
+        if ((rc = launch_gemm(ctx, ctx->ffn_a, L.w_down, ctx->proj, nullptr, T, H, F, kEpiStore, defer))) return rc;
         if (h_partials)
             ZR_HIP(ctx, hipMemcpyAsync(h_partials + ((size_t)l * 2 + 1) * T * H, ctx->proj, sizeof(float) * T * H,
                                        hipMemcpyDeviceToHost, ctx->stream));
     }
     // final residual + norm on the last row of every sequence, LM head, argmax
-    if ((rc = launch_rms_norm(ctx, ctx->hidden, ctx->proj, ctx->hidden, ctx->final_norm, nullptr, ctx->final_a, lo,
+    if ((rc = launch_rms_norm(ctx, ctx->hidden, down, ctx->hidden, ctx->final_norm, nullptr, ctx->final_a, lo,
                               st->last_rows, S, H)))
         return rc;
     float* logits = ctx->logits;

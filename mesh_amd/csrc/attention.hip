@@ -13,7 +13,7 @@
 //            once and serves all of them (the reference instead materialises
 //            a GQA-expanded copy per q head, forward_pass.rs:783-828).
 //   split  = pages [page_begin, page_end) of the tile's visible window.
-// Each split writes (m, l, o[d]) per column; attention_reduce merges splits.
+// Each split writes (m, l, o[d]) per column; attention_merge_kernel merges splits.
 //
 // Per page (16 tokens), with lane l, column c = l % 16, quad q4 = l / 16:
 //   S^T[t][c] = sum_d K[t][d] Q[c][d]     mfma 16x16x32 bf16, K as A operand
@@ -320,57 +320,106 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
 }
 
 // Merge the splits of one (tile, kv head) with more than one split:
-// o = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
+// o = sum_s o_s w_s with w_s = 2^(m_s - M) / sum_r l_r 2^(m_r - M), M the
+// max over splits (m in log2 units).  The weights of up to kChunk splits are
+// computed once per chunk into LDS; each thread then accumulates fixed
+// output elements, consecutive threads reading consecutive columns.
 template <int D>
-__global__ __launch_bounds__(256) void attention_reduce_kernel(const float* __restrict__ part,
-                                                               const int4* __restrict__ tiles,
-                                                               const int* __restrict__ cu_q, int G,
-                                                               int kv_heads, int q_cols,
-                                                               float* __restrict__ out,
-                                                               uint16_t* __restrict__ out_bf16,
-                                                               size_t lo_offset) {
+__global__ __launch_bounds__(256) void attention_merge_kernel(const float* __restrict__ part,
+                                                              const int4* __restrict__ tiles,
+                                                              const int* __restrict__ merge_tiles,
+                                                              const int* __restrict__ cu_q, int G, int kv_heads,
+                                                              int q_cols, float* __restrict__ out,
+                                                              uint16_t* __restrict__ out_bf16, size_t lo_offset) {
+    constexpr int kChunk = 64;
+    constexpr int kPer = 16 * D / 256;  // output elements per thread (16 columns max)
+    __shared__ float sw[kChunk][16];
+    __shared__ float sred[16][16];
     __shared__ float sM[16], sLinv[16];
-    const int tile = blockIdx.x, kvh = blockIdx.y;
+    const int tile = merge_tiles[blockIdx.x], kvh = blockIdx.y;
     const int4 tl = tiles[tile];
     const int seq = tl.x, q0 = tl.y, nq = tl.z, first = tl.w;
     const int nparts = tiles[tile + 1].w - first;
-    if (nparts <= 1) return;  // written by the attention kernel
     const int ncols = min(nq, 16 / G) * G;
     const size_t pstride = (size_t)kv_heads * 16 * (D + 2);
     const float* base = part + ((size_t)first * kv_heads + kvh) * 16 * (D + 2);
-    if (threadIdx.x < ncols) {
-        const int c = threadIdx.x;
+    const int tid = threadIdx.x;
+    // column max over splits: 16 threads per column
+    {
+        const int c = tid & 15, pl = tid >> 4;
         float M = -INFINITY;
-        for (int s = 0; s < nparts; ++s) M = fmaxf(M, base[s * pstride + (size_t)c * (D + 2)]);
+        if (c < ncols)
+            for (int s = pl; s < nparts; s += 16) M = fmaxf(M, base[s * pstride + (size_t)c * (D + 2)]);
+        sred[pl][c] = M;
+        __syncthreads();
+        if (tid < 16) {
+            float m = sred[0][tid];
+#pragma unroll
+            for (int i = 1; i < 16; ++i) m = fmaxf(m, sred[i][tid]);
+            sM[tid] = m;
+        }
+        __syncthreads();
+        const float Mc = sM[c];
         float L = 0.0f;
-        for (int s = 0; s < nparts; ++s) {
-            const float* ps = base + s * pstride + (size_t)c * (D + 2);
-            if (ps[0] != -INFINITY) L += ps[1] * exp2f(ps[0] - M);
+        if (c < ncols)
+            for (int s = pl; s < nparts; s += 16) {
+                const float* ps = base + s * pstride + (size_t)c * (D + 2);
+                const float mv = ps[0];
+                if (mv != -INFINITY) L += ps[1] * exp2f(mv - Mc);
+            }
+        sred[pl][c] = L;
+        __syncthreads();
+        if (tid < 16) {
+            float l = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) l += sred[i][tid];
+            sLinv[tid] = 1.0f / l;
         }
-        sM[c] = M;
-        sLinv[c] = 1.0f / L;
+        __syncthreads();
     }
-    __syncthreads();
-    for (int e = threadIdx.x; e < ncols * D; e += blockDim.x) {
-        const int c = e / D, d = e - c * D;
-        const float M = sM[c];
-        float acc = 0.0f;
-        for (int s = 0; s < nparts; ++s) {
-            const float* ps = base + s * pstride + (size_t)c * (D + 2);
-            const float mv = ps[0];
-            if (mv != -INFINITY) acc += ps[2 + d] * exp2f(mv - M);
+    float acc[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) acc[j] = 0.0f;
+    for (int s0 = 0; s0 < nparts; s0 += kChunk) {
+        const int ns = min(kChunk, nparts - s0);
+        for (int t = tid; t < ns * 16; t += 256) {
+            const int s = t >> 4, c = t & 15;
+            float w = 0.0f;
+            if (c < ncols) {
+                const float mv = base[(s0 + s) * pstride + (size_t)c * (D + 2)];
+                if (mv != -INFINITY) w = exp2f(mv - sM[c]) * sLinv[c];
+            }
+            sw[s][c] = w;
         }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int e = tid + j * 256;
+            const int c = e / D, d = e - c * D;
+            if (c < ncols) {
+                const float* ps = base + (size_t)s0 * pstride + (size_t)c * (D + 2) + 2 + d;
+                float v = acc[j];
+                for (int s = 0; s < ns; ++s) v += ps[s * pstride] * sw[s][c];
+                acc[j] = v;
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int e = tid + j * 256;
+        const int c = e / D, d = e - c * D;
+        if (c >= ncols) continue;
         const int qi = c / G, g = c - qi * G;
         const int row = cu_q[seq] + q0 + qi;
         const size_t o = (size_t)row * q_cols + (size_t)(kvh * G + g) * D + d;
-        const float v = acc * sLinv[c];
         if (out_bf16) {
             uint16_t hi, lo;
-            split_bf16(v, hi, lo);
+            split_bf16(acc[j], hi, lo);
             out_bf16[o] = hi;
             if (lo_offset) out_bf16[lo_offset + o] = lo;
         } else {
-            out[o] = v;
+            out[o] = acc[j];
         }
     }
 }
@@ -403,13 +452,14 @@ static zr_status launch_attn_t(zr_context* ctx, StagedMeta* st, int layer, const
                        dim3(64), 0, ctx->stream, a);
     ZR_LAUNCH_CHECK(ctx);
     timing_mark_end(ctx, kClassAttention, ev);
-    timing_mark_begin(ctx, kClassOther, &ev);
-    hipLaunchKernelGGL((attention_reduce_kernel<D>), dim3(st->n_tiles, ctx->local_kv_heads), dim3(256), 0,
-                       ctx->stream, ctx->attn_part, st->attn_tiles, st->cu_q, ctx->q_per_kv,
-                       ctx->local_kv_heads, ctx->q_cols, out, out_bf16,
-                       (ctx->desc.flags & ZR_FLAG_SPLIT_ACTIVATIONS) ? (size_t)st->total_q * ctx->q_cols : 0);
-    ZR_LAUNCH_CHECK(ctx);
-    timing_mark_end(ctx, kClassOther, ev);
+    if (st->n_merge > 0) {
+        timing_mark_begin(ctx, kClassOther, &ev);
+        hipLaunchKernelGGL((attention_merge_kernel<D>), dim3(st->n_merge, ctx->local_kv_heads), dim3(256), 0,
+                           ctx->stream, ctx->attn_part, st->attn_tiles, st->merge_tiles, st->cu_q, ctx->q_per_kv,
+                           ctx->local_kv_heads, ctx->q_cols, out, out_bf16, a.out_lo_offset);
+        ZR_LAUNCH_CHECK(ctx);
+        timing_mark_end(ctx, kClassOther, ev);
+    }
     return ZR_OK;
 }
 

@@ -496,7 +496,9 @@ static void gemm_dma_launch(const GemmPlan& p, hipStream_t stream, const uint16_
 }
 
 zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_packed, float* c_f32,
-                      uint16_t* c_bf16, int m, int n, int k, int epilogue) {
+                      uint16_t* c_bf16, int m, int n, int k, int epilogue, Slabs* deferred) {
+    if (deferred && (epilogue != kEpiStore || !c_f32 || c_bf16))
+        return set_err(ctx, ZR_E_INVARIANT, "deferred split-K needs an f32 store epilogue");
     if (m <= 0) return ZR_OK;
     if (k % 8 != 0 || k < 8) return set_err(ctx, ZR_E_UNSUPPORTED, "GEMM K=%d must be a multiple of 8", k);
     const GemmPlan p = gemm_plan(m, n, k, epilogue);
@@ -542,6 +544,10 @@ zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_pack
     if (!launched) return set_err(ctx, ZR_E_INVARIANT, "no GEMM kernel for the selected tile configuration");
     ZR_LAUNCH_CHECK(ctx);
     timing_mark_end(ctx, kClassGemm, ev);
+    if (deferred) {
+        *deferred = direct ? Slabs(c_f32) : Slabs(ctx->splitk_ws, p.splits, split_stride);
+        return ZR_OK;
+    }
     if (!direct) {
         timing_mark_begin(ctx, kClassOther, &ev);
         const size_t n_out = epilogue == kEpiSwiGLU ? (size_t)n / 2 : (size_t)n;

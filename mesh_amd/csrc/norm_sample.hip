@@ -31,12 +31,20 @@ zr_status launch_embed(zr_context* ctx, StagedMeta* st, const uint32_t* d_tokens
 }
 
 // y = rms_norm(x (+ residual)) * gamma (tensor_ops.rs:285-304,
-// runtime.rs:919-925).  With residual_in, x_out = x + residual_in is written
-// first (the broadcast_add of forward_pass.rs:2279 / 2304).  row_index
-// selects source rows (e.g. the last token of every sequence for the LM head).
+// runtime.rs:919-925).  With a residual, x_out = x + residual is written
+// first (the broadcast_add of forward_pass.rs:2279 / 2304); the residual may
+// arrive as res_n split-K slabs res_stride floats apart, summed in slab order
+// (the same sum the split-K reduce forms).  row_index selects source rows
+// (the last token of every sequence for the LM head).
+__device__ inline float sum_slabs(const float* p, size_t i, int n, size_t stride) {
+    float v = p[i];
+    for (int s = 1; s < n; ++s) v += p[s * stride + i];
+    return v;
+}
+
 __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__ x,
-                                                       const float* __restrict__ residual_in,
-                                                       float* __restrict__ x_out,
+                                                       const float* __restrict__ residual_in, int res_n,
+                                                       size_t res_stride, float* __restrict__ x_out,
                                                        const float* __restrict__ gamma,
                                                        float* __restrict__ y_f32,
                                                        uint16_t* __restrict__ y_bf16, int split_lo,
@@ -47,13 +55,12 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__
     const int r = blockIdx.x;
     const int src = row_index ? row_index[r] : r;
     const float* xr = x + (size_t)src * cols;
-    const float* rr = residual_in ? residual_in + (size_t)src * cols : nullptr;
     float* xo = x_out ? x_out + (size_t)src * cols : nullptr;
     float ss = 0.0f;
     for (int i = threadIdx.x; i < cols; i += blockDim.x) {
         float v = xr[i];
-        if (rr) {
-            v = v + rr[i];
+        if (residual_in) {
+            v = v + sum_slabs(residual_in, (size_t)src * cols + i, res_n, res_stride);
             xo[i] = v;
         }
         ss += v * v;
@@ -63,7 +70,7 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__
     __syncthreads();
     const float total = red[0] + red[1] + red[2] + red[3];
     const float inv_rms = 1.0f / sqrtf(total / (float)cols + eps);
-    const float* xs = rr ? xo : xr;
+    const float* xs = residual_in ? xo : xr;
     for (int i = threadIdx.x; i < cols; i += blockDim.x) {
         const float v = xs[i] * inv_rms * gamma[i];
         if (y_bf16) {
@@ -77,14 +84,111 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__
     }
 }
 
-zr_status launch_rms_norm(zr_context* ctx, const float* x, const float* residual_in, float* x_out,
+// Same contract for cols % 4 == 0 and cols <= 4 NT NV: every thread of the
+// NT-thread block keeps its NV float4 of the row in registers, so the row is
+// read once.
+template <int NV, int NT>
+__global__ __launch_bounds__(NT) void rms_norm_vec_kernel(const float* __restrict__ x,
+                                                           const float* __restrict__ residual_in, int res_n,
+                                                           size_t res_stride, float* __restrict__ x_out,
+                                                           const float* __restrict__ gamma,
+                                                           float* __restrict__ y_f32,
+                                                           uint16_t* __restrict__ y_bf16, int split_lo,
+                                                           size_t lo_offset,
+                                                           const int* __restrict__ row_index, int cols,
+                                                           float eps) {
+    __shared__ float red[NT / 64];
+    const int r = blockIdx.x;
+    const int src = row_index ? row_index[r] : r;
+    const int n4 = cols >> 2;
+    const size_t base = (size_t)src * cols;
+    float4 v[NV];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int i4 = threadIdx.x + j * NT;
+        if (i4 < n4) {
+            float4 a = *(const float4*)(x + base + 4 * (size_t)i4);
+            if (residual_in) {
+                float4 rr = *(const float4*)(residual_in + base + 4 * (size_t)i4);
+#pragma unroll 4
+                for (int s = 1; s < res_n; ++s) {
+                    const float4 q = *(const float4*)(residual_in + s * res_stride + base + 4 * (size_t)i4);
+                    rr.x += q.x;
+                    rr.y += q.y;
+                    rr.z += q.z;
+                    rr.w += q.w;
+                }
+                a.x = a.x + rr.x;
+                a.y = a.y + rr.y;
+                a.z = a.z + rr.z;
+                a.w = a.w + rr.w;
+                *(float4*)(x_out + base + 4 * (size_t)i4) = a;
+            }
+            v[j] = a;
+            ss += a.x * a.x;
+            ss += a.y * a.y;
+            ss += a.z * a.z;
+            ss += a.w * a.w;
+        }
+    }
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float total = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NT / 64; ++w) total += red[w];
+    const float inv_rms = 1.0f / sqrtf(total / (float)cols + eps);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int i4 = threadIdx.x + j * NT;
+        if (i4 >= n4) continue;
+        const float4 g = *(const float4*)(gamma + 4 * (size_t)i4);
+        float y[4] = {v[j].x * inv_rms * g.x, v[j].y * inv_rms * g.y, v[j].z * inv_rms * g.z,
+                      v[j].w * inv_rms * g.w};
+        const size_t o = (size_t)r * cols + 4 * (size_t)i4;
+        if (y_bf16) {
+            ushort4 hi, lo;
+            split_bf16(y[0], hi.x, lo.x);
+            split_bf16(y[1], hi.y, lo.y);
+            split_bf16(y[2], hi.z, lo.z);
+            split_bf16(y[3], hi.w, lo.w);
+            *(ushort4*)(y_bf16 + o) = hi;
+            if (split_lo) *(ushort4*)(y_bf16 + lo_offset + o) = lo;
+        } else {
+            *(float4*)(y_f32 + o) = make_float4(y[0], y[1], y[2], y[3]);
+        }
+    }
+}
+
+zr_status launch_rms_norm(zr_context* ctx, const float* x, const Slabs& residual, float* x_out,
                           const float* gamma, float* y_f32, uint16_t* y_bf16, int split_lo,
                           const int* row_index, int rows, int cols) {
     if (rows <= 0) return ZR_OK;
     hipEvent_t ev;
     timing_mark_begin(ctx, kClassNormRopeKv, &ev);
-    hipLaunchKernelGGL(rms_norm_kernel, dim3(rows), dim3(256), 0, ctx->stream, x, residual_in, x_out, gamma,
-                       y_f32, y_bf16, split_lo, (size_t)rows * cols, row_index, cols, ctx->desc.rms_norm_eps);
+    const size_t lo_off = (size_t)rows * cols;
+    // few rows: 1024-thread blocks so that each row's loads spread wider
+    const bool vec = cols % 4 == 0;
+    const int nv1024 = (cols + 4095) / 4096, nv256 = (cols + 1023) / 1024;
+#define ZR_RMS_ARGS                                                                                     \
+    x, residual.ptr, residual.n, residual.stride, x_out, gamma, y_f32, y_bf16, split_lo, lo_off, row_index, \
+        cols, ctx->desc.rms_norm_eps
+    if (vec && rows < 128 && nv1024 == 1)
+        hipLaunchKernelGGL((rms_norm_vec_kernel<1, 1024>), dim3(rows), dim3(1024), 0, ctx->stream, ZR_RMS_ARGS);
+    else if (vec && rows < 128 && nv1024 == 2)
+        hipLaunchKernelGGL((rms_norm_vec_kernel<2, 1024>), dim3(rows), dim3(1024), 0, ctx->stream, ZR_RMS_ARGS);
+    else if (vec && nv256 == 1)
+        hipLaunchKernelGGL((rms_norm_vec_kernel<1, 256>), dim3(rows), dim3(256), 0, ctx->stream, ZR_RMS_ARGS);
+    else if (vec && nv256 == 2)
+        hipLaunchKernelGGL((rms_norm_vec_kernel<2, 256>), dim3(rows), dim3(256), 0, ctx->stream, ZR_RMS_ARGS);
+    else if (vec && nv256 <= 4)
+        hipLaunchKernelGGL((rms_norm_vec_kernel<4, 256>), dim3(rows), dim3(256), 0, ctx->stream, ZR_RMS_ARGS);
+    else if (vec && nv256 <= 8)
+        hipLaunchKernelGGL((rms_norm_vec_kernel<8, 256>), dim3(rows), dim3(256), 0, ctx->stream, ZR_RMS_ARGS);
+    else
+        hipLaunchKernelGGL(rms_norm_kernel, dim3(rows), dim3(256), 0, ctx->stream, ZR_RMS_ARGS);
+#undef ZR_RMS_ARGS
     ZR_LAUNCH_CHECK(ctx);
     timing_mark_end(ctx, kClassNormRopeKv, ev);
     return ZR_OK;

@@ -102,7 +102,8 @@ zr_status launch_pack(zr_context* ctx, StagedMeta* st) {
 // slot the host reserved.
 template <typename KV>
 __global__ __launch_bounds__(256) void rope_kv_write_kernel(
-    const float* __restrict__ qkv, int qkv_stride, float* __restrict__ q_out, int q_cols, int kv_cols,
+    const float* __restrict__ qkv, int qkv_n, size_t qkv_slab, int qkv_stride, float* __restrict__ q_out,
+    int q_cols, int kv_cols,
     int D, const int* __restrict__ positions, const int* __restrict__ slot,
     const float* __restrict__ inv_freq, KV* __restrict__ layer_pool, size_t page_elems, int rope) {
 #pragma clang fp contract(off)
@@ -117,13 +118,18 @@ __global__ __launch_bounds__(256) void rope_kv_write_kernel(
     KV* vpage = kpage + (size_t)kv_heads * kPageRows * D;
     // q: q_cols / 2 rotation pairs, k: kv_cols / 2 pairs, v: kv_cols copies
     const int nq = q_cols / 2, nk = kv_cols / 2;
-    for (int j = threadIdx.x; j < nq + nk + kv_cols; j += blockDim.x) {
+    for (int j = blockIdx.y * blockDim.x + threadIdx.x; j < nq + nk + kv_cols; j += gridDim.y * blockDim.x) {
         if (j < nq + nk) {
             const bool is_q = j < nq;
             const int jj = is_q ? j : j - nq;
             const int head = jj / half, i = jj % half;
             const float* src = row + (is_q ? 0 : q_cols) + head * D;
             float a = src[i], b = src[i + half];
+#pragma unroll 4
+            for (int sl = 1; sl < qkv_n; ++sl) {
+                a += src[sl * qkv_slab + i];
+                b += src[sl * qkv_slab + i + half];
+            }
             if (rope) {
                 const float theta = pos * inv_freq[i];
                 const float c = cosf(theta), sn = sinf(theta);
@@ -144,7 +150,10 @@ __global__ __launch_bounds__(256) void rope_kv_write_kernel(
             const int c = j - nq - nk;
             const int head = c / D, d = c % D;
             KV* vt = vpage + (size_t)head * kPageRows * D;
-            store_elem(vt + v_off(r, d, D), row[q_cols + kv_cols + c]);
+            float vv = row[q_cols + kv_cols + c];
+#pragma unroll 4
+            for (int sl = 1; sl < qkv_n; ++sl) vv += row[sl * qkv_slab + q_cols + kv_cols + c];
+            store_elem(vt + v_off(r, d, D), vv);
         }
     }
 }
@@ -153,22 +162,25 @@ static inline size_t page_elems_of(const zr_context* ctx) {
     return (size_t)2 * ctx->kv_cols * kPageRows;
 }
 
-zr_status launch_rope_kv_write(zr_context* ctx, StagedMeta* st, int layer, const float* qkv,
+zr_status launch_rope_kv_write(zr_context* ctx, StagedMeta* st, int layer, const Slabs& qkv,
                                float* q_out, int rope) {
     if (st->total_q == 0) return ZR_OK;
     const size_t pe = page_elems_of(ctx);
     const int stride = ctx->q_cols + 2 * ctx->kv_cols;
+    // one thread per rotation pair / V element: q_cols / 2 + kv_cols / 2 + kv_cols per token
+    const int items = ctx->q_cols / 2 + ctx->kv_cols / 2 + ctx->kv_cols;
+    const dim3 grid(st->total_q, (items + 255) / 256);
     hipEvent_t ev;
     timing_mark_begin(ctx, kClassNormRopeKv, &ev);
     if (ctx->desc.kv_dtype == ZR_DTYPE_BF16) {
         uint16_t* pool = (uint16_t*)ctx->kv_pool + (size_t)layer * ctx->n_pages * pe;
-        hipLaunchKernelGGL(rope_kv_write_kernel<uint16_t>, dim3(st->total_q), dim3(256), 0, ctx->stream,
-                           qkv, stride, q_out, ctx->q_cols, ctx->kv_cols, ctx->head_dim, st->positions,
+        hipLaunchKernelGGL(rope_kv_write_kernel<uint16_t>, grid, dim3(256), 0, ctx->stream,
+                           qkv.ptr, qkv.n, qkv.stride, stride, q_out, ctx->q_cols, ctx->kv_cols, ctx->head_dim, st->positions,
                            st->slot_mapping, ctx->inv_freq, pool, pe, rope);
     } else {
         float* pool = (float*)ctx->kv_pool + (size_t)layer * ctx->n_pages * pe;
-        hipLaunchKernelGGL(rope_kv_write_kernel<float>, dim3(st->total_q), dim3(256), 0, ctx->stream,
-                           qkv, stride, q_out, ctx->q_cols, ctx->kv_cols, ctx->head_dim, st->positions,
+        hipLaunchKernelGGL(rope_kv_write_kernel<float>, grid, dim3(256), 0, ctx->stream,
+                           qkv.ptr, qkv.n, qkv.stride, stride, q_out, ctx->q_cols, ctx->kv_cols, ctx->head_dim, st->positions,
                            st->slot_mapping, ctx->inv_freq, pool, pe, rope);
     }
     ZR_LAUNCH_CHECK(ctx);

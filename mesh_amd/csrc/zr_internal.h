@@ -138,6 +138,7 @@ struct StagedMeta {
     int max_kv = 0;           // max kv_after over sequences
     int n_attn_items = 0;     // attention work items (per kv head)
     int n_tiles = 0;          // attention query tiles (per kv head)
+    int n_merge = 0;          // tiles with more than one split
     bool owns = true;
     // one device allocation holding every array below
     void* dev = nullptr;
@@ -158,15 +159,27 @@ struct StagedMeta {
     int4* attn_items = nullptr; // [n_attn_items] {tile, page_begin, page_end, part_index}
     int4* attn_tiles = nullptr; // [n_tiles] {seq, q0, nq, first_part}
     int* tile_nparts = nullptr; // [n_tiles]
+    int* merge_tiles = nullptr; // [n_merge] tiles the merge kernel combines
     // host copies
     std::vector<int> h_q_len, h_kv_before, h_first_pos, h_first_offset, h_block_tables;
     std::vector<int4> h_items, h_tiles;
-    std::vector<int> h_tile_nparts;
+    std::vector<int> h_tile_nparts, h_merge;
     std::vector<uint32_t> h_tokens;
     std::vector<unsigned char> h_blob;
 };
 
 zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta* st);
+
+// An f32 [rows, cols] operand held as n split-K slabs `stride` floats apart;
+// readers sum the slabs in order (n = 1: a plain array).
+struct Slabs {
+    const float* ptr = nullptr;
+    int n = 1;
+    size_t stride = 0;
+    Slabs() = default;
+    Slabs(const float* p) : ptr(p) {}
+    Slabs(const float* p, int n_, size_t s) : ptr(p), n(n_), stride(s) {}
+};
 
 // Kernel launchers (one per .hip file) ------------------------------------
 zr_status launch_pack(zr_context* ctx, StagedMeta* st);
@@ -174,10 +187,10 @@ zr_status launch_embed(zr_context* ctx, StagedMeta* st, const uint32_t* d_tokens
 // y = rms_norm(x (+ residual_in)) * gamma.  With residual_in, x_out = x +
 // residual_in is written first.  Output as f32 (y_f32) or as the bf16 A operand
 // of the next GEMM (y_bf16: hi [rows, cols] then lo when split_lo).
-zr_status launch_rms_norm(zr_context* ctx, const float* x, const float* residual_in, float* x_out,
+zr_status launch_rms_norm(zr_context* ctx, const float* x, const Slabs& residual, float* x_out,
                           const float* gamma, float* y_f32, uint16_t* y_bf16, int split_lo,
                           const int* row_index, int rows, int cols);
-zr_status launch_rope_kv_write(zr_context* ctx, StagedMeta* st, int layer, const float* qkv,
+zr_status launch_rope_kv_write(zr_context* ctx, StagedMeta* st, int layer, const Slabs& qkv,
                                float* q_out, int rope);
 // out_f32 [T, q_cols] or out_bf16 (A operand of the O projection).
 zr_status launch_attention(zr_context* ctx, StagedMeta* st, int layer, const float* q, float* out_f32,
@@ -195,9 +208,12 @@ struct GemmPlan {
 };
 GemmPlan gemm_plan(int m, int n, int k, int epilogue);
 // C = A @ W (W packed, A bf16 operand).  kEpiStore writes c_f32; kEpiSwiGLU
-// writes silu(gate) * up as the bf16 operand c_bf16 (or f32 c_f32).
+// writes silu(gate) * up as the bf16 operand c_bf16 (or f32 c_f32).  With
+// `deferred` (kEpiStore only) a split-K product is left as its slabs in the
+// split-K workspace for the consumer to sum (valid until the next GEMM);
+// *deferred then describes C either way.
 zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_packed, float* c_f32,
-                      uint16_t* c_bf16, int m, int n, int k, int epilogue);
+                      uint16_t* c_bf16, int m, int n, int k, int epilogue, Slabs* deferred = nullptr);
 zr_status launch_to_bf16_pair(zr_context* ctx, const float* x, size_t n, uint16_t* out, int with_lo);
 zr_status pack_weight(zr_context* ctx, const uint16_t* src /* [K,N] host or device */,
                       int k, int n, uint16_t** out_packed);

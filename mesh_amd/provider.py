@@ -44,7 +44,7 @@ class ExecutionProviderKind(str, Enum):
 FUSED_KERNEL_STAGES = {
     "norm_qkv": ["rms_norm_kernel", "gemm_kernel"],
     "rope_kv_write": ["rope_kv_write_kernel"],
-    "paged_attention": ["paged_attention_kernel", "attention_reduce_kernel"],
+    "paged_attention": ["paged_attention_kernel", "attention_merge_kernel"],
     "residual_mlp": ["rms_norm_kernel", "gemm_kernel", "splitk_reduce_kernel"],
     "device_sampling": ["argmax_partial_kernel", "argmax_final_kernel"],
 }

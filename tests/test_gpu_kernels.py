@@ -258,14 +258,15 @@ def test_gemm_matches_fp64(split, m, k, n):
     ctx.close()
 
 
-def test_rms_norm_matches_oracle():
+@pytest.mark.parametrize("rows,cols", [(37, 4096), (200, 4096), (3, 2050), (5, 8192), (130, 64)])
+def test_rms_norm_matches_oracle(rows, cols):
     geo = ModelGeometry(hidden=256, num_heads=4, num_kv_heads=4, num_layers=1, vocab=64, ffn=256)
     ctx = DeviceContext(geo, kv_dtype="f32", max_tokens=16, max_seqs=4, max_pages_per_seq=4)
     rng = np.random.default_rng(3)
-    x = rng.standard_normal((37, 4096), dtype=np.float32) * 3
-    g = rng.standard_normal(4096, dtype=np.float32)
+    x = rng.standard_normal((rows, cols), dtype=np.float32) * 3
+    g = rng.standard_normal(cols, dtype=np.float32)
     d_x, d_g, d_y = DeviceBuffer.from_numpy(ctx, x), DeviceBuffer.from_numpy(ctx, g), DeviceBuffer(ctx, x.nbytes)
-    ctx.check(ctx.lib.zr_rms_norm(ctx.h, d_x.ptr, d_g.ptr, d_y.ptr, 37, 4096))
+    ctx.check(ctx.lib.zr_rms_norm(ctx.h, d_x.ptr, d_g.ptr, d_y.ptr, rows, cols))
     np.testing.assert_allclose(d_y.download(np.float32, x.shape), O.rms_norm(x, g, 1e-5), rtol=2e-6, atol=2e-6)
     ctx.close()
 
