@@ -161,10 +161,12 @@ class GpuDecodeBench:
         self.ctx.check(self.ctx.lib.zr_device_alloc(self.ctx.h, int(nbytes), C.byref(p)))
         return p.value
 
-    def run(self, first, count, timed):
+    def run(self, first, count, timed, mask=0xF):
+        """Runs staged steps [first, first + count); with `timed`, HIP events are
+        recorded around the launches of the kernel classes in `mask`."""
         ctx, lib = self.ctx, self.ctx.lib
         if timed:
-            ctx.check(lib.zr_timing_begin(ctx.h))
+            ctx.check(lib.zr_timing_begin(ctx.h, mask))
         ctx.check(lib.zr_synchronize(ctx.h))
         t0 = time.perf_counter()
         for i in range(first, first + count):
@@ -189,12 +191,19 @@ class GpuDecodeBench:
         self.ctx.close()
 
 
+BREAKDOWN_STEPS = 2
+
+
 def measure(name, steps, warmup):
-    bench = GpuDecodeBench(name, steps + warmup)
+    """Timed region: `steps` decode steps with HIP events around the attention
+    launches only (the roofline figure).  Then BREAKDOWN_STEPS more steps with
+    events around every kernel class, for the per-class time split."""
+    bench = GpuDecodeBench(name, steps + warmup + BREAKDOWN_STEPS)
     g, B = bench.geo, bench.B
     bench.run(0, warmup, timed=False)
-    dt, ms, n = bench.run(warmup, steps, timed=True)
+    dt, ms_t, n_t = bench.run(warmup, steps, timed=True, mask=1)
     toks = bench.tokens(warmup + steps)
+    _, ms_b, n_b = bench.run(warmup + steps, BREAKDOWN_STEPS, timed=True, mask=0xF)
     assert toks.max() < g.vocab
     ms_per_step = dt / steps * 1000.0
     # attention: algorithmic bytes per launch (K+V of every attended row, bf16;
@@ -202,12 +211,13 @@ def measure(name, steps, warmup):
     timed_rows = bench.kv_rows[warmup:warmup + steps]
     kv_bytes = sum(timed_rows) * g.num_layers * g.kv_cols * 2 * 2
     qo_bytes = steps * g.num_layers * B * g.q_cols * 4 * 2
-    attn_launches = n[0]
+    attn_launches = n_t[0]
     attn_bytes_per_launch = (kv_bytes + qo_bytes) / max(attn_launches, 1)
-    attn_ms_per_launch = ms[0] / max(attn_launches, 1)
+    attn_ms_per_launch = ms_t[0] / max(attn_launches, 1)
     attn_gbs = attn_bytes_per_launch / (attn_ms_per_launch * 1e-3) / 1e9
     sb = np.mean([step_bytes(g, B, r) for r in timed_rows])
-    gemm_tflops = gemm_flops(g, B) * steps / (ms[1] * 1e-3) / 1e12 if ms[1] > 0 else 0.0
+    nb = BREAKDOWN_STEPS
+    gemm_tflops = gemm_flops(g, B) * nb / (ms_b[1] * 1e-3) / 1e12 if ms_b[1] > 0 else 0.0
     roof_tps = B / (sb / (HBM_PEAK_GBS * 1e9))
     result = dict(
         workload=WORKLOADS[name]["desc"], batch=B, layers=g.num_layers,
@@ -215,13 +225,13 @@ def measure(name, steps, warmup):
         tokens_per_s=B / (ms_per_step / 1e3), ms_per_step=ms_per_step,
         step_bytes=float(sb), step_roofline_tokens_per_s=roof_tps,
         step_roofline_frac=(B / (ms_per_step / 1e3)) / roof_tps,
-        kernel_ms_per_step={"attention": ms[0] / steps, "gemm": ms[1] / steps, "norm_rope_kv": ms[2] / steps,
-                            "other": ms[3] / steps},
+        kernel_ms_per_step={"attention": ms_b[0] / nb, "gemm": ms_b[1] / nb, "norm_rope_kv": ms_b[2] / nb,
+                            "other": ms_b[3] / nb},
         attention=dict(launches=attn_launches, bytes_per_launch=attn_bytes_per_launch,
                        avg_ms=attn_ms_per_launch, achieved_gbs=attn_gbs, frac=attn_gbs / HBM_PEAK_GBS),
-        gemm=dict(launches=n[1] // steps, ms_per_step=ms[1] / steps, achieved_tflops=gemm_tflops,
+        gemm=dict(launches=n_b[1] // nb, ms_per_step=ms_b[1] / nb, achieved_tflops=gemm_tflops,
                   frac=gemm_tflops / MFMA_BF16_PEAK_TFLOPS,
-                  weight_gbs=(2 * gemm_flops(g, B) / (2 * B)) * steps / (ms[1] * 1e-3) / 1e9 if ms[1] > 0 else 0.0),
+                  weight_gbs=(gemm_flops(g, B) / B) * nb / (ms_b[1] * 1e-3) / 1e9 if ms_b[1] > 0 else 0.0),
     )
     bench.close()
     return result

@@ -94,7 +94,7 @@ SIGNATURES = [
     ("zr_memcpy_d2h", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]),
     ("zr_fill_normal_bf16", C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_uint64, C.c_float]),
     ("zr_kv_pool_fill_normal", C.c_int, [C.c_void_p, C.c_uint64, C.c_float]),
-    ("zr_timing_begin", C.c_int, [C.c_void_p]),
+    ("zr_timing_begin", C.c_int, [C.c_void_p, C.c_uint]),
     ("zr_timing_end", C.c_int, [C.c_void_p, C.POINTER(C.c_double), c_int_p]),
     # zip_rocm_host.h
     ("zrh_pool_create", C.c_int, [C.c_void_p, c_int_p, C.c_int, c_void_pp]),

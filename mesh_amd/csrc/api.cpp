@@ -41,10 +41,10 @@ zr_status set_global_err(zr_status code, const char* fmt, ...) {
 }
 
 // ------------------------------------------------------------- timing
-void timing_mark_begin(zr_context* ctx, int, hipEvent_t* out) {
+void timing_mark_begin(zr_context* ctx, int cls, hipEvent_t* out) {
     *out = nullptr;
     TimingState& t = ctx->timing;
-    if (!t.enabled) return;
+    if (!t.enabled || !(t.class_mask & (1u << cls))) return;
     if (t.next_event + 2 > t.pool.size()) {
         for (int i = 0; i < 64; ++i) {
             hipEvent_t e;
@@ -840,10 +840,11 @@ zr_status zr_kv_pool_fill_normal(zr_context* ctx, uint64_t seed, float std) {
     return rc;
 }
 
-zr_status zr_timing_begin(zr_context* ctx) {
+zr_status zr_timing_begin(zr_context* ctx, unsigned class_mask) {
     if (!ctx) return set_global_err(ZR_E_INVALID, "null context");
     ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
     ctx->timing.enabled = true;
+    ctx->timing.class_mask = class_mask;
     ctx->timing.spans.clear();
     ctx->timing.next_event = 0;
     return ZR_OK;

@@ -50,6 +50,7 @@ struct LayerDev {
 
 struct TimingState {
     bool enabled = false;
+    unsigned class_mask = 0xF;       // classes that record events
     std::vector<hipEvent_t> pool;    // recycled events
     std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> spans;
     size_t next_event = 0;
