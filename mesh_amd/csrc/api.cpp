@@ -207,6 +207,12 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     st->h_tiles.push_back(make_int4(0, 0, 0, (int)st->h_items.size()));  // sentinel
     st->n_tiles = (int)st->h_tiles.size() - 1;
     st->n_attn_items = (int)st->h_items.size();
+    // dispatch order: longest items first, so the short ones fill the tail
+    st->h_order.resize(st->n_attn_items);
+    for (int i = 0; i < st->n_attn_items; ++i) st->h_order[i] = i;
+    std::stable_sort(st->h_order.begin(), st->h_order.end(), [&](int x, int y) {
+        return st->h_items[x].z - st->h_items[x].y > st->h_items[y].z - st->h_items[y].y;
+    });
     // tiles whose splits need the merge kernel
     st->h_merge.clear();
     for (int t = 0; t < st->n_tiles; ++t)
@@ -234,6 +240,7 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     const size_t o_bt = take(4 * (size_t)S * stride), o_tok = take(4 * (size_t)std::max(total_q, 1));
     const size_t o_items = take(16 * (size_t)st->n_attn_items), o_tiles = take(16 * st->h_tiles.size());
     const size_t o_merge = take(4 * (size_t)std::max(st->n_merge, 1));
+    const size_t o_order = take(4 * (size_t)std::max(st->n_attn_items, 1));
     const size_t host_bytes = off;
     const size_t o_cuq = take(4 * (S + 1)), o_cuk = take(4 * (S + 1)), o_pos = take(4 * (size_t)total_q);
     const size_t o_slot = take(4 * (size_t)total_q), o_seq = take(4 * (size_t)total_q), o_last = take(4 * S);
@@ -258,6 +265,7 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     memcpy(hb + o_items, st->h_items.data(), 16 * (size_t)st->n_attn_items);
     memcpy(hb + o_tiles, st->h_tiles.data(), 16 * st->h_tiles.size());
     if (st->n_merge) memcpy(hb + o_merge, st->h_merge.data(), 4 * (size_t)st->n_merge);
+    if (st->n_attn_items) memcpy(hb + o_order, st->h_order.data(), 4 * (size_t)st->n_attn_items);
     unsigned char* db = (unsigned char*)st->dev;
     st->q_len = (int*)(db + o_qlen);
     st->kv_before = (int*)(db + o_kvb);
@@ -268,6 +276,7 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     st->attn_items = (int4*)(db + o_items);
     st->attn_tiles = (int4*)(db + o_tiles);
     st->merge_tiles = (int*)(db + o_merge);
+    st->attn_order = (int*)(db + o_order);
     st->cu_q = (int*)(db + o_cuq);
     st->cu_k = (int*)(db + o_cuk);
     st->positions = (int*)(db + o_pos);

@@ -170,6 +170,7 @@ struct AttnArgs {
     const int* kv_before;
     const int* cu_q;
     const int4* items;       // {tile, page_begin, page_end, unused}
+    const int* order;        // dispatch rank -> item (longest first)
     const int4* tiles;       // {seq, q0, nq, first_item}
     int G;                   // q heads per kv head
     int kv_heads;
@@ -183,7 +184,10 @@ struct AttnArgs {
 template <typename KV, int D>
 __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
     const int lane = threadIdx.x;
-    const int item = blockIdx.x, kvh = blockIdx.y;
+    // the kv heads of one item are adjacent in dispatch order (they read
+    // neighbouring blocks of the same pages)
+    const int kvh = blockIdx.x % a.kv_heads;
+    const int item = a.order[blockIdx.x / a.kv_heads];
     const int4 it = a.items[item];
     const int4 tl = a.tiles[it.x];
     const int seq = tl.x, q0 = tl.y, nq = tl.z;
@@ -438,6 +442,7 @@ static zr_status launch_attn_t(zr_context* ctx, StagedMeta* st, int layer, const
     a.kv_before = st->kv_before;
     a.cu_q = st->cu_q;
     a.items = st->attn_items;
+    a.order = st->attn_order;
     a.tiles = st->attn_tiles;
     a.G = ctx->q_per_kv;
     a.kv_heads = ctx->local_kv_heads;
@@ -448,7 +453,7 @@ static zr_status launch_attn_t(zr_context* ctx, StagedMeta* st, int layer, const
     a.out_lo_offset = (ctx->desc.flags & ZR_FLAG_SPLIT_ACTIVATIONS) ? (size_t)st->total_q * ctx->q_cols : 0;
     hipEvent_t ev;
     timing_mark_begin(ctx, kClassAttention, &ev);
-    hipLaunchKernelGGL((paged_attention_kernel<KV, D>), dim3(st->n_attn_items, ctx->local_kv_heads),
+    hipLaunchKernelGGL((paged_attention_kernel<KV, D>), dim3(st->n_attn_items * ctx->local_kv_heads),
                        dim3(64), 0, ctx->stream, a);
     ZR_LAUNCH_CHECK(ctx);
     timing_mark_end(ctx, kClassAttention, ev);

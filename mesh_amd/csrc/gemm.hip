@@ -1,18 +1,17 @@
 // Shard projection GEMMs on MFMA: C[M,N] = A[M,K] @ W[K,N].
 //
 // W (bf16 weights, reference [in, out] layout) is repacked once at upload into
-// MFMA B-operand fragments: fragment (nt, kt) is 64 lanes x 8 bf16 where lane l
-// holds W[32*kt + 8*(l/16) + j][16*nt + l%16], j < 8, stored contiguously and
-// fragments of one 16-column tile consecutive along K.  A wavefront streams
-// its weights as perfectly coalesced 1 KiB loads, each element read once per
-// row block, through a register ring PF k-steps deep.
+// MFMA B-operand fragments of v_mfma_f32_32x32x16_bf16 (on gfx950 it issues
+// at the rate of 16x16x32 with twice the work): fragment (nt, kt16) is 64
+// lanes x 8 bf16, lane l holding W[16 kt16 + 8 (l / 32) + j][32 nt + l % 32],
+// j < 8, stored contiguously; fragments of one 32-column tile are consecutive
+// along K (kt16 < 2 ceil(K / 32), zero padded).  A wavefront streams its
+// weights as perfectly coalesced 1 KiB loads.
 // A (activations) arrives as bf16 [M, K] -- or a hi + lo bf16 pair under
-// ZR_FLAG_SPLIT_ACTIVATIONS -- written by the producing kernel; a block
-// stages its A rows through a double-buffered LDS tile shared by the waves
-// that own different column slices.
+// ZR_FLAG_SPLIT_ACTIVATIONS -- written by the producing kernel.
 // Matmul semantics: forward_pass.rs:1696-1714 (w_qkv / w_gate_up column
 // concatenations), 2265 (O), 2290 (down), 2311 (LM head); f32 accumulation.
-// The gate|up concatenation is interleaved per 16 columns so one 32-column
+// The gate|up concatenation is interleaved per 32 columns so one 64-column
 // pair holds matching gate and up values for the SwiGLU epilogue
 // (silu(g) * u, forward_pass.rs:2286-2289).
 #include "zr_internal.h"
@@ -23,48 +22,47 @@
 namespace zr {
 
 size_t packed_weight_elems(int k, int n) {
-    const size_t kt = (size_t)(k + 31) / 32, nt = (size_t)(n + 15) / 16;
-    return kt * nt * 512;
+    const size_t kt16 = 2 * (size_t)((k + 31) / 32), nt = (size_t)(n + 31) / 32;
+    return kt16 * nt * 512;
 }
 
-// dst n-tile `nt_dst0 + i * tile_step` takes source columns [16 i, 16 i + 16)
-// of src [K, n_src] (zero outside).
-__global__ __launch_bounds__(256) void pack_weight_kernel(const uint16_t* __restrict__ src, int K,
-                                                          int n_src, int KT, int nt_dst0,
-                                                          int tile_step, int n_tiles,
+// dst 32-column tile `nt_dst0 + i * tile_step` takes source columns
+// [32 i, 32 i + 32) of src [K, n_src] (zero outside).
+__global__ __launch_bounds__(256) void pack_weight_kernel(const uint16_t* __restrict__ src, int K, int n_src,
+                                                          int KT16, int nt_dst0, int tile_step, int n_tiles,
                                                           uint16_t* __restrict__ dst) {
     const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const size_t total = (size_t)n_tiles * KT * 64;
+    const size_t total = (size_t)n_tiles * KT16 * 64;
     if (gid >= total) return;
     const int lane = (int)(gid % 64);
     const size_t frag = gid / 64;
-    const int kt = (int)(frag % KT);
-    const int i = (int)(frag / KT);
+    const int kt = (int)(frag % KT16);
+    const int i = (int)(frag / KT16);
     const int nt = nt_dst0 + i * tile_step;
-    const int n = i * 16 + (lane & 15);
-    uint16_t* out = dst + (((size_t)nt * KT + kt) * 64 + lane) * 8;
+    const int n = i * 32 + (lane & 31);
+    uint16_t* out = dst + (((size_t)nt * KT16 + kt) * 64 + lane) * 8;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const int k = kt * 32 + (lane >> 4) * 8 + j;
+        const int k = kt * 16 + (lane >> 5) * 8 + j;
         out[j] = (k < K && n < n_src) ? src[(size_t)k * n_src + n] : (uint16_t)0;
     }
 }
 
-static zr_status pack_into(zr_context* ctx, const uint16_t* src, int k, int n, int KT, int nt0,
-                           int step, uint16_t* dst) {
+static zr_status pack_into(zr_context* ctx, const uint16_t* src, int k, int n, int nt0, int step, uint16_t* dst) {
     const size_t bytes = (size_t)k * n * 2;
+    const int KT16 = 2 * ((k + 31) / 32);
     uint16_t* tmp = nullptr;
     ZR_HIP(ctx, hipMalloc(&tmp, bytes));
     hipError_t e = hipMemcpyAsync(tmp, src, bytes, hipMemcpyDefault, ctx->stream);
     if (e == hipSuccess) {
-        const int n_tiles = (n + 15) / 16;
-        const size_t total = (size_t)n_tiles * KT * 64;
+        const int n_tiles = (n + 31) / 32;
+        const size_t total = (size_t)n_tiles * KT16 * 64;
         hipLaunchKernelGGL(pack_weight_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, ctx->stream,
-                           tmp, k, n, KT, nt0, step, n_tiles, dst);
+                           tmp, k, n, KT16, nt0, step, n_tiles, dst);
         e = hipGetLastError();
     }
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-    hipFree(tmp);
+    (void)hipFree(tmp);
     if (e != hipSuccess) return set_err(ctx, ZR_E_HIP, "weight pack failed: %s", hipGetErrorString(e));
     return ZR_OK;
 }
@@ -78,195 +76,91 @@ zr_status pack_weight_concat(zr_context* ctx, const uint16_t* const* srcs, const
                              int k, uint16_t** out) {
     int n_total = 0;
     for (int i = 0; i < count; ++i) {
-        if (count > 1 && widths[i] % 16 != 0)
-            return set_err(ctx, ZR_E_UNSUPPORTED, "concatenated projection width %d is not a multiple of 16",
+        if (count > 1 && widths[i] % 32 != 0)
+            return set_err(ctx, ZR_E_UNSUPPORTED, "concatenated projection width %d is not a multiple of 32",
                            widths[i]);
         n_total += widths[i];
     }
-    const int KT = (k + 31) / 32;
     uint16_t* dst = nullptr;
     ZR_HIP(ctx, hipMalloc(&dst, packed_weight_elems(k, n_total) * 2));
     int nt0 = 0;
     for (int i = 0; i < count; ++i) {
-        zr_status rc = pack_into(ctx, srcs[i], k, widths[i], KT, nt0, 1, dst);
+        zr_status rc = pack_into(ctx, srcs[i], k, widths[i], nt0, 1, dst);
         if (rc != ZR_OK) {
-            hipFree(dst);
+            (void)hipFree(dst);
             return rc;
         }
-        nt0 += (widths[i] + 15) / 16;
+        nt0 += (widths[i] + 31) / 32;
     }
     *out = dst;
     return ZR_OK;
 }
 
-// Interleaved [gate | up]: tile 2b = gate columns [16b, 16b+16), tile 2b+1 = up.
+// Interleaved [gate | up]: tile 2b = gate columns [32b, 32b+32), tile 2b+1 = up.
 zr_status pack_weight_gate_up(zr_context* ctx, const uint16_t* gate, const uint16_t* up, int k, int f,
                               uint16_t** out) {
-    if (f % 16 != 0) return set_err(ctx, ZR_E_UNSUPPORTED, "ffn width %d is not a multiple of 16", f);
-    const int KT = (k + 31) / 32;
+    if (f % 32 != 0) return set_err(ctx, ZR_E_UNSUPPORTED, "ffn width %d is not a multiple of 32", f);
     uint16_t* dst = nullptr;
     ZR_HIP(ctx, hipMalloc(&dst, packed_weight_elems(k, 2 * f) * 2));
-    zr_status rc = pack_into(ctx, gate, k, f, KT, 0, 2, dst);
-    if (rc == ZR_OK) rc = pack_into(ctx, up, k, f, KT, 1, 2, dst);
+    zr_status rc = pack_into(ctx, gate, k, f, 0, 2, dst);
+    if (rc == ZR_OK) rc = pack_into(ctx, up, k, f, 1, 2, dst);
     if (rc != ZR_OK) {
-        hipFree(dst);
+        (void)hipFree(dst);
         return rc;
     }
     *out = dst;
     return ZR_OK;
 }
 
-// ------------------------------------------------------------------ GEMM
-// Block = WAVES_M x WAVES_N wavefronts; wave tile = (16 WM) rows x (16 WN)
-// columns; block tile BM x BN.  grid = (column blocks, K splits, row blocks).
-// Per k-step of 32: one barrier; the next A slice is loaded to registers
-// before the MFMAs and written to the other LDS buffer after them; the
-// weight fragments of k-step kt + PF are requested as soon as step kt's are
-// consumed.
-template <int WM, int WN, int WAVES_M, int WAVES_N, int PF, int HL>
-__global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_kernel(
-    const uint16_t* __restrict__ A, int M, int K, const bf16x8* __restrict__ Wp, int KT, int NT,
-    float* __restrict__ C, int N, int kt_per_split, size_t split_stride) {
-    constexpr int BM = WAVES_M * WM * 16;
-    constexpr int NTHR = WAVES_M * WAVES_N * 64;
-    constexpr int A_CHUNKS = BM * 4 * HL;  // 16-byte chunks of one k-step of A
-    constexpr int A_PER_T = (A_CHUNKS + NTHR - 1) / NTHR;
-    __shared__ bf16x8 lds[2][HL][BM / 16][64];
-
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int wm_idx = wave / WAVES_N, wn_idx = wave % WAVES_N;
-    const int m0 = blockIdx.z * BM;
-    const int nt0 = blockIdx.x * (WAVES_N * WN) + wn_idx * WN;
-    const int kt_begin = blockIdx.y * kt_per_split;
-    const int kt_end = min(KT, kt_begin + kt_per_split);
-    const size_t MK = (size_t)M * K;
-
-    bf16x8 areg[A_PER_T];
-    auto load_a = [&](int kt) {
-#pragma unroll
-        for (int j = 0; j < A_PER_T; ++j) {
-            const int c = tid + j * NTHR;
-            bf16x8 v = bf16x8{};
-            if (c < A_CHUNKS) {
-                const int hl = c / (BM * 4), r = c - hl * (BM * 4);
-                const int m = r >> 2, q = r & 3;
-                const int k = kt * 32 + q * 8;
-                if (m0 + m < M && kt < kt_end && k < K)
-                    v = *(const bf16x8*)(A + hl * MK + (size_t)(m0 + m) * K + k);
-            }
-            areg[j] = v;
-        }
-    };
-    auto store_a = [&](int buf) {
-#pragma unroll
-        for (int j = 0; j < A_PER_T; ++j) {
-            const int c = tid + j * NTHR;
-            if (c < A_CHUNKS) {
-                const int hl = c / (BM * 4), r = c - hl * (BM * 4);
-                const int m = r >> 2, q = r & 3;
-                lds[buf][hl][m >> 4][q * 16 + (m & 15)] = areg[j];
-            }
-        }
-    };
-
-    bf16x8 bring[PF][WN];
-    auto load_b = [&](bf16x8* dst, int kt) {
-#pragma unroll
-        for (int wn = 0; wn < WN; ++wn) {
-            const int nt = nt0 + wn;
-            dst[wn] = (nt < NT && kt < kt_end) ? Wp[((size_t)nt * KT + kt) * 64 + lane] : bf16x8{};
-        }
-    };
-
-    f32x4 acc[WM][WN];
-#pragma unroll
-    for (int mt = 0; mt < WM; ++mt)
-#pragma unroll
-        for (int wn = 0; wn < WN; ++wn) acc[mt][wn] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    load_a(kt_begin);
-    store_a(0);
-#pragma unroll
-    for (int s = 0; s < PF; ++s) load_b(bring[s], kt_begin + s);
-
-    int buf = 0;
-    for (int kb = kt_begin; kb < kt_end; kb += PF) {
-#pragma unroll
-        for (int s = 0; s < PF; ++s) {
-            const int kt = kb + s;
-            if (kt < kt_end) {  // uniform across the block
-                load_a(kt + 1);
-                __syncthreads();
-#pragma unroll
-                for (int mt = 0; mt < WM; ++mt) {
-                    const bf16x8 ah = lds[buf][0][wm_idx * WM + mt][lane];
-#pragma unroll
-                    for (int wn = 0; wn < WN; ++wn)
-                        acc[mt][wn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bring[s][wn], acc[mt][wn], 0, 0, 0);
-                    if (HL == 2) {
-                        const bf16x8 al = lds[buf][HL - 1][wm_idx * WM + mt][lane];
-#pragma unroll
-                        for (int wn = 0; wn < WN; ++wn)
-                            acc[mt][wn] =
-                                __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bring[s][wn], acc[mt][wn], 0, 0, 0);
-                    }
-                }
-                load_b(bring[s], kt + PF);
-                buf ^= 1;
-                store_a(buf);
-            }
-        }
-    }
-
-    float* out = C + (size_t)blockIdx.y * split_stride;
-#pragma unroll
-    for (int mt = 0; mt < WM; ++mt)
-#pragma unroll
-        for (int wn = 0; wn < WN; ++wn) {
-            const int n = (nt0 + wn) * 16 + (lane & 15);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int m = m0 + (wm_idx * WM + mt) * 16 + (lane >> 4) * 4 + i;
-                if (m < M && n < N) out[(size_t)m * N + n] = acc[mt][wn][i];
-            }
-        }
-}
-
-// ------------------------------------------------- GEMM, LDS-DMA pipeline
-// `s_waitcnt vmcnt(n)` with expcnt / lgkmcnt left unconstrained (gfx9
-// encoding: vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
 typedef __attribute__((address_space(3))) void lds_void;
 
-// Both operands go global -> LDS with `global_load_lds_dwordx4` (no
-// registers, no per-lane address math beyond one pointer): every 1 KiB MFMA
-// fragment of a k-step -- A rows (hi, then lo) and packed weight tiles -- is
-// one wave instruction, spread evenly over the block's waves.  STAGES-deep
-// LDS ring: at step i a wave waits (vmcnt) for its own copies of stage i,
-// the block barrier publishes the stage to every wave and retires the slot
-// read at step i-1, which then takes stage i + STAGES - 1.  The compiler
+// Block barrier for the LDS ring: wait until at most N of this wave's vector
+// memory ops (its global_load_lds copies of later stages) are outstanding and
+// all of its LDS reads have returned, then s_barrier.  __syncthreads() would
+// also wait for the later stages' copies (its fence drains vmcnt), which
+// serialises the ring.  The empty asm statements keep the compiler from
+// moving memory operations across the barrier.
+template <int N>
+__device__ __forceinline__ void ring_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));  // vmcnt(N), expcnt(7), lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// ------------------------------------------------------------------ GEMM
+// v_mfma_f32_32x32x16_bf16: A fragment lane l holds A[row l % 32][k 8 (l / 32)
+// + j]; the product lane l, element i is C[8 (i / 4) + 4 (l / 32) + i % 4][l % 32].
+// Block tile BM x BN = (32 WAVES_M WM) x (32 WAVES_N WN); wave tile
+// (32 WM) x (32 WN); a k-step covers 32 of K (two MFMA k-halves).
+// A (activations) goes global -> LDS with `global_load_lds_dwordx4` (no
+// registers): every 1 KiB MFMA fragment of a k-step -- A rows, hi then lo --
+// is one wave instruction, spread evenly over the block's waves.  The
+// weights either take the same path (BDIRECT = 0) or stream straight into a
+// per-wave register ring (BDIRECT = 1).  STAGES-deep ring: the copies of
+// stage i + STAGES - 1 are issued at step i, A and B together, so waiting
+// (vmcnt, in order) for stage i's A also covers its B.  At step i a wave
+// waits for its own copies of stage i, the block barrier publishes the
+// stage to every wave and retires the slot read at step i - 1.  The compiler
 // does not order LDS reads after these copies, hence the explicit waits.
-// Block tile BM x BN = (16 WAVES_M WM) x (16 WAVES_N WN); wave tile
-// (16 WM) x (16 WN).  Grid: 1-D, decoded so that the row blocks of one
-// (column block, split) pair are dispatched 8 apart -- on the same XCD, one
-// after the other -- and share that weight tile through its L2.
-template <int WM, int WN, int WAVES_M, int WAVES_N, int HL, int STAGES>
-__global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_dma_kernel(
+// Grid: 1-D, decoded so that the row blocks of one (column block, split)
+// pair are dispatched 8 apart -- on the same XCD, one after the other -- and
+// share that weight tile through its L2.
+template <int WM, int WN, int WAVES_M, int WAVES_N, int HL, int STAGES, int BDIRECT>
+__global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_kernel(
     const uint16_t* __restrict__ A, int M, int K, const bf16x8* __restrict__ Wp, int KT, int NT,
     float* __restrict__ C, int N, int kt_per_split, int splits, int row_blocks, int col_blocks,
     size_t split_stride) {
     constexpr int NW = WAVES_M * WAVES_N;
     constexpr int BMT = WAVES_M * WM, BNT = WAVES_N * WN;
-    constexpr int FA = HL * BMT, FB = BNT, FS = FA + FB;
-    constexpr int PW = (FS + NW - 1) / NW;  // copies per wave per stage
+    constexpr int FA = HL * BMT * 2, FB = BDIRECT ? 0 : BNT * 2, FS = FA + FB;
+    constexpr int PW = (FS + NW - 1) / NW;  // LDS copies per wave per stage
     constexpr int FSP = PW * NW;            // fragments per stage incl. padding
+    constexpr int VM = PW + (BDIRECT ? 2 * WN : 0);  // vector-memory ops per wave per stage
     static_assert(STAGES >= 2 && STAGES <= 4, "stages");
-    static_assert(PW * (STAGES - 2) < 64, "vmcnt range");
+    static_assert(VM * (STAGES - 2) < 64, "vmcnt range");
+    typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
     __shared__ bf16x8 lds[STAGES][FSP][64];
 
     const int b = blockIdx.x;
@@ -278,71 +172,89 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_dma_kernel(
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int wm_idx = wave / WAVES_N, wn_idx = wave - wm_idx * WAVES_N;
-    const int m0 = rb * BMT * 16;
+    const int m0 = rb * BMT * 32;
     const int nt_blk = cb * BNT;
+    const int KT16 = 2 * KT;
     const int kt_begin = split * kt_per_split;
     const int nsteps = min(KT, kt_begin + kt_per_split) - kt_begin;
     const size_t MK = (size_t)M * K;
 
-    auto issue = [&](int slot, int kt) {
+    bf16x8 breg[BDIRECT ? STAGES : 1][2][WN];
+    auto issue = [&](int slot, int bslot, int kt) {
 #pragma unroll
         for (int i = 0; i < PW; ++i) {
             int f = i * NW + wave;
             const int fs = f < FS ? f : f - FS;  // padding rows repeat a real fragment
             const void* src;
             if (fs < FA) {
-                const int hl = fs / BMT, mt = fs - hl * BMT;
-                const int row = min(m0 + mt * 16 + (lane & 15), M - 1);
-                const int kc = min(kt * 32 + (lane >> 4) * 8, K - 8);
+                const int kh = fs & 1, r = fs >> 1;
+                const int hl = r / BMT, mt = r - hl * BMT;
+                const int row = min(m0 + mt * 32 + (lane & 31), M - 1);
+                const int kc = min(kt * 32 + kh * 16 + (lane >> 5) * 8, K - 8);
                 src = A + (size_t)hl * MK + (size_t)row * K + kc;
             } else {
-                const int nt = min(nt_blk + (fs - FA), NT - 1);
-                src = Wp + ((size_t)nt * KT + kt) * 64 + lane;
+                const int fb = fs - FA;
+                const int nt = min(nt_blk + (fb >> 1), NT - 1);
+                src = Wp + ((size_t)nt * KT16 + 2 * kt + (fb & 1)) * 64 + lane;
             }
             __builtin_amdgcn_global_load_lds(src, (lds_void*)&lds[slot][f][0], 16, 0, 0);
         }
+        if (BDIRECT) {
+#pragma unroll
+            for (int wn = 0; wn < WN; ++wn) {
+                const int nt = min(nt_blk + wn_idx * WN + wn, NT - 1);
+#pragma unroll
+                for (int kh = 0; kh < 2; ++kh)
+                    breg[bslot][kh][wn] = Wp[((size_t)nt * KT16 + 2 * kt + kh) * 64 + lane];
+            }
+        }
     };
 
-    f32x4 acc[WM][WN];
+    f32x16 acc[WM][WN];
 #pragma unroll
     for (int mt = 0; mt < WM; ++mt)
 #pragma unroll
-        for (int wn = 0; wn < WN; ++wn) acc[mt][wn] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int wn = 0; wn < WN; ++wn)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[mt][wn][i] = 0.0f;
 
 #pragma unroll
     for (int s = 0; s < STAGES - 1; ++s)
-        if (s < nsteps) issue(s, kt_begin + s);
+        if (s < nsteps) issue(s, BDIRECT ? s : 0, kt_begin + s);
 
-    int slot = 0;
-    for (int i = 0; i < nsteps; ++i) {
-        const int ahead = min(STAGES - 2, nsteps - 1 - i);  // stages issued after stage i
-        if (STAGES >= 4 && ahead >= 2)
-            wait_vmcnt<PW * (STAGES >= 4 ? 2 : 0)>();
-        else if (STAGES >= 3 && ahead == 1)
-            wait_vmcnt<PW * (STAGES >= 3 ? 1 : 0)>();
-        else
-            wait_vmcnt<0>();
-        __syncthreads();
-        if (i + STAGES - 1 < nsteps) {
-            int ns = slot + STAGES - 1;
-            if (ns >= STAGES) ns -= STAGES;
-            issue(ns, kt_begin + i + STAGES - 1);
-        }
-        const bf16x8* sa = &lds[slot][0][0];
-        const bf16x8* sb = &lds[slot][FA][0];
-        bf16x8 bf[WN];
+    for (int i0 = 0; i0 < nsteps; i0 += STAGES) {
 #pragma unroll
-        for (int wn = 0; wn < WN; ++wn) bf[wn] = sb[(wn_idx * WN + wn) * 64 + lane];
+        for (int u = 0; u < STAGES; ++u) {
+            const int i = i0 + u;
+            if (i >= nsteps) break;
+            const int ahead = min(STAGES - 2, nsteps - 1 - i);  // stages issued after stage i
+            if (STAGES >= 4 && ahead >= 2)
+                ring_barrier<VM * (STAGES >= 4 ? 2 : 0)>();
+            else if (STAGES >= 3 && ahead == 1)
+                ring_barrier<VM * (STAGES >= 3 ? 1 : 0)>();
+            else
+                ring_barrier<0>();
+            const int ns = (u + STAGES - 1) % STAGES;
+            if (i + STAGES - 1 < nsteps) issue(ns, BDIRECT ? ns : 0, kt_begin + i + STAGES - 1);
 #pragma unroll
-        for (int mt = 0; mt < WM; ++mt)
-#pragma unroll
-            for (int hl = 0; hl < HL; ++hl) {
-                const bf16x8 af = sa[(hl * BMT + wm_idx * WM + mt) * 64 + lane];
+            for (int kh = 0; kh < 2; ++kh) {
+                bf16x8 bf[WN];
 #pragma unroll
                 for (int wn = 0; wn < WN; ++wn)
-                    acc[mt][wn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bf[wn], acc[mt][wn], 0, 0, 0);
+                    bf[wn] = BDIRECT ? breg[BDIRECT ? u : 0][kh][wn]
+                                     : lds[u][FA + (wn_idx * WN + wn) * 2 + kh][lane];
+#pragma unroll
+                for (int mt = 0; mt < WM; ++mt)
+#pragma unroll
+                    for (int hl = 0; hl < HL; ++hl) {
+                        const bf16x8 af = lds[u][((hl * BMT + wm_idx * WM + mt) << 1) + kh][lane];
+#pragma unroll
+                        for (int wn = 0; wn < WN; ++wn)
+                            acc[mt][wn] =
+                                __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf[wn], acc[mt][wn], 0, 0, 0);
+                    }
             }
-        if (++slot == STAGES) slot = 0;
+        }
     }
 
     float* out = C + (size_t)split * split_stride;
@@ -350,10 +262,10 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_dma_kernel(
     for (int mt = 0; mt < WM; ++mt)
 #pragma unroll
         for (int wn = 0; wn < WN; ++wn) {
-            const int n = (nt_blk + wn_idx * WN + wn) * 16 + (lane & 15);
+            const int n = (nt_blk + wn_idx * WN + wn) * 32 + (lane & 31);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int m = m0 + (wm_idx * WM + mt) * 16 + (lane >> 4) * 4 + i;
+            for (int i = 0; i < 16; ++i) {
+                const int m = m0 + (wm_idx * WM + mt) * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
                 if (m < M && n < N) out[(size_t)m * N + n] = acc[mt][wn][i];
             }
         }
@@ -361,7 +273,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_dma_kernel(
 
 // Sum of split-K slabs [S][M][N] with the epilogue.
 // kEpiStore:  out_f32[m][n] = sum
-// kEpiSwiGLU: N = 2F interleaved per 16 columns; h = silu(g) * u written as
+// kEpiSwiGLU: N = 2F interleaved per 32 columns; h = silu(g) * u written as
 //             bf16 hi (+ lo) [M, F] (the next GEMM's A operand) or f32.
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, int S, int M, int N,
                                                             size_t split_stride, int epilogue,
@@ -375,11 +287,11 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
         const int m = (int)(idx / n_out), j = (int)(idx % n_out);
         float v;
         if (epilogue == kEpiSwiGLU) {
-            const int gc = (j >> 4) * 32 + (j & 15);
+            const int gc = (j >> 5) * 64 + (j & 31);
             float g = 0.0f, u = 0.0f;
             for (int s = 0; s < S; ++s) {
                 g += ws[s * split_stride + (size_t)m * N + gc];
-                u += ws[s * split_stride + (size_t)m * N + gc + 16];
+                u += ws[s * split_stride + (size_t)m * N + gc + 32];
             }
             v = g / (1.0f + expf(-g)) * u;
         } else {
@@ -415,60 +327,48 @@ zr_status launch_to_bf16_pair(zr_context* ctx, const float* x, size_t n, uint16_
     return ZR_OK;
 }
 
-// Tile configurations (wave tile WM x WN 16x16 tiles; WAVES_M x WAVES_N waves).
-// family 0: register-ring kernel (gemm_kernel), for M <= 64 where the step
-//           streams weights; family 1: LDS-DMA kernel (gemm_dma_kernel), for
-//           M >= 128 where the hi + lo MFMA work dominates.
+// Tile configurations: wave tile WM x WN 32x32 tiles, WAVES_M x WAVES_N waves.
 struct GemmCfg {
-    int family, wm, wn, waves_m, waves_n, stages;
-    int bm() const { return waves_m * wm * 16; }
-    int bn() const { return waves_n * wn * 16; }
+    int wm, wn, waves_m, waves_n, stages, bdirect;
+    bool small;  // many blocks per CU (weight streaming) rather than one
+    int bm() const { return waves_m * wm * 32; }
+    int bn() const { return waves_n * wn * 32; }
 };
 
-static bool dma_enabled() {
-    static const bool on = !(getenv("ZR_GEMM_DMA") && atoi(getenv("ZR_GEMM_DMA")) == 0);
-    return on;
+// Measured on MI355X over the decode shapes with weights streamed from HBM
+// (split activations): 32 x 128 tiles for <= 32 rows; 128-row tiles with
+// 256 columns, or 512 for wide / deep products and the LM head.
+static GemmCfg pick_cfg(int m, int n, int k) {
+    if (m <= 32) return {1, 1, 1, 4, 3, 0, true};
+    if (m <= 64) return {2, 1, 1, 4, 3, 0, true};
+    if (n >= 65536) return {2, 4, 2, 4, 2, 0, false};
+    if (n >= 16384 || k >= 8192) return {2, 4, 2, 4, 3, 0, false};
+    return {2, 2, 2, 4, 3, 0, false};
 }
 
-// Measured on MI355X over the decode shapes with weights streamed from HBM:
-// 2x2 wave tiles with 8 waves suit M <= 64; from 128 rows the LDS-DMA kernel
-// with 128 x 256 block tiles (8 waves, 3 stages) wins, and for very wide N
-// (the LM head) 4 waves with 2 stages, two blocks per CU.
-static GemmCfg pick_cfg(int m, int n) {
-    if (m <= 16) return {0, 1, 2, 1, 8, 0};
-    if (m <= 32) return {0, 2, 2, 1, 8, 0};
-    if (m <= 64) return {0, 4, 2, 1, 8, 0};
-    if (!dma_enabled()) return m <= 128 ? GemmCfg{0, 4, 4, 2, 4, 0} : GemmCfg{0, 8, 4, 2, 4, 0};
-    if (n >= 65536) return {1, 4, 8, 2, 2, 2};
-    return {1, 4, 4, 2, 4, 3};
+static int device_cus() {
+    static const int cus = [] {
+        int v = 256, dev = 0;
+        if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev);
+        return v > 0 ? v : 256;
+    }();
+    return cus;
 }
 
 GemmPlan gemm_plan(int m, int n, int k, int epilogue) {
     GemmPlan p;
-    const GemmCfg c = pick_cfg(m, n);
+    const GemmCfg c = pick_cfg(m, n, k);
     p.KT = (k + 31) / 32;
-    p.NT = (n + 15) / 16;
+    p.NT = (n + 31) / 32;
     p.row_blocks = (m + c.bm() - 1) / c.bm();
-    p.col_blocks = (p.NT + c.bn() / 16 - 1) / (c.bn() / 16);
+    p.col_blocks = (p.NT + c.bn() / 32 - 1) / (c.bn() / 32);
+    // split K (power of two, >= 4 k-steps per split) while the grid fits one
+    // pass over the CUs (one resident block per CU for the large tiles,
+    // about three for the small weight-streaming tiles, at most 16 splits)
+    const int tiles = p.col_blocks * p.row_blocks;
+    const int budget = c.small ? 3 * device_cus() : device_cus();
     int splits = 1;
-    if (c.family == 0) {
-        // split K while the grid has fewer than ~1.5 blocks per CU, keeping at
-        // least 4 k-steps per split
-        static const int target =
-            getenv("ZR_GEMM_TARGET_BLOCKS") ? atoi(getenv("ZR_GEMM_TARGET_BLOCKS")) : 384;
-        while (p.col_blocks * p.row_blocks * splits * 2 <= target && p.KT / (splits * 2) >= 4) splits *= 2;
-    } else {
-        // one resident block per CU (LDS-bound): split K while the grid still
-        // fits one pass over the CUs, keeping at least 4 k-steps per split
-        static const int cus = [] {
-            int v = 256;
-            int dev = 0;
-            if (hipGetDevice(&dev) == hipSuccess)
-                (void)hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev);
-            return v > 0 ? v : 256;
-        }();
-        while (p.col_blocks * p.row_blocks * splits * 2 <= cus && p.KT / (splits * 2) >= 4) splits *= 2;
-    }
+    while (tiles * splits * 2 <= budget && p.KT / (splits * 2) >= 4 && splits < 16) splits *= 2;
     p.kt_per_split = (p.KT + splits - 1) / splits;
     p.splits = (p.KT + p.kt_per_split - 1) / p.kt_per_split;
     p.direct = p.splits == 1 && epilogue == kEpiStore;
@@ -476,21 +376,12 @@ GemmPlan gemm_plan(int m, int n, int k, int epilogue) {
     return p;
 }
 
-template <int WM, int WN, int WAVES_M, int WAVES_N, int HL>
-static void gemm_launch(const GemmPlan& p, hipStream_t stream, const uint16_t* a, int m, int k,
-                        const uint16_t* w, float* c, int n, size_t split_stride) {
-    constexpr int PF = 4;
-    dim3 grid(p.col_blocks, p.splits, p.row_blocks);
-    hipLaunchKernelGGL((gemm_kernel<WM, WN, WAVES_M, WAVES_N, PF, HL>), grid, dim3(WAVES_M * WAVES_N * 64), 0,
-                       stream, a, m, k, (const bf16x8*)w, p.KT, p.NT, c, n, p.kt_per_split, split_stride);
-}
-
-template <int WM, int WN, int WAVES_M, int WAVES_N, int STAGES, int HL>
-static void gemm_dma_launch(const GemmPlan& p, hipStream_t stream, const uint16_t* a, int m, int k,
-                            const uint16_t* w, float* c, int n, size_t split_stride) {
+template <int WM, int WN, int WAVES_M, int WAVES_N, int STAGES, int HL, int BDIRECT>
+static void gemm_launch(const GemmPlan& p, hipStream_t stream, const uint16_t* a, int m, int k, const uint16_t* w,
+                        float* c, int n, size_t split_stride) {
     const int groups = p.col_blocks * p.splits;
     const unsigned blocks = 8u * (unsigned)p.row_blocks * (unsigned)((groups + 7) / 8);
-    hipLaunchKernelGGL((gemm_dma_kernel<WM, WN, WAVES_M, WAVES_N, HL, STAGES>), dim3(blocks),
+    hipLaunchKernelGGL((gemm_kernel<WM, WN, WAVES_M, WAVES_N, HL, STAGES, BDIRECT>), dim3(blocks),
                        dim3(WAVES_M * WAVES_N * 64), 0, stream, a, m, k, (const bf16x8*)w, p.KT, p.NT, c, n,
                        p.kt_per_split, p.splits, p.row_blocks, p.col_blocks, split_stride);
 }
@@ -502,7 +393,7 @@ zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_pack
     if (m <= 0) return ZR_OK;
     if (k % 8 != 0 || k < 8) return set_err(ctx, ZR_E_UNSUPPORTED, "GEMM K=%d must be a multiple of 8", k);
     const GemmPlan p = gemm_plan(m, n, k, epilogue);
-    const GemmCfg cfg = pick_cfg(m, n);
+    const GemmCfg cfg = pick_cfg(m, n, k);
     const bool direct = p.direct && c_f32 && !c_bf16;
     const size_t split_stride = (size_t)m * n;
     if (!direct && (size_t)p.splits * split_stride > ctx->splitk_ws_floats)
@@ -512,35 +403,23 @@ zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_pack
     hipEvent_t ev;
     timing_mark_begin(ctx, kClassGemm, &ev);
     bool launched = false;
-#define ZR_GEMM_CASE(WMV, WNV, WAM, WAN)                                                              \
-    if (!launched && cfg.family == 0 && cfg.wm == WMV && cfg.wn == WNV && cfg.waves_m == WAM &&        \
-        cfg.waves_n == WAN) {                                                                         \
-        if (split_act)                                                                                \
-            gemm_launch<WMV, WNV, WAM, WAN, 2>(p, ctx->stream, a, m, k, w_packed, dst, n, split_stride); \
-        else                                                                                          \
-            gemm_launch<WMV, WNV, WAM, WAN, 1>(p, ctx->stream, a, m, k, w_packed, dst, n, split_stride); \
-        launched = true;                                                                              \
+#define ZR_GEMM_CASE(WMV, WNV, WAM, WAN, ST, BD)                                                       \
+    if (!launched && cfg.wm == WMV && cfg.wn == WNV && cfg.waves_m == WAM && cfg.waves_n == WAN &&      \
+        cfg.stages == ST && cfg.bdirect == BD) {                                                       \
+        if (split_act)                                                                                 \
+            gemm_launch<WMV, WNV, WAM, WAN, ST, 2, BD>(p, ctx->stream, a, m, k, w_packed, dst, n,       \
+                                                       split_stride);                                  \
+        else                                                                                           \
+            gemm_launch<WMV, WNV, WAM, WAN, ST, 1, BD>(p, ctx->stream, a, m, k, w_packed, dst, n,       \
+                                                       split_stride);                                  \
+        launched = true;                                                                               \
     }
-#define ZR_GEMM_DMA_CASE(WMV, WNV, WAM, WAN, ST)                                                      \
-    if (!launched && cfg.family == 1 && cfg.wm == WMV && cfg.wn == WNV && cfg.waves_m == WAM &&        \
-        cfg.waves_n == WAN && cfg.stages == ST) {                                                     \
-        if (split_act)                                                                                \
-            gemm_dma_launch<WMV, WNV, WAM, WAN, ST, 2>(p, ctx->stream, a, m, k, w_packed, dst, n,      \
-                                                       split_stride);                                 \
-        else                                                                                          \
-            gemm_dma_launch<WMV, WNV, WAM, WAN, ST, 1>(p, ctx->stream, a, m, k, w_packed, dst, n,      \
-                                                       split_stride);                                 \
-        launched = true;                                                                              \
-    }
-    ZR_GEMM_CASE(1, 2, 1, 8)
-    ZR_GEMM_CASE(2, 2, 1, 8)
-    ZR_GEMM_CASE(4, 2, 1, 8)
-    ZR_GEMM_CASE(4, 4, 2, 4)
-    ZR_GEMM_CASE(8, 4, 2, 4)
-    ZR_GEMM_DMA_CASE(4, 4, 2, 4, 3)
-    ZR_GEMM_DMA_CASE(4, 8, 2, 2, 2)
+    ZR_GEMM_CASE(1, 1, 1, 4, 3, 0)
+    ZR_GEMM_CASE(2, 1, 1, 4, 3, 0)
+    ZR_GEMM_CASE(2, 4, 2, 4, 2, 0)
+    ZR_GEMM_CASE(2, 4, 2, 4, 3, 0)
+    ZR_GEMM_CASE(2, 2, 2, 4, 3, 0)
 #undef ZR_GEMM_CASE
-#undef ZR_GEMM_DMA_CASE
     if (!launched) return set_err(ctx, ZR_E_INVARIANT, "no GEMM kernel for the selected tile configuration");
     ZR_LAUNCH_CHECK(ctx);
     timing_mark_end(ctx, kClassGemm, ev);

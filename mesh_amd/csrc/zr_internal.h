@@ -161,10 +161,11 @@ struct StagedMeta {
     int4* attn_tiles = nullptr; // [n_tiles] {seq, q0, nq, first_part}
     int* tile_nparts = nullptr; // [n_tiles]
     int* merge_tiles = nullptr; // [n_merge] tiles the merge kernel combines
+    int* attn_order = nullptr;  // [n_attn_items] items by decreasing page count
     // host copies
     std::vector<int> h_q_len, h_kv_before, h_first_pos, h_first_offset, h_block_tables;
     std::vector<int4> h_items, h_tiles;
-    std::vector<int> h_tile_nparts, h_merge;
+    std::vector<int> h_tile_nparts, h_merge, h_order;
     std::vector<uint32_t> h_tokens;
     std::vector<unsigned char> h_blob;
 };
