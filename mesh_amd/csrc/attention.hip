@@ -181,7 +181,7 @@ struct AttnArgs {
     size_t out_lo_offset;
 };
 
-template <typename KV, int D>
+template <typename KV, int D, int RING>
 __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
     const int lane = threadIdx.x;
     // the kv heads of one item are adjacent in dispatch order (they read
@@ -265,7 +265,7 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
 
     // Register ring of RING page sets, consumed in pairs: RING - 2 pages are
     // in flight while a pair is computed.
-    constexpr int RING = sizeof(KV) == 4 ? 4 : 6;
+    static_assert(RING % 2 == 0 && RING >= 4, "ring of page pairs");
     PageRegs<KV, D> ring[RING];
     auto load = [&](PageRegs<KV, D>& r, int p) {
         const KV* base = pool + (size_t)bt[p] * a.page_elems + (size_t)kvh * kv_tile;
@@ -453,8 +453,10 @@ static zr_status launch_attn_t(zr_context* ctx, StagedMeta* st, int layer, const
     a.out_lo_offset = (ctx->desc.flags & ZR_FLAG_SPLIT_ACTIVATIONS) ? (size_t)st->total_q * ctx->q_cols : 0;
     hipEvent_t ev;
     timing_mark_begin(ctx, kClassAttention, &ev);
-    hipLaunchKernelGGL((paged_attention_kernel<KV, D>), dim3(st->n_attn_items * ctx->local_kv_heads),
-                       dim3(64), 0, ctx->stream, a);
+    // bf16 pages: a 6-page ring, one wave per SIMD (measured: a 4-page ring
+    // at two waves per SIMD spills and loses ~20%); f32 pages: 4 pages
+    const dim3 grid(st->n_attn_items * ctx->local_kv_heads);
+    hipLaunchKernelGGL((paged_attention_kernel<KV, D, sizeof(KV) == 4 ? 4 : 6>), grid, dim3(64), 0, ctx->stream, a);
     ZR_LAUNCH_CHECK(ctx);
     timing_mark_end(ctx, kClassAttention, ev);
     if (st->n_merge > 0) {
