@@ -385,9 +385,17 @@ zr_status zrh_prefill(zrh_backend* b, const uint32_t* tokens, int n, float* logi
     const int start = n > window ? n - window : 0;
     b->kv.base_position = start;
     b->position = start;
-    const int ql = n - start;
+    // prompts longer than the context's row capacity run as causal chunks
+    // with the earlier chunks as cached prefix (the same attention rows)
+    const int cap = std::max(b->ctx->desc.max_tokens, 1);
     uint32_t tok;
-    zr_status rc = run_mixed(&b, 1, &ql, tokens + start, false, greedy ? greedy : &tok, logits, nullptr);
+    zr_status rc = ZR_OK;
+    for (int off = start; off < n && !rc; off += cap) {
+        const int ql = std::min(cap, n - off);
+        const bool last = off + ql >= n;
+        rc = run_mixed(&b, 1, &ql, tokens + off, false, last && greedy ? greedy : &tok, last ? logits : nullptr,
+                       nullptr);
+    }
     if (rc) {
         b->kv = saved;
         b->position = saved_pos;

@@ -1,0 +1,191 @@
+"""Decode under KV-cache pressure: session churn, eviction and restore.
+
+The caller side of the provider for the soak configuration (a page pool
+smaller than the sessions' total KV): sessions join (Poisson arrivals) and
+leave (per-step probability), and when the pool cannot hold the next decode
+step the planner evicts sessions the way the reference coordinator does and
+restores them when pages free up.
+
+* Eviction = checkpoint + removal (coordinator.rs:871-894): the session's KV
+  is exported with the segmented retention window (export_kv_cache with
+  max_cached_tokens, forward_pass.rs:2442-2448 -> 1169-1204; the newest
+  `retention` rows) and its pages go back to the pool.
+* Candidate order = select_eviction_candidate (coordinator.rs:937-990) for
+  the default ThroughputFirst mode (api/types.rs:117-121) with every session
+  active and recently used: fewest decode steps served first, then the
+  larger KV footprint.
+* Restore = import_kv_cache (forward_pass.rs:2450-2454 -> 1206-1242): clear,
+  scatter the window into fresh pages, continue at the saved position.
+"""
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass, field
+from typing import Callable, List, Optional
+
+import numpy as np
+
+from .provider import BackendMicrobatchExecutor, DecodeMicrobatchRequest, DeviceContext, KVCacheSnapshot
+
+
+@dataclass
+class SoakSession:
+    sid: int
+    token: int
+    backend: object = None              # RocmExecutionBackend while resident
+    snapshot: Optional[KVCacheSnapshot] = None  # while evicted
+    steps_served: int = 0
+
+
+@dataclass
+class SoakStats:
+    steps: int = 0
+    tokens: int = 0
+    joins: int = 0
+    leaves: int = 0
+    evictions: int = 0
+    restores: int = 0
+    decode_s: float = 0.0
+    evict_s: float = 0.0
+    restore_s: float = 0.0
+    admit_s: float = 0.0
+    wall_s: float = 0.0
+    active_hist: List[int] = field(default_factory=list)
+
+
+class KvPressureSoak:
+    """Runs decode steps over a churning session set on one DeviceContext.
+
+    `admit(session, context_len, rng)` fills a new session's KV through
+    session.backend (a prefill, or a page reservation standing in for one) and
+    returns its first token.  `on_evict(session)` sees each eviction after the
+    snapshot is taken; `on_step(sessions, tokens_out, logits)` sees every
+    step before the sessions' tokens advance."""
+
+    def __init__(self, ctx: DeviceContext, *, max_sessions: int, join_rate: float, leave_prob: float,
+                 retention: int, max_seq_len: int, context_sampler: Callable[[np.random.Generator], int],
+                 admit: Callable[[SoakSession, int, np.random.Generator], int], seed: int,
+                 on_step: Optional[Callable[[List[SoakSession], List[int], np.ndarray], None]] = None,
+                 on_evict: Optional[Callable[[SoakSession], None]] = None):
+        self.ctx = ctx
+        self.max_sessions = max_sessions
+        self.join_rate = join_rate
+        self.leave_prob = leave_prob
+        self.retention = retention
+        self.max_seq_len = max_seq_len
+        self.context_sampler = context_sampler
+        self.admit = admit
+        self.on_step = on_step
+        self.on_evict = on_evict
+        self.rng = np.random.default_rng(seed)
+        self.active: List[SoakSession] = []
+        self.evicted: List[SoakSession] = []   # FIFO
+        self.next_sid = 0
+        self.stats = SoakStats()
+
+    # -- pages --------------------------------------------------------------------------
+    @staticmethod
+    def pages_for(rows: int) -> int:
+        return (rows + 15) // 16 + 1  # a partial first page after a window trim
+
+    def _free(self) -> int:
+        return self.ctx.free_pages
+
+    def _evict_one(self, protect: Optional[SoakSession] = None) -> bool:
+        cands = [s for s in self.active if s is not protect]
+        if not cands:
+            return False
+        victim = min(cands, key=lambda s: (s.steps_served, -s.backend.live_kv_cache_bytes(), s.sid))
+        t0 = time.perf_counter()
+        victim.snapshot = victim.backend.export_kv_cache(self.retention)
+        victim.backend.close()  # pages back to the pool
+        victim.backend = None
+        self.stats.evict_s += time.perf_counter() - t0
+        if self.on_evict is not None:
+            self.on_evict(victim)
+        self.active.remove(victim)
+        self.evicted.append(victim)
+        self.stats.evictions += 1
+        return True
+
+    def _make_room(self, pages: int, protect: Optional[SoakSession] = None) -> bool:
+        while self._free() < pages:
+            if not self._evict_one(protect):
+                return False
+        return True
+
+    # -- churn --------------------------------------------------------------------------
+    def add_session(self, context_len: int) -> Optional[SoakSession]:
+        if not self._make_room(self.pages_for(min(context_len, self.max_seq_len))):
+            return None
+        t0 = time.perf_counter()
+        s = SoakSession(self.next_sid, 0, self.ctx.new_backend(self.max_seq_len))
+        self.next_sid += 1
+        s.token = int(self.admit(s, context_len, self.rng))
+        self.stats.admit_s += time.perf_counter() - t0
+        self.active.append(s)
+        return s
+
+    def _leaves(self):
+        for s in list(self.active):
+            if self.rng.random() < self.leave_prob:
+                s.backend.close()
+                self.active.remove(s)
+                self.stats.leaves += 1
+        for s in list(self.evicted):
+            if self.rng.random() < self.leave_prob:
+                self.evicted.remove(s)
+                self.stats.leaves += 1
+
+    def _joins(self):
+        n = int(self.rng.poisson(self.join_rate))
+        for _ in range(n):
+            if len(self.active) + len(self.evicted) >= self.max_sessions:
+                break
+            L = int(self.context_sampler(self.rng))
+            if self.add_session(L) is not None:
+                self.stats.joins += 1
+
+    def _restores(self):
+        # oldest evictions first, while the pool holds them and the next step
+        while self.evicted:
+            s = self.evicted[0]
+            rows = s.snapshot.cached_tokens if s.snapshot is not None else 0
+            if self._free() < self.pages_for(rows) + len(self.active) + 1:
+                break
+            t0 = time.perf_counter()
+            b = self.ctx.new_backend(self.max_seq_len)
+            if s.snapshot is not None:
+                b.import_kv_cache(s.snapshot)
+            s.backend, s.snapshot = b, None
+            self.stats.restore_s += time.perf_counter() - t0
+            self.evicted.pop(0)
+            self.active.append(s)
+            self.stats.restores += 1
+
+    # -- one decode step ----------------------------------------------------------------
+    def step(self, want_logits: bool = False):
+        t_start = time.perf_counter()
+        self._leaves()
+        self._joins()
+        self._restores()
+        # every resident session may open a new page this step
+        self._make_room(len(self.active))
+        if not self.active:
+            return None
+        reqs = [DecodeMicrobatchRequest(str(s.sid), s.token, s.backend) for s in self.active]
+        t0 = time.perf_counter()
+        outs = BackendMicrobatchExecutor.decode_step_batch(reqs, want_logits=want_logits)
+        self.stats.decode_s += time.perf_counter() - t0
+        toks = [o.sampled_token for o in outs]
+        logits = np.stack([o.logits for o in outs]) if want_logits else None
+        if self.on_step is not None:
+            self.on_step(list(self.active), toks, logits)
+        for s, t in zip(self.active, toks):
+            s.token = int(t)
+            s.steps_served += 1
+        self.stats.steps += 1
+        self.stats.tokens += len(toks)
+        self.stats.active_hist.append(len(self.active))
+        self.stats.wall_s += time.perf_counter() - t_start
+        return toks, logits

@@ -340,6 +340,8 @@ class RocmExecutionBackend:
     def export_kv_cache(self, max_cached_tokens: Optional[int] = None) -> Optional[KVCacheSnapshot]:
         geo = self.ctx.geo
         n = self.cache_seq_len()
+        if max_cached_tokens is not None:
+            n = min(n, max(int(max_cached_tokens), 1))
         k = np.zeros((geo.num_layers, max(n, 1), geo.kv_cols), np.float32)
         v = np.zeros_like(k)
         rows, base, nxt = C.c_int(), C.c_int(), C.c_int()
