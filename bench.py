@@ -97,44 +97,63 @@ def step_bytes(geo, batch, kv_rows_total):
     return weights + 2 * batch * H + kv + act
 
 
+def device_model(name, split=True, max_tokens=None, max_seqs=None):
+    """A DeviceContext holding the workload's model with random-init bf16
+    N(0, 0.02) weights generated on the device (RMSNorm gains 1)."""
+    from mesh_amd import DeviceContext, ModelGeometry, _lib
+
+    w = WORKLOADS[name]
+    g = ModelGeometry(**w["geo"])
+    B = w["batch"]
+    ctx = DeviceContext(g, kv_dtype="bf16", max_tokens=max_tokens or B, max_seqs=max_seqs or B,
+                        max_pages_per_seq=w["max_seq_len"] // 16 + 2, split_activations=split)
+    lib = ctx.lib
+
+    def dev(nbytes):
+        p = C.c_void_p()
+        ctx.check(lib.zr_device_alloc(ctx.h, int(nbytes), C.byref(p)))
+        return p.value
+
+    H, Q, KV, F, V = g.hidden, g.q_cols, g.kv_cols, g.ffn_cols, g.vocab
+    shapes = dict(w_q=(H, Q), w_k=(H, KV), w_v=(H, KV), w_o=(Q, H), w_gate=(H, F), w_up=(H, F), w_down=(F, H))
+    bufs = {k: dev(2 * a * b) for k, (a, b) in shapes.items()}
+    ones = np.ones(H, np.float32)
+    for layer in range(g.num_layers):
+        for i, (k, (a, b)) in enumerate(shapes.items()):
+            ctx.check(lib.zr_fill_normal_bf16(ctx.h, bufs[k], a * b, 1000 * layer + i + 1, 0.02))
+        lw = _lib.LayerWeights()
+        for k in shapes:
+            setattr(lw, k, C.cast(bufs[k], _lib.c_u16_p))
+        lw.attn_norm = ones.ctypes.data_as(_lib.c_f32_p)
+        lw.mlp_norm = ones.ctypes.data_as(_lib.c_f32_p)
+        ctx.check(lib.zr_upload_layer(ctx.h, layer, C.byref(lw)))
+    for b in bufs.values():
+        lib.zr_device_free(ctx.h, b)
+    emb, head = dev(2 * V * H), dev(2 * H * V)
+    ctx.check(lib.zr_fill_normal_bf16(ctx.h, emb, V * H, 777, 0.02))
+    ctx.check(lib.zr_fill_normal_bf16(ctx.h, head, H * V, 778, 0.02))
+    ctx.check(lib.zr_upload_globals(ctx.h, C.cast(emb, _lib.c_u16_p), ones.ctypes.data_as(_lib.c_f32_p),
+                                    C.cast(head, _lib.c_u16_p)))
+    lib.zr_device_free(ctx.h, emb)
+    lib.zr_device_free(ctx.h, head)
+    return ctx, g
+
+
 class GpuDecodeBench:
     """One workload resident on the GPU with `steps_total` decode steps staged."""
 
     def __init__(self, name, steps_total, split=True):
-        from mesh_amd import DeviceContext, ModelGeometry, _lib
+        from mesh_amd import _lib
 
         self._lib = _lib
         w = WORKLOADS[name]
         self.name, self.w = name, w
-        self.geo = g = ModelGeometry(**w["geo"])
         self.B = w["batch"]
         self.ctxlens = w["contexts"]()
         self.max_seq = w["max_seq_len"]
-        self.ctx = DeviceContext(g, kv_dtype="bf16", max_tokens=self.B, max_seqs=self.B,
-                                 max_pages_per_seq=self.max_seq // 16 + 2, split_activations=split)
-        ctx, lib = self.ctx, self.ctx.lib
-        H, Q, KV, F, V = g.hidden, g.q_cols, g.kv_cols, g.ffn_cols, g.vocab
-        shapes = dict(w_q=(H, Q), w_k=(H, KV), w_v=(H, KV), w_o=(Q, H), w_gate=(H, F), w_up=(H, F), w_down=(F, H))
-        bufs = {k: self._dev(2 * a * b) for k, (a, b) in shapes.items()}
-        ones = np.ones(H, np.float32)
-        for layer in range(g.num_layers):
-            for i, (k, (a, b)) in enumerate(shapes.items()):
-                ctx.check(lib.zr_fill_normal_bf16(ctx.h, bufs[k], a * b, 1000 * layer + i + 1, 0.02))
-            lw = _lib.LayerWeights()
-            for k in shapes:
-                setattr(lw, k, C.cast(bufs[k], _lib.c_u16_p))
-            lw.attn_norm = ones.ctypes.data_as(_lib.c_f32_p)
-            lw.mlp_norm = ones.ctypes.data_as(_lib.c_f32_p)
-            ctx.check(lib.zr_upload_layer(ctx.h, layer, C.byref(lw)))
-        for b in bufs.values():
-            lib.zr_device_free(ctx.h, b)
-        emb, head = self._dev(2 * V * H), self._dev(2 * H * V)
-        ctx.check(lib.zr_fill_normal_bf16(ctx.h, emb, V * H, 777, 0.02))
-        ctx.check(lib.zr_fill_normal_bf16(ctx.h, head, H * V, 778, 0.02))
-        ctx.check(lib.zr_upload_globals(ctx.h, C.cast(emb, _lib.c_u16_p), ones.ctypes.data_as(_lib.c_f32_p),
-                                        C.cast(head, _lib.c_u16_p)))
-        lib.zr_device_free(ctx.h, emb)
-        lib.zr_device_free(ctx.h, head)
+        self.ctx, self.geo = device_model(name, split)
+        ctx, lib, g = self.ctx, self.ctx.lib, self.geo
+        V = g.vocab
         # KV pool: every session's context plus the benchmarked steps
         pages = int(sum((min(int(L) + steps_total, self.max_seq) + 15) // 16 + 1 for L in self.ctxlens))
         ctx.create_kv_pool(pages)
@@ -289,6 +308,60 @@ def cpu_baseline(name):
                        f"(T2 - T1) = {step_s:.2f} s; f32 weights/KV as the reference CPU provider")
 
 
+SOAK = dict(workload="llama3_8b_b256", pool_frac=0.85, join_rate=4.0, leave_prob=1 / 64, retention=2048,
+            max_sessions=256, seed=0xC5)
+
+
+def measure_soak(steps, warmup):
+    """Decode steps of the Llama-3-8B-shape model under KV pressure: the page
+    pool holds 85% of the 256 sessions' lognormal contexts; Poisson joins
+    (4 per step), leaves (1/64 per session per step), eviction through the
+    2048-token segmented-window export and restore through import
+    (mesh_amd.kv_pressure).  A joining session's context pages are reserved
+    and hold the pool's synthetic values (standing in for its prefill).
+    value = decoded tokens / wall time of the steps, host path included."""
+    from mesh_amd.kv_pressure import KvPressureSoak
+
+    w = WORKLOADS[SOAK["workload"]]
+    ctx, g = device_model(SOAK["workload"])
+    ctxlens = w["contexts"]()
+    need = int(sum((int(L) + 15) // 16 for L in ctxlens))
+    pool = int(SOAK["pool_frac"] * need)
+    ctx.create_kv_pool(pool)
+    ctx.check(ctx.lib.zr_kv_pool_fill_normal(ctx.h, 4242, 1.0))
+
+    def sample_len(rng):
+        return int(np.clip(np.round(rng.lognormal(math.log(1024), 1.0)), 64, 8192))
+
+    def admit(s, L, rng):
+        s.backend.kv_reserve(L)
+        return int(rng.integers(0, g.vocab))
+
+    soak = KvPressureSoak(ctx, max_sessions=SOAK["max_sessions"], join_rate=SOAK["join_rate"],
+                          leave_prob=SOAK["leave_prob"], retention=SOAK["retention"],
+                          max_seq_len=w["max_seq_len"], context_sampler=sample_len, admit=admit, seed=SOAK["seed"])
+    for L in ctxlens:
+        soak.add_session(int(L))
+    for _ in range(warmup):
+        soak.step()
+    st0 = dict(vars(soak.stats))
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        soak.step()
+    dt = time.perf_counter() - t0
+    st = soak.stats
+    d = lambda k: getattr(st, k) - st0[k]
+    out = dict(value=d("tokens") / dt, unit="tokens/s", steps=steps, pool_pages=pool, pool_frac_of_need=pool / need,
+               mean_active=float(np.mean(st.active_hist[-steps:])), joins=d("joins"), leaves=d("leaves"),
+               evictions=d("evictions"), restores=d("restores"), ms_per_step=dt / steps * 1e3,
+               ms_per_step_decode=d("decode_s") / steps * 1e3, ms_per_step_evict=d("evict_s") / steps * 1e3,
+               ms_per_step_restore=d("restore_s") / steps * 1e3, ms_per_step_admit=d("admit_s") / steps * 1e3,
+               workload="Llama-3-8B-shape decode under KV pressure: pool 85% of 256 lognormal contexts, Poisson "
+                        "joins 4/step, leave 1/64, evict/restore via 2048-token window export/import")
+    ctx.close()
+    return out
+
+
 def calibrate_copy():
     """One plain device-to-device copy of 1 GiB (torch), the reference point
     for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE counters."""
@@ -312,6 +385,7 @@ def main():
     ap.add_argument("--skip-bs32", action="store_true")
     ap.add_argument("--workload", default="llama3_8b_b256", choices=sorted(WORKLOADS))
     ap.add_argument("--calibrate-copy", action="store_true")
+    ap.add_argument("--soak", action="store_true", help="also run the KV-pressure soak leg")
     a = ap.parse_args()
     if a.calibrate_copy:
         calibrate_copy()
@@ -333,6 +407,7 @@ def main():
                     workload=r["workload"], step_roofline_frac=r["step_roofline_frac"],
                     attention_gbs=r["attention"]["achieved_gbs"], kernel_ms_per_step=r["kernel_ms_per_step"],
                     gemm_tflops=r["gemm"]["achieved_tflops"], gemm_weight_gbs=r["gemm"]["weight_gbs"])
+    soak = measure_soak(max(4, a.steps // 2), 2) if a.soak else None
     cpu = None if a.skip_cpu else cpu_baseline(a.workload)
     att = main_r["attention"]
     line = {
@@ -356,6 +431,7 @@ def main():
                       "unit": "TFLOP/s", "frac": main_r["gemm"]["frac"], "mfma_ops_per_flop": 2,
                       "weight_stream_gbs": main_r["gemm"]["weight_gbs"]},
         "bs32": bs32,
+        "soak": soak,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

@@ -202,6 +202,11 @@ zr_status zr_gemm(zr_context* ctx, const float* d_a, const uint16_t* w, float* d
 /* --------------------------------------------------------- device memory --- */
 zr_status zr_device_alloc(zr_context* ctx, size_t bytes, void** out);
 zr_status zr_device_free(zr_context* ctx, void* p);
+/* Pinned host memory (hipHostMalloc), e.g. for KV snapshots that move over
+ * PCIe at full rate.  No reference counterpart (the reference keeps snapshots
+ * in pageable Rust vectors). */
+zr_status zr_host_alloc(zr_context* ctx, size_t bytes, void** out);
+zr_status zr_host_free(zr_context* ctx, void* p);
 zr_status zr_memcpy_h2d(zr_context* ctx, void* dst, const void* src, size_t bytes);
 zr_status zr_memcpy_d2h(zr_context* ctx, void* dst, const void* src, size_t bytes);
 /* Fills device bf16 [n] with N(0, std) draws (Box-Muller over a counter-based

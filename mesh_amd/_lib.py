@@ -90,6 +90,8 @@ SIGNATURES = [
     ("zr_gemm", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),
     ("zr_device_alloc", C.c_int, [C.c_void_p, C.c_size_t, c_void_pp]),
     ("zr_device_free", C.c_int, [C.c_void_p, C.c_void_p]),
+    ("zr_host_alloc", C.c_int, [C.c_void_p, C.c_size_t, C.POINTER(C.c_void_p)]),
+    ("zr_host_free", C.c_int, [C.c_void_p, C.c_void_p]),
     ("zr_memcpy_h2d", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]),
     ("zr_memcpy_d2h", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]),
     ("zr_fill_normal_bf16", C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_uint64, C.c_float]),

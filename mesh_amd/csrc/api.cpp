@@ -481,6 +481,7 @@ void zr_context_destroy(zr_context* ctx) {
         delete ctx->scratch_stage;
     }
     for (hipEvent_t e : ctx->timing.pool) hipEventDestroy(e);
+    if (ctx->kv_stage) (void)hipFree(ctx->kv_stage);
     free_ctx_buffers(ctx);
     if (ctx->stream) hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -698,13 +699,20 @@ static zr_status kv_copy_entry(zr_context* ctx, const int* block_table, int n_pa
     ZR_HIP(ctx, hipSetDevice(ctx->device));
     const int L = ctx->desc.num_layers;
     const size_t elems = (size_t)L * n_rows * ctx->kv_cols;
-    int* d_table = nullptr;
-    float* d_k = nullptr;
-    float* d_v = nullptr;
-    hipError_t e = hipMalloc(&d_table, 4 * (size_t)n_pages);
-    if (e == hipSuccess) e = hipMalloc(&d_k, 4 * elems);
-    if (e == hipSuccess) e = hipMalloc(&d_v, 4 * elems);
-    if (e == hipSuccess) e = hipMemcpyAsync(d_table, block_table, 4 * (size_t)n_pages, hipMemcpyHostToDevice, ctx->stream);
+    // persistent staging (grown on demand): the table and the K / V rows
+    const size_t need = 2 * elems + (size_t)n_pages;
+    if (need > ctx->kv_stage_floats) {
+        ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        if (ctx->kv_stage) (void)hipFree(ctx->kv_stage);
+        ctx->kv_stage = nullptr;
+        ctx->kv_stage_floats = 0;
+        ZR_HIP(ctx, hipMalloc(&ctx->kv_stage, need * sizeof(float)));
+        ctx->kv_stage_floats = need;
+    }
+    float* d_k = ctx->kv_stage;
+    float* d_v = d_k + elems;
+    int* d_table = (int*)(d_v + elems);
+    hipError_t e = hipMemcpyAsync(d_table, block_table, 4 * (size_t)n_pages, hipMemcpyHostToDevice, ctx->stream);
     if (e == hipSuccess && to_pool) e = hipMemcpyAsync(d_k, k, 4 * elems, hipMemcpyDefault, ctx->stream);
     if (e == hipSuccess && to_pool) e = hipMemcpyAsync(d_v, v, 4 * elems, hipMemcpyDefault, ctx->stream);
     zr_status rc = e == hipSuccess ? ZR_OK : set_err(ctx, ZR_E_HIP, "kv copy staging: %s", hipGetErrorString(e));
@@ -716,9 +724,6 @@ static zr_status kv_copy_entry(zr_context* ctx, const int* block_table, int n_pa
     }
     e = hipStreamSynchronize(ctx->stream);
     if (!rc && e != hipSuccess) rc = set_err(ctx, ZR_E_HIP, "kv copy: %s", hipGetErrorString(e));
-    hipFree(d_table);
-    hipFree(d_k);
-    hipFree(d_v);
     return rc;
 }
 
@@ -810,6 +815,23 @@ zr_status zr_device_alloc(zr_context* ctx, size_t bytes, void** out) {
     hipError_t e = hipMalloc(out, bytes ? bytes : 1);
     if (e != hipSuccess) return set_err(ctx, e == hipErrorOutOfMemory ? ZR_E_OOM : ZR_E_HIP, "hipMalloc(%zu): %s",
                                         bytes, hipGetErrorString(e));
+    return ZR_OK;
+}
+
+zr_status zr_host_alloc(zr_context* ctx, size_t bytes, void** out) {
+    if (!ctx || !out) return set_global_err(ZR_E_INVALID, "null argument");
+    *out = nullptr;
+    ZR_HIP(ctx, hipSetDevice(ctx->device));
+    void* p = nullptr;
+    hipError_t e = hipHostMalloc(&p, bytes > 0 ? bytes : 1, hipHostMallocDefault);
+    if (e != hipSuccess) return set_err(ctx, ZR_E_OOM, "hipHostMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    *out = p;
+    return ZR_OK;
+}
+
+zr_status zr_host_free(zr_context* ctx, void* p) {
+    if (!ctx) return set_global_err(ZR_E_INVALID, "null context");
+    if (p) ZR_HIP(ctx, hipHostFree(p));
     return ZR_OK;
 }
 

@@ -102,6 +102,8 @@ struct zr_context {
     size_t argmax_ws_floats = 0;
 
     zr::StagedMeta* scratch_stage = nullptr;  // reused by zr_forward
+    float* kv_stage = nullptr;      // KV gather / scatter staging (rows + table)
+    size_t kv_stage_floats = 0;
     zr::TimingState timing;
 };
 

@@ -80,6 +80,7 @@ class KvPressureSoak:
         self.rng = np.random.default_rng(seed)
         self.active: List[SoakSession] = []
         self.evicted: List[SoakSession] = []   # FIFO
+        self.free_pinned: list = []             # snapshot buffers of restored sessions, reused
         self.next_sid = 0
         self.stats = SoakStats()
 
@@ -97,7 +98,10 @@ class KvPressureSoak:
             return False
         victim = min(cands, key=lambda s: (s.steps_served, -s.backend.live_kv_cache_bytes(), s.sid))
         t0 = time.perf_counter()
-        victim.snapshot = victim.backend.export_kv_cache(self.retention)
+        buf = self.free_pinned.pop() if self.free_pinned else None
+        victim.snapshot = victim.backend.export_kv_cache(self.retention, pinned=True, into=buf)
+        if buf is not None and (victim.snapshot is None or victim.snapshot.storage is not buf):
+            self.free_pinned.append(buf)
         victim.backend.close()  # pages back to the pool
         victim.backend = None
         self.stats.evict_s += time.perf_counter() - t0
@@ -157,6 +161,8 @@ class KvPressureSoak:
             b = self.ctx.new_backend(self.max_seq_len)
             if s.snapshot is not None:
                 b.import_kv_cache(s.snapshot)
+                if s.snapshot.storage is not None:
+                    self.free_pinned.append(s.snapshot.storage)
             s.backend, s.snapshot = b, None
             self.stats.restore_s += time.perf_counter() - t0
             self.evicted.pop(0)
@@ -167,8 +173,8 @@ class KvPressureSoak:
     def step(self, want_logits: bool = False):
         t_start = time.perf_counter()
         self._leaves()
+        self._restores()  # evicted sessions resume before new ones are admitted
         self._joins()
-        self._restores()
         # every resident session may open a new page this step
         self._make_room(len(self.active))
         if not self.active:

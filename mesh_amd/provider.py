@@ -81,6 +81,35 @@ def bf16_bits(x: np.ndarray) -> np.ndarray:
     return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
 
 
+class PinnedBuffer:
+    """Pinned host memory of a context (zr_host_alloc), viewed as numpy."""
+
+    def __init__(self, ctx: "DeviceContext", nbytes: int):
+        self.ctx = ctx
+        p = C.c_void_p()
+        ctx.check(ctx.lib.zr_host_alloc(ctx.h, int(nbytes), C.byref(p)))
+        self.ptr = p.value
+        self.nbytes = int(nbytes)
+        ctx._pinned.add(self)
+
+    def array(self, dtype, shape) -> np.ndarray:
+        n = int(np.prod(shape)) * np.dtype(dtype).itemsize
+        assert n <= self.nbytes
+        buf = (C.c_char * n).from_address(self.ptr)
+        return np.frombuffer(buf, dtype=dtype).reshape(shape)
+
+    def free(self):
+        if getattr(self, "ptr", None) and self.ctx.h:
+            self.ctx.lib.zr_host_free(self.ctx.h, self.ptr)
+        self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 class DeviceBuffer:
     """Device memory owned by a context (zr_device_alloc)."""
 
@@ -180,10 +209,13 @@ class DeviceContext:
         self.h = h.value
         self.pool = None
         self._backends = weakref.WeakSet()
+        self._pinned = weakref.WeakSet()
 
     def close(self):
         for b in list(getattr(self, "_backends", ())):
             b.close()
+        for p in list(getattr(self, "_pinned", ())):
+            p.free()
         if getattr(self, "pool", None) is not None:
             self.lib.zrh_pool_destroy(self.pool)
             self.pool = None
@@ -263,6 +295,7 @@ class KVCacheSnapshot:
     cached_tokens: int
     keys: np.ndarray    # [layers, cached_tokens, kv_cols] f32
     values: np.ndarray
+    storage: object = field(default=None, repr=False, compare=False)  # pinned owner, if any
 
     def first_cached_position(self) -> int:
         return self.next_position - self.cached_tokens
@@ -337,23 +370,39 @@ class RocmExecutionBackend:
     def allocated_pages(self) -> int:
         return self.lib.zrh_allocated_pages(self.h)
 
-    def export_kv_cache(self, max_cached_tokens: Optional[int] = None) -> Optional[KVCacheSnapshot]:
+    def export_kv_cache(self, max_cached_tokens: Optional[int] = None, pinned: bool = False,
+                        into: Optional[PinnedBuffer] = None) -> Optional[KVCacheSnapshot]:
+        """export_kv_cache (backend.rs:73): the newest `max_cached_tokens` rows
+        (all when None) of every layer as f32.  With `pinned`, the snapshot's
+        arrays live in pinned host memory (full-rate PCIe copies): in `into`
+        when it is large enough, else in a new PinnedBuffer."""
         geo = self.ctx.geo
         n = self.cache_seq_len()
         if max_cached_tokens is not None:
             n = min(n, max(int(max_cached_tokens), 1))
-        k = np.zeros((geo.num_layers, max(n, 1), geo.kv_cols), np.float32)
-        v = np.zeros_like(k)
+        shape = (geo.num_layers, max(n, 1), geo.kv_cols)
+        owner = None
+        if pinned:
+            need = 2 * 4 * int(np.prod(shape))
+            owner = into if into is not None and into.ptr and into.nbytes >= need else PinnedBuffer(self.ctx, need)
+            both = owner.array(np.float32, (2,) + shape)
+            k, v = both[0], both[1]
+        else:
+            k = np.zeros(shape, np.float32)
+            v = np.zeros_like(k)
         rows, base, nxt = C.c_int(), C.c_int(), C.c_int()
         self.ctx.check(self.lib.zrh_export_kv(self.h, -1 if max_cached_tokens is None else int(max_cached_tokens),
                                               _ptr(k, C.c_float), _ptr(v, C.c_float), C.byref(rows),
                                               C.byref(base), C.byref(nxt)))
         r = rows.value
         if r == 0:
+            if owner is not None:
+                owner.free()
             return None
-        flat = geo.num_layers * r * geo.kv_cols
-        return KVCacheSnapshot(nxt.value, r, k.reshape(-1)[:flat].reshape(geo.num_layers, r, geo.kv_cols).copy(),
-                               v.reshape(-1)[:flat].reshape(geo.num_layers, r, geo.kv_cols).copy())
+        assert r == n
+        if owner is not None:
+            return KVCacheSnapshot(nxt.value, r, k, v, owner)
+        return KVCacheSnapshot(nxt.value, r, k, v)
 
     def import_kv_cache(self, snap: KVCacheSnapshot):
         k = np.ascontiguousarray(snap.keys, np.float32)
