@@ -9,7 +9,8 @@ import ctypes as C
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libzip_rocm.so")
+# ZR_LIBRARY may name another build of the same library (A/B measurements)
+LIB_PATH = os.environ.get("ZR_LIBRARY") or os.path.join(HERE, "libzip_rocm.so")
 
 c_int_p = C.POINTER(C.c_int)
 c_u32_p = C.POINTER(C.c_uint32)

@@ -431,11 +431,15 @@ zr_status zr_context_create(const zr_model_desc* desc, int device, zr_context** 
         void** p;
         size_t bytes;
     } allocs[] = {
-        {(void**)&ctx->hidden, 4 * T * H},           {(void**)&ctx->xa, 2 * 2 * T * H},
+        {(void**)&ctx->hidden, 4 * T * H},
+        {(void**)&ctx->xa, 2 * 2 * a_plane((int)T, (int)H)},
         {(void**)&ctx->qkv, 4 * T * (Q + 2 * KV)},   {(void**)&ctx->q_rope, 4 * T * Q},
-        {(void**)&ctx->attn_a, 2 * 2 * T * Q},       {(void**)&ctx->proj, 4 * T * H},
-        {(void**)&ctx->ffn_a, 2 * 2 * T * F},        {(void**)&ctx->logits, 4 * S * d.vocab},
-        {(void**)&ctx->final_a, 2 * 2 * S * H},      {(void**)&ctx->tokens_out, 4 * S},
+        {(void**)&ctx->attn_a, 2 * 2 * a_plane((int)T, (int)Q)},
+        {(void**)&ctx->proj, 4 * T * H},
+        {(void**)&ctx->ffn_a, 2 * 2 * a_plane((int)T, (int)F)},
+        {(void**)&ctx->logits, 4 * S * d.vocab},
+        {(void**)&ctx->final_a, 2 * 2 * a_plane((int)S, (int)H)},
+        {(void**)&ctx->tokens_out, 4 * S},
         {(void**)&ctx->inv_freq, 4 * (size_t)ctx->head_dim / 2},
     };
     for (auto& a : allocs) {
@@ -783,12 +787,19 @@ zr_status zr_gemm(zr_context* ctx, const float* d_a, const uint16_t* w, float* d
     zr_status rc = pack_weight(ctx, w, k, n, &packed);
     if (rc) return rc;
     const int lo = (ctx->desc.flags & ZR_FLAG_SPLIT_ACTIVATIONS) ? 1 : 0;
-    const size_t need = gemm_ws_floats(m, n, k, kEpiStore);
+    const int kp = (k + 31) / 32 * 32;  // the packed weights are zero beyond k
+    const size_t need = gemm_ws_floats(m, n, kp, kEpiStore);
     float* saved_ws = ctx->splitk_ws;
     size_t saved_n = ctx->splitk_ws_floats;
     float* tmp_ws = nullptr;
+    float* a_pad = nullptr;
     uint16_t* a16 = nullptr;
-    hipError_t e = hipMalloc(&a16, (size_t)2 * 2 * m * k);
+    hipError_t e = hipMalloc(&a16, (size_t)2 * 2 * a_plane(m, kp));
+    if (e == hipSuccess) e = hipMalloc(&a_pad, (size_t)4 * m * kp);
+    if (e == hipSuccess) e = hipMemsetAsync(a_pad, 0, (size_t)4 * m * kp, ctx->stream);
+    if (e == hipSuccess)
+        e = hipMemcpy2DAsync(a_pad, 4 * (size_t)kp, d_a, 4 * (size_t)k, 4 * (size_t)k, m, hipMemcpyDeviceToDevice,
+                             ctx->stream);
     if (e == hipSuccess && need > saved_n) {
         e = hipMalloc(&tmp_ws, need * 4);
         if (e == hipSuccess) {
@@ -797,15 +808,16 @@ zr_status zr_gemm(zr_context* ctx, const float* d_a, const uint16_t* w, float* d
         }
     }
     if (e != hipSuccess) rc = set_err(ctx, ZR_E_OOM, "gemm workspace: %s", hipGetErrorString(e));
-    if (!rc) rc = launch_to_bf16_pair(ctx, d_a, (size_t)m * k, a16, lo);
-    if (!rc) rc = launch_gemm(ctx, a16, packed, d_c, nullptr, m, n, k, kEpiStore);
+    if (!rc) rc = launch_to_bf16_pair(ctx, a_pad, m, kp, a16, lo);
+    if (!rc) rc = launch_gemm(ctx, a16, packed, d_c, nullptr, m, n, kp, kEpiStore);
     e = hipStreamSynchronize(ctx->stream);
     if (!rc && e != hipSuccess) rc = set_err(ctx, ZR_E_HIP, "gemm: %s", hipGetErrorString(e));
     ctx->splitk_ws = saved_ws;
     ctx->splitk_ws_floats = saved_n;
-    if (tmp_ws) hipFree(tmp_ws);
-    if (a16) hipFree(a16);
-    hipFree(packed);
+    if (tmp_ws) (void)hipFree(tmp_ws);
+    if (a_pad) (void)hipFree(a_pad);
+    if (a16) (void)hipFree(a16);
+    (void)hipFree(packed);
     return rc;
 }
 

@@ -293,21 +293,21 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
     if (a.tiles[it.x + 1].w - tl.w == 1) {
         // the tile has one split: normalise and write the final output here
         const int row = a.cu_q[seq] + q0 + qi;
-        const size_t ob = (size_t)row * a.q_cols + (size_t)(kvh * a.G + g) * D;
         const float inv = 1.0f / lsum;
 #pragma unroll
         for (int db = 0; db < D / 16; ++db)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const size_t o_idx = ob + db * 16 + q4 * 4 + i;
+                const int col = (kvh * a.G + g) * D + db * 16 + q4 * 4 + i;
                 const float v = o[db][i] * inv;
                 if (a.out_bf16) {
                     uint16_t hi, lo;
                     split_bf16(v, hi, lo);
+                    const size_t o_idx = a_pack_index(row, col, a.q_cols);
                     a.out_bf16[o_idx] = hi;
                     if (a.out_lo_offset) a.out_bf16[a.out_lo_offset + o_idx] = lo;
                 } else {
-                    a.out_f32[o_idx] = v;
+                    a.out_f32[(size_t)row * a.q_cols + col] = v;
                 }
             }
         return;
@@ -416,14 +416,15 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(const float* __res
         if (c >= ncols) continue;
         const int qi = c / G, g = c - qi * G;
         const int row = cu_q[seq] + q0 + qi;
-        const size_t o = (size_t)row * q_cols + (size_t)(kvh * G + g) * D + d;
+        const int col = (kvh * G + g) * D + d;
         if (out_bf16) {
             uint16_t hi, lo;
             split_bf16(acc[j], hi, lo);
+            const size_t o = a_pack_index(row, col, q_cols);
             out_bf16[o] = hi;
             if (lo_offset) out_bf16[lo_offset + o] = lo;
         } else {
-            out[o] = acc[j];
+            out[(size_t)row * q_cols + col] = acc[j];
         }
     }
 }
@@ -450,7 +451,7 @@ static zr_status launch_attn_t(zr_context* ctx, StagedMeta* st, int layer, const
     a.part = ctx->attn_part;
     a.out_f32 = out;
     a.out_bf16 = out_bf16;
-    a.out_lo_offset = (ctx->desc.flags & ZR_FLAG_SPLIT_ACTIVATIONS) ? (size_t)st->total_q * ctx->q_cols : 0;
+    a.out_lo_offset = (ctx->desc.flags & ZR_FLAG_SPLIT_ACTIVATIONS) ? a_plane(st->total_q, ctx->q_cols) : 0;
     hipEvent_t ev;
     timing_mark_begin(ctx, kClassAttention, &ev);
     // bf16 pages: a 6-page ring, one wave per SIMD (measured: a 4-page ring

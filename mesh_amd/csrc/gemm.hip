@@ -7,8 +7,9 @@
 // j < 8, stored contiguously; fragments of one 32-column tile are consecutive
 // along K (kt16 < 2 ceil(K / 32), zero padded).  A wavefront streams its
 // weights as perfectly coalesced 1 KiB loads.
-// A (activations) arrives as bf16 [M, K] -- or a hi + lo bf16 pair under
-// ZR_FLAG_SPLIT_ACTIVATIONS -- written by the producing kernel.
+// A (activations) arrives fragment-packed (a_pack_index: 1 KiB fragments of
+// 32 rows x 16 columns) as bf16 -- or a hi + lo bf16 pair under
+// ZR_FLAG_SPLIT_ACTIVATIONS -- written that way by the producing kernel.
 // Matmul semantics: forward_pass.rs:1696-1714 (w_qkv / w_gate_up column
 // concatenations), 2265 (O), 2290 (down), 2311 (LM head); f32 accumulation.
 // The gate|up concatenation is interleaved per 32 columns so one 64-column
@@ -134,30 +135,31 @@ __device__ __forceinline__ void ring_barrier() {
 // + j]; the product lane l, element i is C[8 (i / 4) + 4 (l / 32) + i % 4][l % 32].
 // Block tile BM x BN = (32 WAVES_M WM) x (32 WAVES_N WN); wave tile
 // (32 WM) x (32 WN); a k-step covers 32 of K (two MFMA k-halves).
-// A (activations) goes global -> LDS with `global_load_lds_dwordx4` (no
-// registers): every 1 KiB MFMA fragment of a k-step -- A rows, hi then lo --
-// is one wave instruction, spread evenly over the block's waves.  The
-// weights either take the same path (BDIRECT = 0) or stream straight into a
-// per-wave register ring (BDIRECT = 1).  STAGES-deep ring: the copies of
-// stage i + STAGES - 1 are issued at step i, A and B together, so waiting
-// (vmcnt, in order) for stage i's A also covers its B.  At step i a wave
-// waits for its own copies of stage i, the block barrier publishes the
-// stage to every wave and retires the slot read at step i - 1.  The compiler
-// does not order LDS reads after these copies, hence the explicit waits.
+// Both operands go global -> LDS with `global_load_lds_dwordx4` (no
+// registers): every 1 KiB MFMA fragment of a k-step -- A rows (hi, then lo)
+// and weight tiles -- is one wave instruction, spread evenly over the
+// block's waves.  STAGES-deep ring: the copies of stage i + STAGES - 1 are
+// issued at step i; at step i a wave waits (vmcnt) for its own copies of
+// stage i, the block barrier publishes the stage to every wave and retires
+// the slot read at step i - 1.  The compiler does not order LDS reads after
+// these copies, hence the explicit waits.  (Measured on the decode shapes:
+// streaming the weights into per-wave registers instead, or reading all of
+// a k-step's fragments before its MFMAs, or two k-steps per stage, are each
+// slower.)
 // Grid: 1-D, decoded so that the row blocks of one (column block, split)
 // pair are dispatched 8 apart -- on the same XCD, one after the other -- and
 // share that weight tile through its L2.
-template <int WM, int WN, int WAVES_M, int WAVES_N, int HL, int STAGES, int BDIRECT>
+template <int WM, int WN, int WAVES_M, int WAVES_N, int HL, int STAGES>
 __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_kernel(
     const uint16_t* __restrict__ A, int M, int K, const bf16x8* __restrict__ Wp, int KT, int NT,
     float* __restrict__ C, int N, int kt_per_split, int splits, int row_blocks, int col_blocks,
     size_t split_stride) {
     constexpr int NW = WAVES_M * WAVES_N;
     constexpr int BMT = WAVES_M * WM, BNT = WAVES_N * WN;
-    constexpr int FA = HL * BMT * 2, FB = BDIRECT ? 0 : BNT * 2, FS = FA + FB;
+    constexpr int FA = HL * BMT * 2, FB = BNT * 2, FS = FA + FB;
     constexpr int PW = (FS + NW - 1) / NW;  // LDS copies per wave per stage
     constexpr int FSP = PW * NW;            // fragments per stage incl. padding
-    constexpr int VM = PW + (BDIRECT ? 2 * WN : 0);  // vector-memory ops per wave per stage
+    constexpr int VM = PW;                  // vector-memory ops per wave per stage
     static_assert(STAGES >= 2 && STAGES <= 4, "stages");
     static_assert(VM * (STAGES - 2) < 64, "vmcnt range");
     typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
@@ -175,38 +177,27 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_kernel(
     const int m0 = rb * BMT * 32;
     const int nt_blk = cb * BNT;
     const int KT16 = 2 * KT;
+    const int MT = (M + 31) / 32;  // row tiles of the packed A operand
     const int kt_begin = split * kt_per_split;
     const int nsteps = min(KT, kt_begin + kt_per_split) - kt_begin;
-    const size_t MK = (size_t)M * K;
 
-    bf16x8 breg[BDIRECT ? STAGES : 1][2][WN];
-    auto issue = [&](int slot, int bslot, int kt) {
+    auto issue = [&](int slot, int kt) {
 #pragma unroll
         for (int i = 0; i < PW; ++i) {
             int f = i * NW + wave;
             const int fs = f < FS ? f : f - FS;  // padding rows repeat a real fragment
             const void* src;
             if (fs < FA) {
+                // fragment-packed A: row tile (clamped into the operand), k-slice 2 kt + kh
                 const int kh = fs & 1, r = fs >> 1;
-                const int hl = r / BMT, mt = r - hl * BMT;
-                const int row = min(m0 + mt * 32 + (lane & 31), M - 1);
-                const int kc = min(kt * 32 + kh * 16 + (lane >> 5) * 8, K - 8);
-                src = A + (size_t)hl * MK + (size_t)row * K + kc;
+                const int hl = r / BMT, mt = min(m0 / 32 + (r - hl * BMT), MT - 1);
+                src = (const bf16x8*)A + (((size_t)hl * MT + mt) * KT16 + 2 * kt + kh) * 64 + lane;
             } else {
                 const int fb = fs - FA;
                 const int nt = min(nt_blk + (fb >> 1), NT - 1);
                 src = Wp + ((size_t)nt * KT16 + 2 * kt + (fb & 1)) * 64 + lane;
             }
             __builtin_amdgcn_global_load_lds(src, (lds_void*)&lds[slot][f][0], 16, 0, 0);
-        }
-        if (BDIRECT) {
-#pragma unroll
-            for (int wn = 0; wn < WN; ++wn) {
-                const int nt = min(nt_blk + wn_idx * WN + wn, NT - 1);
-#pragma unroll
-                for (int kh = 0; kh < 2; ++kh)
-                    breg[bslot][kh][wn] = Wp[((size_t)nt * KT16 + 2 * kt + kh) * 64 + lane];
-            }
         }
     };
 
@@ -220,7 +211,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_kernel(
 
 #pragma unroll
     for (int s = 0; s < STAGES - 1; ++s)
-        if (s < nsteps) issue(s, BDIRECT ? s : 0, kt_begin + s);
+        if (s < nsteps) issue(s, kt_begin + s);
 
     for (int i0 = 0; i0 < nsteps; i0 += STAGES) {
 #pragma unroll
@@ -235,14 +226,13 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_kernel(
             else
                 ring_barrier<0>();
             const int ns = (u + STAGES - 1) % STAGES;
-            if (i + STAGES - 1 < nsteps) issue(ns, BDIRECT ? ns : 0, kt_begin + i + STAGES - 1);
+            if (i + STAGES - 1 < nsteps) issue(ns, kt_begin + i + STAGES - 1);
 #pragma unroll
             for (int kh = 0; kh < 2; ++kh) {
                 bf16x8 bf[WN];
 #pragma unroll
                 for (int wn = 0; wn < WN; ++wn)
-                    bf[wn] = BDIRECT ? breg[BDIRECT ? u : 0][kh][wn]
-                                     : lds[u][FA + (wn_idx * WN + wn) * 2 + kh][lane];
+                    bf[wn] = lds[u][FA + (wn_idx * WN + wn) * 2 + kh][lane];
 #pragma unroll
                 for (int mt = 0; mt < WM; ++mt)
 #pragma unroll
@@ -298,38 +288,43 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
             v = 0.0f;
             for (int s = 0; s < S; ++s) v += ws[s * split_stride + (size_t)m * N + j];
         }
-        if (out_bf16) {
+        if (out_bf16) {  // fragment-packed A operand of the next GEMM
             uint16_t hi, lo;
             split_bf16(v, hi, lo);
-            out_bf16[idx] = hi;
-            if (out_lo) out_bf16[total + idx] = lo;
+            const size_t o = a_pack_index(m, j, n_out);
+            out_bf16[o] = hi;
+            if (out_lo) out_bf16[a_plane(M, n_out) + o] = lo;
         } else {
             out_f32[idx] = v;
         }
     }
 }
 
-// f32 [M, K] -> bf16 hi (+ lo) [M, K] (A operand of zr_gemm)
-__global__ __launch_bounds__(256) void to_bf16_pair_kernel(const float* __restrict__ x, size_t n,
+// f32 [rows, K] -> fragment-packed bf16 hi (+ lo) (A operand of zr_gemm)
+__global__ __launch_bounds__(256) void to_bf16_pair_kernel(const float* __restrict__ x, int rows, int K,
                                                            uint16_t* __restrict__ out, int with_lo) {
+    const size_t n = (size_t)rows * K, plane = a_plane(rows, K);
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
         uint16_t hi, lo;
         split_bf16(x[i], hi, lo);
-        out[i] = hi;
-        if (with_lo) out[n + i] = lo;
+        const size_t o = a_pack_index((int)(i / K), (int)(i % K), K);
+        out[o] = hi;
+        if (with_lo) out[plane + o] = lo;
     }
 }
 
-zr_status launch_to_bf16_pair(zr_context* ctx, const float* x, size_t n, uint16_t* out, int with_lo) {
+zr_status launch_to_bf16_pair(zr_context* ctx, const float* x, int rows, int K, uint16_t* out, int with_lo) {
+    if (K % 32 != 0) return set_err(ctx, ZR_E_UNSUPPORTED, "GEMM operand width %d is not a multiple of 32", K);
+    const size_t n = (size_t)rows * K;
     const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 16384);
-    hipLaunchKernelGGL(to_bf16_pair_kernel, dim3(blocks), dim3(256), 0, ctx->stream, x, n, out, with_lo);
+    hipLaunchKernelGGL(to_bf16_pair_kernel, dim3(blocks), dim3(256), 0, ctx->stream, x, rows, K, out, with_lo);
     ZR_LAUNCH_CHECK(ctx);
     return ZR_OK;
 }
 
 // Tile configurations: wave tile WM x WN 32x32 tiles, WAVES_M x WAVES_N waves.
 struct GemmCfg {
-    int wm, wn, waves_m, waves_n, stages, bdirect;
+    int wm, wn, waves_m, waves_n, stages;
     bool small;  // many blocks per CU (weight streaming) rather than one
     int bm() const { return waves_m * wm * 32; }
     int bn() const { return waves_n * wn * 32; }
@@ -339,11 +334,11 @@ struct GemmCfg {
 // (split activations): 32 x 128 tiles for <= 32 rows; 128-row tiles with
 // 256 columns, or 512 for wide / deep products and the LM head.
 static GemmCfg pick_cfg(int m, int n, int k) {
-    if (m <= 32) return {1, 1, 1, 4, 3, 0, true};
-    if (m <= 64) return {2, 1, 1, 4, 3, 0, true};
-    if (n >= 65536) return {2, 4, 2, 4, 2, 0, false};
-    if (n >= 16384 || k >= 8192) return {2, 4, 2, 4, 3, 0, false};
-    return {2, 2, 2, 4, 3, 0, false};
+    if (m <= 32) return {1, 1, 1, 4, 3, true};
+    if (m <= 64) return {2, 1, 1, 4, 3, true};
+    if (n >= 65536) return {2, 4, 2, 4, 2, false};
+    if (n >= 16384 || k >= 8192) return {2, 4, 2, 4, 3, false};
+    return {2, 2, 2, 4, 3, false};
 }
 
 static int device_cus() {
@@ -376,12 +371,12 @@ GemmPlan gemm_plan(int m, int n, int k, int epilogue) {
     return p;
 }
 
-template <int WM, int WN, int WAVES_M, int WAVES_N, int STAGES, int HL, int BDIRECT>
+template <int WM, int WN, int WAVES_M, int WAVES_N, int STAGES, int HL>
 static void gemm_launch(const GemmPlan& p, hipStream_t stream, const uint16_t* a, int m, int k, const uint16_t* w,
                         float* c, int n, size_t split_stride) {
     const int groups = p.col_blocks * p.splits;
     const unsigned blocks = 8u * (unsigned)p.row_blocks * (unsigned)((groups + 7) / 8);
-    hipLaunchKernelGGL((gemm_kernel<WM, WN, WAVES_M, WAVES_N, HL, STAGES, BDIRECT>), dim3(blocks),
+    hipLaunchKernelGGL((gemm_kernel<WM, WN, WAVES_M, WAVES_N, HL, STAGES>), dim3(blocks),
                        dim3(WAVES_M * WAVES_N * 64), 0, stream, a, m, k, (const bf16x8*)w, p.KT, p.NT, c, n,
                        p.kt_per_split, p.splits, p.row_blocks, p.col_blocks, split_stride);
 }
@@ -391,7 +386,7 @@ zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_pack
     if (deferred && (epilogue != kEpiStore || !c_f32 || c_bf16))
         return set_err(ctx, ZR_E_INVARIANT, "deferred split-K needs an f32 store epilogue");
     if (m <= 0) return ZR_OK;
-    if (k % 8 != 0 || k < 8) return set_err(ctx, ZR_E_UNSUPPORTED, "GEMM K=%d must be a multiple of 8", k);
+    if (k % 32 != 0) return set_err(ctx, ZR_E_UNSUPPORTED, "GEMM K=%d must be a multiple of 32", k);
     const GemmPlan p = gemm_plan(m, n, k, epilogue);
     const GemmCfg cfg = pick_cfg(m, n, k);
     const bool direct = p.direct && c_f32 && !c_bf16;
@@ -403,22 +398,20 @@ zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_pack
     hipEvent_t ev;
     timing_mark_begin(ctx, kClassGemm, &ev);
     bool launched = false;
-#define ZR_GEMM_CASE(WMV, WNV, WAM, WAN, ST, BD)                                                       \
+#define ZR_GEMM_CASE(WMV, WNV, WAM, WAN, ST)                                                           \
     if (!launched && cfg.wm == WMV && cfg.wn == WNV && cfg.waves_m == WAM && cfg.waves_n == WAN &&      \
-        cfg.stages == ST && cfg.bdirect == BD) {                                                       \
+        cfg.stages == ST) {                                                                            \
         if (split_act)                                                                                 \
-            gemm_launch<WMV, WNV, WAM, WAN, ST, 2, BD>(p, ctx->stream, a, m, k, w_packed, dst, n,       \
-                                                       split_stride);                                  \
+            gemm_launch<WMV, WNV, WAM, WAN, ST, 2>(p, ctx->stream, a, m, k, w_packed, dst, n, split_stride); \
         else                                                                                           \
-            gemm_launch<WMV, WNV, WAM, WAN, ST, 1, BD>(p, ctx->stream, a, m, k, w_packed, dst, n,       \
-                                                       split_stride);                                  \
+            gemm_launch<WMV, WNV, WAM, WAN, ST, 1>(p, ctx->stream, a, m, k, w_packed, dst, n, split_stride); \
         launched = true;                                                                               \
     }
-    ZR_GEMM_CASE(1, 1, 1, 4, 3, 0)
-    ZR_GEMM_CASE(2, 1, 1, 4, 3, 0)
-    ZR_GEMM_CASE(2, 4, 2, 4, 2, 0)
-    ZR_GEMM_CASE(2, 4, 2, 4, 3, 0)
-    ZR_GEMM_CASE(2, 2, 2, 4, 3, 0)
+    ZR_GEMM_CASE(1, 1, 1, 4, 3)
+    ZR_GEMM_CASE(2, 1, 1, 4, 3)
+    ZR_GEMM_CASE(2, 4, 2, 4, 2)
+    ZR_GEMM_CASE(2, 4, 2, 4, 3)
+    ZR_GEMM_CASE(2, 2, 2, 4, 3)
 #undef ZR_GEMM_CASE
     if (!launched) return set_err(ctx, ZR_E_INVARIANT, "no GEMM kernel for the selected tile configuration");
     ZR_LAUNCH_CHECK(ctx);

@@ -76,8 +76,9 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__
         if (y_bf16) {
             uint16_t hi, lo;
             split_bf16(v, hi, lo);
-            y_bf16[(size_t)r * cols + i] = hi;
-            if (split_lo) y_bf16[lo_offset + (size_t)r * cols + i] = lo;
+            const size_t o = a_pack_index(r, i, cols);
+            y_bf16[o] = hi;
+            if (split_lo) y_bf16[lo_offset + o] = lo;
         } else {
             y_f32[(size_t)r * cols + i] = v;
         }
@@ -146,17 +147,17 @@ __global__ __launch_bounds__(NT) void rms_norm_vec_kernel(const float* __restric
         const float4 g = *(const float4*)(gamma + 4 * (size_t)i4);
         float y[4] = {v[j].x * inv_rms * g.x, v[j].y * inv_rms * g.y, v[j].z * inv_rms * g.z,
                       v[j].w * inv_rms * g.w};
-        const size_t o = (size_t)r * cols + 4 * (size_t)i4;
         if (y_bf16) {
             ushort4 hi, lo;
             split_bf16(y[0], hi.x, lo.x);
             split_bf16(y[1], hi.y, lo.y);
             split_bf16(y[2], hi.z, lo.z);
             split_bf16(y[3], hi.w, lo.w);
+            const size_t o = a_pack_index(r, 4 * i4, cols);  // 4 consecutive columns stay adjacent
             *(ushort4*)(y_bf16 + o) = hi;
             if (split_lo) *(ushort4*)(y_bf16 + lo_offset + o) = lo;
         } else {
-            *(float4*)(y_f32 + o) = make_float4(y[0], y[1], y[2], y[3]);
+            *(float4*)(y_f32 + (size_t)r * cols + 4 * (size_t)i4) = make_float4(y[0], y[1], y[2], y[3]);
         }
     }
 }
@@ -167,7 +168,9 @@ zr_status launch_rms_norm(zr_context* ctx, const float* x, const Slabs& residual
     if (rows <= 0) return ZR_OK;
     hipEvent_t ev;
     timing_mark_begin(ctx, kClassNormRopeKv, &ev);
-    const size_t lo_off = (size_t)rows * cols;
+    if (y_bf16 && cols % 32 != 0)
+        return set_err(ctx, ZR_E_UNSUPPORTED, "GEMM operand width %d is not a multiple of 32", cols);
+    const size_t lo_off = a_plane(rows, cols);
     // few rows: 1024-thread blocks so that each row's loads spread wider
     const bool vec = cols % 4 == 0;
     const int nv1024 = (cols + 4095) / 4096, nv256 = (cols + 1023) / 1024;

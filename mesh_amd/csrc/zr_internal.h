@@ -36,6 +36,20 @@ __device__ inline void split_bf16(float x, uint16_t& hi, uint16_t& lo) {
     lo = f32_to_bf16_bits(x - bf16_bits_to_f32(hi));
 }
 
+// GEMM A operands (bf16 activations) are stored fragment-packed for the
+// 32x32x16 MFMA: the [rows, K] matrix (K a multiple of 32, rows padded to
+// 32) is a sequence of 1 KiB fragments (32-row tile mt, 16-column slice kt16)
+// in which lane l holds row 32 mt + l % 32, columns 16 kt16 + 8 (l / 32)
+// + j, j < 8.  A block of the GEMM then copies every fragment with one
+// contiguous 1 KiB load.  Under ZR_FLAG_SPLIT_ACTIVATIONS the lo halves
+// follow the hi plane: plane size = a_plane(rows, K).
+__host__ __device__ inline size_t a_pack_index(int m, int k, int K) {
+    const int kt16 = K >> 4;
+    const int lane = (m & 31) + (((k >> 3) & 1) << 5);
+    return ((((size_t)(m >> 5) * kt16 + (k >> 4)) << 6) + lane) * 8 + (k & 7);
+}
+__host__ __device__ inline size_t a_plane(int rows, int K) { return (size_t)((rows + 31) & ~31) * K; }
+
 // --------------------------------------------------------------- context
 struct StagedMeta;  // device copy of one microbatch's metadata
 
@@ -218,7 +232,8 @@ GemmPlan gemm_plan(int m, int n, int k, int epilogue);
 // *deferred then describes C either way.
 zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_packed, float* c_f32,
                       uint16_t* c_bf16, int m, int n, int k, int epilogue, Slabs* deferred = nullptr);
-zr_status launch_to_bf16_pair(zr_context* ctx, const float* x, size_t n, uint16_t* out, int with_lo);
+// f32 [rows, K] -> fragment-packed bf16 hi (+ lo) A operand (K % 32 == 0)
+zr_status launch_to_bf16_pair(zr_context* ctx, const float* x, int rows, int K, uint16_t* out, int with_lo);
 zr_status pack_weight(zr_context* ctx, const uint16_t* src /* [K,N] host or device */,
                       int k, int n, uint16_t** out_packed);
 // Packs [K, n1] | [K, n2] | ... (column concatenation) into one packed matrix.
