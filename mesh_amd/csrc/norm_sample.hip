@@ -171,15 +171,16 @@ zr_status launch_rms_norm(zr_context* ctx, const float* x, const Slabs& residual
     if (y_bf16 && cols % 32 != 0)
         return set_err(ctx, ZR_E_UNSUPPORTED, "GEMM operand width %d is not a multiple of 32", cols);
     const size_t lo_off = a_plane(rows, cols);
-    // few rows: 1024-thread blocks so that each row's loads spread wider
+    // 1024-thread blocks (one float4 or two per thread): every row's loads,
+    // split-K slabs included, spread over 16 waves
     const bool vec = cols % 4 == 0;
     const int nv1024 = (cols + 4095) / 4096, nv256 = (cols + 1023) / 1024;
 #define ZR_RMS_ARGS                                                                                     \
     x, residual.ptr, residual.n, residual.stride, x_out, gamma, y_f32, y_bf16, split_lo, lo_off, row_index, \
         cols, ctx->desc.rms_norm_eps
-    if (vec && rows < 128 && nv1024 == 1)
+    if (vec && nv1024 == 1)
         hipLaunchKernelGGL((rms_norm_vec_kernel<1, 1024>), dim3(rows), dim3(1024), 0, ctx->stream, ZR_RMS_ARGS);
-    else if (vec && rows < 128 && nv1024 == 2)
+    else if (vec && nv1024 == 2)
         hipLaunchKernelGGL((rms_norm_vec_kernel<2, 1024>), dim3(rows), dim3(1024), 0, ctx->stream, ZR_RMS_ARGS);
     else if (vec && nv256 == 1)
         hipLaunchKernelGGL((rms_norm_vec_kernel<1, 256>), dim3(rows), dim3(256), 0, ctx->stream, ZR_RMS_ARGS);
