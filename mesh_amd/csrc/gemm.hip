@@ -143,9 +143,9 @@ __device__ __forceinline__ void ring_barrier() {
 // stage i, the block barrier publishes the stage to every wave and retires
 // the slot read at step i - 1.  The compiler does not order LDS reads after
 // these copies, hence the explicit waits.  (Measured on the decode shapes:
-// streaming the weights into per-wave registers instead, or reading all of
-// a k-step's fragments before its MFMAs, or two k-steps per stage, are each
-// slower.)
+// streaming the weights into per-wave registers instead, staging both
+// operands through registers + ds_write, reading all of a k-step's
+// fragments before its MFMAs, or two k-steps per stage, are each slower.)
 // Grid: 1-D, decoded so that the row blocks of one (column block, split)
 // pair are dispatched 8 apart -- on the same XCD, one after the other -- and
 // share that weight tile through its L2.

@@ -1,0 +1,133 @@
+"""Parity at the full benchmark configurations (every layer, real vocab).
+
+C2: TinyLlama-1.1B shape, all 22 layers, 32 sessions with contexts
+    U[128, 2048] (seed 0xC2), two greedy decode steps.
+C3: Llama-3-8B layer shape, 4 layers, full vocab: 4 prefill chunks of 512
+    (prefixes 0, 512, 1000, 1531 -- one page-unaligned) packed with 60 decode
+    sessions (contexts U[256, 4096]) into one varlen microbatch.
+C4: tensor-parallel shard 0 of 2 of Llama-3-8B, all 32 layers, 64 sessions
+    with lognormal contexts (median 1024, sigma 1, clip [64, 8192]): every
+    layer's pre-all-reduce partials and the KV pages written.
+
+Prior context rows are imported as bf16-valued KV snapshots on both sides.
+Weights (N(0, 1/64)) and KV rows (N(0, 1)) are drawn from a 16M-value bf16
+pool at random offsets (tests.testmodels.NormalPool), which keeps set-up time
+down.
+Bars: logits within 1e-2 absolute, greedy tokens equal where the oracle's
+top-2 margin exceeds 1e-3, partials within 1e-2, imported KV rows bit-exact.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from mesh_amd import BackendMicrobatchExecutor, DecodeMicrobatchRequest, KVCacheSnapshot
+from tests.test_gpu_model import _oracle_import, check_logits, make
+from tests.testmodels import NormalPool, geometry, random_weights
+
+pytestmark = pytest.mark.gpu
+
+
+def _snapshot(pool, layers, rows, kv_cols):
+    return KVCacheSnapshot(rows, rows, pool.take((layers, rows, kv_cols)), pool.take((layers, rows, kv_cols)))
+
+
+def _sessions(ctx, pool, layers, kv_cols, ctxlens, max_seq):
+    dev, ref = [], []
+    for L in ctxlens:
+        snap = _snapshot(pool, layers, int(L), kv_cols)
+        b = ctx.new_backend(max_seq)
+        b.import_kv_cache(snap)
+        s = O.Session(layers, kv_cols, 16, max_seq, kv_round_bf16=True)
+        _oracle_import(s, snap)
+        dev.append(b)
+        ref.append(s)
+    return dev, ref
+
+
+def test_c2_tinyllama_all_22_layers_decode():
+    cfg = dict(hidden=2048, num_heads=32, num_kv_heads=4, num_layers=22, vocab=32000, ffn=5632, rms_norm_eps=1e-5,
+               rope_base=10000.0)
+    geo = geometry(cfg)
+    weights = random_weights(cfg, geo, seed=0xC2, std=0.02, pooled=True)
+    rng = np.random.default_rng(0xC2)
+    pool = NormalPool(rng)
+    ctxlens = rng.integers(128, 2049, 32)
+    pages = int(sum((L + 2 + 15) // 16 + 1 for L in ctxlens))
+    ctx, om = make(cfg, geo, weights, "bf16", True, max_tokens=32, max_seqs=32, pages=pages, pps=140)
+    dev, ref = _sessions(ctx, pool, 22, geo["kv_cols"], ctxlens, 4096)
+    toks = rng.integers(0, cfg["vocab"], 32).tolist()
+    for step in range(2):
+        reqs = [DecodeMicrobatchRequest(str(i), t, b) for i, (t, b) in enumerate(zip(toks, dev))]
+        outs = BackendMicrobatchExecutor.decode_step_batch(reqs, want_logits=True)
+        want = om.decode(ref, toks)
+        check_logits(np.stack([o.logits for o in outs]), want, f"C2 step {step}")
+        toks = np.argmax(want, 1).tolist()
+    ctx.close()
+
+
+def test_c3_mixed_prefill_chunks_and_decode_full_vocab():
+    cfg = dict(hidden=4096, num_heads=32, num_kv_heads=8, num_layers=4, vocab=128256, ffn=14336, rms_norm_eps=1e-5,
+               rope_base=500000.0)
+    geo = geometry(cfg)
+    weights = random_weights(cfg, geo, seed=0xC3, std=0.02, pooled=True)
+    rng = np.random.default_rng(0xC3)
+    pool = NormalPool(rng)
+    prefixes = [0, 512, 1000, 1531]
+    dec_ctx = rng.integers(256, 4097, 60)
+    pages = int(sum((p + 512 + 15) // 16 + 1 for p in prefixes) + sum((L + 1 + 15) // 16 + 1 for L in dec_ctx))
+    ctx, om = make(cfg, geo, weights, "bf16", True, max_tokens=4 * 512 + 60, max_seqs=64, pages=pages, pps=300)
+    kv = geo["kv_cols"]
+    dev, ref, chunks = [], [], []
+    for p in prefixes:
+        b = ctx.new_backend(8192)
+        s = O.Session(4, kv, 16, 8192, kv_round_bf16=True)
+        if p:
+            snap = _snapshot(pool, 4, p, kv)
+            b.import_kv_cache(snap)
+            _oracle_import(s, snap)
+        dev.append(b)
+        ref.append(s)
+        chunks.append(rng.integers(0, cfg["vocab"], 512).tolist())
+    d_dev, d_ref = _sessions(ctx, pool, 4, kv, dec_ctx, 8192)
+    dev += d_dev
+    ref += d_ref
+    chunks += [[int(t)] for t in rng.integers(0, cfg["vocab"], 60)]
+    _, logits = BackendMicrobatchExecutor.forward_mixed(dev, chunks, want_logits=True)
+    want = np.stack([om.prefill_chunk(ref[i], chunks[i]) for i in range(4)])
+    want_dec = om.decode(ref[4:], [c[0] for c in chunks[4:]])
+    check_logits(logits[:4], want, "C3 prefill chunks")
+    check_logits(logits[4:], want_dec, "C3 decode rows")
+    for b, s in zip(dev, ref):
+        assert b.cache_seq_len() == s.seq_len() and b.sequence_position() == s.position
+    ctx.close()
+
+
+def test_c4_tp_shard_all_32_layers_partials_and_pages():
+    cfg = dict(hidden=4096, num_heads=32, num_kv_heads=8, num_layers=32, vocab=128256, ffn=14336, rms_norm_eps=1e-5,
+               rope_base=500000.0)
+    geo = geometry(cfg, shard_start=0, shard_end=2048, ffn_cols=O.partition_columns(14336, 0, 2))
+    weights = random_weights(cfg, geo, seed=0xC4, std=0.02, pooled=True)
+    rng = np.random.default_rng(0xC4)
+    pool = NormalPool(rng)
+    ctxlens = np.clip(np.round(rng.lognormal(np.log(1024), 1.0, 64)), 64, 8192).astype(int)
+    pages = int(sum((L + 1 + 15) // 16 + 1 for L in ctxlens))
+    ctx, om = make(cfg, geo, weights, "bf16", True, max_tokens=64, max_seqs=64, pages=pages, pps=8192 // 16 + 2)
+    kv = geo["kv_cols"]
+    dev, ref = _sessions(ctx, pool, 32, kv, ctxlens, 8192)
+    toks = rng.integers(0, cfg["vocab"], 64).tolist()
+    parts = np.zeros((32, 2, 64, 4096), np.float32)
+    reqs = [DecodeMicrobatchRequest(str(i), t, b) for i, (t, b) in enumerate(zip(toks, dev))]
+    outs = BackendMicrobatchExecutor.decode_step_batch(reqs, want_logits=True, partials=parts)
+    want, want_parts = om.decode(ref, toks, want_partials=True)
+    err = float(np.max(np.abs(parts - want_parts)))
+    assert err <= 1e-2, err
+    check_logits(np.stack([o.logits for o in outs]), want, "C4 shard logits")
+    for i in (0, 17, 63):  # KV pages: prior rows bit-exact, the appended row within one bf16 step
+        snap = dev[i].export_kv_cache()
+        for layer in (0, 31):
+            k, v = ref[i].gather(layer)
+            np.testing.assert_array_equal(snap.keys[layer, :-1], k[:-1])
+            np.testing.assert_array_equal(snap.values[layer, :-1], v[:-1])
+            assert np.all(np.abs(snap.keys[layer, -1] - k[-1]) <= 8e-3 * np.abs(k[-1]) + 2e-3)
+            assert np.all(np.abs(snap.values[layer, -1] - v[-1]) <= 8e-3 * np.abs(v[-1]) + 2e-3)
+    ctx.close()

@@ -42,12 +42,45 @@ def constant_weights(cfg, geo):
                 lm_head=full(H, V, 0.08), layers=layers)
 
 
-def random_weights(cfg, geo, seed, std=0.02):
+class NormalPool:
+    """N(0, 1) values for large test tensors: windows of one 16M-value bf16-exact
+    pool at random offsets (every tensor differs; generation costs a copy)."""
+
+    SIZE = 1 << 24
+
+    def __init__(self, rng):
+        self.rng = rng
+        self.pool = round_bf16(rng.standard_normal(2 * self.SIZE, dtype=np.float32))
+
+    def take(self, shape, scale=1.0):
+        n = int(np.prod(shape))
+        out = np.empty(n, np.float32)
+        done = 0
+        while done < n:
+            off = int(self.rng.integers(0, self.SIZE))
+            m = min(n - done, self.SIZE)
+            out[done:done + m] = self.pool[off:off + m]
+            done += m
+        out = out.reshape(shape)
+        if scale != 1.0:
+            out *= np.float32(scale)  # a power of two keeps the values bf16-exact
+        return out
+
+
+def random_weights(cfg, geo, seed, std=0.02, pooled=False):
+    """N(0, std) weights rounded to bf16; `pooled` draws them from a NormalPool
+    scaled by the power of two nearest `std` (1/64 for 0.02), for the
+    full-size configurations."""
     rng = np.random.default_rng(seed)
     H, V = cfg["hidden"], cfg["vocab"]
     Q, KV, F = geo["q_cols"], geo["kv_cols"], geo["ffn_cols"]
+    pool = NormalPool(rng) if pooled else None
+    # pooled: the power of two nearest std, so the pool's bf16 values stay exact
+    pool_scale = float(2.0 ** np.round(np.log2(std)))
 
     def w(r, c):
+        if pool is not None:
+            return pool.take((r, c), pool_scale)
         return round_bf16(rng.standard_normal((r, c), dtype=np.float32) * np.float32(std))
 
     layers = []
