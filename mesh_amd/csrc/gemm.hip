@@ -130,6 +130,13 @@ __device__ __forceinline__ void ring_barrier() {
     asm volatile("" ::: "memory");
 }
 
+// silu(g) * u = g / (1 + e^-g) * u (runtime.rs:927-929, forward_pass.rs:2286-2289),
+// one rounding per operation as written.
+__device__ inline float swiglu(float g, float u) {
+#pragma clang fp contract(off)
+    return g / (1.0f + expf(-g)) * u;
+}
+
 // ------------------------------------------------------------------ GEMM
 // v_mfma_f32_32x32x16_bf16: A fragment lane l holds A[row l % 32][k 8 (l / 32)
 // + j]; the product lane l, element i is C[8 (i / 4) + 4 (l / 32) + i % 4][l % 32].
@@ -149,11 +156,15 @@ __device__ __forceinline__ void ring_barrier() {
 // Grid: 1-D, decoded so that the row blocks of one (column block, split)
 // pair are dispatched 8 apart -- on the same XCD, one after the other -- and
 // share that weight tile through its L2.
-template <int WM, int WN, int WAVES_M, int WAVES_N, int HL, int STAGES>
+// SWIGLU = 1: single split; column tiles come in gate / up pairs (tile 2b is
+// gate, 2b + 1 up, WN even) and silu(g) * u is written straight to H as the
+// next GEMM's fragment-packed bf16 hi (+ lo when h_lo) operand [M, N / 2].
+template <int WM, int WN, int WAVES_M, int WAVES_N, int HL, int STAGES, int SWIGLU>
 __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_kernel(
     const uint16_t* __restrict__ A, int M, int K, const bf16x8* __restrict__ Wp, int KT, int NT,
     float* __restrict__ C, int N, int kt_per_split, int splits, int row_blocks, int col_blocks,
-    size_t split_stride) {
+    size_t split_stride, uint16_t* __restrict__ H, int h_lo) {
+    static_assert(!SWIGLU || WN % 2 == 0, "gate / up tile pairs");
     constexpr int NW = WAVES_M * WAVES_N;
     constexpr int BMT = WAVES_M * WM, BNT = WAVES_N * WN;
     constexpr int FA = HL * BMT * 2, FB = BNT * 2, FS = FA + FB;
@@ -247,18 +258,40 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_kernel(
         }
     }
 
-    float* out = C + (size_t)split * split_stride;
+    if constexpr (SWIGLU) {
+        const int F = N / 2;
+        const size_t plane = a_plane(M, F);
 #pragma unroll
-    for (int mt = 0; mt < WM; ++mt)
+        for (int mt = 0; mt < WM; ++mt)
 #pragma unroll
-        for (int wn = 0; wn < WN; ++wn) {
-            const int n = (nt_blk + wn_idx * WN + wn) * 32 + (lane & 31);
+            for (int p = 0; p < WN / 2; ++p) {
+                const int j = ((nt_blk + wn_idx * WN + 2 * p) >> 1) * 32 + (lane & 31);
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int m = m0 + (wm_idx * WM + mt) * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-                if (m < M && n < N) out[(size_t)m * N + n] = acc[mt][wn][i];
+                for (int i = 0; i < 16; ++i) {
+                    const int m = m0 + (wm_idx * WM + mt) * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+                    if (m < M && j < F) {
+                        uint16_t hi, lo;
+                        split_bf16(swiglu(acc[mt][2 * p][i], acc[mt][2 * p + 1][i]), hi, lo);
+                        const size_t o = a_pack_index(m, j, F);
+                        H[o] = hi;
+                        if (h_lo) H[plane + o] = lo;
+                    }
+                }
             }
-        }
+    } else {
+        float* out = C + (size_t)split * split_stride;
+#pragma unroll
+        for (int mt = 0; mt < WM; ++mt)
+#pragma unroll
+            for (int wn = 0; wn < WN; ++wn) {
+                const int n = (nt_blk + wn_idx * WN + wn) * 32 + (lane & 31);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int m = m0 + (wm_idx * WM + mt) * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+                    if (m < M && n < N) out[(size_t)m * N + n] = acc[mt][wn][i];
+                }
+            }
+    }
 }
 
 // Sum of split-K slabs [S][M][N] with the epilogue.
@@ -283,7 +316,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
                 g += ws[s * split_stride + (size_t)m * N + gc];
                 u += ws[s * split_stride + (size_t)m * N + gc + 32];
             }
-            v = g / (1.0f + expf(-g)) * u;
+            v = swiglu(g, u);
         } else {
             v = 0.0f;
             for (int s = 0; s < S; ++s) v += ws[s * split_stride + (size_t)m * N + j];
@@ -333,7 +366,10 @@ struct GemmCfg {
 // Measured on MI355X over the decode shapes with weights streamed from HBM
 // (split activations): 32 x 128 tiles for <= 32 rows; 128-row tiles with
 // 256 columns, or 512 for wide / deep products and the LM head.
-static GemmCfg pick_cfg(int m, int n, int k) {
+static GemmCfg pick_cfg(int m, int n, int k, int epilogue = kEpiStore) {
+    // SwiGLU fused into the GEMM (one split, gate / up tile pairs in a wave) once
+    // 128-row tiles fill the CUs; small row counts reduce split-K slabs instead
+    if (epilogue == kEpiSwiGLU && m > 64) return {2, 2, 2, 4, 3, false};
     if (m <= 32) return {1, 1, 1, 4, 3, true};
     if (m <= 64) return {2, 1, 1, 4, 3, true};
     if (n >= 65536) return {2, 4, 2, 4, 2, false};
@@ -350,9 +386,11 @@ static int device_cus() {
     return cus;
 }
 
+static bool swiglu_fused(int m, int epilogue) { return epilogue == kEpiSwiGLU && m > 64; }
+
 GemmPlan gemm_plan(int m, int n, int k, int epilogue) {
     GemmPlan p;
-    const GemmCfg c = pick_cfg(m, n, k);
+    const GemmCfg c = pick_cfg(m, n, k, epilogue);
     p.KT = (k + 31) / 32;
     p.NT = (n + 31) / 32;
     p.row_blocks = (m + c.bm() - 1) / c.bm();
@@ -363,22 +401,23 @@ GemmPlan gemm_plan(int m, int n, int k, int epilogue) {
     const int tiles = p.col_blocks * p.row_blocks;
     const int budget = c.small ? 3 * device_cus() : device_cus();
     int splits = 1;
-    while (tiles * splits * 2 <= budget && p.KT / (splits * 2) >= 4 && splits < 16) splits *= 2;
+    while (!swiglu_fused(m, epilogue) && tiles * splits * 2 <= budget && p.KT / (splits * 2) >= 4 && splits < 16)
+        splits *= 2;
     p.kt_per_split = (p.KT + splits - 1) / splits;
     p.splits = (p.KT + p.kt_per_split - 1) / p.kt_per_split;
-    p.direct = p.splits == 1 && epilogue == kEpiStore;
+    p.direct = p.splits == 1 && (epilogue == kEpiStore || swiglu_fused(m, epilogue));
     p.ws_floats = p.direct ? 0 : (size_t)p.splits * m * n;
     return p;
 }
 
-template <int WM, int WN, int WAVES_M, int WAVES_N, int STAGES, int HL>
+template <int WM, int WN, int WAVES_M, int WAVES_N, int STAGES, int HL, int SWIGLU = 0>
 static void gemm_launch(const GemmPlan& p, hipStream_t stream, const uint16_t* a, int m, int k, const uint16_t* w,
-                        float* c, int n, size_t split_stride) {
+                        float* c, int n, size_t split_stride, uint16_t* h = nullptr, int h_lo = 0) {
     const int groups = p.col_blocks * p.splits;
     const unsigned blocks = 8u * (unsigned)p.row_blocks * (unsigned)((groups + 7) / 8);
-    hipLaunchKernelGGL((gemm_kernel<WM, WN, WAVES_M, WAVES_N, HL, STAGES>), dim3(blocks),
+    hipLaunchKernelGGL((gemm_kernel<WM, WN, WAVES_M, WAVES_N, HL, STAGES, SWIGLU>), dim3(blocks),
                        dim3(WAVES_M * WAVES_N * 64), 0, stream, a, m, k, (const bf16x8*)w, p.KT, p.NT, c, n,
-                       p.kt_per_split, p.splits, p.row_blocks, p.col_blocks, split_stride);
+                       p.kt_per_split, p.splits, p.row_blocks, p.col_blocks, split_stride, h, h_lo);
 }
 
 zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_packed, float* c_f32,
@@ -388,8 +427,11 @@ zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_pack
     if (m <= 0) return ZR_OK;
     if (k % 32 != 0) return set_err(ctx, ZR_E_UNSUPPORTED, "GEMM K=%d must be a multiple of 32", k);
     const GemmPlan p = gemm_plan(m, n, k, epilogue);
-    const GemmCfg cfg = pick_cfg(m, n, k);
-    const bool direct = p.direct && c_f32 && !c_bf16;
+    const GemmCfg cfg = pick_cfg(m, n, k, epilogue);
+    if (swiglu_fused(m, epilogue) && (!c_bf16 || c_f32 || n % 64 != 0))
+        return set_err(ctx, ZR_E_INVARIANT, "fused SwiGLU writes the bf16 operand only (N=%d)", n);
+    const bool fused = swiglu_fused(m, epilogue);
+    const bool direct = (p.direct && c_f32 && !c_bf16 && epilogue == kEpiStore) || fused;
     const size_t split_stride = (size_t)m * n;
     if (!direct && (size_t)p.splits * split_stride > ctx->splitk_ws_floats)
         return set_err(ctx, ZR_E_OOM, "split-K workspace too small (%d x %d x %d)", p.splits, m, n);
@@ -398,6 +440,13 @@ zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_pack
     hipEvent_t ev;
     timing_mark_begin(ctx, kClassGemm, &ev);
     bool launched = false;
+    if (fused) {
+        if (split_act)
+            gemm_launch<2, 2, 2, 4, 3, 2, 1>(p, ctx->stream, a, m, k, w_packed, nullptr, n, 0, c_bf16, 1);
+        else
+            gemm_launch<2, 2, 2, 4, 3, 1, 1>(p, ctx->stream, a, m, k, w_packed, nullptr, n, 0, c_bf16, 0);
+        launched = true;
+    }
 #define ZR_GEMM_CASE(WMV, WNV, WAM, WAN, ST)                                                           \
     if (!launched && cfg.wm == WMV && cfg.wn == WNV && cfg.waves_m == WAM && cfg.waves_n == WAN &&      \
         cfg.stages == ST) {                                                                            \
