@@ -130,6 +130,21 @@ __device__ __forceinline__ void ring_barrier() {
     asm volatile("" ::: "memory");
 }
 
+// ring_barrier for `ahead` (block-uniform, 0..MAXA) stages of VM copies
+// each issued after the one waited for.
+template <int VM, int MAXA>
+__device__ __forceinline__ void ring_wait(int ahead) {
+    if constexpr (MAXA > 0) {
+        if (ahead >= MAXA) {
+            ring_barrier<VM * MAXA>();
+            return;
+        }
+        ring_wait<VM, MAXA - 1>(ahead);
+    } else {
+        ring_barrier<0>();
+    }
+}
+
 // silu(g) * u = g / (1 + e^-g) * u (runtime.rs:927-929, forward_pass.rs:2286-2289),
 // one rounding per operation as written.
 __device__ inline float swiglu(float g, float u) {
@@ -145,14 +160,16 @@ __device__ inline float swiglu(float g, float u) {
 // Both operands go global -> LDS with `global_load_lds_dwordx4` (no
 // registers): every 1 KiB MFMA fragment of a k-step -- A rows (hi, then lo)
 // and weight tiles -- is one wave instruction, spread evenly over the
-// block's waves.  STAGES-deep ring: the copies of stage i + STAGES - 1 are
-// issued at step i; at step i a wave waits (vmcnt) for its own copies of
-// stage i, the block barrier publishes the stage to every wave and retires
-// the slot read at step i - 1.  The compiler does not order LDS reads after
-// these copies, hence the explicit waits.  (Measured on the decode shapes:
-// streaming the weights into per-wave registers instead, staging both
-// operands through registers + ds_write, reading all of a k-step's
-// fragments before its MFMAs, or two k-steps per stage, are each slower.)
+// block's waves.  STAGES-deep ring: halfway through step i a wave waits
+// (vmcnt) for its own copies of stage i + 1, the block barrier publishes that
+// stage to every wave and retires slot i (all of its reads have returned),
+// and the copies of stage i + STAGES go into slot i.  The compiler does not
+// order LDS reads after these copies, hence the explicit waits.  (Measured on
+// the decode shapes: 4 or 5 stages instead of 3, streaming the weights into
+// per-wave registers, staging both operands through registers + ds_write,
+// or two k-steps per stage, are each no faster; the per-half register
+// pipeline below is 3-8 % faster than reading each fragment just before
+// its MFMAs.)
 // Grid: 1-D, decoded so that the row blocks of one (column block, split)
 // pair are dispatched 8 apart -- on the same XCD, one after the other -- and
 // share that weight tile through its L2.
@@ -171,7 +188,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_kernel(
     constexpr int PW = (FS + NW - 1) / NW;  // LDS copies per wave per stage
     constexpr int FSP = PW * NW;            // fragments per stage incl. padding
     constexpr int VM = PW;                  // vector-memory ops per wave per stage
-    static_assert(STAGES >= 2 && STAGES <= 4, "stages");
+    static_assert(STAGES >= 2 && STAGES <= 6, "stages");
     static_assert(VM * (STAGES - 2) < 64, "vmcnt range");
     typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
     __shared__ bf16x8 lds[STAGES][FSP][64];
@@ -220,41 +237,60 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_kernel(
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[mt][wn][i] = 0.0f;
 
+    // fragments of one k-half (16 k) in registers: kh 0 / kh 1 alternate so
+    // that one half's LDS reads are in flight while the other's MFMAs run
+    auto load_frags = [&](int slot, int kh, bf16x8* fa, bf16x8* fb) {
+#pragma unroll
+        for (int wn = 0; wn < WN; ++wn) fb[wn] = lds[slot][FA + (wn_idx * WN + wn) * 2 + kh][lane];
+#pragma unroll
+        for (int mt = 0; mt < WM; ++mt)
+#pragma unroll
+            for (int hl = 0; hl < HL; ++hl)
+                fa[mt * HL + hl] = lds[slot][((hl * BMT + wm_idx * WM + mt) << 1) + kh][lane];
+    };
+    constexpr int NM = WM * HL * WN;  // MFMAs per k-half
+    auto mfmas = [&](const bf16x8* fa, const bf16x8* fb, int t0, int t1) {
+#pragma unroll
+        for (int t = 0; t < NM; ++t) {
+            if (t < t0 || t >= t1) continue;
+            const int mt = t / (HL * WN), hl = (t / WN) % HL, wn = t % WN;
+            acc[mt][wn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[mt * HL + hl], fb[wn], acc[mt][wn], 0, 0, 0);
+        }
+    };
+    bf16x8 fa0[WM * HL], fb0[WN], fa1[WM * HL], fb1[WN];
+
 #pragma unroll
     for (int s = 0; s < STAGES - 1; ++s)
         if (s < nsteps) issue(s, kt_begin + s);
-
+    if (nsteps > 0) {
+        ring_wait<VM, STAGES - 2>(min(STAGES - 2, nsteps - 1));
+        if (STAGES - 1 < nsteps) issue(STAGES - 1, kt_begin + STAGES - 1);
+        load_frags(0, 0, fa0, fb0);
+    }
+    // Step i: first MFMA of kh 0, the kh 1 reads, the other kh 0 MFMAs; the
+    // ring barrier for step i + 1 (its copies landed, slot i free) and the
+    // copy of stage i + STAGES into slot i; first MFMA of kh 1, the kh 0 reads
+    // of step i + 1, the other kh 1 MFMAs.  The scheduling barriers keep the
+    // reads where they are.  After the last step the barrier and the reads
+    // are idle (the slot's data is not used).  Each accumulator still sums
+    // (kh 0, hi), (kh 0, lo), (kh 1, hi), (kh 1, lo) per k-step, in k order.
     for (int i0 = 0; i0 < nsteps; i0 += STAGES) {
 #pragma unroll
         for (int u = 0; u < STAGES; ++u) {
             const int i = i0 + u;
             if (i >= nsteps) break;
-            const int ahead = min(STAGES - 2, nsteps - 1 - i);  // stages issued after stage i
-            if (STAGES >= 4 && ahead >= 2)
-                ring_barrier<VM * (STAGES >= 4 ? 2 : 0)>();
-            else if (STAGES >= 3 && ahead == 1)
-                ring_barrier<VM * (STAGES >= 3 ? 1 : 0)>();
-            else
-                ring_barrier<0>();
-            const int ns = (u + STAGES - 1) % STAGES;
-            if (i + STAGES - 1 < nsteps) issue(ns, kt_begin + i + STAGES - 1);
-#pragma unroll
-            for (int kh = 0; kh < 2; ++kh) {
-                bf16x8 bf[WN];
-#pragma unroll
-                for (int wn = 0; wn < WN; ++wn)
-                    bf[wn] = lds[u][FA + (wn_idx * WN + wn) * 2 + kh][lane];
-#pragma unroll
-                for (int mt = 0; mt < WM; ++mt)
-#pragma unroll
-                    for (int hl = 0; hl < HL; ++hl) {
-                        const bf16x8 af = lds[u][((hl * BMT + wm_idx * WM + mt) << 1) + kh][lane];
-#pragma unroll
-                        for (int wn = 0; wn < WN; ++wn)
-                            acc[mt][wn] =
-                                __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf[wn], acc[mt][wn], 0, 0, 0);
-                    }
-            }
+            mfmas(fa0, fb0, 0, 1);
+            __builtin_amdgcn_sched_barrier(0);
+            load_frags(u, 1, fa1, fb1);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(fa0, fb0, 1, NM);
+            ring_wait<VM, STAGES - 2>(max(0, min(STAGES - 2, nsteps - 2 - i)));
+            if (i + STAGES < nsteps) issue(u, kt_begin + i + STAGES);
+            mfmas(fa1, fb1, 0, 1);
+            __builtin_amdgcn_sched_barrier(0);
+            load_frags((u + 1) % STAGES, 0, fa0, fb0);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(fa1, fb1, 1, NM);
         }
     }
 
@@ -373,7 +409,7 @@ static GemmCfg pick_cfg(int m, int n, int k, int epilogue = kEpiStore) {
     if (m <= 32) return {1, 1, 1, 4, 3, true};
     if (m <= 64) return {2, 1, 1, 4, 3, true};
     if (n >= 65536) return {2, 4, 2, 4, 2, false};
-    if (n >= 16384 || k >= 8192) return {2, 4, 2, 4, 3, false};
+    if (n >= 16384) return {2, 4, 2, 4, 3, false};
     return {2, 2, 2, 4, 3, false};
 }
 
