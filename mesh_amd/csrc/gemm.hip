@@ -408,7 +408,8 @@ static GemmCfg pick_cfg(int m, int n, int k, int epilogue = kEpiStore) {
     if (epilogue == kEpiSwiGLU && m > 64) return {2, 2, 2, 4, 3, false};
     if (m <= 32) return {1, 1, 1, 4, 3, true};
     if (m <= 64) return {2, 1, 1, 4, 3, true};
-    if (n >= 65536) return {2, 4, 2, 4, 2, false};
+    // vocabulary-wide heads: 256-row tiles read each weight tile once
+    if (n >= 65536) return m > 128 ? GemmCfg{2, 4, 4, 2, 3, false} : GemmCfg{2, 4, 2, 4, 3, false};
     if (n >= 16384) return {2, 4, 2, 4, 3, false};
     return {2, 2, 2, 4, 3, false};
 }
@@ -494,7 +495,7 @@ zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_pack
     }
     ZR_GEMM_CASE(1, 1, 1, 4, 3)
     ZR_GEMM_CASE(2, 1, 1, 4, 3)
-    ZR_GEMM_CASE(2, 4, 2, 4, 2)
+    ZR_GEMM_CASE(2, 4, 4, 2, 3)
     ZR_GEMM_CASE(2, 4, 2, 4, 3)
     ZR_GEMM_CASE(2, 2, 2, 4, 3)
 #undef ZR_GEMM_CASE
