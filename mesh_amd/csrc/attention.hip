@@ -32,24 +32,25 @@ __device__ inline float shfl_xor(float v, int mask) { return __shfl_xor(v, mask,
 
 template <typename KV, int D> struct PageRegs;
 
-// bf16 pool: K fragment per 32 dims = 8 bf16 (16 B), V fragment per 16 dims = 4 bf16 (8 B)
+// bf16 pool: K fragment per 32 dims = 8 bf16 (16 B); V per 32 dims = 8 bf16
+// (16 B): tokens 4 q4 .. 4 q4 + 3 of dims 32 vb + c, then of 32 vb + 16 + c.
+// Both are one 1 KiB contiguous wave load.
 template <int D> struct PageRegs<uint16_t, D> {
     bf16x8 k[D / 32];
-    bf16x4 v[D / 16];
+    bf16x8 v[D / 32];
     __device__ inline void load(const uint16_t* kp, const uint16_t* vp, int lane) {
 #pragma unroll
         for (int kb = 0; kb < D / 32; ++kb)
             k[kb] = *(const bf16x8*)(kp + ((size_t)kb * kWave + lane) * 8);
-        const int q4 = lane >> 4, c = lane & 15;
 #pragma unroll
-        for (int db = 0; db < D / 16; ++db)
-            v[db] = *(const bf16x4*)(vp + ((size_t)q4 * D + db * 16 + c) * 4);
+        for (int vb = 0; vb < D / 32; ++vb)
+            v[vb] = *(const bf16x8*)(vp + ((size_t)vb * kWave + lane) * 8);
     }
 };
 
 template <int D> struct PageRegs<float, D> {
     f32x4 k[D / 32][2];
-    f32x4 v[D / 16];
+    f32x4 v[D / 32][2];
     __device__ inline void load(const float* kp, const float* vp, int lane) {
 #pragma unroll
         for (int kb = 0; kb < D / 32; ++kb) {
@@ -57,9 +58,12 @@ template <int D> struct PageRegs<float, D> {
             k[kb][0] = src[0];
             k[kb][1] = src[1];
         }
-        const int q4 = lane >> 4, c = lane & 15;
 #pragma unroll
-        for (int db = 0; db < D / 16; ++db) v[db] = *(const f32x4*)(vp + ((size_t)q4 * D + db * 16 + c) * 4);
+        for (int vb = 0; vb < D / 32; ++vb) {
+            const f32x4* src = (const f32x4*)(vp + ((size_t)vb * kWave + lane) * 8);
+            v[vb][0] = src[0];
+            v[vb][1] = src[1];
+        }
     }
 };
 
@@ -119,20 +123,19 @@ __device__ inline f32x4 qk_mfma(const PageRegs<float, D>& pg, const bf16x8* qhi,
 
 // O^T += V^T P^T over a page pair (32 tokens) on the 16x16x32 MFMA: lane l
 // supplies tokens 4*q4 .. 4*q4+3 of page A then of page B for both operands,
-// which is exactly its own score registers for P^T and the concatenation of
-// its two V fragments for V^T.
-__device__ inline bf16x8 cat4(bf16x4 a, bf16x4 b) {
-    return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-}
-
+// which is exactly its own score registers for P^T and, for V^T, the matching
+// 4-token halves of its two pages' V fragments (dims 16 db + c).
 template <int D>
 __device__ inline void pv_mfma2(const PageRegs<uint16_t, D>& pa, const PageRegs<uint16_t, D>& pb, bf16x8 phi,
                                 bf16x8 plo, f32x4* o) {
 #pragma unroll
-    for (int db = 0; db < D / 16; ++db) {
-        const bf16x8 v = cat4(pa.v[db], pb.v[db]);
-        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v, phi, o[db], 0, 0, 0);
-        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v, plo, o[db], 0, 0, 0);
+    for (int vb = 0; vb < D / 32; ++vb) {
+        const bf16x8 v0 = __builtin_shufflevector(pa.v[vb], pb.v[vb], 0, 1, 2, 3, 8, 9, 10, 11);
+        const bf16x8 v1 = __builtin_shufflevector(pa.v[vb], pb.v[vb], 4, 5, 6, 7, 12, 13, 14, 15);
+        o[2 * vb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v0, phi, o[2 * vb], 0, 0, 0);
+        o[2 * vb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v0, plo, o[2 * vb], 0, 0, 0);
+        o[2 * vb + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v1, phi, o[2 * vb + 1], 0, 0, 0);
+        o[2 * vb + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v1, plo, o[2 * vb + 1], 0, 0, 0);
     }
 }
 
@@ -141,8 +144,8 @@ __device__ inline void pv_mfma2(const PageRegs<float, D>& pa, const PageRegs<flo
                                 f32x4* o) {
 #pragma unroll
     for (int db = 0; db < D / 16; ++db) {
-        float vf[8] = {pa.v[db][0], pa.v[db][1], pa.v[db][2], pa.v[db][3],
-                       pb.v[db][0], pb.v[db][1], pb.v[db][2], pb.v[db][3]};
+        const f32x4 va = pa.v[db >> 1][db & 1], vbv = pb.v[db >> 1][db & 1];
+        float vf[8] = {va[0], va[1], va[2], va[3], vbv[0], vbv[1], vbv[2], vbv[3]};
         const bf16x8 vhi = to_bf16x8(vf, false), vlo = to_bf16x8(vf, true);
         o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vhi, phi, o[db], 0, 0, 0);
         o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vhi, plo, o[db], 0, 0, 0);

@@ -6,15 +6,20 @@
 //   K tile: element (t, d) at ((d / 8) * 16 + t) * 8 + d % 8
 //           -> one 1 KiB row of 64 lanes x 16 B is exactly the MFMA A-operand
 //              fragment (token = lane % 16, 8 dims per lane) for 32 dims.
-//   V tile: element (t, d) at ((t / 4) * head_dim + d) * 4 + t % 4
-//           -> a lane's 4 consecutive tokens of one dim form the 16x16x16
-//              MFMA operand of the P.V product.
+//   V tile: element (t, d) at ((((d / 32) * 4 + t / 4) * 16 + d % 16) * 2
+//           + (d / 16) % 2) * 4 + t % 4
+//           -> 4 consecutive tokens of one dim are one P.V MFMA operand
+//              lane; dims d and d + 16 sit next to each other, so a lane
+//              loads both with one 16 B (bf16) load and a wave reads 1 KiB
+//              contiguous per 32 dims.
 #include "zr_internal.h"
 
 namespace zr {
 
 __device__ inline size_t k_off(int t, int d) { return ((size_t)(d >> 3) * kPageRows + t) * 8 + (d & 7); }
-__device__ inline size_t v_off(int t, int d, int D) { return ((size_t)(t >> 2) * D + d) * 4 + (t & 3); }
+__device__ inline size_t v_off(int t, int d, int) {
+    return (((((size_t)(d >> 5) * 4 + (t >> 2)) * 16 + (d & 15)) * 2 + ((d >> 4) & 1)) * 4) + (t & 3);
+}
 
 template <typename T> __device__ inline void store_elem(T* p, float x);
 template <> __device__ inline void store_elem<float>(float* p, float x) { *p = x; }

@@ -155,7 +155,8 @@ def test_c1_raw_page_row_holds_appended_kv_in_pool_layout():
     for h in range(4):
         for d in range(64):
             assert kblk[h][((d // 8) * 16 + row) * 8 + d % 8] == K[s][-1][h * 64 + d]
-            assert vblk[h][((row // 4) * 64 + d) * 4 + row % 4] == V[s][-1][h * 64 + d]
+            v_off = ((((d // 32) * 4 + row // 4) * 16 + d % 16) * 2 + (d // 16) % 2) * 4 + row % 4
+            assert vblk[h][v_off] == V[s][-1][h * 64 + d]
     ctx.close()
 
 
