@@ -205,18 +205,6 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
     // Q^T as the MFMA B operand (lane holds Q[c][32*kb + 8*q4 + j]) as bf16
     // hi + lo fragments, parked in LDS to keep registers for the page ring.
     __shared__ bf16x8 qs[2][D / 32][64];
-    {
-        const int row = a.cu_q[seq] + q0 + (col_valid ? qi : 0);
-        const float* qp = a.q + (size_t)row * a.q_cols + (size_t)(kvh * a.G + g) * D;
-#pragma unroll
-        for (int kb = 0; kb < D / 32; ++kb) {
-            float x[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) x[j] = col_valid ? qp[kb * 32 + q4 * 8 + j] : 0.0f;
-            qs[0][kb][lane] = to_bf16x8(x, false);
-            qs[1][kb][lane] = to_bf16x8(x, true);
-        }
-    }
     const bf16x8* qhi = qs[0][0];
     const bf16x8* qlo = qs[1][0];
 
@@ -274,17 +262,39 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
         const KV* base = pool + (size_t)bt[p] * a.page_elems + (size_t)kvh * kv_tile;
         r.load(base, base + v_block, lane);
     };
-    const int pend = it.z;
+    // Q row of this lane's column, fetched before the first pages so that its
+    // wait (in-order vmcnt) does not also wait for them
+    f32x4 qx[D / 32][2];
+    {
+        const int row = a.cu_q[seq] + q0 + (col_valid ? qi : 0);
+        const float* qp = a.q + (size_t)row * a.q_cols + (size_t)(kvh * a.G + g) * D + q4 * 8;
 #pragma unroll
-    for (int r = 0; r < RING - 2; ++r)
-        if (it.y + r < pend) load(ring[r], it.y + r);
+        for (int kb = 0; kb < D / 32; ++kb) {
+            qx[kb][0] = col_valid ? *(const f32x4*)(qp + kb * 32) : f32x4{0.f, 0.f, 0.f, 0.f};
+            qx[kb][1] = col_valid ? *(const f32x4*)(qp + kb * 32 + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    const int pend = it.z;
+    // Every ring slot is loaded unconditionally (past the split's end, the
+    // last page again, an L2 hit): with no conditional loads the compiler
+    // can wait for exactly the slot it computes on (in-order vmcnt) instead
+    // of conservatively draining the newest pages' loads too.
+#pragma unroll
+    for (int r = 0; r < RING - 2; ++r) load(ring[r], min(it.y + r, pend - 1));
+#pragma unroll
+    for (int kb = 0; kb < D / 32; ++kb) {
+        const float x[8] = {qx[kb][0][0], qx[kb][0][1], qx[kb][0][2], qx[kb][0][3],
+                            qx[kb][1][0], qx[kb][1][1], qx[kb][1][2], qx[kb][1][3]};
+        qs[0][kb][lane] = to_bf16x8(x, false);
+        qs[1][kb][lane] = to_bf16x8(x, true);
+    }
     for (int p = it.y; p < pend; p += RING) {
 #pragma unroll
         for (int r = 0; r < RING; r += 2) {
             const int pp = p + r;
             if (pp >= pend) break;
-            if (pp + RING - 2 < pend) load(ring[(r + RING - 2) % RING], pp + RING - 2);
-            if (pp + RING - 1 < pend) load(ring[(r + RING - 1) % RING], pp + RING - 1);
+            load(ring[(r + RING - 2) % RING], min(pp + RING - 2, pend - 1));
+            load(ring[(r + RING - 1) % RING], min(pp + RING - 1, pend - 1));
             const bool has_b = pp + 1 < pend;
             process2(ring[r], has_b ? ring[r + 1] : ring[r], pp, has_b);
         }
