@@ -174,6 +174,7 @@ struct AttnArgs {
     const int* cu_q;
     const int4* items;       // {tile, page_begin, page_end, unused}
     const int* order;        // dispatch rank -> item (longest first)
+    int n_items;
     const int4* tiles;       // {seq, q0, nq, first_item}
     int G;                   // q heads per kv head
     int kv_heads;
@@ -187,10 +188,16 @@ struct AttnArgs {
 template <typename KV, int D, int RING>
 __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
     const int lane = threadIdx.x;
-    // the kv heads of one item are adjacent in dispatch order (they read
-    // neighbouring blocks of the same pages)
-    const int kvh = blockIdx.x % a.kv_heads;
-    const int item = a.order[blockIdx.x / a.kv_heads];
+    // Workgroups go to the 8 XCDs round-robin (XCD = blockIdx % 8).  Block
+    // b = 8 kv_heads grp + 8 kvh + x runs kv head kvh of dispatch rank
+    // 8 grp + x, so every kv head of one item -- all of its pages' bytes --
+    // is read through the same XCD (its L2 and its address translation).
+    const int per_grp = 8 * a.kv_heads;
+    const int rem = blockIdx.x % per_grp;
+    const int kvh = rem >> 3;
+    const int rank = (blockIdx.x / per_grp) * 8 + (rem & 7);
+    if (rank >= a.n_items) return;
+    const int item = a.order[rank];
     const int4 it = a.items[item];
     const int4 tl = a.tiles[it.x];
     const int seq = tl.x, q0 = tl.y, nq = tl.z;
@@ -457,6 +464,7 @@ static zr_status launch_attn_t(zr_context* ctx, StagedMeta* st, int layer, const
     a.cu_q = st->cu_q;
     a.items = st->attn_items;
     a.order = st->attn_order;
+    a.n_items = st->n_attn_items;
     a.tiles = st->attn_tiles;
     a.G = ctx->q_per_kv;
     a.kv_heads = ctx->local_kv_heads;
@@ -469,7 +477,7 @@ static zr_status launch_attn_t(zr_context* ctx, StagedMeta* st, int layer, const
     timing_mark_begin(ctx, kClassAttention, &ev);
     // bf16 pages: a 6-page ring, one wave per SIMD (measured: a 4-page ring
     // at two waves per SIMD spills and loses ~20%); f32 pages: 4 pages
-    const dim3 grid(st->n_attn_items * ctx->local_kv_heads);
+    const dim3 grid(((st->n_attn_items + 7) / 8) * 8 * ctx->local_kv_heads);
     hipLaunchKernelGGL((paged_attention_kernel<KV, D, sizeof(KV) == 4 ? 4 : 6>), grid, dim3(64), 0, ctx->stream, a);
     ZR_LAUNCH_CHECK(ctx);
     timing_mark_end(ctx, kClassAttention, ev);
