@@ -432,14 +432,12 @@ GemmPlan gemm_plan(int m, int n, int k, int epilogue) {
     p.NT = (n + 31) / 32;
     p.row_blocks = (m + c.bm() - 1) / c.bm();
     p.col_blocks = (p.NT + c.bn() / 32 - 1) / (c.bn() / 32);
-    // split K (power of two, >= 4 k-steps per split) while the grid fits one
-    // pass over the CUs (one resident block per CU for the large tiles,
-    // about three for the small weight-streaming tiles, at most 16 splits)
+    // split K as far as the grid fits one pass over the CUs (one resident
+    // block per CU for the large tiles, about three for the small
+    // weight-streaming tiles), >= 4 k-steps per split, at most 16 splits
     const int tiles = p.col_blocks * p.row_blocks;
     const int budget = c.small ? 3 * device_cus() : device_cus();
-    int splits = 1;
-    while (!swiglu_fused(m, epilogue) && tiles * splits * 2 <= budget && p.KT / (splits * 2) >= 4 && splits < 16)
-        splits *= 2;
+    const int splits = swiglu_fused(m, epilogue) ? 1 : std::max(1, std::min(std::min(16, budget / tiles), p.KT / 4));
     p.kt_per_split = (p.KT + splits - 1) / splits;
     p.splits = (p.KT + p.kt_per_split - 1) / p.kt_per_split;
     p.direct = p.splits == 1 && (epilogue == kEpiStore || swiglu_fused(m, epilogue));
