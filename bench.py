@@ -192,8 +192,8 @@ class GpuDecodeBench:
             ctx.check(lib.zr_forward_staged_async(ctx.h, self.staged[i], self.tok[i % 2], self.tok[(i + 1) % 2], None))
         ctx.check(lib.zr_synchronize(ctx.h))
         dt = time.perf_counter() - t0
-        ms = (C.c_double * 4)()
-        n = (C.c_int * 4)()
+        ms = (C.c_double * 5)()
+        n = (C.c_int * 5)()
         if timed:
             ctx.check(lib.zr_timing_end(ctx.h, ms, n))
         return dt, list(ms), list(n)

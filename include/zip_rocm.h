@@ -185,6 +185,17 @@ zr_status zr_kv_gather(zr_context* ctx, const int* block_table, int n_pages, int
  * logical rows first_row.. of the window described by block_table. */
 zr_status zr_kv_scatter(zr_context* ctx, const int* block_table, int n_pages, int first_offset,
                         int first_row, int n_rows, const float* src_k, const float* src_v);
+/* KV snapshot wire format (KVCache::to_bytes, kv_cache.rs:880-887: ciborium
+ * 0.2.2 CBOR of the cache DeviceKVCache::export_snapshot builds,
+ * forward_pass.rs:1169-1204): gathers rows [first_row, first_row + n_rows)
+ * like zr_kv_gather and encodes the document on the device.  base_position is
+ * the absolute position of the first exported row; the config map holds this
+ * context's layers, the model's kv heads, head_dim and cfg_max_seq_len.
+ * out == NULL: only *out_len.  capacity < the document: ZR_E_INVALID with
+ * *out_len set.  out is host memory (pinned for full-rate copies). */
+zr_status zr_kv_export_cbor(zr_context* ctx, const int* block_table, int n_pages, int first_offset, int first_row,
+                            int n_rows, long long base_position, int cfg_max_seq_len, uint8_t* out, size_t capacity,
+                            size_t* out_len);
 /* Raw page access for bit-exact checks: copies `n_pages` pages of `layer`
  * (K then V, pool dtype, pool layout) into host memory. */
 zr_status zr_kv_read_pages(zr_context* ctx, int layer, const int* pages, int n_pages, void* dst);
@@ -219,9 +230,9 @@ zr_status zr_kv_pool_fill_normal(zr_context* ctx, uint64_t seed, float std);
 /* Per-kernel-class timing with HIP events on the context stream (enabled
  * between begin/end) around the launches of the classes set in class_mask
  * (bit c for class c).  Classes: 0 attention, 1 gemm, 2 norm/rope/kv,
- * 3 other.  No reference counterpart (measurement only). */
+ * 3 other, 4 KV snapshot encode.  No reference counterpart (measurement only). */
 zr_status zr_timing_begin(zr_context* ctx, unsigned class_mask);
-zr_status zr_timing_end(zr_context* ctx, double* ms_by_class /* [4] */, int* launches_by_class /* [4] */);
+zr_status zr_timing_end(zr_context* ctx, double* ms_by_class /* [5] */, int* launches_by_class /* [5] */);
 
 #ifdef __cplusplus
 }

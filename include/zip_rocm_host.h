@@ -81,6 +81,21 @@ zr_status zrh_export_kv(const zrh_backend* b, int max_cached_tokens, float* k, f
  * fresh pages, validates cached_tokens and base_position. */
 zr_status zrh_import_kv(zrh_backend* b, const float* k, const float* v, int rows, int base_position,
                         int next_position);
+/* export_kv_cache -> export_snapshot (forward_pass.rs:1169-1204) as its wire
+ * bytes: the KVCacheSnapshot blob (KVCacheBlob::from_cache, kv_cache.rs:77-84,
+ * encoding FullSnapshotCbor) = KVCache::to_bytes (880-887) of the newest
+ * min(seq_len, max(max_cached_tokens, 1)) rows (all if < 0).  The sequence
+ * state goes to *next_position / *cached_tokens (KVSequenceState, 20-26).
+ * Empty cache: *out_len = 0, no document (export_snapshot returns None).
+ * out == NULL: size query; capacity short: ZR_E_INVALID with *out_len set. */
+zr_status zrh_export_kv_cbor(const zrh_backend* b, int max_cached_tokens, uint8_t* out, size_t capacity,
+                             size_t* out_len, int* next_position, int* cached_tokens);
+/* import_kv_cache -> import_snapshot (1206-1242) from the wire bytes:
+ * KVCacheSnapshot::decode_cache (kv_cache.rs:115-141) checks the document
+ * against the sequence state (cached_tokens, first cached position), then the
+ * rows are scattered into fresh pages as zrh_import_kv does. */
+zr_status zrh_import_kv_cbor(zrh_backend* b, const uint8_t* bytes, size_t len, int next_position,
+                             int cached_tokens);
 /* ForwardPass::clear_cache (2423-2426). */
 void zrh_clear(zrh_backend* b);
 /* Eviction under KV pressure: every global page bound to the session goes

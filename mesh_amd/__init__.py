@@ -5,9 +5,10 @@ include/zip_rocm.h); this package is its Python mirror of zip's provider
 interface (mesh_amd.provider).
 """
 from .provider import (BackendMicrobatchExecutor, DecodeMicrobatchOutput, DecodeMicrobatchRequest,
-                       DeviceBuffer, DeviceContext, ExecutionProviderKind, KVCacheSnapshot, ModelGeometry,
-                       RocmExecutionBackend, bf16_bits, device_info, probe_provider)
+                       DeviceBuffer, DeviceContext, ExecutionProviderKind, KVCacheBlob, KVCacheSnapshot,
+                       KVCacheWireSnapshot, KVSequenceState, ModelGeometry, RocmExecutionBackend, bf16_bits,
+                       device_info, probe_provider)
 
 __all__ = ["BackendMicrobatchExecutor", "DecodeMicrobatchOutput", "DecodeMicrobatchRequest", "DeviceBuffer",
-           "DeviceContext", "ExecutionProviderKind", "KVCacheSnapshot", "ModelGeometry", "RocmExecutionBackend",
-           "bf16_bits", "device_info", "probe_provider"]
+           "DeviceContext", "ExecutionProviderKind", "KVCacheBlob", "KVCacheSnapshot", "KVCacheWireSnapshot",
+           "KVSequenceState", "ModelGeometry", "RocmExecutionBackend", "bf16_bits", "device_info", "probe_provider"]

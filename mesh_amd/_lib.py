@@ -19,6 +19,7 @@ c_f32_p = C.POINTER(C.c_float)
 c_void_pp = C.POINTER(C.c_void_p)
 
 ZR_OK = 0
+ZR_E_INVALID = -1
 ZR_DTYPE_F32 = 0
 ZR_DTYPE_BF16 = 1
 ZR_FLAG_SPLIT_ACTIVATIONS = 1
@@ -85,6 +86,8 @@ SIGNATURES = [
     ("zr_attention", C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]),
     ("zr_kv_gather", C.c_int, [C.c_void_p, c_int_p, C.c_int, C.c_int, C.c_int, C.c_int, c_f32_p, c_f32_p]),
     ("zr_kv_scatter", C.c_int, [C.c_void_p, c_int_p, C.c_int, C.c_int, C.c_int, C.c_int, c_f32_p, c_f32_p]),
+    ("zr_kv_export_cbor", C.c_int, [C.c_void_p, c_int_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_longlong, C.c_int,
+                                    C.c_void_p, C.c_size_t, C.POINTER(C.c_size_t)]),
     ("zr_kv_read_pages", C.c_int, [C.c_void_p, C.c_int, c_int_p, C.c_int, C.c_void_p]),
     ("zr_argmax", C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
     ("zr_rms_norm", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int]),
@@ -119,6 +122,9 @@ SIGNATURES = [
     ("zrh_block_table", C.c_int, [C.c_void_p, c_u32_p, c_int_p, c_int_p, c_int_p, C.c_int]),
     ("zrh_export_kv", C.c_int, [C.c_void_p, C.c_int, c_f32_p, c_f32_p, c_int_p, c_int_p, c_int_p]),
     ("zrh_import_kv", C.c_int, [C.c_void_p, c_f32_p, c_f32_p, C.c_int, C.c_int, C.c_int]),
+    ("zrh_export_kv_cbor", C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_size_t, C.POINTER(C.c_size_t), c_int_p,
+                                     c_int_p]),
+    ("zrh_import_kv_cbor", C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_int]),
     ("zrh_clear", None, [C.c_void_p]),
     ("zrh_release_pages", C.c_int, [C.c_void_p]),
     ("zrh_kv_reserve", C.c_int, [C.c_void_p, C.c_int]),

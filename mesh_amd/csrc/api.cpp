@@ -486,6 +486,8 @@ void zr_context_destroy(zr_context* ctx) {
     }
     for (hipEvent_t e : ctx->timing.pool) hipEventDestroy(e);
     if (ctx->kv_stage) (void)hipFree(ctx->kv_stage);
+    if (ctx->cbor_ws) (void)hipFree(ctx->cbor_ws);
+    if (ctx->cbor_out) (void)hipFree(ctx->cbor_out);
     free_ctx_buffers(ctx);
     if (ctx->stream) hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -687,8 +689,8 @@ zr_status zr_attention(zr_context* ctx, zr_staged* s, int layer, const float* d_
 }
 
 static zr_status kv_copy_entry(zr_context* ctx, const int* block_table, int n_pages, int first_offset, int first_row,
-                               int n_rows, float* k, float* v, int to_pool) {
-    if (!ctx || !block_table || !k || !v) return set_global_err(ZR_E_INVALID, "null argument");
+                               int n_rows, float* k, float* v, int to_pool, float** d_rows = nullptr) {
+    if (!ctx || !block_table || (!d_rows && (!k || !v))) return set_global_err(ZR_E_INVALID, "null argument");
     if (!ctx->kv_pool) return set_err(ctx, ZR_E_INVALID, "KV pool not created");
     if (n_rows <= 0) return ZR_OK;
     if (first_offset < 0 || first_offset >= kPageRows || first_row < 0)
@@ -708,6 +710,8 @@ static zr_status kv_copy_entry(zr_context* ctx, const int* block_table, int n_pa
     if (need > ctx->kv_stage_floats) {
         ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
         if (ctx->kv_stage) (void)hipFree(ctx->kv_stage);
+    if (ctx->cbor_ws) (void)hipFree(ctx->cbor_ws);
+    if (ctx->cbor_out) (void)hipFree(ctx->cbor_out);
         ctx->kv_stage = nullptr;
         ctx->kv_stage_floats = 0;
         ZR_HIP(ctx, hipMalloc(&ctx->kv_stage, need * sizeof(float)));
@@ -721,6 +725,10 @@ static zr_status kv_copy_entry(zr_context* ctx, const int* block_table, int n_pa
     if (e == hipSuccess && to_pool) e = hipMemcpyAsync(d_v, v, 4 * elems, hipMemcpyDefault, ctx->stream);
     zr_status rc = e == hipSuccess ? ZR_OK : set_err(ctx, ZR_E_HIP, "kv copy staging: %s", hipGetErrorString(e));
     if (!rc) rc = launch_kv_copy(ctx, 0, L, d_table, first_offset, first_row, n_rows, d_k, d_v, to_pool);
+    if (d_rows) {  // gather into the device staging only ([L][rows][Kc] K, then V)
+        *d_rows = d_k;
+        return rc;
+    }
     if (!rc && !to_pool) {
         e = hipMemcpyAsync(k, d_k, 4 * elems, hipMemcpyDefault, ctx->stream);
         if (e == hipSuccess) e = hipMemcpyAsync(v, d_v, 4 * elems, hipMemcpyDefault, ctx->stream);
@@ -739,6 +747,22 @@ zr_status zr_kv_gather(zr_context* ctx, const int* block_table, int n_pages, int
 zr_status zr_kv_scatter(zr_context* ctx, const int* block_table, int n_pages, int first_offset, int first_row,
                         int n_rows, const float* src_k, const float* src_v) {
     return kv_copy_entry(ctx, block_table, n_pages, first_offset, first_row, n_rows, (float*)src_k, (float*)src_v, 1);
+}
+
+zr_status zr_kv_export_cbor(zr_context* ctx, const int* block_table, int n_pages, int first_offset, int first_row,
+                            int n_rows, long long base_position, int cfg_max_seq_len, uint8_t* out, size_t capacity,
+                            size_t* out_len) {
+    if (!ctx || !block_table || !out_len) return set_global_err(ZR_E_INVALID, "null argument");
+    if (n_rows <= 0) return set_err(ctx, ZR_E_INVALID, "empty KV export has no CBOR document");
+    if (base_position < 0 || cfg_max_seq_len < 0) return set_err(ctx, ZR_E_INVALID, "negative position or length");
+    float* d_k = nullptr;
+    zr_status rc = kv_copy_entry(ctx, block_table, n_pages, first_offset, first_row, n_rows, nullptr, nullptr, 0, &d_k);
+    if (rc) return rc;
+    const int L = ctx->desc.num_layers;
+    const float* d_v = d_k + (size_t)L * n_rows * ctx->kv_cols;
+    // KVCacheConfig of the device cache (forward_pass.rs:1791-1796): the model's kv heads and head_dim
+    const int cfg[4] = {L, ctx->desc.num_kv_heads, ctx->head_dim, cfg_max_seq_len};
+    return launch_kv_cbor(ctx, d_k, d_v, L, n_rows, ctx->kv_cols, base_position, cfg, out, capacity, out_len);
 }
 
 zr_status zr_kv_read_pages(zr_context* ctx, int layer, const int* pages, int n_pages, void* dst) {
@@ -898,8 +922,8 @@ zr_status zr_timing_begin(zr_context* ctx, unsigned class_mask) {
 zr_status zr_timing_end(zr_context* ctx, double* ms_by_class, int* launches_by_class) {
     if (!ctx) return set_global_err(ZR_E_INVALID, "null context");
     ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    double ms[4] = {0, 0, 0, 0};
-    int n[4] = {0, 0, 0, 0};
+    double ms[kTimingClasses] = {};
+    int n[kTimingClasses] = {};
     for (auto& sp : ctx->timing.spans) {
         float t = 0.0f;
         if (hipEventElapsedTime(&t, sp.second.first, sp.second.second) == hipSuccess) {

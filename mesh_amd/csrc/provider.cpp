@@ -545,6 +545,65 @@ zr_status zrh_import_kv(zrh_backend* b, const float* k, const float* v, int rows
     return ZR_OK;
 }
 
+zr_status zrh_export_kv_cbor(const zrh_backend* cb, int max_cached_tokens, uint8_t* out, size_t capacity,
+                             size_t* out_len, int* next_position, int* cached_tokens) {
+    zrh_backend* b = (zrh_backend*)cb;
+    if (!b || !out_len) return set_global_err(ZR_E_INVALID, "null argument");
+    const SessionKV& kv = b->kv;
+    if (kv.base_position + kv.seq_len != b->position)
+        return set_err(b->ctx, ZR_E_INVARIANT, "Device KV export next_position %d does not match cache next position %d",
+                       b->position, kv.base_position + kv.seq_len);
+    if (next_position) *next_position = b->position;
+    if (cached_tokens) *cached_tokens = 0;
+    *out_len = 0;
+    if (kv.seq_len == 0) return ZR_OK;
+    if (!b->ctx) return set_global_err(ZR_E_INVALID, "bookkeeping-only pool has no device context");
+    int keep = kv.seq_len;
+    if (max_cached_tokens >= 0) keep = std::min(keep, std::max(max_cached_tokens, 1));
+    std::vector<int> table;
+    int foff = 0;
+    zr_status rc = device_table(b, table, &foff);
+    // the retained rows start at base_position + dropped rows (KVCache::retain_suffix, kv_cache.rs:847-872)
+    if (!rc)
+        rc = zr_kv_export_cbor(b->ctx, table.data(), (int)table.size(), foff, kv.seq_len - keep, keep,
+                               (long long)kv.base_position + (kv.seq_len - keep), b->max_seq_len, out, capacity,
+                               out_len);
+    if (rc) return rc;
+    if (cached_tokens) *cached_tokens = keep;
+    return ZR_OK;
+}
+
+zr_status zrh_import_kv_cbor(zrh_backend* b, const uint8_t* bytes, size_t len, int next_position,
+                             int cached_tokens) {
+    if (!b || (!bytes && len)) return set_global_err(ZR_E_INVALID, "null argument");
+    zr_context* ctx = b->ctx;
+    // KVSequenceState::validate (kv_cache.rs:50-58)
+    if (cached_tokens < 0 || cached_tokens > next_position)
+        return set_err(ctx, ZR_E_INVALID, "KV sequence state is invalid: cached_tokens %d exceeds next_position %d",
+                       cached_tokens, next_position);
+    zr::KvCborDoc doc;
+    std::string err;
+    if (!zr::kv_cbor_decode(bytes, len, &doc, &err))
+        return set_err(ctx, ZR_E_INVALID, "Failed to deserialize KV cache: %s", err.c_str());
+    // KVCacheSnapshot::validate_with_cache (kv_cache.rs:121-141)
+    if (doc.rows != cached_tokens)
+        return set_err(ctx, ZR_E_INVALID, "KV snapshot cached token mismatch: payload has %lld tokens, sequence metadata says %d",
+                       doc.rows, cached_tokens);
+    if (doc.base_position != (long long)next_position - cached_tokens)
+        return set_err(ctx, ZR_E_INVALID, "KV snapshot base position mismatch: payload starts at %lld, sequence metadata says %d",
+                       doc.base_position, next_position - cached_tokens);
+    if (doc.rows > 0 && ctx) {
+        if (doc.layers != ctx->desc.num_layers)
+            return set_err(ctx, ZR_E_INVALID, "KV snapshot has %d layers, the model has %d", doc.layers,
+                           ctx->desc.num_layers);
+        if (doc.cols != ctx->kv_cols)
+            return set_err(ctx, ZR_E_INVALID, "KV cache append width mismatch: snapshot rows of %lld, cache rows of %d",
+                           doc.cols, ctx->kv_cols);
+    }
+    return zrh_import_kv(b, doc.rows ? doc.k.data() : nullptr, doc.rows ? doc.v.data() : nullptr, (int)doc.rows,
+                         (int)doc.base_position, next_position);
+}
+
 void zrh_clear(zrh_backend* b) {
     if (!b) return;
     clear_kv(b->kv);

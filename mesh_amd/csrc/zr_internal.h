@@ -64,7 +64,7 @@ struct LayerDev {
 
 struct TimingState {
     bool enabled = false;
-    unsigned class_mask = 0xF;       // classes that record events
+    unsigned class_mask = 0x1F;      // classes that record events
     std::vector<hipEvent_t> pool;    // recycled events
     std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> spans;
     size_t next_event = 0;
@@ -118,6 +118,10 @@ struct zr_context {
     zr::StagedMeta* scratch_stage = nullptr;  // reused by zr_forward
     float* kv_stage = nullptr;      // KV gather / scatter staging (rows + table)
     size_t kv_stage_floats = 0;
+    void* cbor_ws = nullptr;        // KV snapshot encoder: chunk sizes / offsets / header tables
+    size_t cbor_ws_bytes = 0;
+    void* cbor_out = nullptr;       // KV snapshot encoder: the document on the device
+    size_t cbor_out_bytes = 0;
     zr::TimingState timing;
 };
 
@@ -144,7 +148,8 @@ zr_status set_global_err(zr_status code, const char* fmt, ...);
     } while (0)
 
 // Timing of kernel classes (HIP events on the context stream).
-enum { kClassAttention = 0, kClassGemm = 1, kClassNormRopeKv = 2, kClassOther = 3 };
+enum { kClassAttention = 0, kClassGemm = 1, kClassNormRopeKv = 2, kClassOther = 3, kClassKvCbor = 4 };
+constexpr int kTimingClasses = 5;
 void timing_mark_begin(zr_context* ctx, int cls, hipEvent_t* out);
 void timing_mark_end(zr_context* ctx, int cls, hipEvent_t begin);
 
@@ -243,5 +248,24 @@ size_t packed_weight_elems(int k, int n);
 
 zr_status launch_fill_normal_bf16(zr_context* ctx, uint16_t* dst, size_t n, uint64_t seed, float std);
 zr_status launch_fill_pool_normal(zr_context* ctx, uint64_t seed, float std);
+
+// KV snapshot wire format (kv_cbor.hip) -----------------------------------
+// Fixed byte strings of the KVCache CBOR document around the 2L float arrays:
+// entry a < 2L precedes array a (K of layer a / 2 or V), the last follows the
+// last array.
+struct KvCborLayout {
+    std::vector<uint8_t> bytes;
+    std::vector<uint32_t> off, len;
+};
+KvCborLayout kv_cbor_layout(int layers, int rows, int cols, long long base_position, const int cfg[4]);
+zr_status launch_kv_cbor(zr_context* ctx, const float* d_k, const float* d_v, int layers, int rows, int cols,
+                         long long base_position, const int cfg[4], uint8_t* out, size_t capacity, size_t* out_len);
+struct KvCborDoc {
+    int layers = 0;
+    long long rows = 0, cols = 0, base_position = 0;
+    long long cfg[4] = {0, 0, 0, 0};  // num_layers, num_heads, head_dim, max_seq_len
+    std::vector<float> k, v;          // [layers][rows][cols]
+};
+bool kv_cbor_decode(const uint8_t* bytes, size_t len, KvCborDoc* doc, std::string* err);
 
 }  // namespace zr

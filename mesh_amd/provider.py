@@ -301,6 +301,34 @@ class KVCacheSnapshot:
         return self.next_position - self.cached_tokens
 
 
+@dataclass
+class KVSequenceState:
+    """KVSequenceState (kv_cache.rs:20-26)."""
+    next_position: int
+    cached_tokens: int
+
+    def first_cached_position(self) -> int:
+        return self.next_position - self.cached_tokens
+
+
+@dataclass
+class KVCacheBlob:
+    """KVCacheBlob (kv_cache.rs:68-100): encoding + the serialized KVCache."""
+    encoding: str  # "FullSnapshotCbor" (KVCacheEncoding, kv_cache.rs:12-17)
+    data: memoryview = field(repr=False)
+    storage: object = field(default=None, repr=False, compare=False)  # pinned owner, if any
+
+    def size_bytes(self) -> int:
+        return len(self.data)
+
+
+@dataclass
+class KVCacheWireSnapshot:
+    """KVCacheSnapshot (kv_cache.rs:102-107) with its blob as wire bytes."""
+    sequence: KVSequenceState
+    blob: KVCacheBlob
+
+
 class RocmExecutionBackend:
     """One session's ExecutionBackend on the rocm provider (zrh_backend)."""
 
@@ -409,6 +437,47 @@ class RocmExecutionBackend:
         v = np.ascontiguousarray(snap.values, np.float32)
         self.ctx.check(self.lib.zrh_import_kv(self.h, _ptr(k, C.c_float), _ptr(v, C.c_float), snap.cached_tokens,
                                               snap.first_cached_position(), snap.next_position))
+
+    def export_kv_snapshot(self, max_cached_tokens: Optional[int] = None,
+                           pinned: bool = False) -> Optional[KVCacheWireSnapshot]:
+        """export_kv_cache (backend.rs:73) as the reference's snapshot: sequence
+        state + KVCache::to_bytes (kv_cache.rs:880-887) encoded on the device.
+        With `pinned`, the bytes live in pinned host memory."""
+        geo = self.ctx.geo
+        n = self.cache_seq_len()
+        if n == 0:
+            return None
+        if max_cached_tokens is not None:
+            n = min(n, max(int(max_cached_tokens), 1))
+        # f16 / f32 items: at most 5 B a float, plus the fixed map and key bytes
+        bound = 5 * 2 * geo.num_layers * n * geo.kv_cols + 128 * (2 * geo.num_layers + 1) + 512
+        mc = -1 if max_cached_tokens is None else int(max_cached_tokens)
+        size, nxt, cached = C.c_size_t(), C.c_int(), C.c_int()
+        for attempt in range(2):
+            owner = PinnedBuffer(self.ctx, bound) if pinned else None
+            buf = owner.array(np.uint8, (bound,)) if pinned else np.empty(bound, np.uint8)
+            rc = self.lib.zrh_export_kv_cbor(self.h, mc, buf.ctypes.data, bound, C.byref(size), C.byref(nxt),
+                                             C.byref(cached))
+            if rc == _lib.ZR_E_INVALID and size.value > bound and attempt == 0:  # NaN items take 9 B
+                bound = size.value
+                if owner is not None:
+                    owner.free()
+                continue
+            self.ctx.check(rc)
+            break
+        if cached.value == 0:
+            return None
+        data = memoryview(buf)[:size.value]
+        return KVCacheWireSnapshot(KVSequenceState(nxt.value, cached.value),
+                                   KVCacheBlob("FullSnapshotCbor", data, owner))
+
+    def import_kv_snapshot(self, snap: KVCacheWireSnapshot):
+        """import_kv_cache (backend.rs:74) from the reference's snapshot bytes."""
+        if snap.blob.encoding != "FullSnapshotCbor":
+            raise ValueError(f"unsupported KV snapshot encoding {snap.blob.encoding}")
+        data = np.frombuffer(snap.blob.data, np.uint8)
+        self.ctx.check(self.lib.zrh_import_kv_cbor(self.h, data.ctypes.data if data.size else None, data.size,
+                                                   snap.sequence.next_position, snap.sequence.cached_tokens))
 
     def clear(self):
         self.lib.zrh_clear(self.h)

@@ -58,6 +58,11 @@ def lib():
         L.or_prefill.argtypes = [C.c_void_p, C.c_void_p, u32p, C.c_int, f32p]
         L.or_prefill_chunk.argtypes = [C.c_void_p, C.c_void_p, u32p, C.c_int, f32p, f32p]
         L.or_matmul.argtypes = [f32p, f32p, f32p, C.c_int, C.c_int, C.c_int]
+        L.or_cbor_uint.argtypes = [C.c_int, C.c_uint64, C.c_void_p]
+        L.or_cbor_float.argtypes = [C.c_float, C.c_void_p]
+        L.or_kv_cbor_encode.restype = C.c_int64
+        L.or_kv_cbor_encode.argtypes = [f32p, f32p, C.c_int, C.c_int, C.c_int, C.c_int64, C.c_int, C.c_int,
+                                        C.c_int, C.c_int, C.c_void_p, C.c_int64]
         L.or_rms_norm.argtypes = [f32p, f32p, f32p, C.c_int, C.c_int, C.c_float]
         L.or_silu.argtypes = [f32p, f32p, C.c_int64]
         L.or_apply_rope.argtypes = [f32p, f32p, C.c_int, C.c_int, u32p, C.c_int, C.c_float]
@@ -193,6 +198,36 @@ def resolve_shard_layout(hidden, num_heads, num_kv_heads, shard_start, shard_end
     _check(lib().or_resolve_shard_layout(hidden, num_heads, num_kv_heads, shard_start, shard_end,
                                          C.byref(lay), _u(idx)))
     return lay, idx[:lay.local_q_heads].tolist()
+
+
+def cbor_uint(major, v):
+    """RFC 8949 head of `major` with argument v (shortest form)."""
+    buf = (C.c_uint8 * 9)()
+    n = lib().or_cbor_uint(int(major), int(v), buf)
+    return bytes(buf[:n])
+
+
+def cbor_float(x):
+    """ciborium's float item for an f32 (narrowest exact of half / single / double)."""
+    buf = (C.c_uint8 * 9)()
+    n = lib().or_cbor_float(float(np.float32(x)), buf)
+    return bytes(buf[:n])
+
+
+def kv_cbor_encode(k, v, base_position, cfg_num_layers, cfg_num_heads, cfg_head_dim, cfg_max_seq_len):
+    """KVCache::to_bytes (kv_cache.rs:880-887) of an export_snapshot cache; k, v [layers, rows, cols] f32."""
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    L, rows, cols = k.shape
+    args = (_f(k), _f(v), L, rows, cols, int(base_position), cfg_num_layers, cfg_num_heads, cfg_head_dim,
+            cfg_max_seq_len)
+    n = lib().or_kv_cbor_encode(*args, None, 0)
+    if n < 0:
+        raise ValueError("bad KV cache shape")
+    out = np.zeros(n, np.uint8)
+    m = lib().or_kv_cbor_encode(*args, out.ctypes.data_as(C.c_void_p), n)
+    assert m == n
+    return out.tobytes()
 
 
 def partition_columns(total, position, workers):

@@ -149,6 +149,17 @@ int or_pack(int nseq, const int* q_len, const int* kv_before, const int* first_p
             const int* first_offset, const int* block_tables, int max_pages, int page_rows,
             int* cu_q, int* cu_k, int* positions, int* slot_mapping, int* seq_ids);
 
+/* ------------------------------------------------------ KV snapshot CBOR (kv_cbor.c) */
+/* Head of major type `major` with argument v (RFC 8949 section 3), shortest form; returns bytes. */
+int or_cbor_uint(int major, uint64_t v, uint8_t* out);
+/* ciborium's float item for an f32 (narrowest exact of half / single / double); returns bytes. */
+int or_cbor_float(float x, uint8_t* out);
+/* KVCache::to_bytes (kv_cache.rs:880-887) of an export_snapshot cache: k, v = [num_layers][rows][cols].
+ * Returns the byte count (out NULL: count only), -2 when capacity is too small, -1 on bad sizes. */
+int64_t or_kv_cbor_encode(const float* k, const float* v, int num_layers, int rows, int cols,
+                          int64_t base_position, int cfg_num_layers, int cfg_num_heads, int cfg_head_dim,
+                          int cfg_max_seq_len, uint8_t* out, int64_t capacity);
+
 #ifdef __cplusplus
 }
 #endif
