@@ -362,6 +362,62 @@ def measure_soak(steps, warmup):
     return out
 
 
+def measure_kv_snapshot(reps=5):
+    """KV snapshot wire bytes at the 256-session Llama-3-8B shape: one
+    session's 2048-token eviction window (32 layers x 2048 rows x 1024 f32 per
+    K and V) exported as KVCache::to_bytes (zrh_export_kv_cbor) into pinned
+    host memory.  The encoder kernels are timed with HIP events (class 4);
+    their algorithmic bytes are the f32 rows read once and the document
+    written once.  The CPU leg is the oracle's encoder on the same rows."""
+    from mesh_amd import DeviceContext, KVCacheSnapshot, ModelGeometry
+
+    g = ModelGeometry(hidden=4096, num_heads=32, num_kv_heads=8, num_layers=32, vocab=64, ffn=64)
+    ctx = DeviceContext(g, kv_dtype="bf16", max_tokens=64, max_seqs=8, max_pages_per_seq=8192 // 16 + 2)
+    rows, window = 3000, 2048
+    ctx.create_kv_pool(rows // 16 + 8)
+    rng = np.random.default_rng(0xC5)
+    k = rng.standard_normal((32, rows, g.kv_cols), np.float32)
+    v = rng.standard_normal((32, rows, g.kv_cols), np.float32)
+    b = ctx.new_backend(8192)
+    b.import_kv_cache(KVCacheSnapshot(rows, rows, k, v))
+    del k, v
+    lib = ctx.lib
+    snap = b.export_kv_snapshot(window, pinned=True)  # warm-up (workspaces, staging)
+    enc_ms, wall_ms = [], []
+    for _ in range(reps):
+        ctx.check(lib.zr_timing_begin(ctx.h, 1 << 4))
+        t0 = time.perf_counter()
+        snap = b.export_kv_snapshot(window, pinned=True)
+        wall_ms.append((time.perf_counter() - t0) * 1e3)
+        ms = (C.c_double * 5)()
+        n = (C.c_int * 5)()
+        ctx.check(lib.zr_timing_end(ctx.h, ms, n))
+        enc_ms.append(ms[4])
+    floats = 2 * 32 * window * g.kv_cols
+    doc = snap.blob.size_bytes()
+    alg = 4 * floats + doc
+    enc = float(np.median(enc_ms))
+    out = dict(workload="one session's 2048-token window, 32 layers x 1024 kv cols, bf16 pool -> f32 KVCache CBOR",
+               floats=floats, document_bytes=doc, bytes_per_float=doc / floats,
+               encode_ms=enc, export_ms=float(np.median(wall_ms)),
+               roofline={"bound": "hbm", "kernel": "cbor_count_kernel + cbor_scan_kernel + cbor_write_kernel",
+                         "achieved": alg / (enc * 1e6), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": alg / (enc * 1e6) / HBM_PEAK_GBS, "algorithmic_bytes": alg})
+    ref = b.export_kv_cache(window)
+    ctx.close()
+    try:
+        import oracle as O
+
+        t0 = time.perf_counter()
+        O.kv_cbor_encode(ref.keys, ref.values, rows - window, 32, 8, 128, 8192)
+        cpu_s = time.perf_counter() - t0
+        out["cpu_baseline"] = dict(value=doc / cpu_s / 1e6, unit="MB/s of document", cores=1, kind="port",
+                                   sample="the same document (oracle/kv_cbor.c, one thread)")
+    except Exception as e:  # the oracle is a checker; its absence only drops this leg
+        out["cpu_baseline"] = {"error": str(e)}
+    return out
+
+
 def calibrate_copy():
     """One plain device-to-device copy of 1 GiB (torch), the reference point
     for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE counters."""
@@ -386,6 +442,7 @@ def main():
     ap.add_argument("--workload", default="llama3_8b_b256", choices=sorted(WORKLOADS))
     ap.add_argument("--calibrate-copy", action="store_true")
     ap.add_argument("--soak", action="store_true", help="also run the KV-pressure soak leg")
+    ap.add_argument("--skip-kv-snapshot", action="store_true", help="skip the KV snapshot wire-format leg")
     a = ap.parse_args()
     if a.calibrate_copy:
         calibrate_copy()
@@ -408,6 +465,7 @@ def main():
                     attention_gbs=r["attention"]["achieved_gbs"], kernel_ms_per_step=r["kernel_ms_per_step"],
                     gemm_tflops=r["gemm"]["achieved_tflops"], gemm_weight_gbs=r["gemm"]["weight_gbs"])
     soak = measure_soak(max(4, a.steps // 2), 2) if a.soak else None
+    kv_snapshot = None if a.skip_kv_snapshot else measure_kv_snapshot()
     cpu = None if a.skip_cpu else cpu_baseline(a.workload)
     att = main_r["attention"]
     line = {
@@ -432,6 +490,7 @@ def main():
                       "weight_stream_gbs": main_r["gemm"]["weight_gbs"]},
         "bs32": bs32,
         "soak": soak,
+        "kv_snapshot": kv_snapshot,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
