@@ -26,7 +26,7 @@
 // The float stream is the 2L arrays in document order (K of layer 0, V of
 // layer 0, K of layer 1, ...).  Everything between two arrays (and before
 // the first, after the last) is a fixed byte string built on the host.  The
-// device pass is a byte-size count per 4096-float chunk, an exclusive scan of
+// device pass is a byte-size count per 2048-float chunk, an exclusive scan of
 // the chunk sizes, and a write pass that lays each chunk's bytes out in LDS
 // (chunk-local scan over its threads) and stores them with 16 B vector
 // stores into the chunk's slot of the output.
@@ -40,9 +40,9 @@ namespace zr {
 namespace {
 
 constexpr int kCborThreads = 256;
-constexpr int kCborPerThread = 16;
+constexpr int kCborPerThread = 8;
 constexpr int kCborChunk = kCborThreads * kCborPerThread;  // floats per block
-constexpr int kCborStage = 45056;                           // LDS bytes of one chunk (bound checked on the host)
+constexpr int kCborStage = 22528;                           // LDS bytes of one chunk (bound checked on the host)
 
 // binary16 bits of an f32 when the value is exactly a binary16 (see header).
 __host__ __device__ inline bool cbor_half(uint32_t u, uint32_t* h) {
@@ -114,11 +114,12 @@ struct CborArgs {
     const uint32_t* hdr_off;   // [arrays + 1]
     const uint32_t* hdr_len;   // [arrays + 1]
     uint32_t* chunk_bytes;     // [chunks]
-    unsigned long long* chunk_off;  // [chunks + 1]
+    unsigned long long* chunk_off;  // [chunks]: offset inside the chunk's group of 1024
+    unsigned long long* group_off;  // [groups + 1]: group offsets, then the document size
     uint8_t* out;
 };
 
-// This thread's 16 floats (one array: n is a multiple of 16) and their bytes,
+// This thread's 8 floats (one array: n is a multiple of 16) and their bytes,
 // including the prefix of an array that starts here and the suffix after the
 // last float of the stream.
 struct ThreadSpan {
@@ -128,9 +129,9 @@ struct ThreadSpan {
     long long within;
 };
 
-__device__ inline ThreadSpan thread_span(const CborArgs& a) {
+__device__ inline ThreadSpan thread_span(const CborArgs& a, long long chunk) {
     ThreadSpan t;
-    t.i0 = (long long)blockIdx.x * kCborChunk + (long long)threadIdx.x * kCborPerThread;
+    t.i0 = chunk * kCborChunk + (long long)threadIdx.x * kCborPerThread;
     const long long left = a.total - t.i0;
     t.count = left <= 0 ? 0 : (left < kCborPerThread ? (int)left : kCborPerThread);
     t.array = t.count ? (int)(t.i0 / a.n) : 0;
@@ -138,11 +139,11 @@ __device__ inline ThreadSpan thread_span(const CborArgs& a) {
     return t;
 }
 
-__device__ inline void load16(const CborArgs& a, const ThreadSpan& t, uint32_t* u) {
+__device__ inline void load_floats(const CborArgs& a, const ThreadSpan& t, uint32_t* u) {
     const float* src = ((t.array & 1) ? a.v : a.k) + (long long)(t.array >> 1) * a.n + t.within;
     const uint4* s4 = (const uint4*)src;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < kCborPerThread / 4; ++q) {
         const uint4 w = s4[q];
         u[4 * q] = w.x;
         u[4 * q + 1] = w.y;
@@ -173,48 +174,80 @@ __device__ inline uint32_t block_sum(uint32_t x, uint32_t* red) {
 
 __global__ __launch_bounds__(kCborThreads) void cbor_count_kernel(CborArgs a) {
     __shared__ uint32_t red[kCborThreads / 64];
-    const ThreadSpan t = thread_span(a);
+    const ThreadSpan t = thread_span(a, blockIdx.x);
     uint32_t u[kCborPerThread];
-    if (t.count) load16(a, t, u);
+    if (t.count) load_floats(a, t, u);
     const uint32_t b = block_sum(thread_bytes(a, t, u), red);
     if (threadIdx.x == 0) a.chunk_bytes[blockIdx.x] = b;
 }
 
-// One block: exclusive scan of the chunk sizes into chunk_off[0..chunks].
-__global__ __launch_bounds__(1024) void cbor_scan_kernel(const uint32_t* __restrict__ bytes, int chunks,
-                                                         unsigned long long* __restrict__ off) {
-    __shared__ unsigned long long part[1024];
-    const int tid = threadIdx.x;
-    const int per = (chunks + 1023) / 1024;
-    const int c0 = min(chunks, tid * per), c1 = min(chunks, c0 + per);
-    unsigned long long s = 0;
-    for (int c = c0; c < c1; ++c) s += bytes[c];
-    part[tid] = s;
+// Exclusive scan of the chunk sizes in two levels: each 1024-thread block
+// scans 1024 chunks (chunk_off = offset inside its group) and writes the
+// group's total; one block then scans the group totals (group_off, and the
+// document size at group_off[groups]).
+__device__ inline unsigned long long block_exclusive_1024(unsigned long long x, unsigned long long* wtot,
+                                                         unsigned long long* total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    unsigned long long incl = x;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const unsigned long long y = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += y;
+    }
+    if (lane == 63) wtot[wave] = incl;
     __syncthreads();
-    for (int d = 1; d < 1024; d <<= 1) {  // inclusive Hillis-Steele scan
-        const unsigned long long x = tid >= d ? part[tid - d] : 0ull;
-        __syncthreads();
-        part[tid] += x;
-        __syncthreads();
+    unsigned long long base = 0, all = 0;
+    for (int w = 0; w < 16; ++w) {
+        if (w < wave) base += wtot[w];
+        all += wtot[w];
     }
-    unsigned long long run = part[tid] - s;
-    for (int c = c0; c < c1; ++c) {
-        off[c] = run;
-        run += bytes[c];
-    }
-    if (tid == 1023) off[chunks] = part[1023];
+    *total = all;
+    return base + incl - x;
 }
 
+__global__ __launch_bounds__(1024) void cbor_scan_groups_kernel(const uint32_t* __restrict__ bytes, int chunks,
+                                                                unsigned long long* __restrict__ off,
+                                                                unsigned long long* __restrict__ group_tot) {
+    __shared__ unsigned long long wtot[16];
+    const int c = blockIdx.x * 1024 + threadIdx.x;
+    unsigned long long total;
+    const unsigned long long ex = block_exclusive_1024(c < chunks ? bytes[c] : 0u, wtot, &total);
+    if (c < chunks) off[c] = ex;
+    if (threadIdx.x == 0) group_tot[blockIdx.x] = total;
+}
+
+__global__ __launch_bounds__(1024) void cbor_scan_top_kernel(const unsigned long long* __restrict__ group_tot,
+                                                             int groups, unsigned long long* __restrict__ group_off) {
+    __shared__ unsigned long long wtot[16];
+    unsigned long long run = 0;
+    for (int g0 = 0; g0 < groups; g0 += 1024) {  // block-uniform loop
+        const int g = g0 + threadIdx.x;
+        unsigned long long total;
+        const unsigned long long ex = block_exclusive_1024(g < groups ? group_tot[g] : 0ull, wtot, &total);
+        if (g < groups) group_off[g] = run + ex;
+        run += total;
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) group_off[groups] = run;
+}
+
+// One block per chunk.  A thread whose 8 floats are all halves (the common
+// case for bf16-valued rows) and hold no header bytes builds its 24 bytes as
+// 6 little-endian words (f9 hi lo per float), shifts them to the LDS word
+// grid and stores whole words (edge words, shared with the neighbours, byte
+// by byte); other threads store byte by byte.  The chunk then leaves LDS in
+// 16 B vector stores.
 __global__ __launch_bounds__(kCborThreads) void cbor_write_kernel(CborArgs a) {
     __shared__ __align__(16) uint8_t stage[kCborStage + 16];
     __shared__ uint32_t wsum[kCborThreads / 64];
-    const ThreadSpan t = thread_span(a);
-    uint32_t u[kCborPerThread];
-    if (t.count) load16(a, t, u);
-    const uint32_t mine = thread_bytes(a, t, u);
-    // exclusive scan of `mine` over the block
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    uint32_t incl = mine;
+    const int c = blockIdx.x;
+    const unsigned long long g = a.chunk_off[c] + a.group_off[c >> 10];
+    uint32_t u[kCborPerThread];
+    const ThreadSpan t = thread_span(a, c);
+    if (t.count) load_floats(a, t, u);
+    const uint32_t mine = thread_bytes(a, t, u);
+    uint32_t incl = mine;  // exclusive scan of `mine` over the block
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
         const uint32_t y = __shfl_up(incl, o, 64);
@@ -222,19 +255,53 @@ __global__ __launch_bounds__(kCborThreads) void cbor_write_kernel(CborArgs a) {
     }
     if (lane == 63) wsum[wave] = incl;
     __syncthreads();
-    uint32_t base = 0;
-    for (int w = 0; w < wave; ++w) base += wsum[w];
-    uint32_t total = 0;
+    uint32_t base = 0, total = 0;
 #pragma unroll
-    for (int w = 0; w < kCborThreads / 64; ++w) total += wsum[w];
-    const unsigned long long g = a.chunk_off[blockIdx.x];
+    for (int w = 0; w < kCborThreads / 64; ++w) {
+        if (w < wave) base += wsum[w];
+        total += wsum[w];
+    }
     const uint32_t shift = (uint32_t)(g & 15u);  // stage byte s <-> output byte (g & ~15) + s
-    uint8_t* o = stage + shift + base + (incl - mine);
-    if (t.count) {
+    const uint32_t off = shift + base + (incl - mine);
+    uint32_t hv[kCborPerThread];
+    bool all_half = t.count && t.within != 0 && t.i0 + kCborPerThread < a.total;
+#pragma unroll
+    for (int j = 0; j < kCborPerThread; ++j) {
+        uint32_t h = 0;
+        all_half = cbor_half(u[j], &h) && all_half;
+        hv[j] = h;
+    }
+    if (all_half) {
+        constexpr int NW = 3 * kCborPerThread / 4;
+        uint32_t w[NW];
+#pragma unroll
+        for (int q = 0; q < kCborPerThread / 4; ++q) {  // f9 a1 a0 f9 | b1 b0 f9 c1 | c0 f9 d1 d0
+            const uint32_t h0 = hv[4 * q], h1 = hv[4 * q + 1], h2 = hv[4 * q + 2], h3 = hv[4 * q + 3];
+            w[3 * q] = 0xf9u | ((h0 >> 8) << 8) | ((h0 & 0xffu) << 16) | (0xf9u << 24);
+            w[3 * q + 1] = (h1 >> 8) | ((h1 & 0xffu) << 8) | (0xf9u << 16) | ((h2 >> 8) << 24);
+            w[3 * q + 2] = (h2 & 0xffu) | (0xf9u << 8) | ((h3 >> 8) << 16) | ((h3 & 0xffu) << 24);
+        }
+        const uint32_t sb = off & 3u, wb = off >> 2;
+        uint32_t* sw = (uint32_t*)stage;
+        if (sb == 0) {
+#pragma unroll
+            for (int i = 0; i < NW; ++i) sw[wb + i] = w[i];
+        } else {
+            const uint32_t lsh = 8 * sb, rsh = 32 - lsh;
+            const uint32_t first = w[0] << lsh;  // bytes sb..3 of word wb are ours
+            for (uint32_t b = sb; b < 4; ++b) stage[(wb << 2) + b] = (uint8_t)(first >> (8 * b));
+#pragma unroll
+            for (int k = 1; k < NW; ++k) sw[wb + k] = (w[k] << lsh) | (w[k - 1] >> rsh);
+            const uint32_t last = w[NW - 1] >> rsh;  // bytes 0..sb-1 of word wb + NW are ours
+            for (uint32_t b = 0; b < sb; ++b) stage[((wb + NW) << 2) + b] = (uint8_t)(last >> (8 * b));
+        }
+    } else if (t.count) {
+        uint8_t* o = stage + off;
         if (t.within == 0) {
             const uint8_t* h = a.hdr + a.hdr_off[t.array];
             for (uint32_t i = 0; i < a.hdr_len[t.array]; ++i) *o++ = h[i];
         }
+#pragma unroll
         for (int j = 0; j < kCborPerThread; ++j) {
             cbor_float_write(u[j], o);
             o += cbor_float_size(u[j]);
@@ -360,7 +427,8 @@ zr_status launch_kv_cbor(zr_context* ctx, const float* d_k, const float* d_v, in
         return set_err(ctx, ZR_E_UNSUPPORTED, "KV rows of %lld floats per layer too short for the CBOR chunking", n);
     // workspace: chunk sizes, offsets, header tables (grown on demand)
     const size_t tab = lay.off.size();
-    const size_t need = 16 + (size_t)chunks * 4 + ((size_t)chunks + 1) * 8 + tab * 8 + lay.bytes.size() + 64;
+    const long long groups = (chunks + 1023) / 1024;
+    const size_t need = 64 + (size_t)chunks * 12 + (2 * (size_t)groups + 1) * 8 + tab * 8 + lay.bytes.size();
     if (need > ctx->cbor_ws_bytes) {
         ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
         if (ctx->cbor_ws) (void)hipFree(ctx->cbor_ws);
@@ -371,7 +439,9 @@ zr_status launch_kv_cbor(zr_context* ctx, const float* d_k, const float* d_v, in
     }
     uint8_t* ws = (uint8_t*)ctx->cbor_ws;
     unsigned long long* d_off = (unsigned long long*)ws;
-    uint32_t* d_bytes = (uint32_t*)(ws + ((size_t)chunks + 1) * 8);
+    unsigned long long* d_gtot = d_off + chunks;
+    unsigned long long* d_goff = d_gtot + groups;
+    uint32_t* d_bytes = (uint32_t*)(d_goff + groups + 1);
     uint32_t* d_hoff = d_bytes + chunks;
     uint32_t* d_hlen = d_hoff + tab;
     uint8_t* d_hdr = (uint8_t*)(d_hlen + tab);
@@ -392,16 +462,20 @@ zr_status launch_kv_cbor(zr_context* ctx, const float* d_k, const float* d_v, in
     a.hdr_len = d_hlen;
     a.chunk_bytes = d_bytes;
     a.chunk_off = d_off;
+    a.group_off = d_goff;
     a.out = nullptr;
     hipEvent_t ev;
     timing_mark_begin(ctx, kClassKvCbor, &ev);
     hipLaunchKernelGGL(cbor_count_kernel, dim3((unsigned)chunks), dim3(kCborThreads), 0, ctx->stream, a);
     ZR_LAUNCH_CHECK(ctx);
-    hipLaunchKernelGGL(cbor_scan_kernel, dim3(1), dim3(1024), 0, ctx->stream, d_bytes, (int)chunks, d_off);
+    hipLaunchKernelGGL(cbor_scan_groups_kernel, dim3((unsigned)groups), dim3(1024), 0, ctx->stream, d_bytes,
+                       (int)chunks, d_off, d_gtot);
+    ZR_LAUNCH_CHECK(ctx);
+    hipLaunchKernelGGL(cbor_scan_top_kernel, dim3(1), dim3(1024), 0, ctx->stream, d_gtot, (int)groups, d_goff);
     ZR_LAUNCH_CHECK(ctx);
     timing_mark_end(ctx, kClassKvCbor, ev);
     unsigned long long doc = 0;
-    ZR_HIP(ctx, hipMemcpyAsync(&doc, d_off + chunks, 8, hipMemcpyDeviceToHost, ctx->stream));
+    ZR_HIP(ctx, hipMemcpyAsync(&doc, d_goff + groups, 8, hipMemcpyDeviceToHost, ctx->stream));
     ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
     if (out_len) *out_len = (size_t)doc;
     if (!out) return ZR_OK;
