@@ -202,6 +202,21 @@ zr_status zr_kv_read_pages(zr_context* ctx, int layer, const int* pages, int n_p
 /* Greedy argmax over rows of a device [rows, cols] f32 matrix (first index on
  * ties; runtime.rs:561-570). */
 zr_status zr_argmax(zr_context* ctx, const float* d_x, int rows, int cols, uint32_t* d_out);
+/* Stochastic sampling of device logits [rows, cols] f32, per row with its own
+ * temperature, top_p and seed (host arrays): sample_tokens_device_with_seeds
+ * (runtime.rs:534-601) as the batched decode path groups it
+ * (sample_fast_path_logits_batch, backend.rs:275-316).  temperature <= 0 or
+ * top_p <= 0: argmax.  Cumulative sums are exact integer sums of
+ * round(p * 2^36) (deterministic; the reference's candle reduction orders are
+ * unspecified).  d_out: device u32 [rows]. */
+zr_status zr_sample(zr_context* ctx, const float* d_logits, int rows, int cols, const float* temperature,
+                    const float* top_p, const uint64_t* seeds, uint32_t* d_out);
+/* The same on the logits of the context's last forward (its first `rows`
+ * rows, one per sequence of that microbatch); tokens to host memory.  For
+ * ProviderRuntimeCore::sample (forward_pass.rs:2046-2086) on device logits
+ * and the batched decode path. */
+zr_status zr_sample_last_logits(zr_context* ctx, int rows, const float* temperature, const float* top_p,
+                                const uint64_t* seeds, uint32_t* out_tokens);
 /* y = rms_norm(x) * gamma (tensor_ops.rs:285-304), device f32 [rows, cols]. */
 zr_status zr_rms_norm(zr_context* ctx, const float* d_x, const float* d_gamma, float* d_y, int rows,
                       int cols);

@@ -49,6 +49,15 @@ zr_status zrh_decode_step(zrh_backend* b, uint32_t token, float* logits, uint32_
  * [layers][2][n][hidden] -- each nullable. */
 zr_status zrh_decode_step_batch(zrh_backend* const* backends, int n, const uint32_t* tokens, uint32_t* out_tokens,
                                 float* out_logits, float* out_partials);
+/* decode_step_batch with per-request sampling (DecodeMicrobatchRequest
+ * temperature / top_p / sampling_seed, backend.rs:90-105): the fused step,
+ * then sample_fast_path_logits_batch (275-316) on the step's device logits
+ * (zr_sample semantics; rows with temperature <= 0 or top_p <= 0 keep the
+ * argmax).  out_tokens is required.  If sampling fails after the step, the
+ * sessions have advanced (the step is not rolled back), as in the reference. */
+zr_status zrh_decode_step_batch_sampled(zrh_backend* const* backends, int n, const uint32_t* tokens,
+                                        const float* temperature, const float* top_p, const uint64_t* seeds,
+                                        uint32_t* out_tokens, float* out_logits, float* out_partials);
 /* Mixed chunked-prefill + decode microbatch: session i appends q_len[i]
  * tokens at its current position (tokens packed back to back); logits come
  * from the last row of every session. */

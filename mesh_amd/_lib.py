@@ -90,6 +90,9 @@ SIGNATURES = [
                                     C.c_void_p, C.c_size_t, C.POINTER(C.c_size_t)]),
     ("zr_kv_read_pages", C.c_int, [C.c_void_p, C.c_int, c_int_p, C.c_int, C.c_void_p]),
     ("zr_argmax", C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
+    ("zr_sample", C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, c_f32_p, c_f32_p, C.POINTER(C.c_uint64),
+                            C.c_void_p]),
+    ("zr_sample_last_logits", C.c_int, [C.c_void_p, C.c_int, c_f32_p, c_f32_p, C.POINTER(C.c_uint64), c_u32_p]),
     ("zr_rms_norm", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int]),
     ("zr_gemm", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),
     ("zr_device_alloc", C.c_int, [C.c_void_p, C.c_size_t, c_void_pp]),
@@ -111,6 +114,8 @@ SIGNATURES = [
     ("zrh_prefill", C.c_int, [C.c_void_p, c_u32_p, C.c_int, c_f32_p, c_u32_p]),
     ("zrh_decode_step", C.c_int, [C.c_void_p, C.c_uint32, c_f32_p, c_u32_p]),
     ("zrh_decode_step_batch", C.c_int, [c_void_pp, C.c_int, c_u32_p, c_u32_p, c_f32_p, c_f32_p]),
+    ("zrh_decode_step_batch_sampled", C.c_int, [c_void_pp, C.c_int, c_u32_p, c_f32_p, c_f32_p,
+                                                C.POINTER(C.c_uint64), c_u32_p, c_f32_p, c_f32_p]),
     ("zrh_forward_mixed", C.c_int, [c_void_pp, C.c_int, c_int_p, c_u32_p, c_u32_p, c_f32_p, c_f32_p]),
     ("zrh_stage_mixed", C.c_int, [c_void_pp, C.c_int, c_int_p, c_u32_p, c_void_pp]),
     ("zrh_cache_seq_len", C.c_int, [C.c_void_p]),

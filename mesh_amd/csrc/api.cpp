@@ -488,6 +488,7 @@ void zr_context_destroy(zr_context* ctx) {
     if (ctx->kv_stage) (void)hipFree(ctx->kv_stage);
     if (ctx->cbor_ws) (void)hipFree(ctx->cbor_ws);
     if (ctx->cbor_out) (void)hipFree(ctx->cbor_out);
+    if (ctx->sample_ws) (void)hipFree(ctx->sample_ws);
     free_ctx_buffers(ctx);
     if (ctx->stream) hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -712,6 +713,7 @@ static zr_status kv_copy_entry(zr_context* ctx, const int* block_table, int n_pa
         if (ctx->kv_stage) (void)hipFree(ctx->kv_stage);
     if (ctx->cbor_ws) (void)hipFree(ctx->cbor_ws);
     if (ctx->cbor_out) (void)hipFree(ctx->cbor_out);
+    if (ctx->sample_ws) (void)hipFree(ctx->sample_ws);
         ctx->kv_stage = nullptr;
         ctx->kv_stage_floats = 0;
         ZR_HIP(ctx, hipMalloc(&ctx->kv_stage, need * sizeof(float)));
@@ -794,6 +796,29 @@ zr_status zr_argmax(zr_context* ctx, const float* d_x, int rows, int cols, uint3
     zr_status rc = launch_argmax(ctx, d_x, rows, cols, d_out);
     if (!rc) ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
     return rc;
+}
+
+zr_status zr_sample(zr_context* ctx, const float* d_logits, int rows, int cols, const float* temperature,
+                    const float* top_p, const uint64_t* seeds, uint32_t* d_out) {
+    if (!ctx || !d_logits || !temperature || !top_p || !seeds || !d_out)
+        return set_global_err(ZR_E_INVALID, "null argument");
+    if (rows <= 0 || cols <= 0) return set_err(ctx, ZR_E_INVALID, "Device sampling received an empty logits tensor");
+    zr_status rc = launch_sample(ctx, d_logits, rows, cols, temperature, top_p, seeds, d_out);
+    if (!rc) ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return rc;
+}
+
+zr_status zr_sample_last_logits(zr_context* ctx, int rows, const float* temperature, const float* top_p,
+                                const uint64_t* seeds, uint32_t* out_tokens) {
+    if (!ctx || !out_tokens) return set_global_err(ZR_E_INVALID, "null argument");
+    if (!ctx->logits || !ctx->tokens_out) return set_err(ctx, ZR_E_INVALID, "no logits to sample");
+    if (rows <= 0 || rows > ctx->desc.max_seqs)
+        return set_err(ctx, ZR_E_INVALID, "Device sampling received %d rows", rows);
+    zr_status rc = launch_sample(ctx, ctx->logits, rows, ctx->desc.vocab, temperature, top_p, seeds, ctx->tokens_out);
+    if (rc) return rc;
+    ZR_HIP(ctx, hipMemcpyAsync(out_tokens, ctx->tokens_out, 4 * (size_t)rows, hipMemcpyDeviceToHost, ctx->stream));
+    ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return ZR_OK;
 }
 
 zr_status zr_rms_norm(zr_context* ctx, const float* d_x, const float* d_gamma, float* d_y, int rows, int cols) {

@@ -418,6 +418,26 @@ zr_status zrh_decode_step_batch(zrh_backend* const* backends, int n, const uint3
     return run_mixed(backends, n, ones.data(), tokens, true, out_tokens, out_logits, out_partials);
 }
 
+zr_status zrh_decode_step_batch_sampled(zrh_backend* const* backends, int n, const uint32_t* tokens,
+                                        const float* temperature, const float* top_p, const uint64_t* seeds,
+                                        uint32_t* out_tokens, float* out_logits, float* out_partials) {
+    if (!backends || !tokens || n <= 0) return set_global_err(ZR_E_INVALID, "Decode microbatch requires at least one backend and token");
+    if (!temperature || !top_p || !seeds || !out_tokens) return set_global_err(ZR_E_INVALID, "null argument");
+    std::vector<int> ones(n, 1);
+    zr_status rc = run_mixed(backends, n, ones.data(), tokens, true, out_tokens, out_logits, out_partials);
+    if (rc) return rc;
+    bool stochastic = false;
+    for (int i = 0; i < n; ++i) stochastic |= temperature[i] > 0.0f && top_p[i] > 0.0f;
+    if (!stochastic) return ZR_OK;  // the argmax of the forward is the answer
+    // the step itself succeeded; a sampling failure is reported as such (backend.rs:137-151)
+    rc = zr_sample_last_logits(backends[0]->ctx, n, temperature, top_p, seeds, out_tokens);
+    if (rc) {
+        const std::string why = zr_last_error(backends[0]->ctx);
+        set_err(backends[0]->ctx, rc, "Device stochastic sampling failed: %s", why.c_str());
+    }
+    return rc;
+}
+
 zr_status zrh_forward_mixed(zrh_backend* const* backends, int n, const int* q_len, const uint32_t* tokens,
                             uint32_t* out_tokens, float* out_logits, float* out_partials) {
     if (!backends || !tokens || !q_len || n <= 0) return set_global_err(ZR_E_INVALID, "null argument");

@@ -122,6 +122,8 @@ struct zr_context {
     size_t cbor_ws_bytes = 0;
     void* cbor_out = nullptr;       // KV snapshot encoder: the document on the device
     size_t cbor_out_bytes = 0;
+    void* sample_ws = nullptr;      // stochastic sampling: per-row parameters
+    size_t sample_ws_bytes = 0;
     zr::TimingState timing;
 };
 
@@ -222,6 +224,9 @@ zr_status launch_kv_copy(zr_context* ctx, int layer_begin, int layer_end, const 
                          int first_offset, int first_row, int n_rows, float* k, float* v,
                          int to_pool);
 zr_status launch_argmax(zr_context* ctx, const float* x, int rows, int cols, uint32_t* out);
+// sample_tokens_device_with_seeds per row (sample.hip); parameters are host arrays
+zr_status launch_sample(zr_context* ctx, const float* d_logits, int rows, int cols, const float* temperature,
+                        const float* top_p, const uint64_t* seeds, uint32_t* d_out);
 
 enum GemmEpilogue { kEpiStore = 0, kEpiSwiGLU = 1 };
 struct GemmPlan {

@@ -373,12 +373,11 @@ class RocmExecutionBackend:
 
     def sample(self, logits: np.ndarray, temperature: float, top_p: float, seed: int) -> int:
         """ForwardPass::sample (forward_pass.rs:2046-2086): greedy when temperature <= 0
-        or (temperature == 1 and top_p >= 1).  The greedy id was computed on the GPU
-        with the logits; stochastic sampling is not provided by this provider yet."""
+        or (temperature == 1 and top_p >= 1) -- the argmax computed on the GPU with the
+        logits; otherwise sample_token_device (runtime.rs:622-632) on the GPU."""
         if temperature <= 0.0 or (temperature == 1.0 and top_p >= 1.0):
             return self.last_greedy
-        raise ZrError(-5, "Device stochastic sampling failed: temperature/top-p sampling is not "
-                          "implemented by the rocm provider")
+        return sample_device(self.ctx, np.asarray(logits, np.float32)[None], [temperature], [top_p], [seed])[0]
 
     def cache_seq_len(self) -> int:
         return self.lib.zrh_cache_seq_len(self.h)
@@ -505,6 +504,26 @@ class RocmExecutionBackend:
         self.ctx.check(self.lib.zrh_retain_suffix(self.h, keep))
 
 
+def sample_device(ctx: "DeviceContext", logits: np.ndarray, temperature, top_p, seeds) -> List[int]:
+    """sample_tokens_device_with_seeds (runtime.rs:534-601) per row with its own
+    temperature / top_p / seed, on the GPU (zr_sample)."""
+    x = np.ascontiguousarray(logits, np.float32)
+    rows, cols = x.shape
+    temps = np.ascontiguousarray(temperature, np.float32)
+    tops = np.ascontiguousarray(top_p, np.float32)
+    sd = np.ascontiguousarray(seeds, np.uint64)
+    d_x = DeviceBuffer.from_numpy(ctx, x)
+    d_out = DeviceBuffer(ctx, 4 * rows)
+    try:
+        ctx.check(ctx.lib.zr_sample(ctx.h, d_x.ptr, rows, cols, _ptr(temps, C.c_float), _ptr(tops, C.c_float),
+                                    _ptr(sd, C.c_uint64), d_out.ptr))
+        out = d_out.download(np.uint32, (rows,))
+    finally:
+        d_x.free()
+        d_out.free()
+    return [int(t) for t in out]
+
+
 @dataclass
 class DecodeMicrobatchRequest:
     session_id: str
@@ -541,18 +560,25 @@ class BackendMicrobatchExecutor:
         for r in requests:
             if r.backend.ctx is not ctx:
                 raise ZrError(-1, "Fast-path decode batch requires one shared model residency")
-            if not (r.temperature <= 0.0 or r.top_p <= 0.0):
-                raise ZrError(-5, "Device stochastic sampling failed: temperature/top-p sampling is not "
-                                  "implemented by the rocm provider")
         n = len(requests)
         toks = np.ascontiguousarray([r.token for r in requests], np.uint32)
         out_tokens = np.zeros(n, np.uint32)
         logits = np.zeros((n, ctx.geo.vocab), np.float32) if want_logits else None
         ptrs, _keep = _backend_array([r.backend for r in requests])
+        stochastic = any(r.temperature > 0.0 and r.top_p > 0.0 for r in requests)
         t0 = time.perf_counter()
-        ctx.check(ctx.lib.zrh_decode_step_batch(ptrs, n, _ptr(toks, C.c_uint32), _ptr(out_tokens, C.c_uint32),
-                                                _ptr(logits, C.c_float) if logits is not None else None,
-                                                _ptr(partials, C.c_float) if partials is not None else None))
+        lg = _ptr(logits, C.c_float) if logits is not None else None
+        pa = _ptr(partials, C.c_float) if partials is not None else None
+        if stochastic:  # sample_fast_path_logits_batch (backend.rs:275-316) on the device logits
+            temps = np.ascontiguousarray([r.temperature for r in requests], np.float32)
+            tops = np.ascontiguousarray([r.top_p for r in requests], np.float32)
+            seeds = np.ascontiguousarray([r.sampling_seed for r in requests], np.uint64)
+            ctx.check(ctx.lib.zrh_decode_step_batch_sampled(ptrs, n, _ptr(toks, C.c_uint32), _ptr(temps, C.c_float),
+                                                            _ptr(tops, C.c_float), _ptr(seeds, C.c_uint64),
+                                                            _ptr(out_tokens, C.c_uint32), lg, pa))
+        else:
+            ctx.check(ctx.lib.zrh_decode_step_batch(ptrs, n, _ptr(toks, C.c_uint32), _ptr(out_tokens, C.c_uint32),
+                                                    lg, pa))
         ms = int((time.perf_counter() - t0) * 1000)
         return [DecodeMicrobatchOutput(r.session_id, logits[i] if logits is not None else None, int(out_tokens[i]), ms)
                 for i, r in enumerate(requests)]

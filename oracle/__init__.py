@@ -72,6 +72,9 @@ def lib():
         L.or_sample_token.argtypes = [f32p, C.c_int, C.c_float, C.c_float, C.c_uint64]
         L.or_sample_token.restype = C.c_uint32
         L.or_sample_threshold.argtypes = [C.c_uint64]
+        L.or_sample_token_device.restype = C.c_uint32
+        L.or_sample_token_device.argtypes = [f32p, C.c_int, C.c_float, C.c_float, C.c_uint64,
+                                             C.POINTER(C.c_double)]
         L.or_sample_threshold.restype = C.c_float
         L.or_causal_attention_with_prefix.argtypes = [f32p, f32p, f32p, f32p, C.c_int, C.c_int,
                                                       C.c_int, C.c_float, C.c_int]
@@ -155,6 +158,14 @@ def sample_greedy(logits):
 def sample_token(logits, temperature, top_p, seed):
     x = f32(logits)
     return int(lib().or_sample_token(_f(x), x.size, temperature, top_p, seed))
+
+
+def sample_token_device(logits, temperature, top_p, seed):
+    """runtime.rs:534-601 device sampler for one row -> (token, margin)."""
+    x = f32(logits)
+    m = C.c_double()
+    t = lib().or_sample_token_device(_f(x), x.size, float(temperature), float(top_p), int(seed), C.byref(m))
+    return int(t), m.value
 
 
 def sample_threshold(seed):

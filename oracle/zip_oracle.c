@@ -187,7 +187,7 @@ uint32_t or_sample_token(const float* logits, int n, float temperature, float to
     float selected_sum = 0.0f;
     for (int i = 0; i < cutoff; ++i) selected_sum += ip[i].p;
     const float r = or_sample_threshold(seed);
-    uint32_t result = (uint32_t)ip[0].idx;
+    uint32_t result = n > 0 ? (uint32_t)ip[0].idx : 0;
     if (top_p >= 1.0f) {
         float c = 0.0f;
         for (int i = 0; i < n; ++i) {
@@ -211,6 +211,111 @@ uint32_t or_sample_token(const float* logits, int n, float temperature, float to
     }
 done:
     free(scaled);
+    free(probs);
+    free(ip);
+    free(tmp);
+    return result;
+}
+
+typedef struct {
+    int idx;
+    double p;
+} idx_prob64;
+
+static void stable_sort_desc64(idx_prob64* v, int n, idx_prob64* tmp) {
+    for (int width = 1; width < n; width *= 2) {
+        for (int lo = 0; lo < n; lo += 2 * width) {
+            int mid = lo + width < n ? lo + width : n;
+            int hi = lo + 2 * width < n ? lo + 2 * width : n;
+            int i = lo, j = mid, k = lo;
+            while (i < mid && j < hi) tmp[k++] = (v[j].p > v[i].p) ? v[j++] : v[i++];
+            while (i < mid) tmp[k++] = v[i++];
+            while (j < hi) tmp[k++] = v[j++];
+        }
+        memcpy(v, tmp, sizeof(idx_prob64) * (size_t)n);
+    }
+}
+
+/* runtime.rs:534-601 (sample_tokens_device_with_seeds), the batched decode
+ * path's sampler (backend.rs:275-316), for one row: temperature scaling as
+ * affine(1 / T) (f32(x * f32(1 / T)), 555-563), softmax, then
+ * top_p >= 1: the first index whose cumulative probability reaches tau;
+ * top_p < 1: probabilities sorted descending (ties in index order), kept
+ * while the cumulative sum before them is below top_p (apply_top_p_device,
+ * 461-482), renormalised, first crossing of tau in sorted order.  No
+ * crossing: position 0 (argmax of an all-zero mask, 517-518).  tau = the
+ * SplitMix64 threshold of the seed (483-497).  temperature <= 0 or
+ * top_p <= 0: argmax, first index on ties.
+ * The reference leaves the reduction orders of its softmax sum and cumsums to
+ * the candle kernels, so no f32 evaluation order is the reference's: the
+ * softmax and the cumulative sums are evaluated here in f64 on the f32 scaled
+ * logits (accurate to ~1e-12 at 128k columns, where a sequential f32 cumsum
+ * drifts by ~1e-4), and *margin receives the f64 distance from tau and top_p
+ * to the nearest cumulative boundary the decision depends on.  An f32
+ * evaluation in any order returns this token whenever its rounding error
+ * stays below that margin. */
+uint32_t or_sample_token_device(const float* logits, int n, float temperature, float top_p, uint64_t seed,
+                                double* margin) {
+    if (margin) *margin = INFINITY;
+    if (temperature <= 0.0f || top_p <= 0.0f) return or_sample_greedy(logits, n);
+    const float mul = 1.0f / temperature;
+    double* probs = (double*)malloc(sizeof(double) * (size_t)n);
+    float max_val = -INFINITY;
+    for (int i = 0; i < n; ++i) {
+        const float x = temperature == 1.0f ? logits[i] : logits[i] * mul;
+        probs[i] = x;
+        max_val = fmaxf(max_val, x);
+    }
+    double sum = 0.0;
+    for (int i = 0; i < n; ++i) {
+        probs[i] = exp(probs[i] - (double)max_val);
+        sum += probs[i];
+    }
+    for (int i = 0; i < n; ++i) probs[i] /= sum;
+    const double tau = (double)or_sample_threshold(seed);
+    uint32_t result = 0;
+    if (top_p >= 1.0f) {
+        double c = 0.0, best = INFINITY;
+        int found = 0;
+        for (int i = 0; i < n; ++i) {
+            c += probs[i];
+            if (fabs(c - tau) < best) best = fabs(c - tau);
+            if (!found && c >= tau) {
+                result = (uint32_t)i;
+                found = 1;
+            }
+        }
+        if (margin) *margin = best;
+        free(probs);
+        return result;
+    }
+    idx_prob64* ip = (idx_prob64*)malloc(sizeof(idx_prob64) * (size_t)n);
+    idx_prob64* tmp = (idx_prob64*)malloc(sizeof(idx_prob64) * (size_t)n);
+    for (int i = 0; i < n; ++i) ip[i] = (idx_prob64){i, probs[i]};
+    stable_sort_desc64(ip, n, tmp);
+    /* keep sorted position j while the sum before it is below top_p */
+    double before = 0.0, denom = 0.0, mp = INFINITY;
+    int kept = 0;
+    for (int j = 0; j < n; ++j) {
+        if (fabs(before - (double)top_p) < mp) mp = fabs(before - (double)top_p);
+        if (before < (double)top_p) {
+            kept = j + 1;
+            denom += ip[j].p;
+        }
+        before += ip[j].p;
+    }
+    double c = 0.0, mt = INFINITY;
+    int found = 0;
+    for (int j = 0; j < kept; ++j) {
+        c += ip[j].p;
+        if (fabs(c / denom - tau) < mt) mt = fabs(c / denom - tau);
+        if (!found && c / denom >= tau) {
+            result = (uint32_t)ip[j].idx;
+            found = 1;
+        }
+    }
+    if (!found) result = (uint32_t)ip[0].idx;
+    if (margin) *margin = mp < mt ? mp : mt;
     free(probs);
     free(ip);
     free(tmp);

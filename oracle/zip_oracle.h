@@ -52,6 +52,11 @@ uint32_t or_sample_greedy(const float* logits, int n);
 /* tensor_ops.rs:394-458 (deterministic_sample_threshold at 372-388). */
 uint32_t or_sample_token(const float* logits, int n, float temperature, float top_p, uint64_t seed);
 float or_sample_threshold(uint64_t seed);
+/* The batched decode path's device sampler (runtime.rs:534-601) for one row, in f64 on the f32 scaled
+ * logits; *margin (nullable) is the distance from tau / top_p to the nearest cumulative boundary the
+ * decision depends on. */
+uint32_t or_sample_token_device(const float* logits, int n, float temperature, float top_p, uint64_t seed,
+                                double* margin);
 /* forward_pass.rs:1317-1372: causal attention with a cached prefix, one head.
  * q [q_rows, d], k/v [kv_rows, d]; row r sees keys [0, prefix + r]. */
 int or_causal_attention_with_prefix(const float* q, const float* k, const float* v, float* out,
