@@ -418,6 +418,68 @@ def measure_kv_snapshot(reps=5):
     return out
 
 
+def measure_sampling(reps=5):
+    """Device sampling of the decode batch's logits at the 256-session
+    Llama-3-8B shape: 256 rows x 128256 f32 logits already in HBM, sampled by
+    zr_sample as sample_tokens_device_with_seeds (runtime.rs:534-601) with
+    per-row seeds, in the three modes the path has: greedy (T = 0), full
+    distribution (T = 0.7, top_p = 1) and nucleus (T = 0.7, top_p = 0.9).
+    sample_kernel is timed with HIP events (class 3); its algorithmic bytes
+    are the logits read once and one token written per row.  The CPU leg is
+    the oracle's f64 restatement on a bounded sample of rows."""
+    from mesh_amd import DeviceBuffer, DeviceContext, ModelGeometry
+
+    rows, vocab = 256, 128256
+    g = ModelGeometry(hidden=256, num_heads=4, num_kv_heads=2, num_layers=1, vocab=vocab, ffn=64)
+    ctx = DeviceContext(g, kv_dtype="f32", max_tokens=8, max_seqs=8, max_pages_per_seq=8)
+    rng = np.random.default_rng(0x5A)
+    x = (rng.standard_normal((rows, vocab)) * 3).astype(np.float32)
+    d_x = DeviceBuffer.from_numpy(ctx, x)
+    d_out = DeviceBuffer(ctx, 4 * rows)
+    seeds = rng.integers(0, 2 ** 63, rows, dtype=np.uint64)
+    lib = ctx.lib
+    f32p, u64p = C.POINTER(C.c_float), C.POINTER(C.c_uint64)
+    alg = rows * vocab * 4 + rows * 4
+    modes = {}
+    for name, t, p in (("greedy", 0.0, 1.0), ("full", 0.7, 1.0), ("nucleus", 0.7, 0.9)):
+        temps = np.full(rows, t, np.float32)
+        tops = np.full(rows, p, np.float32)
+        args = (ctx.h, d_x.ptr, rows, vocab, temps.ctypes.data_as(f32p), tops.ctypes.data_as(f32p),
+                seeds.ctypes.data_as(u64p), d_out.ptr)
+        ctx.check(lib.zr_sample(*args))  # warm-up
+        times = []
+        for _ in range(reps):
+            ctx.check(lib.zr_timing_begin(ctx.h, 1 << 3))
+            ctx.check(lib.zr_sample(*args))
+            ms = (C.c_double * 5)()
+            n = (C.c_int * 5)()
+            ctx.check(lib.zr_timing_end(ctx.h, ms, n))
+            times.append(ms[3])
+        k_ms = float(np.median(times))
+        modes[name] = dict(kernel_ms=k_ms, achieved=alg / (k_ms * 1e6), frac=alg / (k_ms * 1e6) / HBM_PEAK_GBS)
+    d_x.free()
+    d_out.free()
+    ctx.close()
+    nuc = modes["nucleus"]
+    out = dict(workload="256 rows x 128256 f32 logits (one decode step of 256 sessions), per-row seeds",
+               modes=modes,
+               roofline={"bound": "hbm", "kernel": "sample_kernel (nucleus)", "achieved": nuc["achieved"],
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": nuc["frac"], "algorithmic_bytes": alg})
+    try:
+        import oracle as O
+
+        sample = 8
+        t0 = time.perf_counter()
+        for r in range(sample):
+            O.sample_token_device(x[r], 0.7, 0.9, int(seeds[r]))
+        cpu_s = time.perf_counter() - t0
+        out["cpu_baseline"] = dict(value=sample / cpu_s, unit="rows/s (nucleus)", cores=1, kind="port",
+                                   sample=f"{sample} rows of the same logits (oracle, f64, one thread)")
+    except Exception as e:  # the oracle is a checker; its absence only drops this leg
+        out["cpu_baseline"] = {"error": str(e)}
+    return out
+
+
 def calibrate_copy():
     """One plain device-to-device copy of 1 GiB (torch), the reference point
     for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE counters."""
@@ -443,6 +505,7 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true")
     ap.add_argument("--soak", action="store_true", help="also run the KV-pressure soak leg")
     ap.add_argument("--skip-kv-snapshot", action="store_true", help="skip the KV snapshot wire-format leg")
+    ap.add_argument("--skip-sampling", action="store_true", help="skip the device sampling leg")
     a = ap.parse_args()
     if a.calibrate_copy:
         calibrate_copy()
@@ -466,6 +529,7 @@ def main():
                     gemm_tflops=r["gemm"]["achieved_tflops"], gemm_weight_gbs=r["gemm"]["weight_gbs"])
     soak = measure_soak(max(4, a.steps // 2), 2) if a.soak else None
     kv_snapshot = None if a.skip_kv_snapshot else measure_kv_snapshot()
+    sampling = None if a.skip_sampling else measure_sampling()
     cpu = None if a.skip_cpu else cpu_baseline(a.workload)
     att = main_r["attention"]
     line = {
@@ -491,6 +555,7 @@ def main():
         "bs32": bs32,
         "soak": soak,
         "kv_snapshot": kv_snapshot,
+        "sampling": sampling,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

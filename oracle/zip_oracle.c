@@ -2,8 +2,9 @@
  * zip_oracle.c -- CPU restatement of the zip engine's hot path.
  *
  * TEST INFRASTRUCTURE ONLY (the checker; see zip_oracle.h).  Plain C11 + OpenMP,
- * f32 throughout, built with -ffp-contract=off so every multiply and add rounds
- * as the reference's Rust f32 code does.  OpenMP only splits independent output
+ * f32 throughout (except or_sample_token_device, which states an f32 rule of
+ * unspecified evaluation order in f64), built with -ffp-contract=off so every
+ * multiply and add rounds as the reference's Rust f32 code does.  OpenMP only splits independent output
  * elements; it never reorders an accumulation.
  */
 #include "zip_oracle.h"
@@ -251,9 +252,10 @@ static void stable_sort_desc64(idx_prob64* v, int n, idx_prob64* tmp) {
  * softmax and the cumulative sums are evaluated here in f64 on the f32 scaled
  * logits (accurate to ~1e-12 at 128k columns, where a sequential f32 cumsum
  * drifts by ~1e-4), and *margin receives the f64 distance from tau and top_p
- * to the nearest cumulative boundary the decision depends on.  An f32
- * evaluation in any order returns this token whenever its rounding error
- * stays below that margin. */
+ * to the nearest cumulative boundary the decision depends on (0 when the
+ * sampled element has an unequal near-tie, below).  An f32 evaluation in any
+ * order returns this token whenever its rounding error stays below that
+ * margin. */
 uint32_t or_sample_token_device(const float* logits, int n, float temperature, float top_p, uint64_t seed,
                                 double* margin) {
     if (margin) *margin = INFINITY;
@@ -305,16 +307,31 @@ uint32_t or_sample_token_device(const float* logits, int n, float temperature, f
         before += ip[j].p;
     }
     double c = 0.0, mt = INFINITY;
-    int found = 0;
+    int found = 0, jr = 0;
     for (int j = 0; j < kept; ++j) {
         c += ip[j].p;
         if (fabs(c / denom - tau) < mt) mt = fabs(c / denom - tau);
         if (!found && c / denom >= tau) {
-            result = (uint32_t)ip[j].idx;
+            jr = j;
             found = 1;
         }
     }
-    if (!found) result = (uint32_t)ip[0].idx;
+    result = (uint32_t)ip[jr].idx;
+    /* The sampled element's identity: an element whose probability lies within
+     * an f32 evaluation's relative error of it (expf, the division, and the
+     * rounding of y - max, ~1.2e-7 per unit of |y - max|) may sort on either
+     * side of it there, and then sits at the crossing instead.  Equal scaled
+     * logits give equal probabilities in every evaluation (ties in column
+     * order), so only unequal near-ties make the token ambiguous: margin 0. */
+    {
+        const int id = ip[jr].idx;
+        const float yj = temperature == 1.0f ? logits[id] : logits[id] * mul;
+        const double pj = ip[jr].p, tol = 1e-6 * (1.0 + fabs((double)yj - (double)max_val)) * pj;
+        for (int q = jr - 1; q >= 0 && ip[q].p - pj <= tol; --q)
+            if (ip[q].p != pj) mt = 0.0;
+        for (int q = jr + 1; q < n && pj - ip[q].p <= tol; ++q)
+            if (ip[q].p != pj) mt = 0.0;
+    }
     if (margin) *margin = mp < mt ? mp : mt;
     free(probs);
     free(ip);

@@ -79,6 +79,33 @@ def test_ties_and_peaked_rows():
     ctx.close()
 
 
+@pytest.mark.parametrize("cols", [16384, 16383])
+def test_large_buckets_and_long_ties(cols):
+    # rows whose crossing bucket holds more than the 8192 candidates resolved in
+    # LDS: uniform (one run of equal probabilities), a narrow spread of
+    # distinct logits 1.2e-5 apart (refined by the next bits), a long run of
+    # ties among distinct values, and quantised logits (many ties, resolved in
+    # column order)
+    ctx = _ctx(cols)
+    rng = np.random.default_rng(cols + 1)
+    kinds = 4
+    per = 24
+    x = np.zeros((kinds * per, cols), np.float32)
+    for r in range(per):
+        x[per + r] = rng.permutation(np.linspace(0.0, 0.2, cols, dtype=np.float32))
+        x[2 * per + r] = rng.standard_normal(cols).astype(np.float32)
+        x[2 * per + r, rng.permutation(cols)[:12000]] = 0.25
+        x[3 * per + r] = (np.round(rng.standard_normal(cols) * 2) / 2).astype(np.float32)
+    rows = kinds * per
+    temps = rng.choice([1.0, 0.8], rows).astype(np.float32)
+    tops = rng.choice([1.0, 0.9, 0.5, 0.2], rows).astype(np.float32)
+    seeds = rng.integers(0, 2 ** 63, rows, dtype=np.uint64)
+    got = sample_device(ctx, x, temps, tops, seeds)
+    assert _check(x, temps, tops, seeds, got) >= rows // 3
+    assert sample_device(ctx, x, temps, tops, seeds) == got
+    ctx.close()
+
+
 def test_decode_batch_samples_its_own_logits():
     cfg = dict(SMALL)
     geo = geometry(cfg)
