@@ -209,8 +209,10 @@ __device__ inline void better(float& bv, int& bi, float v, int i) {
 
 constexpr int kArgmaxChunk = 4096;
 
+// vec: cols % 4 == 0 and x 16-byte aligned; a thread then issues its four
+// float4 loads of the chunk (4096 columns = 256 threads x 4 x 4) at once.
 __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __restrict__ x, int cols,
-                                                             int chunks, float* __restrict__ ws) {
+                                                             int chunks, int vec, float* __restrict__ ws) {
     __shared__ float sv[4];
     __shared__ int si[4];
     const int r = blockIdx.y, ch = blockIdx.x;
@@ -218,7 +220,28 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __rest
     const float* xr = x + (size_t)r * cols;
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int i = c0 + threadIdx.x; i < c1; i += blockDim.x) better(bv, bi, xr[i], i);
+    if (vec) {
+        const float4* x4 = reinterpret_cast<const float4*>(xr);
+        const int j0 = c0 >> 2, j1 = c1 >> 2;
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int j = j0 + (int)threadIdx.x + u * 256;
+            v[u] = j < j1 ? x4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int j = j0 + (int)threadIdx.x + u * 256;
+            if (j < j1) {
+                better(bv, bi, v[u].x, 4 * j);
+                better(bv, bi, v[u].y, 4 * j + 1);
+                better(bv, bi, v[u].z, 4 * j + 2);
+                better(bv, bi, v[u].w, 4 * j + 3);
+            }
+        }
+    } else {
+        for (int i = c0 + threadIdx.x; i < c1; i += blockDim.x) better(bv, bi, xr[i], i);
+    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
         const float ov = __shfl_xor(bv, off, 64);
@@ -261,7 +284,9 @@ zr_status launch_argmax(zr_context* ctx, const float* x, int rows, int cols, uin
     const int chunks = (cols + kArgmaxChunk - 1) / kArgmaxChunk;
     if ((size_t)rows * chunks * 2 > ctx->argmax_ws_floats)
         return set_err(ctx, ZR_E_OOM, "argmax workspace too small");
-    hipLaunchKernelGGL(argmax_partial_kernel, dim3(chunks, rows), dim3(256), 0, ctx->stream, x, cols, chunks,
+    static_assert(kArgmaxChunk == 256 * 4 * 4, "one float4 group per thread");
+    const int vec = (cols % 4 == 0) && ((uintptr_t)x % 16 == 0);
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(chunks, rows), dim3(256), 0, ctx->stream, x, cols, chunks, vec,
                        ctx->argmax_ws);
     ZR_LAUNCH_CHECK(ctx);
     hipLaunchKernelGGL(argmax_final_kernel, dim3(rows), dim3(64), 0, ctx->stream, ctx->argmax_ws, chunks, out);

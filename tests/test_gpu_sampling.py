@@ -106,6 +106,29 @@ def test_large_buckets_and_long_ties(cols):
     ctx.close()
 
 
+def test_device_tokens_equal_host_sampler_small_vocab():
+    # away from decision boundaries the device sampler returns the host
+    # sampler's token (tensor_ops.rs:394-458; the reference checks the same on
+    # two rows, tensor_ops.rs:641-669).  At 1000 columns the host's sequential
+    # f32 sums stay within ~1e-6 of exact, far inside the margin.
+    ctx = _ctx(1000)
+    rng = np.random.default_rng(641)
+    rows = 64
+    x = (rng.standard_normal((rows, 1000)) * 2).astype(np.float32)
+    temps = rng.choice([0.85, 0.7, 1.35], rows).astype(np.float32)
+    tops = rng.choice([1.0, 0.72, 0.9, 0.5], rows).astype(np.float32)
+    seeds = rng.integers(0, 2 ** 63, rows, dtype=np.uint64)
+    got = sample_device(ctx, x, temps, tops, seeds)
+    compared = 0
+    for r in range(rows):
+        _, margin = O.sample_token_device(x[r], float(temps[r]), float(tops[r]), int(seeds[r]))
+        if margin > MARGIN:
+            assert got[r] == O.sample_token(x[r], float(temps[r]), float(tops[r]), int(seeds[r])), r
+            compared += 1
+    assert compared >= rows - 3
+    ctx.close()
+
+
 def test_decode_batch_samples_its_own_logits():
     cfg = dict(SMALL)
     geo = geometry(cfg)

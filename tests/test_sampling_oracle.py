@@ -75,3 +75,24 @@ def test_draws_follow_the_nucleus_distribution():
         counts[O.sample_token_device(x, t, top_p, seed)[0]] += 1
     np.testing.assert_allclose(counts / draws, want, atol=0.01)
     assert counts[want == 0].sum() == 0
+
+
+def test_device_rule_equals_host_sampler_away_from_boundaries():
+    # The reference asserts device == host sampling on its two examples
+    # (tensor_ops.rs:641-669).  The rules differ only in rounding (x / T against
+    # x * f32(1 / T), f32 sums) and in "c > tau" against "c >= tau", so on rows
+    # whose decision lies away from every boundary the host sampler
+    # (tensor_ops.rs:394-458) returns the same token.
+    rng = np.random.default_rng(29)
+    checked = 0
+    for trial in range(600):
+        n = int(rng.integers(2, 400))
+        x = (rng.standard_normal(n) * float(rng.choice([0.5, 1.5, 4.0]))).astype(np.float32)
+        t = float(rng.choice([0.85, 0.7, 1.35, 2.0]))
+        p = float(rng.choice([1.0, 0.72, 0.9, 0.5, 0.2]))
+        seed = int(rng.integers(0, 2 ** 63))
+        tok, margin = O.sample_token_device(x, t, p, seed)
+        if margin > 1e-5:
+            assert tok == O.sample_token(x, t, p, seed), (trial, n, t, p, seed)
+            checked += 1
+    assert checked > 560
