@@ -207,8 +207,9 @@ zr_status zr_argmax(zr_context* ctx, const float* d_x, int rows, int cols, uint3
  * (runtime.rs:534-601) as the batched decode path groups it
  * (sample_fast_path_logits_batch, backend.rs:275-316).  temperature <= 0 or
  * top_p <= 0: argmax.  Cumulative sums are exact integer sums of
- * round(p * 2^36) (deterministic; the reference's candle reduction orders are
- * unspecified).  d_out: device u32 [rows]. */
+ * round(exp(y - max) * 2^36) compared with exact integer targets
+ * (deterministic; the reference's candle reduction orders are unspecified).
+ * cols <= 2^20 (ZR_E_INVALID otherwise).  d_out: device u32 [rows]. */
 zr_status zr_sample(zr_context* ctx, const float* d_logits, int rows, int cols, const float* temperature,
                     const float* top_p, const uint64_t* seeds, uint32_t* d_out);
 /* The same on the logits of the context's last forward (its first `rows`
