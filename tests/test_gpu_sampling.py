@@ -17,6 +17,7 @@ import pytest
 
 import oracle as O
 from mesh_amd import BackendMicrobatchExecutor, DecodeMicrobatchRequest, DeviceBuffer, DeviceContext, ModelGeometry
+from mesh_amd._lib import ZR_E_INVALID, ZrError
 from mesh_amd.provider import sample_device
 from tests.test_gpu_model import SMALL, make
 from tests.testmodels import geometry, random_weights
@@ -149,4 +150,31 @@ def test_decode_batch_samples_its_own_logits():
         if temps[i] <= 0 or tops[i] <= 0:
             assert got[i] == int(np.argmax(logits[i]))
     assert all(b.sequence_position() == 10 for b in backends)
+    ctx.close()
+
+
+def test_error_paths_launch_nothing():
+    # empty (zero rows or columns) or over-wide logits are rejected before any
+    # launch, with the reference's message for the empty case
+    # (runtime.rs:548-552)
+    ctx = _ctx(1000)
+    lib = ctx.lib
+    one = np.ones(1, np.float32)
+    seed = np.zeros(1, np.uint64)
+    f32p = O.C.POINTER(O.C.c_float)
+    u64p = O.C.POINTER(O.C.c_uint64)
+    d_x = DeviceBuffer(ctx, 16)
+    d_out = DeviceBuffer(ctx, 16)
+    args = (one.ctypes.data_as(f32p), one.ctypes.data_as(f32p), seed.ctypes.data_as(u64p), d_out.ptr)
+    with pytest.raises(ZrError) as e:
+        ctx.check(lib.zr_sample(ctx.h, d_x.ptr, 1, 0, *args))
+    assert e.value.status == ZR_E_INVALID and "empty logits" in str(e.value)
+    with pytest.raises(ZrError) as e:
+        ctx.check(lib.zr_sample(ctx.h, d_x.ptr, 1, (1 << 20) + 1, *args))
+    assert e.value.status == ZR_E_INVALID and "at most" in str(e.value)
+    with pytest.raises(ZrError) as e:
+        ctx.check(lib.zr_sample(ctx.h, d_x.ptr, 0, 4, *args))
+    assert e.value.status == ZR_E_INVALID and "empty logits" in str(e.value)
+    d_x.free()
+    d_out.free()
     ctx.close()
