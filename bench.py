@@ -413,7 +413,7 @@ def measure_kv_snapshot(reps=5):
         cpu_s = time.perf_counter() - t0
         out["cpu_baseline"] = dict(value=doc / cpu_s / 1e6, unit="MB/s of document", cores=1, kind="port",
                                    sample="the same document (oracle/kv_cbor.c, one thread)")
-    except Exception as e:  # the oracle is a checker; its absence only drops this leg
+    except Exception as e:  # the oracle is test infrastructure; its absence only drops this leg
         out["cpu_baseline"] = {"error": str(e)}
     return out
 
@@ -475,7 +475,7 @@ def measure_sampling(reps=5):
         cpu_s = time.perf_counter() - t0
         out["cpu_baseline"] = dict(value=sample / cpu_s, unit="rows/s (nucleus)", cores=1, kind="port",
                                    sample=f"{sample} rows of the same logits (oracle, f64, one thread)")
-    except Exception as e:  # the oracle is a checker; its absence only drops this leg
+    except Exception as e:  # the oracle is test infrastructure; its absence only drops this leg
         out["cpu_baseline"] = {"error": str(e)}
     return out
 
@@ -512,7 +512,7 @@ def main():
         return
     if a.gpus != 1:
         print(json.dumps({"error": "this provider runs one worker's shard on one GPU; --gpus must be 1 "
-                                   "(multi-GPU sharding is a design note, not part of this build)"}))
+                                   "(sharding across GPUs is described, not implemented)"}))
         sys.exit(2)
     from mesh_amd import probe_provider
 

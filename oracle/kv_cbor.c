@@ -1,7 +1,7 @@
 /*
  * kv_cbor.c -- CPU restatement of the KV snapshot wire format.
  *
- * TEST INFRASTRUCTURE ONLY (the checker for the device encoder and the host
+ * TEST INFRASTRUCTURE ONLY (the test oracle for the device encoder and the host
  * decoder of the rocm provider).  Only tests/, __graft_entry__.smoke() and the
  * cpu_baseline leg of bench.py load it.
  *

@@ -1,7 +1,7 @@
 /*
  * zip_oracle.c -- CPU restatement of the zip engine's hot path.
  *
- * TEST INFRASTRUCTURE ONLY (the checker; see zip_oracle.h).  Plain C11 + OpenMP,
+ * TEST INFRASTRUCTURE ONLY (the test oracle; see zip_oracle.h).  Plain C11 + OpenMP,
  * f32 throughout (except or_sample_token_device, which states an f32 rule of
  * unspecified evaluation order in f64), built with -ffp-contract=off so every
  * multiply and add rounds as the reference's Rust f32 code does.  OpenMP only splits independent output

@@ -1,7 +1,7 @@
 /*
  * zip_oracle.h -- CPU restatement of the zip engine's hot path (saint0x/mesh).
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker for the HIP provider:
+ * TEST INFRASTRUCTURE ONLY.  This library is the test oracle for the HIP provider:
  * only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load
  * it.  The product path (mesh_amd/) never links or calls it.
  *
