@@ -302,7 +302,14 @@ def cpu_baseline(name):
     per_layer = max(times[2] - times[1], 1e-9)
     step_s = times[1] + (geo["num_layers"] - 1) * per_layer
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return dict(value=B / step_s, unit="tokens/s", cores=threads, kind="port",
+    model_name = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            model_name = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), model_name)
+    except OSError:
+        pass
+    return dict(value=B / step_s, unit="tokens/s", cores=threads, kind="port", cpu_model=model_name,
+                affinity_cpus=len(os.sched_getaffinity(0)), nproc=os.cpu_count(),
                 sample=f"oracle decode microbatch of the same {B} sessions and contexts with 1 and 2 layers of "
                        f"the model ({times[1]:.2f} s, {times[2]:.2f} s); step = T1 + {geo['num_layers'] - 1} x "
                        f"(T2 - T1) = {step_s:.2f} s; f32 weights/KV as the reference CPU provider")
