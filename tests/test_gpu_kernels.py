@@ -289,3 +289,54 @@ def test_argmax_first_index_on_ties_and_large_vocab():
     assert got.tolist() == want
     assert got[:4].tolist() == [1, 3, 0, 128255]
     ctx.close()
+
+
+# -------------------------------- the benchmarked launch: 256 sessions --
+def test_c5_shape_attention_256_sessions_matches_oracle():
+    # The attention launch of the 256-session decode benchmark: Llama-3-8B
+    # attention shape (32 q heads, 8 kv heads, head_dim 128), bf16 pool, the
+    # benchmark's lognormal contexts (seed 0xC5: median 1024, sigma 1, clipped
+    # to [64, 8192]; sum ~395k keys) with the launch's own split sizing (~96
+    # pages per split, so long sessions merge several splits).  All 32 heads
+    # of a sample of sessions (the longest, the shortest and six more) are
+    # checked against the oracle; every output must be finite.
+    ctxlens = np.clip(np.round(np.random.default_rng(0xC5).lognormal(math.log(1024), 1.0, 256)), 64,
+                      8192).astype(np.int64)
+    B, H, KVC, D = 256, 4096, 1024, 128
+    geo = ModelGeometry(hidden=H, num_heads=32, num_kv_heads=8, num_layers=1, vocab=64, ffn=64)
+    ctx = DeviceContext(geo, kv_dtype="bf16", max_tokens=B, max_seqs=B, max_pages_per_seq=520)
+    ctx.create_kv_pool(int(((ctxlens + 15) // 16).sum()) + B)
+    rng = np.random.default_rng(0xA5)
+    rows = 1 << 16
+    big = rng.standard_normal((rows, KVC), dtype=np.float32)  # K / V rows: per-session windows of one array
+    koff = [(s * 7919) % (rows - 8192) for s in range(B)]
+    voff = [(s * 104729 + 12345) % (rows - 8192) for s in range(B)]
+    backends = [ctx.new_backend(8320) for _ in range(B)]
+    for s, b in enumerate(backends):
+        L = int(ctxlens[s])
+        b.import_kv_cache(_snapshot(big[koff[s]:koff[s] + L - 1], big[voff[s]:voff[s] + L - 1]))
+    st = stage_mixed(ctx, backends, [1] * B)
+    qkv = rng.standard_normal((B, H + 2 * KVC), dtype=np.float32)
+    d_qkv = DeviceBuffer.from_numpy(ctx, qkv)
+    d_q = DeviceBuffer(ctx, 4 * B * H)
+    d_o = DeviceBuffer(ctx, 4 * B * H)
+    ctx.check(ctx.lib.zr_rope_kv_write(ctx.h, st, 0, d_qkv.ptr, d_q.ptr, 0))
+    ctx.check(ctx.lib.zr_attention(ctx.h, st, 0, d_q.ptr, d_o.ptr))
+    out = d_o.download(np.float32, (B, H))
+    ctx.lib.zr_staged_destroy(st)
+    assert np.isfinite(out).all()
+    sample = sorted({int(np.argmax(ctxlens)), int(np.argmin(ctxlens))} |
+                    {int(x) for x in np.random.default_rng(7).choice(B, 6, replace=False)})
+    for s in sample:
+        L = int(ctxlens[s])
+        k = O.round_bf16(np.concatenate([big[koff[s]:koff[s] + L - 1], qkv[s:s + 1, H:H + KVC]]))
+        v = O.round_bf16(np.concatenate([big[voff[s]:voff[s] + L - 1], qkv[s:s + 1, H + KVC:]]))
+        want = np.zeros(H, np.float32)
+        for h in range(32):
+            kvh = h // 4
+            want[h * D:(h + 1) * D] = O.causal_attention_with_prefix(
+                qkv[s, h * D:(h + 1) * D][None], np.ascontiguousarray(k[:, kvh * D:(kvh + 1) * D]),
+                np.ascontiguousarray(v[:, kvh * D:(kvh + 1) * D]), 1 / math.sqrt(D), L - 1)[0]
+        err = max_rel_err_rows(out[s], want, D)
+        assert err <= ATTN_RTOL, (s, L, err)
+    ctx.close()
