@@ -111,14 +111,23 @@ __global__ __launch_bounds__(NT) void rms_norm_vec_kernel(const float* __restric
         if (i4 < n4) {
             float4 a = *(const float4*)(x + base + 4 * (size_t)i4);
             if (residual_in) {
-                float4 rr = *(const float4*)(residual_in + base + 4 * (size_t)i4);
-#pragma unroll 4
-                for (int s = 1; s < res_n; ++s) {
-                    const float4 q = *(const float4*)(residual_in + s * res_stride + base + 4 * (size_t)i4);
-                    rr.x += q.x;
-                    rr.y += q.y;
-                    rr.z += q.z;
-                    rr.w += q.w;
+                // slabs summed in slab order, their loads issued 8 at a time
+                const float* rp = residual_in + base + 4 * (size_t)i4;
+                float4 rr = *(const float4*)rp;
+                for (int s0 = 1; s0 < res_n; s0 += 8) {
+                    float4 q[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u)
+                        q[u] = s0 + u < res_n ? *(const float4*)(rp + (size_t)(s0 + u) * res_stride)
+                                              : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                    for (int u = 0; u < 8; ++u)
+                        if (s0 + u < res_n) {
+                            rr.x += q[u].x;
+                            rr.y += q[u].y;
+                            rr.z += q[u].z;
+                            rr.w += q[u].w;
+                        }
                 }
                 a.x = a.x + rr.x;
                 a.y = a.y + rr.y;
