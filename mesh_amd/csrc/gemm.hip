@@ -399,21 +399,6 @@ struct GemmCfg {
     int bn() const { return waves_n * wn * 32; }
 };
 
-// Measured on MI355X over the decode shapes with weights streamed from HBM
-// (split activations): 32 x 128 tiles for <= 32 rows; 128-row tiles with
-// 256 columns, or 512 for wide / deep products and the LM head.
-static GemmCfg pick_cfg(int m, int n, int k, int epilogue = kEpiStore) {
-    // SwiGLU fused into the GEMM (one split, gate / up tile pairs in a wave) once
-    // 128-row tiles fill the CUs; small row counts reduce split-K slabs instead
-    if (epilogue == kEpiSwiGLU && m > 64) return {2, 2, 2, 4, 3, false};
-    if (m <= 32) return {1, 1, 1, 4, 3, true};
-    if (m <= 64) return {2, 1, 1, 4, 3, true};
-    // vocabulary-wide heads: 256-row tiles read each weight tile once
-    if (n >= 65536) return m > 128 ? GemmCfg{2, 4, 4, 2, 3, false} : GemmCfg{2, 4, 2, 4, 3, false};
-    if (n >= 16384) return {2, 4, 2, 4, 3, false};
-    return {2, 2, 2, 4, 3, false};
-}
-
 static int device_cus() {
     static const int cus = [] {
         int v = 256, dev = 0;
@@ -421,6 +406,27 @@ static int device_cus() {
         return v > 0 ? v : 256;
     }();
     return cus;
+}
+
+// Measured on MI355X over the decode shapes with weights streamed from HBM
+// (split activations): 32 x 128 tiles for <= 32 rows; 128-row tiles with
+// 256 columns, or 512 for wide / deep products and the LM head.
+static GemmCfg pick_cfg(int m, int n, int k, int epilogue = kEpiStore) {
+    // SwiGLU fused into the GEMM (one split, gate / up tile pairs in a wave) once
+    // 128-row tiles fill the CUs; small row counts reduce split-K slabs instead.
+    // 128 x 512 tiles once they alone fill two passes over the CUs (prefill-sized
+    // row counts: gate/up at 2108 rows 838-850 us against 910-1117 with 128 x 256).
+    if (epilogue == kEpiSwiGLU && m > 64) {
+        const int wide_tiles = ((m + 127) / 128) * ((n + 511) / 512);
+        if (wide_tiles >= 2 * device_cus()) return {2, 4, 2, 4, 3, false};
+        return {2, 2, 2, 4, 3, false};
+    }
+    if (m <= 32) return {1, 1, 1, 4, 3, true};
+    if (m <= 64) return {2, 1, 1, 4, 3, true};
+    // vocabulary-wide heads: 256-row tiles read each weight tile once
+    if (n >= 65536) return m > 128 ? GemmCfg{2, 4, 4, 2, 3, false} : GemmCfg{2, 4, 2, 4, 3, false};
+    if (n >= 16384) return {2, 4, 2, 4, 3, false};
+    return {2, 2, 2, 4, 3, false};
 }
 
 static bool swiglu_fused(int m, int epilogue) { return epilogue == kEpiSwiGLU && m > 64; }
@@ -437,7 +443,25 @@ GemmPlan gemm_plan(int m, int n, int k, int epilogue) {
     // weight-streaming tiles), >= 4 k-steps per split, at most 16 splits
     const int tiles = p.col_blocks * p.row_blocks;
     const int budget = c.small ? 3 * device_cus() : device_cus();
-    const int splits = swiglu_fused(m, epilogue) ? 1 : std::max(1, std::min(std::min(16, budget / tiles), p.KT / 4));
+    int splits = swiglu_fused(m, epilogue) ? 1 : std::max(1, std::min(std::min(16, budget / tiles), p.KT / 4));
+    if (!swiglu_fused(m, epilogue) && !c.small && tiles > budget) {
+        // More tiles than one pass: up to 4 splits when they fill the last
+        // pass better.  Cost in passes of unsplit blocks: ceil(tiles S / CUs) / S,
+        // plus per extra split one more f32 slab written and read back
+        // (8 M N bytes at ~5 TB/s) against one pass of the hi + lo MFMA work
+        // (4 BM BN K per CU at ~1.2 PFLOP/s): 480 tiles / (K CUs).  At 2108 rows
+        // this picks S = 3 for O (K 4096) and 4 for down (K 14336): -20 to -30 %
+        // per GEMM; QKV's slabs cost more than its tail (S = 1).
+        const double slab = 480.0 * tiles / ((double)k * budget);
+        double best = 1e30;
+        for (int s = 1; s <= 4 && s <= std::max(1, p.KT / 4); ++s) {
+            const double cost = (double)(((size_t)tiles * s + budget - 1) / budget) / s + slab * (s - 1);
+            if (cost < best - 1e-9) {
+                best = cost;
+                splits = s;
+            }
+        }
+    }
     p.kt_per_split = (p.KT + splits - 1) / splits;
     p.splits = (p.KT + p.kt_per_split - 1) / p.kt_per_split;
     p.direct = p.splits == 1 && (epilogue == kEpiStore || swiglu_fused(m, epilogue));
@@ -475,7 +499,13 @@ zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_pack
     hipEvent_t ev;
     timing_mark_begin(ctx, kClassGemm, &ev);
     bool launched = false;
-    if (fused) {
+    if (fused && cfg.wn == 4) {
+        if (split_act)
+            gemm_launch<2, 4, 2, 4, 3, 2, 1>(p, ctx->stream, a, m, k, w_packed, nullptr, n, 0, c_bf16, 1);
+        else
+            gemm_launch<2, 4, 2, 4, 3, 1, 1>(p, ctx->stream, a, m, k, w_packed, nullptr, n, 0, c_bf16, 0);
+        launched = true;
+    } else if (fused) {
         if (split_act)
             gemm_launch<2, 2, 2, 4, 3, 2, 1>(p, ctx->stream, a, m, k, w_packed, nullptr, n, 0, c_bf16, 1);
         else

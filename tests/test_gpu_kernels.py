@@ -237,7 +237,9 @@ def test_kv_gather_scatter_round_trip_with_partial_first_page(kv_dtype):
 # -------------------------------------------------------------- GEMM etc --
 @pytest.mark.parametrize("split", [True, False])
 @pytest.mark.parametrize("m,k,n", [(1, 64, 100), (7, 256, 4112), (32, 2048, 2048), (100, 512, 1000),
-                                   (256, 4096, 1024), (300, 128, 64), (128, 4104, 4112), (130, 520, 66000)])
+                                   (256, 4096, 1024), (300, 128, 64), (128, 4104, 4112), (130, 520, 66000),
+                                   # more 128 x 256 tiles than CUs: K split 3 and 4 ways to fill the last pass
+                                   (2108, 4096, 4096), (2108, 14336, 4096)])
 def test_gemm_matches_fp64(split, m, k, n):
     geo = ModelGeometry(hidden=256, num_heads=4, num_kv_heads=4, num_layers=1, vocab=64, ffn=256)
     ctx = DeviceContext(geo, kv_dtype="f32", max_tokens=16, max_seqs=4, max_pages_per_seq=4, split_activations=split)

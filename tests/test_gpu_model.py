@@ -221,6 +221,33 @@ def test_mixed_chunked_prefill_and_decode_microbatch():
     ctx.close()
 
 
+def test_prefill_rows_wide_ffn_partials():
+    """1200 prefill rows against FFN 14336: the gate/up GEMM takes its
+    128 x 512-column fused SwiGLU tiles (10 x 56 tiles, two passes over the
+    CUs).  Per-layer pre-all-reduce partials (O, down) and logits against the
+    oracle; the second chunk continues a page-unaligned 300-row prefix."""
+    cfg = dict(hidden=256, num_heads=4, num_kv_heads=2, num_layers=1, vocab=512, ffn=14336, rms_norm_eps=1e-5,
+               rope_base=10000.0)
+    geo = geometry(cfg)
+    weights = random_weights(cfg, geo, seed=77, std=0.02)
+    ctx, om = make(cfg, geo, weights, "f32", True, max_tokens=1200, max_seqs=4, pages=512, pps=128)
+    rng = np.random.default_rng(77)
+    dev = [ctx.new_backend(), ctx.new_backend()]
+    ref = [O.Session(1, geo["kv_cols"]), O.Session(1, geo["kv_cols"])]
+    snap = _random_snapshot(rng, 1, 300, geo["kv_cols"], bf16=False)
+    dev[1].import_kv_cache(snap)
+    _oracle_import(ref[1], snap)
+    chunks = [rng.integers(0, cfg["vocab"], 600).tolist() for _ in range(2)]
+    parts = np.zeros((1, 2, 1200, cfg["hidden"]), np.float32)
+    _, got = BackendMicrobatchExecutor.forward_mixed(dev, chunks, partials=parts)
+    wants = [om.prefill_chunk(s, c, want_partials=True) for s, c in zip(ref, chunks)]
+    want_parts = np.concatenate([p for _, p in wants], axis=2)
+    err = float(np.max(np.abs(parts - want_parts)))
+    assert err <= 1e-2, err
+    check_logits(got, np.stack([w for w, _ in wants]), "wide FFN prefill")
+    ctx.close()
+
+
 def test_tp_shard_partials_and_kv_pages():
     """Tensor-parallel shard 0 of 2 at Llama-3-8B head geometry (16 of 32 q
     heads, 4 of 8 kv heads, FFN columns 7168 of 14336), executed locally with
