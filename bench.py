@@ -487,6 +487,97 @@ def measure_sampling(reps=5):
     return out
 
 
+MIXED_WORKLOAD = dict(
+    geo=dict(hidden=4096, num_heads=32, num_kv_heads=8, num_layers=4, vocab=128256, ffn=14336, rope_base=500000.0),
+    batch=64, max_seq_len=8192, contexts=None,
+    desc="Mixed chunked-prefill + decode microbatch at the Llama-3-8B layer shape, 4 layers: 4 prefill chunks "
+         "of 512 rows (prefixes 0, 512, 1000, 1531) + 60 decode sessions (contexts U[256, 4096]) packed into "
+         "2108 varlen rows, page 16 from a seeded permutation of the pool, bf16 weights + bf16 KV")
+
+
+def measure_mixed(reps=5):
+    """The MFMA-bound configuration: one mixed microbatch of 2108 rows through
+    4 Llama-3-8B-shape layers (QKV / O / gate-up / down GEMMs at M = 2108, LM
+    head on the 64 last rows).  Every timed microbatch runs on its own set of
+    64 sessions, so each has exactly this shape (the chunks' prefixes do not
+    grow).  Reported: rows/s, the per-class kernel split (HIP events, a second
+    pass over the same staged microbatches), and the GEMMs' algorithmic
+    TFLOP/s against the 2.5 PFLOP/s dense bf16 peak (executed MFMA work is
+    2x: hi + lo activations)."""
+    from mesh_amd import _lib
+
+    WORKLOADS["llama3_layers4_mixed"] = MIXED_WORKLOAD
+    sets = reps + 1
+    ctx, g = device_model("llama3_layers4_mixed", True, max_tokens=4 * 512 + 60, max_seqs=64)
+    lib = ctx.lib
+    rng = np.random.default_rng(0xC3)
+    prefixes = [0, 512, 1000, 1531]
+    dec = rng.integers(256, 4097, 60)
+    per_set = int(sum((p + 512 + 15) // 16 + 1 for p in prefixes) + sum((int(L) + 1 + 15) // 16 + 1 for L in dec))
+    n_pages = per_set * sets
+    ctx.create_kv_pool(n_pages, rng.permutation(n_pages))
+    ctx.check(lib.zr_kv_pool_fill_normal(ctx.h, 4242, 1.0))
+    q_len = np.array([512] * 4 + [1] * 60, np.int32)
+    rows = int(q_len.sum())
+    staged, keep = [], []
+    for _ in range(sets):
+        bks = [ctx.new_backend(8192) for _ in range(64)]
+        for b, L in zip(bks, prefixes + [int(x) for x in dec]):
+            if L:
+                b.kv_reserve(int(L))
+        arr = (C.c_void_p * 64)(*[b.h for b in bks])
+        st = C.c_void_p()
+        ctx.check(lib.zrh_stage_mixed(C.cast(arr, C.POINTER(C.c_void_p)), 64, q_len.ctypes.data_as(_lib.c_int_p),
+                                      None, C.byref(st)))
+        staged.append(st.value)
+        keep.append((bks, arr))
+
+    def dev(nbytes):
+        ptr = C.c_void_p()
+        ctx.check(lib.zr_device_alloc(ctx.h, int(nbytes), C.byref(ptr)))
+        return ptr.value
+
+    tok, out = dev(4 * rows), dev(4 * 64)
+    t = rng.integers(0, g.vocab, rows).astype(np.uint32)
+    ctx.check(lib.zr_memcpy_h2d(ctx.h, tok, t.ctypes.data, t.nbytes))
+
+    def run(idx, mask):
+        if mask:
+            ctx.check(lib.zr_timing_begin(ctx.h, mask))
+        ctx.check(lib.zr_synchronize(ctx.h))
+        t0 = time.perf_counter()
+        for i in idx:
+            ctx.check(lib.zr_forward_staged_async(ctx.h, staged[i], tok, out, None))
+        ctx.check(lib.zr_synchronize(ctx.h))
+        dt = time.perf_counter() - t0
+        ms = (C.c_double * 5)()
+        n = (C.c_int * 5)()
+        if mask:
+            ctx.check(lib.zr_timing_end(ctx.h, ms, n))
+        return dt, list(ms)
+
+    run([0], 0)
+    dt, _ = run(range(1, sets), 0)
+    _, ms = run(range(1, sets), 0xF)
+    toks = np.zeros(64, np.uint32)
+    ctx.check(lib.zr_memcpy_d2h(ctx.h, toks.ctypes.data, out, toks.nbytes))
+    assert toks.max() < g.vocab
+    for st in staged:
+        lib.zr_staged_destroy(st)
+    ctx.close()
+    H, Q, KV, F, V, L = g.hidden, g.q_cols, g.kv_cols, g.ffn_cols, g.vocab, g.num_layers
+    flops = 2.0 * rows * L * (H * (Q + 2 * KV) + Q * H + H * 2 * F + F * H) + 2.0 * 64 * H * V
+    gemm_ms = ms[1] / reps
+    tflops = flops / (gemm_ms * 1e-3) / 1e12
+    return dict(workload=MIXED_WORKLOAD["desc"], rows=rows, value=rows * reps / dt, unit="rows/s",
+                ms_per_microbatch=dt / reps * 1e3,
+                kernel_ms_per_microbatch={"attention": ms[0] / reps, "gemm": gemm_ms,
+                                          "norm_rope_kv": ms[2] / reps, "other": ms[3] / reps},
+                gemm_mfma={"achieved": tflops, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                           "frac": tflops / MFMA_BF16_PEAK_TFLOPS, "mfma_ops_per_flop": 2,
+                           "executed_frac": 2 * tflops / MFMA_BF16_PEAK_TFLOPS, "flops_per_microbatch": flops})
+
+
 def calibrate_copy():
     """One plain device-to-device copy of 1 GiB (torch), the reference point
     for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE counters."""
@@ -513,6 +604,7 @@ def main():
     ap.add_argument("--soak", action="store_true", help="also run the KV-pressure soak leg")
     ap.add_argument("--skip-kv-snapshot", action="store_true", help="skip the KV snapshot wire-format leg")
     ap.add_argument("--skip-sampling", action="store_true", help="skip the device sampling leg")
+    ap.add_argument("--skip-mixed", action="store_true", help="skip the mixed prefill + decode microbatch leg")
     a = ap.parse_args()
     if a.calibrate_copy:
         calibrate_copy()
@@ -537,6 +629,7 @@ def main():
     soak = measure_soak(max(4, a.steps // 2), 2) if a.soak else None
     kv_snapshot = None if a.skip_kv_snapshot else measure_kv_snapshot()
     sampling = None if a.skip_sampling else measure_sampling()
+    mixed = None if a.skip_mixed else measure_mixed()
     cpu = None if a.skip_cpu else cpu_baseline(a.workload)
     att = main_r["attention"]
     line = {
@@ -563,6 +656,7 @@ def main():
         "soak": soak,
         "kv_snapshot": kv_snapshot,
         "sampling": sampling,
+        "mixed_prefill": mixed,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

@@ -183,10 +183,31 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     const int G = ctx->q_per_kv, qpt = 16 / G;
     st->h_tiles.clear();
     st->h_items.clear();
+    st->h_pblocks.clear();
+    st->h_psplits.clear();
+    // sequences with >= 128 / G rows (prefill chunks) go to the prefill kernel
+    // as blocks of 128 / G rows (bf16 pools, G dividing 32)
+    int prows = 0;
+    if (ctx->desc.kv_dtype == ZR_DTYPE_BF16 && G <= 32 && 32 % G == 0 &&
+        (ctx->head_dim == 64 || ctx->head_dim == 128))
+        prows = 128 / G;
+    if (const char* env = getenv("ZR_ATTN_PREFILL"))
+        if (atoi(env) == 0) prows = 0;
     std::vector<int> tile_pages;
-    long total_pages = 0;
+    std::vector<int4> pblk;  // prefill blocks {seq, r0, nrows, pages}
+    long total_pages = 0, total_ktiles = 0;
     for (int s = 0; s < S; ++s) {
         const int ql = mb->q_len[s], kb = mb->kv_before[s], fo = mb->first_offset[s];
+        if (prows && ql >= prows) {
+            for (int r0 = 0; r0 < ql; r0 += prows) {
+                const int nr = std::min(prows, ql - r0);
+                const int last_visible = kb + r0 + nr - 1;
+                const int pages = (fo + last_visible + 1 + kPageRows - 1) / kPageRows;
+                pblk.push_back(make_int4(s, r0, nr, pages));
+                total_ktiles += (pages + 1) / 2;
+            }
+            continue;
+        }
         for (int q0 = 0; q0 < ql; q0 += qpt) {
             const int nq = std::min(qpt, ql - q0);
             const int last_visible = kb + q0 + nq - 1;  // logical index of the tile's last key
@@ -207,22 +228,72 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
         for (int pb = 0; pb < tile_pages[t]; pb += pps)
             st->h_items.push_back(make_int4((int)t, pb, std::min(tile_pages[t], pb + pps), 0));
     }
-    st->h_tiles.push_back(make_int4(0, 0, 0, (int)st->h_items.size()));  // sentinel
-    st->n_tiles = (int)st->h_tiles.size() - 1;
+    const int n_decode_tiles = (int)st->h_tiles.size();
     st->n_attn_items = (int)st->h_items.size();
+    // Prefill blocks split along their key tiles (32 keys each) so the causal
+    // triangle and unequal prefixes even out: about 512 workgroups (two
+    // resident per CU), at least 16 key tiles per split (at the 2108-row mixed
+    // microbatch, 16 to 48 tiles and no split at all measured within 3 %: the
+    // merge costs what the balance gains).  A block with several splits writes
+    // partials per 16-column group (16 / G rows x G heads, the decode tiles'
+    // layout), one item per (group, split) after the decode items, and its
+    // groups join the merge list as tiles.
+    int tps = (int)std::max<long>(16, (total_ktiles * ctx->local_kv_heads + 511) / 512);
+    if (const char* env = getenv("ZR_ATTN_PREFILL_TILES_PER_SPLIT")) tps = std::max(1, atoi(env));
+    if (G > 16) tps = 1 << 30;  // a 16-column group must hold whole rows
+    int next_item = st->n_attn_items;
+    for (const int4& b : pblk) {
+        const int nt = (b.w + 1) / 2;
+        const int ns = (nt + tps - 1) / tps;
+        if (ns <= 1) {
+            st->h_pblocks.push_back(b);
+            st->h_psplits.push_back(make_int4(0, nt, -1, 1));
+            continue;
+        }
+        const int rows_per_group = 16 / G;
+        const int groups = (b.z + rows_per_group - 1) / rows_per_group;
+        for (int sp = 0; sp < ns; ++sp) {
+            st->h_pblocks.push_back(b);
+            st->h_psplits.push_back(make_int4((int)((long)sp * nt / ns), (int)((long)(sp + 1) * nt / ns),
+                                              next_item + sp, ns));
+        }
+        for (int k = 0; k < groups; ++k)
+            st->h_tiles.push_back(make_int4(b.x, b.y + k * rows_per_group,
+                                            std::min(rows_per_group, b.z - k * rows_per_group), next_item + k * ns));
+        next_item += groups * ns;
+    }
+    st->n_part_items = next_item;
+    st->h_tiles.push_back(make_int4(0, 0, 0, next_item));  // sentinel
+    st->n_tiles = (int)st->h_tiles.size() - 1;
     // dispatch order: longest items first, so the short ones fill the tail
     st->h_order.resize(st->n_attn_items);
     for (int i = 0; i < st->n_attn_items; ++i) st->h_order[i] = i;
     std::stable_sort(st->h_order.begin(), st->h_order.end(), [&](int x, int y) {
         return st->h_items[x].z - st->h_items[x].y > st->h_items[y].z - st->h_items[y].y;
     });
-    // tiles whose splits need the merge kernel
+    // tiles whose splits need the merge kernel (every prefill group tile has several)
     st->h_merge.clear();
     for (int t = 0; t < st->n_tiles; ++t)
-        if (st->h_tiles[t + 1].w - st->h_tiles[t].w > 1) st->h_merge.push_back(t);
+        if (t >= n_decode_tiles || st->h_tiles[t + 1].w - st->h_tiles[t].w > 1) st->h_merge.push_back(t);
     st->n_merge = (int)st->h_merge.size();
+    // prefill work units: most key tiles first
+    {
+        std::vector<int> ord(st->h_pblocks.size());
+        for (size_t i = 0; i < ord.size(); ++i) ord[i] = (int)i;
+        std::stable_sort(ord.begin(), ord.end(), [&](int x, int y) {
+            return st->h_psplits[x].y - st->h_psplits[x].x > st->h_psplits[y].y - st->h_psplits[y].x;
+        });
+        std::vector<int4> b2(ord.size()), s2(ord.size());
+        for (size_t i = 0; i < ord.size(); ++i) {
+            b2[i] = st->h_pblocks[ord[i]];
+            s2[i] = st->h_psplits[ord[i]];
+        }
+        st->h_pblocks.swap(b2);
+        st->h_psplits.swap(s2);
+    }
+    st->n_pblocks = (int)st->h_pblocks.size();
 
-    const size_t need_part = (size_t)st->n_attn_items * ctx->local_kv_heads * 16 * (ctx->head_dim + 2);
+    const size_t need_part = (size_t)st->n_part_items * ctx->local_kv_heads * 16 * (ctx->head_dim + 2);
     if (need_part > ctx->attn_part_floats) {
         hipStreamSynchronize(ctx->stream);
         if (ctx->attn_part) hipFree(ctx->attn_part);
@@ -244,6 +315,8 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     const size_t o_items = take(16 * (size_t)st->n_attn_items), o_tiles = take(16 * st->h_tiles.size());
     const size_t o_merge = take(4 * (size_t)std::max(st->n_merge, 1));
     const size_t o_order = take(4 * (size_t)std::max(st->n_attn_items, 1));
+    const size_t o_pblk = take(16 * (size_t)std::max(st->n_pblocks, 1));
+    const size_t o_psplit = take(16 * (size_t)std::max(st->n_pblocks, 1));
     const size_t host_bytes = off;
     const size_t o_cuq = take(4 * (S + 1)), o_cuk = take(4 * (S + 1)), o_pos = take(4 * (size_t)total_q);
     const size_t o_slot = take(4 * (size_t)total_q), o_seq = take(4 * (size_t)total_q), o_last = take(4 * S);
@@ -269,6 +342,8 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     memcpy(hb + o_tiles, st->h_tiles.data(), 16 * st->h_tiles.size());
     if (st->n_merge) memcpy(hb + o_merge, st->h_merge.data(), 4 * (size_t)st->n_merge);
     if (st->n_attn_items) memcpy(hb + o_order, st->h_order.data(), 4 * (size_t)st->n_attn_items);
+    if (st->n_pblocks) memcpy(hb + o_pblk, st->h_pblocks.data(), 16 * (size_t)st->n_pblocks);
+    if (st->n_pblocks) memcpy(hb + o_psplit, st->h_psplits.data(), 16 * (size_t)st->n_pblocks);
     unsigned char* db = (unsigned char*)st->dev;
     st->q_len = (int*)(db + o_qlen);
     st->kv_before = (int*)(db + o_kvb);
@@ -280,6 +355,8 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     st->attn_tiles = (int4*)(db + o_tiles);
     st->merge_tiles = (int*)(db + o_merge);
     st->attn_order = (int*)(db + o_order);
+    st->pblocks = (int4*)(db + o_pblk);
+    st->psplits = (int4*)(db + o_psplit);
     st->cu_q = (int*)(db + o_cuq);
     st->cu_k = (int*)(db + o_cuk);
     st->positions = (int*)(db + o_pos);

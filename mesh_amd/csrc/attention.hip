@@ -6,6 +6,11 @@
 //   o = softmax(q . K^T / sqrt(d)) . V, query row r of a chunk sees keys
 //   [0, prefix + r].
 //
+// Two kernels share one launch slot: sequences with at least 128 / G query
+// rows in a bf16 pool (prefill chunks) run paged_prefill_attention_kernel
+// (further below); every other row (decode rows, short chunks, f32 pools)
+// runs paged_attention_kernel.
+//
 // Work decomposition.  A workgroup is one wavefront (64 lanes).  It owns one
 // kv head of one "tile" and a contiguous range of KV pages (a split):
 //   tile   = up to 16 / G queries of one sequence, so the 16 MFMA columns are
@@ -343,6 +348,257 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
         for (int i = 0; i < 4; ++i) out[2 + db * 16 + q4 * 4 + i] = o[db][i];
 }
 
+// ------------------------------------------------------------ prefill blocks
+// Sequences with at least 128 / G query rows (prefill chunks) run here, bf16
+// pools only.  A workgroup of 4 waves owns one kv head of one block of
+// 128 / G query rows: 128 columns = (row, q head of the kv head) pairs, 32
+// per wave.  Every 32-key tile (two pages) of the block's visible window is
+// copied once into an LDS ring with global_load_lds (the pool's page layout,
+// no registers) and serves all 128 columns, where the decode tiles above
+// would read each page once per 16 columns.
+// Per tile and wave, on v_mfma_f32_32x32x16_bf16 (lane l, h = l / 32):
+//   S[key][col] = sum_d K[key][d] Q[col][d]: K (A operand) is one 16 B LDS read
+//     per lane and 16 dims (key l % 32, dims 16 ks + 8 h .. + 7 = one chunk of
+//     the page's K layout); Q^T (B operand) as bf16 hi + lo in registers.
+//     The lane gets S[8 (i / 4) + 4 h + i % 4][l % 32], i < 16.
+//   online softmax per column: 16 keys in the lane, the other 16 in lane l ^ 32.
+//   O[d][col] += sum_key V[key][d] P[key][col]: the summation index k = 8 h + j
+//     of k-step ks2 stands for key 16 ks2 + 8 (j / 4) + 4 h + j % 4, so P's B
+//     fragment is the lane's own scores i = 8 ks2 + j (hi + lo), and V^T's A
+//     fragment is two 8-byte runs of the page's V layout (rows 4 h .. 4 h + 3
+//     and 8 + 4 h .. of dim 32 db + l % 32).
+// Causal mask: column (row r, head g) sees logical keys j <= kv_before + r.
+struct PrefillArgs {
+    const float* q;          // [T, q_cols]
+    int q_cols;
+    const uint16_t* pool;    // layer base of the pool (bf16)
+    size_t page_elems;
+    int stride;              // block table row stride (the table is a kernel argument)
+    const int* first_offset;
+    const int* kv_before;
+    const int* cu_q;
+    const int4* blocks;      // per work unit: {seq, r0, nrows, pages}, most key tiles first
+    const int4* splits;      // per work unit: {first key tile, end key tile, partial item, splits of the block}
+    int n_blocks;
+    float* part;             // [items][kv_heads][16][D + 2] partials of blocks with splits > 1
+    int G;                   // q heads per kv head (divides 32)
+    int kv_heads;
+    float scale_log2;        // log2(e) / sqrt(d)
+    float* out_f32;
+    uint16_t* out_bf16;
+    size_t out_lo_offset;
+};
+
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+
+__device__ inline float pair_max(float x) {
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ inline float pair_sum(float x) {
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+template <int D, int STAGES>
+__global__ __launch_bounds__(256, 2) void paged_prefill_attention_kernel(PrefillArgs a,
+                                                                      const int* __restrict__ block_tables) {
+    constexpr int NW = 4;
+    constexpr int CHUNKS = 8 * D;   // 16 B chunks per stage: 2 pages x (K, V) x 16 rows x D bf16
+    constexpr int VM = D / 32;      // global_load_lds per wave per stage (1 KiB each)
+    static_assert(CHUNKS == NW * VM * 64, "stage copy split");
+    __shared__ bf16x8 lds[STAGES][CHUNKS];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // block-uniform values in scalar registers
+    const int rank = __builtin_amdgcn_readfirstlane(blockIdx.x / a.kv_heads);
+    const int kvh = blockIdx.x - rank * a.kv_heads;
+    const int4 blk = a.blocks[rank];
+    const int4 spl = a.splits[rank];
+    const int seq = __builtin_amdgcn_readfirstlane(blk.x), r0 = __builtin_amdgcn_readfirstlane(blk.y);
+    const int nrows = __builtin_amdgcn_readfirstlane(blk.z), npages = __builtin_amdgcn_readfirstlane(blk.w);
+    const int kt0 = __builtin_amdgcn_readfirstlane(spl.x), kt1 = __builtin_amdgcn_readfirstlane(spl.y);
+    const int h = lane >> 5;
+    const int col = lane & 31;
+    const int rpw = 32 / a.G;  // query rows per wave
+    const int rloc = wave * rpw + col / a.G, g = col - (col / a.G) * a.G;
+    const bool valid = rloc < nrows;
+    const int kvb = __builtin_amdgcn_readfirstlane(a.kv_before[seq]);
+    const int foff = __builtin_amdgcn_readfirstlane(a.first_offset[seq]);
+    const int jmax = kvb + r0 + (valid ? rloc : 0);  // last visible logical key of this column
+    const int grow = __builtin_amdgcn_readfirstlane(a.cu_q[seq]) + r0 + (valid ? rloc : 0);
+
+    const uint16_t* pool = a.pool;
+    // (a restrict kernel argument: nothing here writes it, so its reads are scalar loads)
+    const int* bt = block_tables + (size_t)seq * a.stride;
+    const size_t kv_tile = (size_t)kPageRows * D;
+    const size_t v_block = (size_t)a.kv_heads * kv_tile;
+    // stage of key tile kt into ring slot `slot`: chunk group f = i NW + wave
+    // is (page pp, K or V, 1 KiB group) of the tile's two pages; a page past
+    // the window's end repeats the last page (its keys are masked)
+    auto issue = [&](int slot, int kt) {
+#pragma unroll
+        for (int i = 0; i < VM; ++i) {
+            const int f = i * NW + wave;
+            const int pp = f / (2 * VM), kv = (f / VM) & 1, grp = f % VM;
+            const int page = __builtin_amdgcn_readfirstlane(bt[min(2 * kt + pp, npages - 1)]);
+            const uint16_t* src = pool + (size_t)page * a.page_elems + (kv ? v_block : 0) + (size_t)kvh * kv_tile +
+                                  ((size_t)grp * 64 + lane) * 8;
+            __builtin_amdgcn_global_load_lds(src, (lds_void*)&lds[slot][f * 64], 16, 0, 0);
+        }
+    };
+
+    f32x16 o[D / 32];
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
+    float m = -INFINITY, lsum = 0.0f;
+
+    // key tiles [kt0, kt1) of the block's window; a tile needs the causal mask
+    // only if it may hold a key before the window (first_offset) or after the
+    // block's first row's last visible key
+    const int ntiles = kt1 - kt0;
+    const int jfree = kvb + r0;  // keys <= jfree are visible to every row of the block
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s)
+        if (s < ntiles) issue(s, kt0 + s);
+    // Q^T fragments (B operand): lane holds Q[col][16 ks + 8 h + j] * log2(e) / sqrt(d)
+    // as hi + lo (scores come out in log2 units).  Loaded after the first
+    // stages' copies are issued, so both latencies overlap.
+    bf16x8 qh[D / 16], ql[D / 16];
+    {
+        const float* qp = a.q + (size_t)grow * a.q_cols + (size_t)(kvh * a.G + g) * D + 8 * h;
+#pragma unroll
+        for (int ks = 0; ks < D / 16; ++ks) {
+            float x[8];
+            const f32x4 x0 = valid ? *(const f32x4*)(qp + 16 * ks) : f32x4{0.f, 0.f, 0.f, 0.f};
+            const f32x4 x1 = valid ? *(const f32x4*)(qp + 16 * ks + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                x[j] = x0[j] * a.scale_log2;
+                x[4 + j] = x1[j] * a.scale_log2;
+            }
+            qh[ks] = to_bf16x8(x, false);
+            ql[ks] = to_bf16x8(x, true);
+        }
+    }
+    for (int t = 0; t < ntiles; ++t) {
+        const int slot = t % STAGES;
+        const int it = kt0 + t;
+        ring_wait<VM, STAGES - 2>(min(STAGES - 2, ntiles - 1 - t));
+        if (t + STAGES - 1 < ntiles) issue((t + STAGES - 1) % STAGES, kt0 + t + STAGES - 1);
+        const bf16x8* st = lds[slot];
+        // S = K Q^T over D
+        f32x16 s;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[i] = 0.0f;
+        const int kbase = ((lane >> 4) & 1) * 2 * (2 * D) + (lane & 15);  // page pp = (l % 32) / 16, row l % 16
+#pragma unroll
+        for (int ks = 0; ks < D / 16; ++ks) {
+            const bf16x8 kf = st[kbase + (2 * ks + h) * 16];
+            s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qh[ks], s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, ql[ks], s, 0, 0, 0);
+        }
+        // online softmax step over the tile's 32 keys
+        float sc[16];
+        float tmax = -INFINITY;
+        if (it * 32 - foff >= 0 && it * 32 + 31 - foff <= jfree) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                sc[i] = s[i];
+                tmax = fmaxf(tmax, sc[i]);
+            }
+        } else {
+            const int jbase = it * 32 + 4 * h - foff;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int j = jbase + 8 * (i >> 2) + (i & 3);
+                sc[i] = (j >= 0 && j <= jmax) ? s[i] : -INFINITY;
+                tmax = fmaxf(tmax, sc[i]);
+            }
+        }
+        tmax = pair_max(tmax);
+        const float m_new = fmaxf(m, tmax);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m - m_use);
+        float pr[16];
+        float psum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            pr[i] = __builtin_amdgcn_exp2f(sc[i] - m_use);
+            psum += pr[i];
+        }
+        lsum = lsum * alpha + psum;
+        m = m_new;
+        // rescale O only when some column's max moved (rare once it settles)
+        if (__any(alpha != 1.0f)) {
+#pragma unroll
+            for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+        }
+        // O += V^T P over the tile's two pages (k-steps ks2)
+        const bf16x4* sv = (const bf16x4*)st;
+#pragma unroll
+        for (int ks2 = 0; ks2 < 2; ++ks2) {
+            const bf16x8 ph = to_bf16x8(pr + 8 * ks2, false), pl = to_bf16x8(pr + 8 * ks2, true);
+            const int vbase = (2 * ks2 + 1) * 4 * D;  // 8-byte units of page ks2's V block
+#pragma unroll
+            for (int db = 0; db < D / 32; ++db) {
+                // unit of (rows 4 q .. 4 q + 3, dim d): ((d / 32 * 4 + q) * 16 + d % 16) * 2 + d / 16 % 2
+                const int u = ((db * 4 + h) * 16 + (lane & 15)) * 2 + ((lane >> 4) & 1);
+                const bf16x4 v0 = sv[vbase + u], v1 = sv[vbase + u + 2 * 16 * 2];
+                const bf16x8 vf = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, ph, o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pl, o[db], 0, 0, 0);
+            }
+        }
+    }
+    lsum = pair_sum(lsum);
+    if (!valid) return;
+    if (spl.w > 1) {
+        // one split of several: (m, l, o) of this column into the item of its
+        // 16-column group (16 / G rows x G heads, the decode tiles' layout);
+        // attention_merge_kernel combines the splits
+        const int item = spl.z + ((wave * 32 + col) >> 4) * spl.w;
+        float* out = a.part + (((size_t)item * a.kv_heads + kvh) * 16 + (col & 15)) * (D + 2);
+        if (h == 0) {
+            out[0] = m;
+            out[1] = lsum;
+        }
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) out[2 + db * 32 + 8 * (i >> 2) + 4 * h + (i & 3)] = o[db][i];
+        return;
+    }
+    const float inv = 1.0f / lsum;
+    const int ocol0 = (kvh * a.G + g) * D;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) {
+            const int d = db * 32 + 8 * i4 + 4 * h;
+            if (a.out_bf16) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    uint16_t hi, lo;
+                    split_bf16(o[db][4 * i4 + i] * inv, hi, lo);
+                    const size_t oi = a_pack_index(grow, ocol0 + d + i, a.q_cols);
+                    a.out_bf16[oi] = hi;
+                    if (a.out_lo_offset) a.out_bf16[a.out_lo_offset + oi] = lo;
+                }
+            } else {
+                const f32x4 v = {o[db][4 * i4] * inv, o[db][4 * i4 + 1] * inv, o[db][4 * i4 + 2] * inv,
+                                 o[db][4 * i4 + 3] * inv};
+                *(f32x4*)(a.out_f32 + (size_t)grow * a.q_cols + ocol0 + d) = v;
+            }
+        }
+}
+
 // Merge the splits of one (tile, kv head) with more than one split:
 // o = sum_s o_s w_s with w_s = 2^(m_s - M) / sum_r l_r 2^(m_r - M), M the
 // max over splits (m in log2 units).  The weights of up to kChunk splits are
@@ -475,11 +731,42 @@ static zr_status launch_attn_t(zr_context* ctx, StagedMeta* st, int layer, const
     a.out_lo_offset = (ctx->desc.flags & ZR_FLAG_SPLIT_ACTIVATIONS) ? a_plane(st->total_q, ctx->q_cols) : 0;
     hipEvent_t ev;
     timing_mark_begin(ctx, kClassAttention, &ev);
-    // bf16 pages: a 6-page ring, one wave per SIMD (measured: a 4-page ring
-    // at two waves per SIMD spills and loses ~20%); f32 pages: 4 pages
-    const dim3 grid(((st->n_attn_items + 7) / 8) * 8 * ctx->local_kv_heads);
-    hipLaunchKernelGGL((paged_attention_kernel<KV, D, sizeof(KV) == 4 ? 4 : 6>), grid, dim3(64), 0, ctx->stream, a);
-    ZR_LAUNCH_CHECK(ctx);
+    if (st->n_attn_items > 0) {
+        // bf16 pages: a 6-page ring, one wave per SIMD (measured: a 4-page ring
+        // at two waves per SIMD spills and loses ~20%); f32 pages: 4 pages
+        const dim3 grid(((st->n_attn_items + 7) / 8) * 8 * ctx->local_kv_heads);
+        hipLaunchKernelGGL((paged_attention_kernel<KV, D, sizeof(KV) == 4 ? 4 : 6>), grid, dim3(64), 0, ctx->stream,
+                           a);
+        ZR_LAUNCH_CHECK(ctx);
+    }
+    if constexpr (sizeof(KV) == 2) {
+        if (st->n_pblocks > 0) {
+            PrefillArgs pa;
+            pa.q = q;
+            pa.q_cols = a.q_cols;
+            pa.pool = (const uint16_t*)a.pool;
+            pa.page_elems = a.page_elems;
+            pa.stride = a.stride;
+            pa.first_offset = a.first_offset;
+            pa.kv_before = a.kv_before;
+            pa.cu_q = a.cu_q;
+            pa.blocks = st->pblocks;
+            pa.splits = st->psplits;
+            pa.n_blocks = st->n_pblocks;
+            pa.part = ctx->attn_part;
+            pa.G = a.G;
+            pa.kv_heads = a.kv_heads;
+            pa.scale_log2 = a.scale_log2;
+            pa.out_f32 = out;
+            pa.out_bf16 = out_bf16;
+            pa.out_lo_offset = a.out_lo_offset;
+            // one workgroup per (block, kv head): kv head = block index mod kv_heads, so
+            // with kv_heads dividing 8 a kv head's pages stay on the XCDs it maps to
+            hipLaunchKernelGGL((paged_prefill_attention_kernel<D, 4>), dim3(st->n_pblocks * ctx->local_kv_heads),
+                               dim3(256), 0, ctx->stream, pa, st->block_tables);
+            ZR_LAUNCH_CHECK(ctx);
+        }
+    }
     timing_mark_end(ctx, kClassAttention, ev);
     if (st->n_merge > 0) {
         timing_mark_begin(ctx, kClassOther, &ev);
@@ -494,8 +781,8 @@ static zr_status launch_attn_t(zr_context* ctx, StagedMeta* st, int layer, const
 
 zr_status launch_attention(zr_context* ctx, StagedMeta* st, int layer, const float* q, float* out,
                            uint16_t* out_bf16) {
-    if (st->n_attn_items == 0) return ZR_OK;
-    const size_t need = (size_t)st->n_attn_items * ctx->local_kv_heads * 16 * (ctx->head_dim + 2);
+    if (st->n_attn_items == 0 && st->n_pblocks == 0) return ZR_OK;
+    const size_t need = (size_t)st->n_part_items * ctx->local_kv_heads * 16 * (ctx->head_dim + 2);
     if (need > ctx->attn_part_floats)
         return set_err(ctx, ZR_E_OOM, "attention partial workspace too small: need %zu floats, have %zu",
                        need, ctx->attn_part_floats);

@@ -113,38 +113,6 @@ zr_status pack_weight_gate_up(zr_context* ctx, const uint16_t* gate, const uint1
     return ZR_OK;
 }
 
-typedef __attribute__((address_space(3))) void lds_void;
-
-// Block barrier for the LDS ring: wait until at most N of this wave's vector
-// memory ops (its global_load_lds copies of later stages) are outstanding and
-// all of its LDS reads have returned, then s_barrier.  __syncthreads() would
-// also wait for the later stages' copies (its fence drains vmcnt), which
-// serialises the ring.  The empty asm statements keep the compiler from
-// moving memory operations across the barrier.
-template <int N>
-__device__ __forceinline__ void ring_barrier() {
-    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));  // vmcnt(N), expcnt(7), lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
-
-// ring_barrier for `ahead` (block-uniform, 0..MAXA) stages of VM copies
-// each issued after the one waited for.
-template <int VM, int MAXA>
-__device__ __forceinline__ void ring_wait(int ahead) {
-    if constexpr (MAXA > 0) {
-        if (ahead >= MAXA) {
-            ring_barrier<VM * MAXA>();
-            return;
-        }
-        ring_wait<VM, MAXA - 1>(ahead);
-    } else {
-        ring_barrier<0>();
-    }
-}
-
 // silu(g) * u = g / (1 + e^-g) * u (runtime.rs:927-929, forward_pass.rs:2286-2289),
 // one rounding per operation as written.
 __device__ inline float swiglu(float g, float u) {

@@ -30,10 +30,13 @@ __host__ __device__ inline float bf16_bits_to_f32(uint16_t h) {
     return __builtin_bit_cast(float, (uint32_t)h << 16);
 }
 
-// Split x into bf16 hi + lo with x ~= hi + lo to ~2^-16 relative.
+// Split x into bf16 hi + lo with x ~= hi + lo to ~2^-16 relative.  The casts
+// compile to gfx950's v_cvt_pk_bf16_f32 (round to nearest even): the same bits
+// as f32_to_bf16_bits for every input but NaN, without its NaN branch.
 __device__ inline void split_bf16(float x, uint16_t& hi, uint16_t& lo) {
-    hi = f32_to_bf16_bits(x);
-    lo = f32_to_bf16_bits(x - bf16_bits_to_f32(hi));
+    const __bf16 h = (__bf16)x;
+    hi = __builtin_bit_cast(uint16_t, h);
+    lo = __builtin_bit_cast(uint16_t, (__bf16)(x - (float)h));
 }
 
 // GEMM A operands (bf16 activations) are stored fragment-packed for the
@@ -51,6 +54,39 @@ __host__ __device__ inline size_t a_pack_index(int m, int k, int K) {
 __host__ __device__ inline size_t a_plane(int rows, int K) { return (size_t)((rows + 31) & ~31) * K; }
 
 // --------------------------------------------------------------- context
+typedef __attribute__((address_space(3))) void lds_void;
+
+// LDS rings fed by global_load_lds (GEMM operands, prefill K/V pages).
+// Block barrier for the LDS ring: wait until at most N of this wave's vector
+// memory ops (its global_load_lds copies of later stages) are outstanding and
+// all of its LDS reads have returned, then s_barrier.  __syncthreads() would
+// also wait for the later stages' copies (its fence drains vmcnt), which
+// serialises the ring.  The empty asm statements keep the compiler from
+// moving memory operations across the barrier.
+template <int N>
+__device__ __forceinline__ void ring_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));  // vmcnt(N), expcnt(7), lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// ring_barrier for `ahead` (block-uniform, 0..MAXA) stages of VM copies
+// each issued after the one waited for.
+template <int VM, int MAXA>
+__device__ __forceinline__ void ring_wait(int ahead) {
+    if constexpr (MAXA > 0) {
+        if (ahead >= MAXA) {
+            ring_barrier<VM * MAXA>();
+            return;
+        }
+        ring_wait<VM, MAXA - 1>(ahead);
+    } else {
+        ring_barrier<0>();
+    }
+}
+
 struct StagedMeta;  // device copy of one microbatch's metadata
 
 struct LayerDev {
@@ -163,6 +199,8 @@ struct StagedMeta {
     int n_attn_items = 0;     // attention work items (per kv head)
     int n_tiles = 0;          // attention query tiles (per kv head)
     int n_merge = 0;          // tiles with more than one split
+    int n_pblocks = 0;        // prefill work units (block, key split) per kv head
+    int n_part_items = 0;     // partial items: decode items, then prefill (group, split) items
     bool owns = true;
     // one device allocation holding every array below
     void* dev = nullptr;
@@ -185,9 +223,11 @@ struct StagedMeta {
     int* tile_nparts = nullptr; // [n_tiles]
     int* merge_tiles = nullptr; // [n_merge] tiles the merge kernel combines
     int* attn_order = nullptr;  // [n_attn_items] items by decreasing page count
+    int4* pblocks = nullptr;    // [n_pblocks] {seq, r0, nrows, pages}, most key tiles first
+    int4* psplits = nullptr;    // [n_pblocks] {first key tile, end key tile, item, splits}
     // host copies
     std::vector<int> h_q_len, h_kv_before, h_first_pos, h_first_offset, h_block_tables;
-    std::vector<int4> h_items, h_tiles;
+    std::vector<int4> h_items, h_tiles, h_pblocks, h_psplits;
     std::vector<int> h_tile_nparts, h_merge, h_order;
     std::vector<uint32_t> h_tokens;
     std::vector<unsigned char> h_blob;

@@ -203,6 +203,57 @@ def test_chunked_prefill_attention_causal_with_prefix(kv_dtype):
     ctx.close()
 
 
+def test_prefill_blocks_llama3_heads_trimmed_windows_and_decode_rows():
+    """Chunked-prefill attention at Llama-3 heads (32 q / 8 kv, head_dim 128,
+    bf16 pool): chunks of 512, 100, 33 and 32 rows (whole and partial 32-row
+    query blocks) against prefixes of 0, 1531, 700 and 40 rows, where the
+    700-row window was trimmed by retain_suffix so its first page starts at
+    row 9; two decode rows (one also trimmed) share the microbatch."""
+    geo = ModelGeometry(hidden=4096, num_heads=32, num_kv_heads=8, num_layers=1, vocab=64, ffn=64)
+    ctx = DeviceContext(geo, kv_dtype="bf16", max_tokens=1024, max_seqs=8, max_pages_per_seq=160)
+    ctx.create_kv_pool(1024)
+    rng = np.random.default_rng(12)
+    cases = [(0, 512, 0), (1531, 100, 0), (700, 33, 57), (40, 32, 0), (300, 1, 0), (77, 1, 25)]  # (window, chunk, trimmed)
+    backends, Ks, Vs = [], [], []
+    for p, c, trim in cases:
+        b = ctx.new_backend(max_seq_len=4096)
+        k = rng.standard_normal((trim + p + c, 1024), dtype=np.float32)
+        v = rng.standard_normal((trim + p + c, 1024), dtype=np.float32)
+        if trim + p:
+            b.import_kv_cache(_snapshot(k[:trim + p], v[:trim + p]))
+        if trim:
+            b.retain_suffix(p)
+            assert b.block_table()[0][1] == trim % 16
+        backends.append(b)
+        Ks.append(k)
+        Vs.append(v)
+    chunks = [c for _, c, _ in cases]
+    T = sum(chunks)
+    Q = rng.standard_normal((T, 4096), dtype=np.float32)
+    newk = np.concatenate([k[t + p:] for k, (p, _, t) in zip(Ks, cases)])
+    newv = np.concatenate([v[t + p:] for v, (p, _, t) in zip(Vs, cases)])
+    st = stage_mixed(ctx, backends, chunks)
+    d_qkv = DeviceBuffer.from_numpy(ctx, np.concatenate([Q, newk, newv], 1))
+    d_q = DeviceBuffer(ctx, Q.nbytes)
+    d_o = DeviceBuffer(ctx, Q.nbytes)
+    ctx.check(ctx.lib.zr_rope_kv_write(ctx.h, st, 0, d_qkv.ptr, d_q.ptr, 0))
+    ctx.check(ctx.lib.zr_attention(ctx.h, st, 0, d_q.ptr, d_o.ptr))
+    out = d_o.download(np.float32, Q.shape)
+    ctx.lib.zr_staged_destroy(st)
+    row = 0
+    for s, (p, c, trim) in enumerate(cases):
+        k, v = O.round_bf16(Ks[s][trim:]), O.round_bf16(Vs[s][trim:])
+        for h in range(32):
+            kvh = h // 4
+            want = O.causal_attention_with_prefix(Q[row:row + c, h * 128:(h + 1) * 128],
+                                                  k[:, kvh * 128:(kvh + 1) * 128], v[:, kvh * 128:(kvh + 1) * 128],
+                                                  1 / math.sqrt(128), p)
+            err = max_rel_err_rows(out[row:row + c, h * 128:(h + 1) * 128], want, 128)
+            assert err <= ATTN_RTOL, (s, h, err)
+        row += c
+    ctx.close()
+
+
 # ------------------------------------------------------- gather / scatter --
 @pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
 def test_kv_gather_scatter_round_trip_with_partial_first_page(kv_dtype):
