@@ -605,6 +605,8 @@ def main():
     ap.add_argument("--skip-kv-snapshot", action="store_true", help="skip the KV snapshot wire-format leg")
     ap.add_argument("--skip-sampling", action="store_true", help="skip the device sampling leg")
     ap.add_argument("--skip-mixed", action="store_true", help="skip the mixed prefill + decode microbatch leg")
+    ap.add_argument("--mixed-only", action="store_true",
+                    help="run only the mixed prefill + decode microbatch leg (for profiling its kernels)")
     a = ap.parse_args()
     if a.calibrate_copy:
         calibrate_copy()
@@ -618,6 +620,9 @@ def main():
     ok, err = probe_provider(0)
     if not ok:
         raise SystemExit(f"rocm provider unavailable: {err}")
+    if a.mixed_only:
+        print(json.dumps({"mixed_prefill": measure_mixed(max(1, a.steps))}))
+        return
     main_r = measure(a.workload, a.steps, a.warmup)
     bs32 = None
     if not a.skip_bs32 and a.workload != "tinyllama_b32":
