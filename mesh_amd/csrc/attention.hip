@@ -83,6 +83,23 @@ __device__ inline bf16x8 to_bf16x8(const float* x, bool lo_part) {
     return r;
 }
 
+// x[0..7] as bf16 hi + lo fragments, two values per v_cvt_pk_bf16_f32 (the
+// same bits as split_bf16)
+__device__ inline void split_bf16x8(const float* x, bf16x8& hi, bf16x8& lo) {
+    typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2;
+    typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const f32x2 v = {x[2 * j], x[2 * j + 1]};
+        const bf16x2 h = __builtin_convertvector(v, bf16x2);
+        const bf16x2 l = __builtin_convertvector(v - __builtin_convertvector(h, f32x2), bf16x2);
+        hi[2 * j] = h[0];
+        hi[2 * j + 1] = h[1];
+        lo[2 * j] = l[0];
+        lo[2 * j + 1] = l[1];
+    }
+}
+
 __device__ inline bf16x4 to_bf16x4(const float* x, bool lo_part) {
     bf16x4 r;
 #pragma unroll
@@ -502,49 +519,50 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attention_kernel(Prefill
             s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qh[ks], s, 0, 0, 0);
             s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, ql[ks], s, 0, 0, 0);
         }
-        // online softmax step over the tile's 32 keys
-        float sc[16];
-        float tmax = -INFINITY;
-        if (it * 32 - foff >= 0 && it * 32 + 31 - foff <= jfree) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                sc[i] = s[i];
-                tmax = fmaxf(tmax, sc[i]);
-            }
-        } else {
+        // online softmax step over the tile's 32 keys; the causal mask only on
+        // tiles that can hold a key before the window or past the block's
+        // first row (a uniform branch, kept out of the common path)
+        if (it * 32 - foff < 0 || it * 32 + 31 - foff > jfree) {
+            asm volatile("" ::: "memory");
             const int jbase = it * 32 + 4 * h - foff;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int j = jbase + 8 * (i >> 2) + (i & 3);
-                sc[i] = (j >= 0 && j <= jmax) ? s[i] : -INFINITY;
-                tmax = fmaxf(tmax, sc[i]);
+                if (j < 0 || j > jmax) s[i] = -INFINITY;
             }
         }
-        tmax = pair_max(tmax);
-        const float m_new = fmaxf(m, tmax);
-        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m - m_use);
-        float pr[16];
-        float psum = 0.0f;
+        float tmax = s[0];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            pr[i] = __builtin_amdgcn_exp2f(sc[i] - m_use);
-            psum += pr[i];
-        }
-        lsum = lsum * alpha + psum;
-        m = m_new;
-        // rescale O only when some column's max moved (rare once it settles)
-        if (__any(alpha != 1.0f)) {
+        for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, s[i]);
+        tmax = pair_max(tmax);
+        // Lazy rescale: a column keeps its running max m until a tile's max
+        // exceeds it by more than 8 (log2 units), so P <= 2^8 and O and l are
+        // rescaled only when some column of the wave moves that far (the first
+        // tile with a visible key, then rarely).  The result is the same
+        // softmax: O and l share the scale.
+        if (__any(tmax > m + 8.0f)) {
+            const float m_new = tmax > m + 8.0f ? tmax : m;
+            const float alpha = __builtin_amdgcn_exp2f(m - m_new);  // 0 while m = -inf
+            lsum *= alpha;
 #pragma unroll
             for (int db = 0; db < D / 32; ++db)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+            m = m_new;
+        }
+        const float m_use = m == -INFINITY ? 0.0f : m;
+        float pr[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            pr[i] = __builtin_amdgcn_exp2f(s[i] - m_use);
+            lsum += pr[i];
         }
         // O += V^T P over the tile's two pages (k-steps ks2)
         const bf16x4* sv = (const bf16x4*)st;
 #pragma unroll
         for (int ks2 = 0; ks2 < 2; ++ks2) {
-            const bf16x8 ph = to_bf16x8(pr + 8 * ks2, false), pl = to_bf16x8(pr + 8 * ks2, true);
+            bf16x8 ph, pl;
+            split_bf16x8(pr + 8 * ks2, ph, pl);
             const int vbase = (2 * ks2 + 1) * 4 * D;  // 8-byte units of page ks2's V block
 #pragma unroll
             for (int db = 0; db < D / 32; ++db) {
