@@ -252,8 +252,40 @@ def measure(name, steps, warmup):
                   frac=gemm_tflops / MFMA_BF16_PEAK_TFLOPS,
                   weight_gbs=(gemm_flops(g, B) / B) * nb / (ms_b[1] * 1e-3) / 1e9 if ms_b[1] > 0 else 0.0),
     )
+    result["kv_append"] = measure_kv_append(bench)
     bench.close()
     return result
+
+
+def measure_kv_append(bench, reps=5):
+    """RoPE + KV append (the RopeKvWrite stage, rope_kv_write_kernel) alone:
+    one launch over a decode step's rows (layer 0, the last staged step, after
+    the timed region), HIP events of class 2.  Algorithmic bytes: the f32 QKV
+    row read, the rotated f32 Q written, and the new K and V rows written into
+    their bf16 pages."""
+    ctx, lib, g = bench.ctx, bench.ctx.lib, bench.geo
+    T = bench.B
+    width = g.q_cols + 2 * g.kv_cols
+    qkv = np.random.default_rng(3).standard_normal((T, width)).astype(np.float32)
+    d_qkv, d_q = bench._dev(qkv.nbytes), bench._dev(4 * T * g.q_cols)
+    ctx.check(lib.zr_memcpy_h2d(ctx.h, d_qkv, qkv.ctypes.data, qkv.nbytes))
+    st = bench.staged[-1]
+    ctx.check(lib.zr_rope_kv_write(ctx.h, st, 0, d_qkv, d_q, 1))  # warm-up
+    times = []
+    for _ in range(reps):
+        ctx.check(lib.zr_timing_begin(ctx.h, 1 << 2))
+        ctx.check(lib.zr_rope_kv_write(ctx.h, st, 0, d_qkv, d_q, 1))
+        ms = (C.c_double * 5)()
+        n = (C.c_int * 5)()
+        ctx.check(lib.zr_timing_end(ctx.h, ms, n))
+        times.append(ms[2])
+    lib.zr_device_free(ctx.h, d_qkv)
+    lib.zr_device_free(ctx.h, d_q)
+    k_ms = float(np.median(times))
+    alg = T * width * 4 + T * g.q_cols * 4 + T * 2 * g.kv_cols * 2
+    return dict(kernel="rope_kv_write_kernel", rows=T, kernel_ms=k_ms, algorithmic_bytes=alg,
+                achieved_gbs=alg / (k_ms * 1e6), frac=alg / (k_ms * 1e6) / HBM_PEAK_GBS,
+                note="one launch is a few MB, so it is launch/latency-bound rather than HBM-bound")
 
 
 # ------------------------------------------------------------- CPU baseline --
@@ -410,6 +442,40 @@ def measure_kv_snapshot(reps=5):
                roofline={"bound": "hbm", "kernel": "cbor_count_kernel + cbor_scan_groups_kernel + cbor_scan_top_kernel + cbor_write_kernel",
                          "achieved": alg / (enc * 1e6), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": alg / (enc * 1e6) / HBM_PEAK_GBS, "algorithmic_bytes": alg})
+    # the gather and scatter kernels alone (kv_copy_kernel, HIP events of
+    # timing class 3), device memory on both sides: the same window read from
+    # the bf16 pages into f32 rows, and those rows written back (identical bytes)
+    table = b.block_table()
+    pages = np.ascontiguousarray([gp for _, _, _, gp in table], np.int32)
+    fbytes = 32 * window * g.kv_cols * 4
+
+    def dev(nbytes):
+        ptr = C.c_void_p()
+        ctx.check(lib.zr_device_alloc(ctx.h, int(nbytes), C.byref(ptr)))
+        return ptr.value
+
+    d_k, d_v = dev(fbytes), dev(fbytes)
+    i32p = C.POINTER(C.c_int)
+    targs = (ctx.h, pages.ctypes.data_as(i32p), int(pages.size), int(table[0][1]), rows - window, window)
+    copy_ms = {}
+    fk, fv = C.cast(d_k, C.POINTER(C.c_float)), C.cast(d_v, C.POINTER(C.c_float))
+    for name, fn in (("gather", lib.zr_kv_gather), ("scatter", lib.zr_kv_scatter)):
+        ctx.check(fn(*targs, fk, fv))
+        ts = []
+        for _ in range(reps):
+            ctx.check(lib.zr_timing_begin(ctx.h, 1 << 3))
+            ctx.check(fn(*targs, fk, fv))
+            ms = (C.c_double * 5)()
+            n = (C.c_int * 5)()
+            ctx.check(lib.zr_timing_end(ctx.h, ms, n))
+            ts.append(ms[3])
+        copy_ms[name] = float(np.median(ts))
+    lib.zr_device_free(ctx.h, d_k)
+    lib.zr_device_free(ctx.h, d_v)
+    cbytes = 2 * fbytes + 2 * 32 * window * g.kv_cols * 2  # f32 rows + bf16 pages, K and V
+    out["kv_copy"] = {name: dict(kernel="kv_copy_kernel", ms=t, algorithmic_bytes=cbytes,
+                                 achieved_gbs=cbytes / (t * 1e6), frac=cbytes / (t * 1e6) / HBM_PEAK_GBS)
+                      for name, t in copy_ms.items()}
     ref = b.export_kv_cache(window)
     ctx.close()
     try:
@@ -654,6 +720,7 @@ def main():
         "step_roofline": {"tokens_per_s": main_r["step_roofline_tokens_per_s"], "frac": main_r["step_roofline_frac"],
                           "bytes_per_step": main_r["step_bytes"]},
         "kernel_ms_per_step": main_r["kernel_ms_per_step"],
+        "kv_append": main_r["kv_append"],
         "gemm_mfma": {"achieved": main_r["gemm"]["achieved_tflops"], "peak": MFMA_BF16_PEAK_TFLOPS,
                       "unit": "TFLOP/s", "frac": main_r["gemm"]["frac"], "mfma_ops_per_flop": 2,
                       "weight_stream_gbs": main_r["gemm"]["weight_gbs"]},

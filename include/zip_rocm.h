@@ -246,7 +246,8 @@ zr_status zr_kv_pool_fill_normal(zr_context* ctx, uint64_t seed, float std);
 /* Per-kernel-class timing with HIP events on the context stream (enabled
  * between begin/end) around the launches of the classes set in class_mask
  * (bit c for class c).  Classes: 0 attention, 1 gemm, 2 norm/rope/kv,
- * 3 other, 4 KV snapshot encode.  No reference counterpart (measurement only). */
+ * 3 other (split merges, split-K reduce, argmax, sampling, KV gather/scatter),
+ * 4 KV snapshot encode.  No reference counterpart (measurement only). */
 zr_status zr_timing_begin(zr_context* ctx, unsigned class_mask);
 zr_status zr_timing_end(zr_context* ctx, double* ms_by_class /* [5] */, int* launches_by_class /* [5] */);
 

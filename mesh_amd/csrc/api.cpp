@@ -789,9 +789,6 @@ static zr_status kv_copy_entry(zr_context* ctx, const int* block_table, int n_pa
     if (need > ctx->kv_stage_floats) {
         ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
         if (ctx->kv_stage) (void)hipFree(ctx->kv_stage);
-    if (ctx->cbor_ws) (void)hipFree(ctx->cbor_ws);
-    if (ctx->cbor_out) (void)hipFree(ctx->cbor_out);
-    if (ctx->sample_ws) (void)hipFree(ctx->sample_ws);
         ctx->kv_stage = nullptr;
         ctx->kv_stage_floats = 0;
         ZR_HIP(ctx, hipMalloc(&ctx->kv_stage, need * sizeof(float)));

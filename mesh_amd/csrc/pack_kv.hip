@@ -196,33 +196,90 @@ zr_status launch_rope_kv_write(zr_context* ctx, StagedMeta* st, int layer, const
 // ------------------------------------------------------ gather / scatter
 // Logical window row j of a sequence lives at physical row first_offset + j of
 // its page list (interior spans are full pages; only the first span may start
-// mid-page after retain_suffix).  grid = (n_rows, layers).
+// mid-page after retain_suffix).  One workgroup per (page of the range, layer);
+// its threads sweep the page's 8-element groups, which are contiguous in the
+// pool layout (16 B in bf16 pools):
+//   K group (g, r):    row r, dims 8 g .. 8 g + 7 of one head;
+//   V group (q, dd):   rows 4 q .. 4 q + 3 of dims d and d + 16, d = 32 (g / 4) + dd.
+// Consecutive threads take consecutive groups, so the page side is read or
+// written in whole 1 KiB wave segments and each row side in 128 B runs.  Only
+// rows [first_row, first_row + n_rows) are copied: a scatter writes the other
+// rows of a boundary V group element by element, leaving them untouched.
 template <typename KV>
-__global__ __launch_bounds__(256) void kv_copy_kernel(KV* __restrict__ pool, size_t page_elems,
-                                                      int n_pages_pool, int layer_begin,
-                                                      const int* __restrict__ table, int first_offset,
-                                                      int first_row, int n_rows, int kv_cols, int D,
-                                                      float* __restrict__ k, float* __restrict__ v,
+struct alignas(8 * sizeof(KV)) Group8 {
+    KV x[8];
+};
+
+template <typename KV>
+__global__ __launch_bounds__(256) void kv_copy_kernel(KV* __restrict__ pool, size_t page_elems, int n_pages_pool,
+                                                      int layer_begin, const int* __restrict__ table,
+                                                      int first_offset, int first_row, int n_rows, int kv_heads,
+                                                      int D, float* __restrict__ k, float* __restrict__ v,
                                                       int to_pool) {
-    const int i = blockIdx.x;
-    const int l = blockIdx.y;
-    const int layer = layer_begin + l;
-    const int prow = first_offset + first_row + i;
-    const int page = table[prow / kPageRows], r = prow % kPageRows;
-    KV* kpage = pool + ((size_t)layer * n_pages_pool + page) * page_elems;
-    KV* vpage = kpage + (size_t)kv_cols * kPageRows;
-    float* kd = k + ((size_t)l * n_rows + i) * kv_cols;
-    float* vd = v + ((size_t)l * n_rows + i) * kv_cols;
-    for (int c = threadIdx.x; c < kv_cols; c += blockDim.x) {
-        const int head = c / D, d = c % D;
-        KV* kp = kpage + (size_t)head * kPageRows * D + k_off(r, d);
-        KV* vp = vpage + (size_t)head * kPageRows * D + v_off(r, d, D);
-        if (to_pool) {
-            store_elem(kp, kd[c]);
-            store_elem(vp, vd[c]);
-        } else {
-            kd[c] = load_elem(kp);
-            vd[c] = load_elem(vp);
+    const int slot = blockIdx.x, l = blockIdx.y;
+    const int p0 = (first_offset + first_row) / kPageRows;
+    const int page = table[p0 + slot];
+    const int rbase = (p0 + slot) * kPageRows - first_offset - first_row;  // output row of page row 0
+    const int r_lo = max(0, -rbase), r_hi = min(kPageRows, n_rows - rbase);
+    const size_t kv_cols = (size_t)kv_heads * D;
+    const int tile = kPageRows * D;           // elements of one head's K (or V) tile
+    const int groups = kv_heads * tile / 8;   // 8-element groups per K (or V) block
+    Group8<KV>* kp = (Group8<KV>*)(pool + ((size_t)(layer_begin + l) * n_pages_pool + page) * page_elems);
+    Group8<KV>* vp = kp + groups;
+    // output row of page row r (r_lo <= r < r_hi, so rbase + r >= 0)
+    auto krow = [&](int r) { return k + ((size_t)l * n_rows + (rbase + r)) * kv_cols; };
+    auto vrow = [&](int r) { return v + ((size_t)l * n_rows + (rbase + r)) * kv_cols; };
+    for (int gi = threadIdx.x; gi < groups; gi += blockDim.x) {
+        const int h = gi / (tile / 8), cg = gi - h * (tile / 8);
+        // K: group cg = g * 16 + r
+        {
+            const int g = cg >> 4, r = cg & 15;
+            if (r >= r_lo && r < r_hi) {
+                float* row = krow(r) + (size_t)h * D + 8 * g;
+                if (to_pool) {
+                    Group8<KV> gr;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) store_elem(&gr.x[j], row[j]);
+                    kp[gi] = gr;
+                } else {
+                    const Group8<KV> gr = kp[gi];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) row[j] = load_elem(&gr.x[j]);
+                }
+            }
+        }
+        // V: group cg = ((d / 32) * 4 + q) * 16 + dd holds rows 4 q + i of dims d (i) and d + 16 (4 + i)
+        {
+            const int dd = cg & 15, q = (cg >> 4) & 3, d = (cg >> 6) * 32 + dd;
+            const int r0 = 4 * q;
+            if (r0 + 3 < r_lo || r0 >= r_hi) continue;
+            const size_t c0 = (size_t)h * D + d;  // column of dim d
+            if (to_pool) {
+                if (r0 >= r_lo && r0 + 3 < r_hi) {
+                    Group8<KV> gr;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        store_elem(&gr.x[i], vrow(r0 + i)[c0]);
+                        store_elem(&gr.x[4 + i], vrow(r0 + i)[c0 + 16]);
+                    }
+                    vp[gi] = gr;
+                } else {
+                    KV* e = vp[gi].x;
+                    for (int i = 0; i < 4; ++i)
+                        if (r0 + i >= r_lo && r0 + i < r_hi) {
+                            store_elem(&e[i], vrow(r0 + i)[c0]);
+                            store_elem(&e[4 + i], vrow(r0 + i)[c0 + 16]);
+                        }
+                }
+            } else {
+                const Group8<KV> gr = vp[gi];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (r0 + i >= r_lo && r0 + i < r_hi) {
+                        vrow(r0 + i)[c0] = load_elem(&gr.x[i]);
+                        vrow(r0 + i)[c0 + 16] = load_elem(&gr.x[4 + i]);
+                    }
+            }
         }
     }
 }
@@ -231,16 +288,22 @@ zr_status launch_kv_copy(zr_context* ctx, int layer_begin, int layer_end, const 
                          int first_offset, int first_row, int n_rows, float* k, float* v, int to_pool) {
     if (n_rows <= 0 || layer_end <= layer_begin) return ZR_OK;
     const size_t pe = page_elems_of(ctx);
-    dim3 grid(n_rows, layer_end - layer_begin);
+    const int p0 = (first_offset + first_row) / kPageRows;
+    const int p1 = (first_offset + first_row + n_rows - 1) / kPageRows;
+    dim3 grid(p1 - p0 + 1, layer_end - layer_begin);
+    const int kvh = ctx->kv_cols / ctx->head_dim;
+    hipEvent_t ev;
+    timing_mark_begin(ctx, kClassOther, &ev);  // not on the decode path: class "other" holds it alone there
     if (ctx->desc.kv_dtype == ZR_DTYPE_BF16)
         hipLaunchKernelGGL(kv_copy_kernel<uint16_t>, grid, dim3(256), 0, ctx->stream,
                            (uint16_t*)ctx->kv_pool, pe, ctx->n_pages, layer_begin, d_table, first_offset,
-                           first_row, n_rows, ctx->kv_cols, ctx->head_dim, k, v, to_pool);
+                           first_row, n_rows, kvh, ctx->head_dim, k, v, to_pool);
     else
         hipLaunchKernelGGL(kv_copy_kernel<float>, grid, dim3(256), 0, ctx->stream, (float*)ctx->kv_pool,
-                           pe, ctx->n_pages, layer_begin, d_table, first_offset, first_row, n_rows,
-                           ctx->kv_cols, ctx->head_dim, k, v, to_pool);
+                           pe, ctx->n_pages, layer_begin, d_table, first_offset, first_row, n_rows, kvh,
+                           ctx->head_dim, k, v, to_pool);
     ZR_LAUNCH_CHECK(ctx);
+    timing_mark_end(ctx, kClassOther, ev);
     return ZR_OK;
 }
 

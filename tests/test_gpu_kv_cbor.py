@@ -155,3 +155,30 @@ def test_llama3_shape_2048_token_window_document():
     assert got.size == len(want)
     assert np.array_equal(got, np.frombuffer(want, np.uint8))
     ctx.close()
+
+
+def test_workspaces_survive_kv_staging_growth():
+    """The KV gather staging grows on demand; growing it must leave the CBOR
+    encoder's and the sampler's workspaces in place.  On one context: sample
+    a batch and encode a document, grow the staging with a larger gather,
+    then sample and encode again: the same tokens and the same bytes, equal
+    to the oracle's document."""
+    from mesh_amd.provider import sample_device
+
+    ctx, geo = _ctx("bf16", layers=2, kv_heads=4, head_dim=64, pages=512)
+    small = _fill(ctx, geo, 40, 45, seed=3, specials=False)
+    big = _fill(ctx, geo, 1500, 1500, seed=4, specials=False)
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((6, 64)).astype(np.float32)
+    temps = np.array([0.7, 1.0, 0.0, 1.3, 0.5, 0.9], np.float32)
+    tops = np.array([0.9, 1.0, 1.0, 0.5, 0.95, 0.8], np.float32)
+    seeds = rng.integers(0, 2 ** 63, 6, dtype=np.uint64)
+    want, _ = _want(ctx, geo, small)
+    t1 = sample_device(ctx, x, temps, tops, seeds)
+    d1 = bytes(small.export_kv_snapshot().blob.data)
+    big.export_kv_cache()  # 1500 rows x 2 layers: a larger staging than the first export's
+    t2 = sample_device(ctx, x, temps, tops, seeds)
+    d2 = bytes(small.export_kv_snapshot().blob.data)
+    assert t1 == t2
+    assert d1 == want and d2 == want
+    ctx.close()
