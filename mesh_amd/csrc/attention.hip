@@ -541,14 +541,17 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attention_kernel(Prefill
         // tile with a visible key, then rarely).  The result is the same
         // softmax: O and l share the scale.
         if (__any(tmax > m + 8.0f)) {
-            const float m_new = tmax > m + 8.0f ? tmax : m;
-            const float alpha = __builtin_amdgcn_exp2f(m - m_new);  // 0 while m = -inf
+            // only the lanes whose max moves rescale (alpha 0 while m = -inf);
+            // the others keep alpha = 1 exactly, also a column with no visible
+            // key yet (m = -inf, where m - m would be NaN)
+            const bool up = tmax > m + 8.0f;
+            const float alpha = up ? __builtin_amdgcn_exp2f(m - tmax) : 1.0f;
+            if (up) m = tmax;
             lsum *= alpha;
 #pragma unroll
             for (int db = 0; db < D / 32; ++db)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
-            m = m_new;
         }
         const float m_use = m == -INFINITY ? 0.0f : m;
         float pr[16];

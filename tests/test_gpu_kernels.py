@@ -254,6 +254,57 @@ def test_prefill_blocks_llama3_heads_trimmed_windows_and_decode_rows():
     ctx.close()
 
 
+@pytest.mark.parametrize("heads,kv_heads,D", [(8, 8, 64), (8, 4, 128), (32, 8, 128), (16, 2, 64)])
+def test_prefill_blocks_gqa_groups_with_forced_splits(monkeypatch, heads, kv_heads, D):
+    """The prefill kernel at G = 1, 2, 4 and 8 (blocks of 128, 64, 32 and 16
+    rows; merge groups of 16, 8, 4 and 2 rows), with its key splits forced to
+    2 tiles (ZR_ATTN_PREFILL_TILES_PER_SPLIT) so every block of these chunks
+    goes through the partials and the merge.  The page-unaligned prefix puts
+    the causal edge inside waves: a split can start past some rows' last
+    visible key while the wave's other rows see keys in it (those columns
+    must keep a zero weight, not NaN)."""
+    monkeypatch.setenv("ZR_ATTN_PREFILL_TILES_PER_SPLIT", "2")
+    G = heads // kv_heads
+    prows = 128 // G
+    q_cols, kv_cols = heads * D, kv_heads * D
+    geo = ModelGeometry(hidden=q_cols, num_heads=heads, num_kv_heads=kv_heads, num_layers=1, vocab=64, ffn=64)
+    ctx = DeviceContext(geo, kv_dtype="bf16", max_tokens=512, max_seqs=4, max_pages_per_seq=64)
+    ctx.create_kv_pool(256)
+    rng = np.random.default_rng(G)
+    prefixes, chunks = [0, 203], [prows + 5, 2 * prows]
+    backends, Ks, Vs = [ctx.new_backend() for _ in prefixes], [], []
+    for b, p, c in zip(backends, prefixes, chunks):
+        k = rng.standard_normal((p + c, kv_cols), dtype=np.float32)
+        v = rng.standard_normal((p + c, kv_cols), dtype=np.float32)
+        Ks.append(k)
+        Vs.append(v)
+        if p:
+            b.import_kv_cache(_snapshot(k[:p], v[:p]))
+    T = sum(chunks)
+    Q = rng.standard_normal((T, q_cols), dtype=np.float32)
+    newk = np.concatenate([k[p:] for k, p in zip(Ks, prefixes)])
+    newv = np.concatenate([v[p:] for v, p in zip(Vs, prefixes)])
+    st = stage_mixed(ctx, backends, chunks)
+    d_qkv = DeviceBuffer.from_numpy(ctx, np.concatenate([Q, newk, newv], 1))
+    d_q = DeviceBuffer(ctx, Q.nbytes)
+    d_o = DeviceBuffer(ctx, Q.nbytes)
+    ctx.check(ctx.lib.zr_rope_kv_write(ctx.h, st, 0, d_qkv.ptr, d_q.ptr, 0))
+    ctx.check(ctx.lib.zr_attention(ctx.h, st, 0, d_q.ptr, d_o.ptr))
+    out = d_o.download(np.float32, Q.shape)
+    ctx.lib.zr_staged_destroy(st)
+    row = 0
+    for s, (p, c) in enumerate(zip(prefixes, chunks)):
+        k, v = O.round_bf16(Ks[s]), O.round_bf16(Vs[s])
+        for h in range(heads):
+            kvh = h // G
+            want = O.causal_attention_with_prefix(Q[row:row + c, h * D:(h + 1) * D], k[:, kvh * D:(kvh + 1) * D],
+                                                  v[:, kvh * D:(kvh + 1) * D], 1 / math.sqrt(D), p)
+            err = max_rel_err_rows(out[row:row + c, h * D:(h + 1) * D], want, D)
+            assert err <= ATTN_RTOL, (s, h, err)
+        row += c
+    ctx.close()
+
+
 # ------------------------------------------------------- gather / scatter --
 @pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
 def test_kv_gather_scatter_round_trip_with_partial_first_page(kv_dtype):
