@@ -198,3 +198,18 @@ def test_host_page_tables_match_oracle_on_random_sequences(seed):
         assert b.pages() == o.allocated_pages(0)
     b.close()
     _lib.load().zrh_pool_destroy(pool)
+
+
+def test_stage_map_names_kernels_that_exist():
+    """Every kernel FUSED_KERNEL_STAGES lists (the executor contract's stages,
+    engine.rs:240-273) is a __global__ function of the HIP sources."""
+    import glob
+    import re
+
+    from mesh_amd.provider import FUSED_KERNEL_STAGES
+
+    src = "".join(open(f).read() for f in glob.glob(os.path.join(ROOT, "mesh_amd", "csrc", "*.hip")))
+    defined = set(re.findall(r"__global__\s+(?:__launch_bounds__\([^)]*\)\s*)?void\s+(\w+)\s*\(", src))
+    for stage, kernels in FUSED_KERNEL_STAGES.items():
+        for k in kernels:
+            assert k in defined, (stage, k)
