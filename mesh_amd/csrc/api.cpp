@@ -218,10 +218,11 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
         }
     }
     // ~96 pages per split at 256 sessions x 8 kv heads x ~1.5k tokens (measured
-    // best on MI355X with longest-first dispatch); at least 8 pages, which
-    // measured best at 32 sessions (fewer merges; 4 and 5 pages lose ~3%)
+    // best on MI355X with longest-first dispatch); at least 12 pages, which
+    // measured best at 32 sessions (fewer merges: 6, 8, 16 and 24 pages are
+    // 0.3-3 % slower there)
     const long target_wgs = 2048;
-    int pps = (int)std::min<long>(4096, std::max<long>(8, (total_pages * ctx->local_kv_heads + target_wgs - 1) / target_wgs));
+    int pps = (int)std::min<long>(4096, std::max<long>(12, (total_pages * ctx->local_kv_heads + target_wgs - 1) / target_wgs));
     if (const char* env = getenv("ZR_ATTN_PAGES_PER_SPLIT")) pps = std::max(1, atoi(env));
     for (size_t t = 0; t < st->h_tiles.size(); ++t) {
         st->h_tiles[t].w = (int)st->h_items.size();
