@@ -248,37 +248,64 @@ __global__ __launch_bounds__(256) void kv_copy_kernel(KV* __restrict__ pool, siz
                 }
             }
         }
-        // V: group cg = ((d / 32) * 4 + q) * 16 + dd holds rows 4 q + i of dims d (i) and d + 16 (4 + i)
-        {
-            const int dd = cg & 15, q = (cg >> 4) & 3, d = (cg >> 6) * 32 + dd;
-            const int r0 = 4 * q;
-            if (r0 + 3 < r_lo || r0 >= r_hi) continue;
-            const size_t c0 = (size_t)h * D + d;  // column of dim d
+    }
+    // V: group cg = ((d / 32) * 4 + q) * 16 + dd holds rows 4 q + i of dims d (i)
+    // and d + 16 (4 + i).  A thread takes 4 consecutive groups (dims d .. d + 3,
+    // one 64 B run of the page) and moves the 4 rows as float4 runs of dims
+    // d .. d + 3 and d + 16 .. d + 19; a quad cut by the row range goes element
+    // by element.
+    const int quads = kv_heads * D / 2;
+    for (int qi = threadIdx.x; qi < quads; qi += blockDim.x) {
+        const int h = qi / (D / 2), cg0 = (qi - h * (D / 2)) * 4;
+        const int q = (cg0 >> 4) & 3, d0 = (cg0 >> 6) * 32 + (cg0 & 15);
+        const int r0 = 4 * q;
+        if (r0 + 3 < r_lo || r0 >= r_hi) continue;
+        Group8<KV>* gp = vp + (size_t)h * (tile / 8) + cg0;
+        const size_t c0 = (size_t)h * D + d0;  // column of dim d0
+        if (r0 >= r_lo && r0 + 3 < r_hi) {
             if (to_pool) {
-                if (r0 >= r_lo && r0 + 3 < r_hi) {
+                f32x4 lo4[4], hi4[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    lo4[i] = *(const f32x4*)(vrow(r0 + i) + c0);
+                    hi4[i] = *(const f32x4*)(vrow(r0 + i) + c0 + 16);
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
                     Group8<KV> gr;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        store_elem(&gr.x[i], vrow(r0 + i)[c0]);
-                        store_elem(&gr.x[4 + i], vrow(r0 + i)[c0 + 16]);
+                        store_elem(&gr.x[i], lo4[i][j]);
+                        store_elem(&gr.x[4 + i], hi4[i][j]);
                     }
-                    vp[gi] = gr;
-                } else {
-                    KV* e = vp[gi].x;
-                    for (int i = 0; i < 4; ++i)
-                        if (r0 + i >= r_lo && r0 + i < r_hi) {
-                            store_elem(&e[i], vrow(r0 + i)[c0]);
-                            store_elem(&e[4 + i], vrow(r0 + i)[c0 + 16]);
-                        }
+                    gp[j] = gr;
                 }
             } else {
-                const Group8<KV> gr = vp[gi];
+                Group8<KV> gr[4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    if (r0 + i >= r_lo && r0 + i < r_hi) {
-                        vrow(r0 + i)[c0] = load_elem(&gr.x[i]);
-                        vrow(r0 + i)[c0 + 16] = load_elem(&gr.x[4 + i]);
+                for (int j = 0; j < 4; ++j) gr[j] = gp[j];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    *(f32x4*)(vrow(r0 + i) + c0) = f32x4{load_elem(&gr[0].x[i]), load_elem(&gr[1].x[i]),
+                                                        load_elem(&gr[2].x[i]), load_elem(&gr[3].x[i])};
+                    *(f32x4*)(vrow(r0 + i) + c0 + 16) =
+                        f32x4{load_elem(&gr[0].x[4 + i]), load_elem(&gr[1].x[4 + i]), load_elem(&gr[2].x[4 + i]),
+                              load_elem(&gr[3].x[4 + i])};
+                }
+            }
+        } else {
+            for (int j = 0; j < 4; ++j) {
+                KV* e = gp[j].x;
+                for (int i = 0; i < 4; ++i) {
+                    if (r0 + i < r_lo || r0 + i >= r_hi) continue;
+                    if (to_pool) {
+                        store_elem(&e[i], vrow(r0 + i)[c0 + j]);
+                        store_elem(&e[4 + i], vrow(r0 + i)[c0 + 16 + j]);
+                    } else {
+                        vrow(r0 + i)[c0 + j] = load_elem(&e[i]);
+                        vrow(r0 + i)[c0 + 16 + j] = load_elem(&e[4 + i]);
                     }
+                }
             }
         }
     }
