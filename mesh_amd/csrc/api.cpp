@@ -525,10 +525,12 @@ zr_status zr_context_create(const zr_model_desc* desc, int device, zr_context** 
         e = hipMalloc(a.p, a.bytes);
         if (e != hipSuccess) return fail(e, "hipMalloc activations");
     }
-    // split-K workspace: max over microbatch row counts of every GEMM shape
+    // split-K workspace: max over every row count a microbatch can have (the
+    // plan changes with m, so no grid of sample sizes bounds it): 1..T rows
+    // for the layer GEMMs, 1..S for the LM head
     size_t ws = 0;
-    for (size_t m = 1; m <= T + 15; m += (m < 16 ? 15 : 16)) {
-        const int mm = (int)std::min(m, T);
+    for (size_t m = 1; m <= T; ++m) {
+        const int mm = (int)m;
         ws = std::max(ws, gemm_ws_floats(mm, (int)(Q + 2 * KV), (int)H, kEpiStore));
         ws = std::max(ws, gemm_ws_floats(mm, (int)H, (int)Q, kEpiStore));
         ws = std::max(ws, gemm_ws_floats(mm, (int)(2 * F), (int)H, kEpiSwiGLU));

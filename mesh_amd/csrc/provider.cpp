@@ -16,6 +16,10 @@ using zr::set_global_err;
 struct zrh_pool {
     zr_context* ctx = nullptr;
     std::vector<int> free_list;  // LIFO: pop_back
+    // Global pages popped while a host call is open, in pop order, so that a
+    // failed call can give them back (PoolTxn).
+    std::vector<int> popped;
+    int txn_depth = 0;
 };
 
 namespace {
@@ -54,6 +58,34 @@ struct zrh_backend {
 
 namespace {
 
+// A host call that fails leaves the pool as it found it.  Sessions restore
+// their saved page tables on failure, and the global pages that were bound to
+// them during the call go back onto the free list in reverse pop order, which
+// restores the LIFO order exactly.  Calls nest (a chunked prefill runs one
+// microbatch per chunk): each rolls back only what was popped after its mark.
+class PoolTxn {
+  public:
+    explicit PoolTxn(zrh_pool* pool) : pool_(pool), mark_(pool ? pool->popped.size() : 0) {
+        if (pool_) ++pool_->txn_depth;
+    }
+    ~PoolTxn() {
+        if (pool_ && --pool_->txn_depth == 0) pool_->popped.clear();
+    }
+    PoolTxn(const PoolTxn&) = delete;
+    PoolTxn& operator=(const PoolTxn&) = delete;
+    void rollback() {
+        if (!pool_) return;
+        while (pool_->popped.size() > mark_) {
+            pool_->free_list.push_back(pool_->popped.back());
+            pool_->popped.pop_back();
+        }
+    }
+
+  private:
+    zrh_pool* pool_;
+    size_t mark_;
+};
+
 zr_status fail(zrh_backend* b, zr_status code, const char* msg, int a = 0, int c = 0, int d = 0) {
     return set_err(b ? b->ctx : nullptr, code, msg, a, c, d);
 }
@@ -77,6 +109,7 @@ zr_status allocate_page(zrh_backend* b, int* out) {
     PageEntry pe;
     pe.global = b->pool->free_list.back();
     b->pool->free_list.pop_back();
+    if (b->pool->txn_depth) b->pool->popped.push_back(pe.global);
     pe.active = true;
     kv.pages.push_back(pe);
     *out = (int)kv.pages.size() - 1;
@@ -224,20 +257,37 @@ struct Assembled {
 
 // One microbatch row per session: trim the window for the incoming rows, then
 // reserve them (attention_output 1446-1452 / the batched decode 2703-2723).
+// Saved session state of one microbatch, restored when the call fails.
+struct Saved {
+    std::vector<SessionKV> kv;
+    std::vector<int> pos;
+    void restore(zrh_backend* const* backends, int n, PoolTxn& txn) {
+        for (int i = 0; i < n && i < (int)kv.size(); ++i) {
+            backends[i]->kv = kv[i];
+            backends[i]->position = pos[i];
+        }
+        txn.rollback();
+    }
+};
+
+// Every session of a microbatch draws from the same pool (one pool per
+// context), so one PoolTxn covers the call.
 zr_status assemble(zrh_backend* const* backends, int n, const int* q_len, bool decode_only, Assembled& out,
-                   std::vector<SessionKV>& saved, std::vector<int>& saved_pos) {
-    if (n <= 0 || !backends) return set_global_err(ZR_E_INVALID, "Decode microbatch requires at least one backend and token");
+                   Saved& saved, PoolTxn& txn) {
+    if (n <= 0 || !backends || !backends[0])
+        return set_global_err(ZR_E_INVALID, "Decode microbatch requires at least one backend and token");
     zr_context* ctx = backends[0]->ctx;
     std::vector<std::vector<int>> tables(n);
-    saved.clear();
-    saved_pos.clear();
+    saved.kv.clear();
+    saved.pos.clear();
     for (int i = 0; i < n; ++i) {
         zrh_backend* b = backends[i];
         if (!b || b->ctx != ctx) return set_err(ctx, ZR_E_INVALID, "microbatch mixes contexts");
+        if (b->pool != backends[0]->pool) return set_err(ctx, ZR_E_INVALID, "microbatch mixes KV pools");
         for (int j = 0; j < i; ++j)
             if (backends[j] == b) return set_err(ctx, ZR_E_INVALID, "session %d appears twice in one microbatch", i);
-        saved.push_back(b->kv);
-        saved_pos.push_back(b->position);
+        saved.kv.push_back(b->kv);
+        saved.pos.push_back(b->position);
     }
     out = Assembled();
     zr_status rc = ZR_OK;
@@ -277,10 +327,7 @@ zr_status assemble(zrh_backend* const* backends, int n, const int* q_len, bool d
         out.stride = std::max(out.stride, (int)tables[i].size());
     }
     if (rc) {
-        for (int i = 0; i < n; ++i) {
-            backends[i]->kv = saved[i];
-            backends[i]->position = saved_pos[i];
-        }
+        saved.restore(backends, n, txn);
         return rc;
     }
     out.tables.assign((size_t)n * out.stride, 0);
@@ -303,19 +350,20 @@ zr_microbatch as_microbatch(const Assembled& a, const uint32_t* tokens) {
 
 zr_status run_mixed(zrh_backend* const* backends, int n, const int* q_len, const uint32_t* tokens, bool decode_only,
                     uint32_t* out_tokens, float* out_logits, float* out_partials) {
-    if (!backends[0]->ctx) return set_global_err(ZR_E_INVALID, "bookkeeping-only pool has no device context");
+    if (n <= 0 || !backends || !backends[0])
+        return set_global_err(ZR_E_INVALID, "Decode microbatch requires at least one backend and token");
+    PoolTxn txn(backends[0]->pool);
     Assembled a;
-    std::vector<SessionKV> saved;
-    std::vector<int> saved_pos;
-    zr_status rc = assemble(backends, n, q_len, decode_only, a, saved, saved_pos);
+    Saved saved;
+    zr_status rc = assemble(backends, n, q_len, decode_only, a, saved, txn);
     if (rc) return rc;
+    // the page tables of a bookkeeping-only pool are assembled (and rolled
+    // back) like any other; only the compute needs a device
+    if (!backends[0]->ctx) rc = set_global_err(ZR_E_INVALID, "bookkeeping-only pool has no device context");
     zr_microbatch mb = as_microbatch(a, tokens);
-    rc = zr_forward(backends[0]->ctx, &mb, out_tokens, out_logits, out_partials);
+    if (!rc) rc = zr_forward(backends[0]->ctx, &mb, out_tokens, out_logits, out_partials);
     if (rc) {
-        for (int i = 0; i < n; ++i) {
-            backends[i]->kv = saved[i];
-            backends[i]->position = saved_pos[i];
-        }
+        saved.restore(backends, n, txn);
         return rc;
     }
     for (int i = 0; i < n; ++i) backends[i]->position += q_len[i];
@@ -376,6 +424,7 @@ void zrh_backend_destroy(zrh_backend* b) {
 zr_status zrh_prefill(zrh_backend* b, const uint32_t* tokens, int n, float* logits, uint32_t* greedy) {
     if (!b || !tokens) return set_global_err(ZR_E_INVALID, "null argument");
     if (n <= 0) return set_err(b->ctx, ZR_E_INVALID, "Cannot prefill an empty prompt without an explicit BOS policy");
+    PoolTxn txn(b->pool);
     const SessionKV saved = b->kv;
     const int saved_pos = b->position;
     // clear_cache + keep the last window (forward_pass.rs:2101-2105)
@@ -387,7 +436,7 @@ zr_status zrh_prefill(zrh_backend* b, const uint32_t* tokens, int n, float* logi
     b->position = start;
     // prompts longer than the context's row capacity run as causal chunks
     // with the earlier chunks as cached prefix (the same attention rows)
-    const int cap = std::max(b->ctx->desc.max_tokens, 1);
+    const int cap = std::max(b->ctx ? b->ctx->desc.max_tokens : window, 1);
     uint32_t tok;
     zr_status rc = ZR_OK;
     for (int off = start; off < n && !rc; off += cap) {
@@ -399,6 +448,7 @@ zr_status zrh_prefill(zrh_backend* b, const uint32_t* tokens, int n, float* logi
     if (rc) {
         b->kv = saved;
         b->position = saved_pos;
+        txn.rollback();
     }
     return rc;
 }
@@ -446,20 +496,17 @@ zr_status zrh_forward_mixed(zrh_backend* const* backends, int n, const int* q_le
 
 zr_status zrh_stage_mixed(zrh_backend* const* backends, int n, const int* q_len, const uint32_t* tokens,
                           zr_staged** out) {
-    if (!backends || !q_len || !out || n <= 0) return set_global_err(ZR_E_INVALID, "null argument");
-    if (!backends[0]->ctx) return set_global_err(ZR_E_INVALID, "bookkeeping-only pool has no device context");
+    if (!backends || !backends[0] || !q_len || !out || n <= 0) return set_global_err(ZR_E_INVALID, "null argument");
+    PoolTxn txn(backends[0]->pool);
     Assembled a;
-    std::vector<SessionKV> saved;
-    std::vector<int> saved_pos;
-    zr_status rc = assemble(backends, n, q_len, false, a, saved, saved_pos);
+    Saved saved;
+    zr_status rc = assemble(backends, n, q_len, false, a, saved, txn);
     if (rc) return rc;
+    if (!backends[0]->ctx) rc = set_global_err(ZR_E_INVALID, "bookkeeping-only pool has no device context");
     zr_microbatch mb = as_microbatch(a, tokens);
-    rc = zr_stage(backends[0]->ctx, &mb, out);
+    if (!rc) rc = zr_stage(backends[0]->ctx, &mb, out);
     if (rc) {
-        for (int i = 0; i < n; ++i) {
-            backends[i]->kv = saved[i];
-            backends[i]->position = saved_pos[i];
-        }
+        saved.restore(backends, n, txn);
         return rc;
     }
     for (int i = 0; i < n; ++i) backends[i]->position += q_len[i];
@@ -534,6 +581,7 @@ zr_status zrh_import_kv(zrh_backend* b, const float* k, const float* v, int rows
     if (base_position != next_position - rows)
         return set_err(b->ctx, ZR_E_INVALID, "KV snapshot base position mismatch: payload starts at %d, sequence metadata says %d",
                        base_position, next_position - rows);
+    PoolTxn txn(b->pool);
     const SessionKV saved = b->kv;
     const int saved_pos = b->position;
     clear_kv(b->kv);
@@ -541,13 +589,14 @@ zr_status zrh_import_kv(zrh_backend* b, const float* k, const float* v, int rows
     zr_status rc = ZR_OK;
     if (rows > 0) {
         if (!k || !v) rc = set_err(b->ctx, ZR_E_INVALID, "null import buffers");
-        if (!b->ctx) rc = set_global_err(ZR_E_INVALID, "bookkeeping-only pool has no device context");
         const int max_seq = std::max(b->max_seq_len, 1);
         const int keep = std::min(rows, max_seq);
         if (!rc) rc = append_rows(b, keep);
         if (!rc && b->kv.seq_len != rows)
             rc = set_err(b->ctx, ZR_E_INVARIANT, "Recovered device KV cache length %d does not match snapshot cached token count %d",
                          b->kv.seq_len, rows);
+        // page tables of a bookkeeping-only pool are built (and rolled back); the copy needs a device
+        if (!rc && !b->ctx) rc = set_global_err(ZR_E_INVALID, "bookkeeping-only pool has no device context");
         std::vector<int> table;
         int foff = 0;
         if (!rc) rc = device_table(b, table, &foff);
@@ -559,6 +608,7 @@ zr_status zrh_import_kv(zrh_backend* b, const float* k, const float* v, int rows
     if (rc) {
         b->kv = saved;
         b->position = saved_pos;
+        txn.rollback();
         return rc;
     }
     b->position = next_position;
@@ -642,10 +692,12 @@ zr_status zrh_release_pages(zrh_backend* b) {
 zr_status zrh_kv_reserve(zrh_backend* b, int rows) {
     if (!b) return set_global_err(ZR_E_INVALID, "null backend");
     if (rows <= 0) return set_err(b->ctx, ZR_E_INVALID, "Device KV append received an empty key shape");
+    PoolTxn txn(b->pool);
     const SessionKV saved = b->kv;
     zr_status rc = append_rows(b, rows);
     if (rc) {
         b->kv = saved;
+        txn.rollback();
         return rc;
     }
     b->position = b->kv.base_position + b->kv.seq_len;

@@ -213,3 +213,105 @@ def test_stage_map_names_kernels_that_exist():
     for stage, kernels in FUSED_KERNEL_STAGES.items():
         for k in kernels:
             assert k in defined, (stage, k)
+
+
+# ------------------------------------------------- rollback of failed calls --
+def test_failed_multi_page_reserve_returns_global_pages():
+    # 48 rows need 3 pages, the pool has 2: the call fails after binding 2
+    lib = _lib.load()
+    pool = host_pool(2)
+    b = HostBackend(pool, 4096)
+    with pytest.raises(_lib.ZrError) as e:
+        b.reserve(48)
+    assert "KV pool exhausted" in str(e.value)
+    assert b.seq_len == 0 and b.pages() == 0
+    assert lib.zrh_pool_free_pages(pool) == 2
+    b.close()
+    assert lib.zrh_pool_free_pages(pool) == 2
+    lib.zrh_pool_destroy(pool)
+
+
+def test_failed_reserve_keeps_the_pool_lifo_order():
+    order = np.random.default_rng(3).permutation(8)
+    pool = host_pool(8, order)
+    expect = order[::-1].tolist()  # LIFO pops from the end of the initial order
+    b = HostBackend(pool, 4096)
+    b.reserve(16 * 5)
+    with pytest.raises(_lib.ZrError):
+        b.reserve(16 * 4)  # 3 pages left
+    _, g = b.table()
+    assert g == expect[:5]
+    b.reserve(16 * 3)
+    _, g = b.table()
+    assert g == expect  # the rolled-back pages come out again in order
+    b.close()
+    _lib.load().zrh_pool_destroy(pool)
+
+
+def _decode_batch(backends, tokens):
+    lib = _lib.load()
+    arr = (C.c_void_p * len(backends))(*[b.h for b in backends])
+    tok = np.ascontiguousarray(tokens, np.uint32)
+    out = np.zeros(len(backends), np.uint32)
+    return lib.zrh_decode_step_batch(arr, len(backends), tok.ctypes.data_as(_lib.c_u32_p),
+                                     out.ctypes.data_as(_lib.c_u32_p), None, None)
+
+
+def test_failed_multi_session_assemble_returns_global_pages():
+    # three sessions on full pages each need a new page; the pool has one
+    lib = _lib.load()
+    pool = host_pool(4)
+    bs = [HostBackend(pool, 4096) for _ in range(3)]
+    for b in bs:
+        b.reserve(16)
+    before = [b.table() for b in bs]
+    assert lib.zrh_pool_free_pages(pool) == 1
+    rc = _decode_batch(bs, [1, 2, 3])
+    assert rc == -2 and "KV pool exhausted" in lib.zr_global_last_error().decode()
+    assert lib.zrh_pool_free_pages(pool) == 1
+    assert [b.table() for b in bs] == before
+    assert [b.seq_len for b in bs] == [16, 16, 16]
+    for b in bs:
+        b.close()
+    assert lib.zrh_pool_free_pages(pool) == 4
+    lib.zrh_pool_destroy(pool)
+
+
+def test_microbatch_without_device_rolls_back_its_page_tables():
+    # assembly succeeds (pages bound), the compute is refused: nothing sticks
+    lib = _lib.load()
+    pool = host_pool(8)
+    bs = [HostBackend(pool, 4096) for _ in range(2)]
+    for b in bs:
+        b.reserve(16)
+    free = lib.zrh_pool_free_pages(pool)
+    before = [b.table() for b in bs]
+    rc = _decode_batch(bs, [5, 6])
+    assert rc == -1 and "bookkeeping-only" in lib.zr_global_last_error().decode()
+    assert lib.zrh_pool_free_pages(pool) == free
+    assert [b.table() for b in bs] == before
+    assert [lib.zrh_sequence_position(b.h) for b in bs] == [16, 16]
+    for b in bs:
+        b.close()
+    lib.zrh_pool_destroy(pool)
+
+
+def test_failed_import_and_prefill_return_global_pages():
+    lib = _lib.load()
+    pool = host_pool(3)
+    b = HostBackend(pool, 4096)
+    b.reserve(20)
+    before = b.table()
+    k = np.zeros((1, 64, 2), np.float32)
+    # 64 rows need 4 pages; the session holds 2 and the pool 1
+    rc = lib.zrh_import_kv(b.h, k.ctypes.data_as(_lib.c_f32_p), k.ctypes.data_as(_lib.c_f32_p), 64, 0, 64)
+    assert rc == -2
+    assert lib.zrh_pool_free_pages(pool) == 1 and b.table() == before and b.seq_len == 20
+    # a prefill that fits is assembled, then refused for lack of a device
+    toks = np.arange(40, dtype=np.uint32)
+    rc = lib.zrh_prefill(b.h, toks.ctypes.data_as(_lib.c_u32_p), 40, None, None)
+    assert rc == -1
+    assert lib.zrh_pool_free_pages(pool) == 1 and b.table() == before and b.seq_len == 20
+    b.close()
+    assert lib.zrh_pool_free_pages(pool) == 3
+    lib.zrh_pool_destroy(pool)
