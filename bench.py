@@ -97,9 +97,12 @@ def step_bytes(geo, batch, kv_rows_total):
     return weights + 2 * batch * H + kv + act
 
 
-def device_model(name, split=True, max_tokens=None, max_seqs=None):
+def device_model(name, split=True, max_tokens=None, max_seqs=None, host_weights=None):
     """A DeviceContext holding the workload's model with random-init bf16
-    N(0, 0.02) weights generated on the device (RMSNorm gains 1)."""
+    N(0, 0.02) weights generated on the device (RMSNorm gains 1).  A dict
+    passed as `host_weights` receives host copies of the generated weights as
+    bf16 bit patterns in the reference [in, out] layout (embedding, lm_head,
+    final_norm, layers), e.g. for a parity check of the same model."""
     from mesh_amd import DeviceContext, ModelGeometry, _lib
 
     w = WORKLOADS[name]
@@ -118,9 +121,21 @@ def device_model(name, split=True, max_tokens=None, max_seqs=None):
     shapes = dict(w_q=(H, Q), w_k=(H, KV), w_v=(H, KV), w_o=(Q, H), w_gate=(H, F), w_up=(H, F), w_down=(F, H))
     bufs = {k: dev(2 * a * b) for k, (a, b) in shapes.items()}
     ones = np.ones(H, np.float32)
+
+    def download(ptr, shape):
+        out = np.empty(shape, np.uint16)
+        ctx.check(lib.zr_memcpy_d2h(ctx.h, out.ctypes.data, ptr, out.nbytes))
+        return out
+
+    if host_weights is not None:
+        host_weights["layers"] = []
     for layer in range(g.num_layers):
         for i, (k, (a, b)) in enumerate(shapes.items()):
             ctx.check(lib.zr_fill_normal_bf16(ctx.h, bufs[k], a * b, 1000 * layer + i + 1, 0.02))
+        if host_weights is not None:
+            hw = {k: download(bufs[k], shp) for k, shp in shapes.items()}
+            hw["attn_norm"], hw["mlp_norm"] = ones, ones
+            host_weights["layers"].append(hw)
         lw = _lib.LayerWeights()
         for k in shapes:
             setattr(lw, k, C.cast(bufs[k], _lib.c_u16_p))
@@ -134,15 +149,21 @@ def device_model(name, split=True, max_tokens=None, max_seqs=None):
     ctx.check(lib.zr_fill_normal_bf16(ctx.h, head, H * V, 778, 0.02))
     ctx.check(lib.zr_upload_globals(ctx.h, C.cast(emb, _lib.c_u16_p), ones.ctypes.data_as(_lib.c_f32_p),
                                     C.cast(head, _lib.c_u16_p)))
+    if host_weights is not None:
+        host_weights["embedding"] = download(emb, (V, H))
+        host_weights["lm_head"] = download(head, (H, V))
+        host_weights["final_norm"] = ones
     lib.zr_device_free(ctx.h, emb)
     lib.zr_device_free(ctx.h, head)
     return ctx, g
 
 
 class GpuDecodeBench:
-    """One workload resident on the GPU with `steps_total` decode steps staged."""
+    """One workload resident on the GPU with `steps_total` decode steps staged.
+    `model` = (DeviceContext, ModelGeometry) reuses a model built by
+    device_model (its KV pool is replaced; the caller keeps the context)."""
 
-    def __init__(self, name, steps_total, split=True):
+    def __init__(self, name, steps_total, split=True, model=None):
         from mesh_amd import _lib
 
         self._lib = _lib
@@ -151,7 +172,8 @@ class GpuDecodeBench:
         self.B = w["batch"]
         self.ctxlens = w["contexts"]()
         self.max_seq = w["max_seq_len"]
-        self.ctx, self.geo = device_model(name, split)
+        self.owns_ctx = model is None
+        self.ctx, self.geo = device_model(name, split) if model is None else model
         ctx, lib, g = self.ctx, self.ctx.lib, self.geo
         V = g.vocab
         # KV pool: every session's context plus the benchmarked steps
@@ -207,7 +229,15 @@ class GpuDecodeBench:
         for st in self.staged:
             self.ctx.lib.zr_staged_destroy(st)
         self.staged = []
-        self.ctx.close()
+        for p in self.tok:
+            self.ctx.lib.zr_device_free(self.ctx.h, p)
+        self.tok = []
+        if self.owns_ctx:
+            self.ctx.close()
+        else:
+            for b in self.backends:
+                b.close()
+        self.backends = []
 
 
 BREAKDOWN_STEPS = 2

@@ -154,9 +154,15 @@ void zr_staged_destroy(zr_staged* st);
 /* Enqueues the forward pass on the context stream without synchronising.
  * d_tokens: device [sum q_len] input ids, or NULL to use the staged ids.
  * d_out_tokens: device [num_seqs] greedy ids (may be d_tokens of a later
- * decode step); d_out_logits nullable device [num_seqs, vocab]. */
+ * decode step); d_out_logits nullable device [num_seqs, vocab].
+ * Ids fed from device memory are checked on the device (host ids are checked
+ * when staged): the next zr_synchronize returns ZR_E_INVALID with
+ * "Token {id} out of vocabulary bounds {vocab}" for the first bad id
+ * (embed_tokens, tensor_ops.rs:482-490).  That microbatch's outputs and the
+ * KV rows it appended are then meaningless; nothing is read out of bounds. */
 zr_status zr_forward_staged_async(zr_context* ctx, zr_staged* st, const uint32_t* d_tokens,
                                   uint32_t* d_out_tokens, float* d_out_logits);
+/* Waits for the context stream; reports a device-fed id error (above). */
 zr_status zr_synchronize(zr_context* ctx);
 
 /* ------------------------------------------------------ op-level entries --- */

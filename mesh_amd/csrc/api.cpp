@@ -119,9 +119,10 @@ static void free_ctx_buffers(zr_context* ctx) {
     void* bufs[] = {ctx->hidden, ctx->xa, ctx->qkv, ctx->q_rope, ctx->attn_a, ctx->proj, ctx->ffn_a,
                     ctx->logits, ctx->final_a, ctx->tokens_out, ctx->splitk_ws, ctx->attn_part,
                     ctx->argmax_ws, ctx->inv_freq, ctx->kv_pool, ctx->embedding, ctx->lm_head,
-                    ctx->final_norm};
+                    ctx->final_norm, ctx->d_token_err};
     for (void* b : bufs)
         if (b) hipFree(b);
+    if (ctx->h_token_err) hipHostFree(ctx->h_token_err);
     for (auto& L : ctx->layers) {
         void* lb[] = {L.w_qkv, L.w_o, L.w_gate_up, L.w_down, L.attn_norm, L.mlp_norm};
         for (void* b : lb)
@@ -388,7 +389,7 @@ static zr_status run_forward(zr_context* ctx, StagedMeta* st, const uint32_t* d_
     const int T = st->total_q, S = st->num_seqs, H = d.hidden, F = d.ffn_cols;
     (void)S;
     const int QKV = ctx->q_cols + 2 * ctx->kv_cols;
-    if ((rc = launch_embed(ctx, st, d_tokens ? d_tokens : st->tokens))) return rc;
+    if ((rc = launch_embed(ctx, st, d_tokens ? d_tokens : st->tokens, d_tokens != nullptr))) return rc;
     const int lo = (d.flags & ZR_FLAG_SPLIT_ACTIVATIONS) ? 1 : 0;
     // split-K products are left as slabs for the next kernel to sum, except
     // where the caller asked for the per-layer partials (those are copied out)
@@ -432,6 +433,11 @@ static zr_status run_forward(zr_context* ctx, StagedMeta* st, const uint32_t* d_
     if (d_out_logits)
         ZR_HIP(ctx, hipMemcpyAsync(d_out_logits, logits, sizeof(float) * S * d.vocab, hipMemcpyDeviceToDevice,
                                    ctx->stream));
+    if (d_tokens) {  // the id check of device-fed tokens, read by zr_synchronize
+        ZR_HIP(ctx, hipMemcpyAsync(ctx->h_token_err, ctx->d_token_err, sizeof(unsigned long long),
+                                   hipMemcpyDeviceToHost, ctx->stream));
+        ctx->token_check_pending = true;
+    }
     return ZR_OK;
 }
 
@@ -520,6 +526,7 @@ zr_status zr_context_create(const zr_model_desc* desc, int device, zr_context** 
         {(void**)&ctx->final_a, 2 * 2 * a_plane((int)S, (int)H)},
         {(void**)&ctx->tokens_out, 4 * S},
         {(void**)&ctx->inv_freq, 4 * (size_t)ctx->head_dim / 2},
+        {(void**)&ctx->d_token_err, sizeof(unsigned long long)},
     };
     for (auto& a : allocs) {
         e = hipMalloc(a.p, a.bytes);
@@ -551,6 +558,11 @@ zr_status zr_context_create(const zr_model_desc* desc, int device, zr_context** 
         inv[i] = 1.0f / powf(d.rope_base, (float)i * 2.0f / (float)ctx->head_dim);
     e = hipMemcpy(ctx->inv_freq, inv.data(), inv.size() * 4, hipMemcpyHostToDevice);
     if (e != hipSuccess) return fail(e, "hipMemcpy inv_freq");
+    e = hipHostMalloc((void**)&ctx->h_token_err, sizeof(unsigned long long), hipHostMallocDefault);
+    if (e != hipSuccess) return fail(e, "hipHostMalloc token check word");
+    *ctx->h_token_err = ~0ull;
+    e = hipMemcpy(ctx->d_token_err, ctx->h_token_err, sizeof(unsigned long long), hipMemcpyHostToDevice);
+    if (e != hipSuccess) return fail(e, "hipMemcpy token check word");
     ctx->layers.resize(d.num_layers);
     ctx->scratch_stage = new StagedMeta();
     *out = ctx;
@@ -711,6 +723,18 @@ zr_status zr_forward_staged_async(zr_context* ctx, zr_staged* s, const uint32_t*
 zr_status zr_synchronize(zr_context* ctx) {
     if (!ctx) return set_global_err(ZR_E_INVALID, "null context");
     ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (ctx->token_check_pending) {
+        ctx->token_check_pending = false;
+        const unsigned long long bad = *ctx->h_token_err;
+        if (bad != ~0ull) {
+            const unsigned long long none = ~0ull;
+            *ctx->h_token_err = none;
+            ZR_HIP(ctx, hipMemcpy(ctx->d_token_err, &none, sizeof none, hipMemcpyHostToDevice));
+            // embed_tokens (tensor_ops.rs:482-490)
+            return set_err(ctx, ZR_E_INVALID, "Token %u out of vocabulary bounds %d", (unsigned)(bad & 0xffffffffu),
+                           ctx->desc.vocab);
+        }
+    }
     return ZR_OK;
 }
 

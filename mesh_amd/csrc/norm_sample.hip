@@ -10,22 +10,30 @@ __device__ inline float wave_sum(float v) {
 }
 
 // Row gather of the bf16 embedding table into the f32 residual stream
-// (forward_pass.rs:2230-2237; embed_tokens tensor_ops.rs:482-500).
+// (forward_pass.rs:2230-2237; embed_tokens tensor_ops.rs:482-500).  Host ids
+// are validated before staging.  Ids fed from device memory are checked here:
+// the first out-of-vocabulary one (lowest row) is recorded in *err as
+// (row << 32 | id) for the host to report, and its row gathers row 0 so that
+// nothing is read out of bounds.
 __global__ __launch_bounds__(256) void embed_kernel(const uint32_t* __restrict__ tokens,
                                                     const uint16_t* __restrict__ table, int H, int V,
-                                                    float* __restrict__ hidden) {
+                                                    float* __restrict__ hidden, unsigned long long* err) {
     const int t = blockIdx.x;
     uint32_t id = tokens[t];
-    if (id >= (uint32_t)V) id = 0;  // validated on the host; never read out of bounds
+    if (id >= (uint32_t)V) {
+        if (err && threadIdx.x == 0) atomicMin(err, ((unsigned long long)t << 32) | id);
+        id = 0;
+    }
     const uint16_t* src = table + (size_t)id * H;
     float* dst = hidden + (size_t)t * H;
     for (int i = threadIdx.x; i < H; i += blockDim.x) dst[i] = bf16_bits_to_f32(src[i]);
 }
 
-zr_status launch_embed(zr_context* ctx, StagedMeta* st, const uint32_t* d_tokens) {
+zr_status launch_embed(zr_context* ctx, StagedMeta* st, const uint32_t* d_tokens, bool check_ids) {
     if (st->total_q == 0) return ZR_OK;
     hipLaunchKernelGGL(embed_kernel, dim3(st->total_q), dim3(256), 0, ctx->stream, d_tokens,
-                       ctx->embedding, ctx->desc.hidden, ctx->desc.vocab, ctx->hidden);
+                       ctx->embedding, ctx->desc.hidden, ctx->desc.vocab, ctx->hidden,
+                       check_ids ? ctx->d_token_err : nullptr);
     ZR_LAUNCH_CHECK(ctx);
     return ZR_OK;
 }
@@ -288,19 +296,24 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restric
     if (threadIdx.x == 0) out[r] = bi == 0x7fffffff ? 0u : (uint32_t)bi;
 }
 
-zr_status launch_argmax(zr_context* ctx, const float* x, int rows, int cols, uint32_t* out) {
+// Both argmax kernels over `ws` (rows x chunks (value, index) pairs).
+static zr_status argmax_into(zr_context* ctx, const float* x, int rows, int cols, uint32_t* out, float* ws,
+                             size_t ws_floats) {
     if (rows <= 0) return ZR_OK;
     const int chunks = (cols + kArgmaxChunk - 1) / kArgmaxChunk;
-    if ((size_t)rows * chunks * 2 > ctx->argmax_ws_floats)
-        return set_err(ctx, ZR_E_OOM, "argmax workspace too small");
+    if ((size_t)rows * chunks * 2 > ws_floats) return set_err(ctx, ZR_E_OOM, "argmax workspace too small");
     static_assert(kArgmaxChunk == 256 * 4 * 4, "one float4 group per thread");
     const int vec = (cols % 4 == 0) && ((uintptr_t)x % 16 == 0);
     hipLaunchKernelGGL(argmax_partial_kernel, dim3(chunks, rows), dim3(256), 0, ctx->stream, x, cols, chunks, vec,
-                       ctx->argmax_ws);
+                       ws);
     ZR_LAUNCH_CHECK(ctx);
-    hipLaunchKernelGGL(argmax_final_kernel, dim3(rows), dim3(64), 0, ctx->stream, ctx->argmax_ws, chunks, out);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(rows), dim3(64), 0, ctx->stream, ws, chunks, out);
     ZR_LAUNCH_CHECK(ctx);
     return ZR_OK;
+}
+
+zr_status launch_argmax(zr_context* ctx, const float* x, int rows, int cols, uint32_t* out) {
+    return argmax_into(ctx, x, rows, cols, out, ctx->argmax_ws, ctx->argmax_ws_floats);
 }
 
 }  // namespace zr

@@ -160,6 +160,13 @@ struct zr_context {
     size_t cbor_out_bytes = 0;
     void* sample_ws = nullptr;      // stochastic sampling: per-row parameters
     size_t sample_ws_bytes = 0;
+    // Device-fed token ids out of the vocabulary: the embedding kernel keeps
+    // the smallest (row << 32 | id) here (all ones = none); a forward pass fed
+    // from device memory copies it to the pinned host word, which
+    // zr_synchronize checks.
+    unsigned long long* d_token_err = nullptr;
+    unsigned long long* h_token_err = nullptr;
+    bool token_check_pending = false;
     zr::TimingState timing;
 };
 
@@ -248,7 +255,8 @@ struct Slabs {
 
 // Kernel launchers (one per .hip file) ------------------------------------
 zr_status launch_pack(zr_context* ctx, StagedMeta* st);
-zr_status launch_embed(zr_context* ctx, StagedMeta* st, const uint32_t* d_tokens);
+// check_ids: record out-of-vocabulary ids in ctx->d_token_err (device-fed ids)
+zr_status launch_embed(zr_context* ctx, StagedMeta* st, const uint32_t* d_tokens, bool check_ids);
 // y = rms_norm(x (+ residual_in)) * gamma.  With residual_in, x_out = x +
 // residual_in is written first.  Output as f32 (y_f32) or as the bf16 A operand
 // of the next GEMM (y_bf16: hi [rows, cols] then lo when split_lo).

@@ -54,6 +54,10 @@ def lib():
         L.or_model_free.argtypes = [C.c_void_p]
         L.or_model_set_globals.argtypes = [C.c_void_p, f32p, f32p, f32p]
         L.or_model_set_layer.argtypes = [C.c_void_p, C.c_int] + [f32p] * 9
+        u16p = C.POINTER(C.c_uint16)
+        L.or_model_set_globals_bf16.argtypes = [C.c_void_p, u16p, f32p, u16p]
+        L.or_model_set_layer_bf16.argtypes = [C.c_void_p, C.c_int] + [u16p] * 7 + [f32p] * 2
+        L.or_matmul_bf16w.argtypes = [f32p, u16p, f32p, C.c_int, C.c_int, C.c_int]
         L.or_decode_microbatch.argtypes = [C.c_void_p, C.POINTER(C.c_void_p), C.c_int, u32p, f32p, f32p]
         L.or_prefill.argtypes = [C.c_void_p, C.c_void_p, u32p, C.c_int, f32p]
         L.or_prefill_chunk.argtypes = [C.c_void_p, C.c_void_p, u32p, C.c_int, f32p, f32p]
@@ -357,7 +361,10 @@ class ModelConfig(C.Structure):
 
 
 class Model:
-    """Weights are f32 numpy arrays in the reference [in, out] layout (kept alive here)."""
+    """Weights are numpy arrays in the reference [in, out] layout (kept alive
+    here): f32 values, or uint16 bf16 bit patterns for every matrix (the
+    embedding, LM head and the seven layer matrices; norms stay f32), which
+    gives bit-identical results in half the host memory."""
 
     def __init__(self, cfg: dict, weights: dict):
         c = ModelConfig(cfg["hidden"], cfg["num_heads"], cfg["num_kv_heads"], cfg["num_layers"],
@@ -375,12 +382,26 @@ class Model:
             self._keep.append(a)
             return _f(a)
 
-        _check(lib().or_model_set_globals(self.h, keep(weights["embedding"]), keep(weights["final_norm"]),
-                                          keep(weights["lm_head"])))
+        def keep16(a):
+            a = np.ascontiguousarray(a, np.uint16)
+            self._keep.append(a)
+            return a.ctypes.data_as(C.POINTER(C.c_uint16))
+
+        mats = ("w_q", "w_k", "w_v", "w_o", "w_gate", "w_up", "w_down")
+        self.bf16 = np.asarray(weights["embedding"]).dtype == np.uint16
+        if self.bf16:
+            _check(lib().or_model_set_globals_bf16(self.h, keep16(weights["embedding"]), keep(weights["final_norm"]),
+                                                   keep16(weights["lm_head"])))
+        else:
+            _check(lib().or_model_set_globals(self.h, keep(weights["embedding"]), keep(weights["final_norm"]),
+                                              keep(weights["lm_head"])))
         for l, lw in enumerate(weights["layers"]):
-            _check(lib().or_model_set_layer(self.h, l, keep(lw["w_q"]), keep(lw["w_k"]), keep(lw["w_v"]),
-                                            keep(lw["w_o"]), keep(lw["w_gate"]), keep(lw["w_up"]),
-                                            keep(lw["w_down"]), keep(lw["attn_norm"]), keep(lw["mlp_norm"])))
+            if self.bf16:
+                _check(lib().or_model_set_layer_bf16(self.h, l, *[keep16(lw[k]) for k in mats],
+                                                     keep(lw["attn_norm"]), keep(lw["mlp_norm"])))
+            else:
+                _check(lib().or_model_set_layer(self.h, l, *[keep(lw[k]) for k in mats], keep(lw["attn_norm"]),
+                                                keep(lw["mlp_norm"])))
 
     def __del__(self):
         if getattr(self, "h", None):

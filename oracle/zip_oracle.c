@@ -837,17 +837,58 @@ int or_session_import(or_session* s, const float* k, const float* v, int rows, i
 
 /* =========================================================== model ====== */
 
+/* A weight matrix [in, out] held as f32 values or as bf16 bit patterns.
+ * bf16 -> f32 is exact, so both forms give bit-identical products. */
 typedef struct {
-    const float *w_q, *w_k, *w_v, *w_o, *w_gate, *w_up, *w_down, *attn_norm, *mlp_norm;
+    const float* f;
+    const uint16_t* h;
+} wmat;
+
+typedef struct {
+    wmat w_q, w_k, w_v, w_o, w_gate, w_up, w_down;
+    const float *attn_norm, *mlp_norm;
 } layer_w;
 
 struct or_model {
     or_model_config cfg;
     or_shard_layout lay;
     uint32_t* kv_idx;
-    const float *embedding, *final_norm, *lm_head;
+    wmat embedding, lm_head;
+    const float* final_norm;
     layer_w* layers;
 };
+
+/* or_matmul with b as bf16 bit patterns: the same loop order and the same f32
+ * products (the upcast is exact), so the result is bit-identical to
+ * or_matmul on the f32 values of b. */
+int or_matmul_bf16w(const float* a, const uint16_t* b, float* c, int m, int k, int n) {
+    if (m < 0 || k < 0 || n < 0) return fail("Matmul shape mismatch: %dx%d @ %dx%d", m, k, k, n);
+    memset(c, 0, sizeof(float) * (size_t)m * (size_t)n);
+    const int ib = 16, jb = 256;
+    const int nib = (m + ib - 1) / ib, njb = (n + jb - 1) / jb;
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int it = 0; it < nib; ++it) {
+        for (int blk = 0; blk < njb; ++blk) {
+            const int i0 = it * ib, i1 = i0 + ib < m ? i0 + ib : m;
+            const int j0 = blk * jb, j1 = j0 + jb < n ? j0 + jb : n;
+            float bf[256];
+            for (int kk = 0; kk < k; ++kk) {
+                const uint16_t* b_row = b + (size_t)kk * n;
+                for (int j = j0; j < j1; ++j) bf[j - j0] = or_bf16_to_f32(b_row[j]);
+                for (int i = i0; i < i1; ++i) {
+                    const float a_ik = a[(size_t)i * k + kk];
+                    float* out_row = c + (size_t)i * n;
+                    for (int j = j0; j < j1; ++j) out_row[j] += a_ik * bf[j - j0];
+                }
+            }
+        }
+    }
+    return 0;
+}
+
+static int mm(const float* a, wmat b, float* c, int m, int k, int n) {
+    return b.h ? or_matmul_bf16w(a, b.h, c, m, k, n) : or_matmul(a, b.f, c, m, k, n);
+}
 
 or_model* or_model_new(const or_model_config* cfg) {
     or_shard_layout lay;
@@ -874,9 +915,17 @@ void or_model_free(or_model* m) {
 
 int or_model_set_globals(or_model* m, const float* embedding, const float* final_norm,
                          const float* lm_head) {
-    m->embedding = embedding;
+    m->embedding = (wmat){embedding, NULL};
     m->final_norm = final_norm;
-    m->lm_head = lm_head;
+    m->lm_head = (wmat){lm_head, NULL};
+    return 0;
+}
+
+int or_model_set_globals_bf16(or_model* m, const uint16_t* embedding, const float* final_norm,
+                              const uint16_t* lm_head) {
+    m->embedding = (wmat){NULL, embedding};
+    m->final_norm = final_norm;
+    m->lm_head = (wmat){NULL, lm_head};
     return 0;
 }
 
@@ -884,7 +933,18 @@ int or_model_set_layer(or_model* m, int layer, const float* w_q, const float* w_
                        const float* w_v, const float* w_o, const float* w_gate, const float* w_up,
                        const float* w_down, const float* attn_norm, const float* mlp_norm) {
     if (layer < 0 || layer >= m->cfg.num_layers) return fail("Invalid layer index: %d", layer);
-    m->layers[layer] = (layer_w){w_q, w_k, w_v, w_o, w_gate, w_up, w_down, attn_norm, mlp_norm};
+    m->layers[layer] = (layer_w){{w_q, NULL}, {w_k, NULL}, {w_v, NULL}, {w_o, NULL}, {w_gate, NULL},
+                                 {w_up, NULL}, {w_down, NULL}, attn_norm, mlp_norm};
+    return 0;
+}
+
+int or_model_set_layer_bf16(or_model* m, int layer, const uint16_t* w_q, const uint16_t* w_k,
+                            const uint16_t* w_v, const uint16_t* w_o, const uint16_t* w_gate,
+                            const uint16_t* w_up, const uint16_t* w_down, const float* attn_norm,
+                            const float* mlp_norm) {
+    if (layer < 0 || layer >= m->cfg.num_layers) return fail("Invalid layer index: %d", layer);
+    m->layers[layer] = (layer_w){{NULL, w_q}, {NULL, w_k}, {NULL, w_v}, {NULL, w_o}, {NULL, w_gate},
+                                 {NULL, w_up}, {NULL, w_down}, attn_norm, mlp_norm};
     return 0;
 }
 
@@ -894,7 +954,13 @@ static int embed(const or_model* m, const uint32_t* tokens, int n, float* out) {
     for (int i = 0; i < n; ++i) {
         if ((int)tokens[i] >= m->cfg.vocab || (int)tokens[i] < 0)
             return fail("Token %u out of vocabulary bounds %d", tokens[i], m->cfg.vocab);
-        memcpy(out + (size_t)i * H, m->embedding + (size_t)tokens[i] * H, sizeof(float) * (size_t)H);
+        float* dst = out + (size_t)i * H;
+        if (m->embedding.h) {
+            const uint16_t* src = m->embedding.h + (size_t)tokens[i] * H;
+            for (int j = 0; j < H; ++j) dst[j] = or_bf16_to_f32(src[j]);
+        } else {
+            memcpy(dst, m->embedding.f + (size_t)tokens[i] * H, sizeof(float) * (size_t)H);
+        }
     }
     return 0;
 }
@@ -972,11 +1038,11 @@ static int mlp_block(const or_model* m, const layer_w* Lw, float* hidden, scratc
     if (part_o) memcpy(part_o, w->o, 4 * RH);
     for (size_t i = 0; i < RH; ++i) hidden[i] = hidden[i] + w->o[i];
     if (or_rms_norm(hidden, Lw->mlp_norm, w->normed, rows, H, m->cfg.rms_norm_eps) < 0) return -1;
-    if (or_matmul(w->normed, Lw->w_gate, w->gate, rows, H, F) < 0) return -1;
-    if (or_matmul(w->normed, Lw->w_up, w->up, rows, H, F) < 0) return -1;
+    if (mm(w->normed, Lw->w_gate, w->gate, rows, H, F) < 0) return -1;
+    if (mm(w->normed, Lw->w_up, w->up, rows, H, F) < 0) return -1;
     or_silu(w->gate, w->mlp, (int64_t)rows * F);
     for (size_t i = 0; i < (size_t)rows * F; ++i) w->mlp[i] = w->mlp[i] * w->up[i];
-    if (or_matmul(w->mlp, Lw->w_down, w->down, rows, F, H) < 0) return -1;
+    if (mm(w->mlp, Lw->w_down, w->down, rows, F, H) < 0) return -1;
     if (part_down) memcpy(part_down, w->down, 4 * RH);
     for (size_t i = 0; i < RH; ++i) hidden[i] = hidden[i] + w->down[i];
     return 0;
@@ -1009,9 +1075,9 @@ int or_decode_microbatch(const or_model* m, or_session** sessions, int batch,
     for (int l = 0; rc >= 0 && l < m->cfg.num_layers; ++l) {
         const layer_w* Lw = &m->layers[l];
         rc = or_rms_norm(hidden, Lw->attn_norm, w.normed, batch, H, m->cfg.rms_norm_eps);
-        if (rc >= 0) rc = or_matmul(w.normed, Lw->w_q, w.q, batch, H, Q);
-        if (rc >= 0) rc = or_matmul(w.normed, Lw->w_k, w.k, batch, H, KV);
-        if (rc >= 0) rc = or_matmul(w.normed, Lw->w_v, w.v, batch, H, KV);
+        if (rc >= 0) rc = mm(w.normed, Lw->w_q, w.q, batch, H, Q);
+        if (rc >= 0) rc = mm(w.normed, Lw->w_k, w.k, batch, H, KV);
+        if (rc >= 0) rc = mm(w.normed, Lw->w_v, w.v, batch, H, KV);
         if (rc >= 0) rc = or_apply_rope(w.q, w.qr, batch, Q, positions, d, m->cfg.rope_base);
         if (rc >= 0) rc = or_apply_rope(w.k, w.kr, batch, KV, positions, d, m->cfg.rope_base);
         /* sessions are independent: each one's trim / append / attention
@@ -1041,7 +1107,7 @@ int or_decode_microbatch(const or_model* m, or_session** sessions, int batch,
             }
         }
         if (bad) rc = -1;
-        if (rc >= 0) rc = or_matmul(w.attn, Lw->w_o, w.o, batch, Q, H);
+        if (rc >= 0) rc = mm(w.attn, Lw->w_o, w.o, batch, Q, H);
         if (rc >= 0) {
             float* po = partials ? partials + ((size_t)l * 2 + 0) * (size_t)batch * H : NULL;
             float* pd = partials ? partials + ((size_t)l * 2 + 1) * (size_t)batch * H : NULL;
@@ -1049,7 +1115,7 @@ int or_decode_microbatch(const or_model* m, or_session** sessions, int batch,
         }
     }
     if (rc >= 0) rc = or_rms_norm(hidden, m->final_norm, w.normed, batch, H, m->cfg.rms_norm_eps);
-    if (rc >= 0 && logits) rc = or_matmul(w.normed, m->lm_head, logits, batch, H, m->cfg.vocab);
+    if (rc >= 0 && logits) rc = mm(w.normed, m->lm_head, logits, batch, H, m->cfg.vocab);
     if (rc >= 0)
         for (int b = 0; b < batch; ++b) sessions[b]->position += 1;
     scratch_free(&w);
@@ -1073,9 +1139,9 @@ static int forward_tokens(const or_model* m, or_session* s, const uint32_t* toke
     for (int l = 0; rc >= 0 && l < m->cfg.num_layers; ++l) {
         const layer_w* Lw = &m->layers[l];
         rc = or_rms_norm(hidden, Lw->attn_norm, w.normed, n, H, m->cfg.rms_norm_eps);
-        if (rc >= 0) rc = or_matmul(w.normed, Lw->w_q, w.q, n, H, Q);
-        if (rc >= 0) rc = or_matmul(w.normed, Lw->w_k, w.k, n, H, KV);
-        if (rc >= 0) rc = or_matmul(w.normed, Lw->w_v, w.v, n, H, KV);
+        if (rc >= 0) rc = mm(w.normed, Lw->w_q, w.q, n, H, Q);
+        if (rc >= 0) rc = mm(w.normed, Lw->w_k, w.k, n, H, KV);
+        if (rc >= 0) rc = mm(w.normed, Lw->w_v, w.v, n, H, KV);
         if (rc < 0) break;
         const int cur = s->layers[l].seq_len;
         const int max_seq = s->max_seq_len > 1 ? s->max_seq_len : 1;
@@ -1094,7 +1160,7 @@ static int forward_tokens(const or_model* m, or_session* s, const uint32_t* toke
         if (rc >= 0) rc = or_apply_rope(w.k, w.kr, n, KV, positions, d, m->cfg.rope_base);
         if (rc >= 0) rc = or_session_append_layer(s, l, w.kr, w.v, n);
         if (rc >= 0) rc = session_attention(m, s, l, w.qr, Q, n, prefix, w.attn);
-        if (rc >= 0) rc = or_matmul(w.attn, Lw->w_o, w.o, n, Q, H);
+        if (rc >= 0) rc = mm(w.attn, Lw->w_o, w.o, n, Q, H);
         if (rc >= 0) {
             float* po = partials ? partials + ((size_t)l * 2 + 0) * (size_t)n * H : NULL;
             float* pd = partials ? partials + ((size_t)l * 2 + 1) * (size_t)n * H : NULL;
@@ -1103,7 +1169,7 @@ static int forward_tokens(const or_model* m, or_session* s, const uint32_t* toke
     }
     if (rc >= 0) rc = or_rms_norm(hidden, m->final_norm, w.normed, n, H, m->cfg.rms_norm_eps);
     if (rc >= 0 && logits)
-        rc = or_matmul(w.normed + (size_t)(n - 1) * H, m->lm_head, logits, 1, H, m->cfg.vocab);
+        rc = mm(w.normed + (size_t)(n - 1) * H, m->lm_head, logits, 1, H, m->cfg.vocab);
     scratch_free(&w);
     free(hidden);
     free(positions);

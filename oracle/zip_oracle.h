@@ -125,6 +125,17 @@ int or_model_set_globals(or_model* m, const float* embedding /*[V,H]*/,
 int or_model_set_layer(or_model* m, int layer, const float* w_q, const float* w_k,
                        const float* w_v, const float* w_o, const float* w_gate, const float* w_up,
                        const float* w_down, const float* attn_norm, const float* mlp_norm);
+/* The same model with bf16 bit-pattern weights (bf16 -> f32 is exact, so the
+ * results are bit-identical to the f32 form of the same values); halves the
+ * host memory of full-width models. */
+int or_model_set_globals_bf16(or_model* m, const uint16_t* embedding, const float* final_norm,
+                              const uint16_t* lm_head);
+int or_model_set_layer_bf16(or_model* m, int layer, const uint16_t* w_q, const uint16_t* w_k,
+                            const uint16_t* w_v, const uint16_t* w_o, const uint16_t* w_gate,
+                            const uint16_t* w_up, const uint16_t* w_down, const float* attn_norm,
+                            const float* mlp_norm);
+/* or_matmul with b given as bf16 bit patterns (bit-identical results). */
+int or_matmul_bf16w(const float* a, const uint16_t* b, float* c, int m, int k, int n);
 
 /* ForwardPass::fast_path_decode_microbatch (forward_pass.rs:2143-2319) over B
  * sessions with the same model.  logits [B, V]; partials (nullable)

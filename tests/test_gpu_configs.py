@@ -31,7 +31,10 @@ def _snapshot(pool, layers, rows, kv_cols):
     return KVCacheSnapshot(rows, rows, pool.take((layers, rows, kv_cols)), pool.take((layers, rows, kv_cols)))
 
 
-def _sessions(ctx, pool, layers, kv_cols, ctxlens, max_seq):
+def _sessions(ctx, pool, layers, kv_cols, ctxlens, max_seq, f32_mirror=None):
+    """Device sessions and oracle sessions (bf16 KV rounding) holding the same
+    imported windows; `f32_mirror` (a list) also receives oracle sessions that
+    keep f32 KV, as the reference's CPU provider does (forward_pass.rs:259-262)."""
     dev, ref = [], []
     for L in ctxlens:
         snap = _snapshot(pool, layers, int(L), kv_cols)
@@ -39,9 +42,20 @@ def _sessions(ctx, pool, layers, kv_cols, ctxlens, max_seq):
         b.import_kv_cache(snap)
         s = O.Session(layers, kv_cols, 16, max_seq, kv_round_bf16=True)
         _oracle_import(s, snap)
+        if f32_mirror is not None:
+            s32 = O.Session(layers, kv_cols, 16, max_seq, kv_round_bf16=False)
+            _oracle_import(s32, snap)
+            f32_mirror.append(s32)
         dev.append(b)
         ref.append(s)
     return dev, ref
+
+
+def _drift(got, want32, label):
+    """Logit distance of the bf16-KV device step from the f32-KV oracle."""
+    err = float(np.max(np.abs(got - want32)))
+    print(f"{label}: bf16 KV vs f32-KV oracle max |logit diff| = {err:.3g}", flush=True)
+    return err
 
 
 def test_c2_tinyllama_all_22_layers_decode():
@@ -54,14 +68,52 @@ def test_c2_tinyllama_all_22_layers_decode():
     ctxlens = rng.integers(128, 2049, 32)
     pages = int(sum((L + 2 + 15) // 16 + 1 for L in ctxlens))
     ctx, om = make(cfg, geo, weights, "bf16", True, max_tokens=32, max_seqs=32, pages=pages, pps=140)
-    dev, ref = _sessions(ctx, pool, 22, geo["kv_cols"], ctxlens, 4096)
+    ref32 = []
+    dev, ref = _sessions(ctx, pool, 22, geo["kv_cols"], ctxlens, 4096, f32_mirror=ref32)
     toks = rng.integers(0, cfg["vocab"], 32).tolist()
     for step in range(2):
         reqs = [DecodeMicrobatchRequest(str(i), t, b) for i, (t, b) in enumerate(zip(toks, dev))]
         outs = BackendMicrobatchExecutor.decode_step_batch(reqs, want_logits=True)
+        got = np.stack([o.logits for o in outs])
         want = om.decode(ref, toks)
-        check_logits(np.stack([o.logits for o in outs]), want, f"C2 step {step}")
+        check_logits(got, want, f"C2 step {step}")
+        # the unmodified reference semantics keep the appended rows in f32
+        assert _drift(got, om.decode(ref32, toks), f"C2 step {step}") <= 1e-2
         toks = np.argmax(want, 1).tolist()
+    ctx.close()
+
+
+def test_c2_prefilled_sessions_bf16_kv_drift_from_f32_kv_oracle():
+    """TinyLlama shape, all 22 layers: sessions prefilled through the model, so
+    every cached K / V row is the model's own output, stored as bf16 on the
+    device and as f32 by the f32-KV oracle (the reference's CPU provider,
+    forward_pass.rs:259-262); then decode steps.  Measures the drift that bf16
+    KV storage alone adds against the unmodified semantics."""
+    cfg = dict(hidden=2048, num_heads=32, num_kv_heads=4, num_layers=22, vocab=32000, ffn=5632, rms_norm_eps=1e-5,
+               rope_base=10000.0)
+    geo = geometry(cfg)
+    weights = random_weights(cfg, geo, seed=0xC2 + 1, std=0.02, pooled=True)
+    rng = np.random.default_rng(0xC2 + 1)
+    prompts = [rng.integers(0, cfg["vocab"], n).tolist() for n in (48, 96, 130, 200)]
+    ctx, om = make(cfg, geo, weights, "bf16", True, max_tokens=256, max_seqs=8, pages=128, pps=32)
+    dev = [ctx.new_backend(4096) for _ in prompts]
+    ref = [O.Session(22, geo["kv_cols"], 16, 4096, kv_round_bf16=True) for _ in prompts]
+    ref32 = [O.Session(22, geo["kv_cols"], 16, 4096, kv_round_bf16=False) for _ in prompts]
+    toks, worst = [], 0.0
+    for b, s, s32, p in zip(dev, ref, ref32, prompts):
+        got = b.prefill(p)
+        want = om.prefill(s, p)
+        check_logits(got, want, f"prefill of {len(p)}")
+        worst = max(worst, _drift(got, om.prefill(s32, p), f"prefill of {len(p)} tokens"))
+        toks.append(int(np.argmax(want)))
+    for step in range(4):
+        reqs = [DecodeMicrobatchRequest(str(i), t, b) for i, (t, b) in enumerate(zip(toks, dev))]
+        got = np.stack([o.logits for o in BackendMicrobatchExecutor.decode_step_batch(reqs, want_logits=True)])
+        want = om.decode(ref, toks)
+        check_logits(got, want, f"decode step {step}")
+        worst = max(worst, _drift(got, om.decode(ref32, toks), f"decode step {step}"))
+        toks = np.argmax(want, 1).tolist()
+    assert worst <= 1e-2, worst
     ctx.close()
 
 
@@ -113,7 +165,8 @@ def test_c4_tp_shard_all_32_layers_partials_and_pages():
     pages = int(sum((L + 1 + 15) // 16 + 1 for L in ctxlens))
     ctx, om = make(cfg, geo, weights, "bf16", True, max_tokens=64, max_seqs=64, pages=pages, pps=8192 // 16 + 2)
     kv = geo["kv_cols"]
-    dev, ref = _sessions(ctx, pool, 32, kv, ctxlens, 8192)
+    ref32 = []
+    dev, ref = _sessions(ctx, pool, 32, kv, ctxlens, 8192, f32_mirror=ref32)
     toks = rng.integers(0, cfg["vocab"], 64).tolist()
     parts = np.zeros((32, 2, 64, 4096), np.float32)
     reqs = [DecodeMicrobatchRequest(str(i), t, b) for i, (t, b) in enumerate(zip(toks, dev))]
@@ -121,7 +174,9 @@ def test_c4_tp_shard_all_32_layers_partials_and_pages():
     want, want_parts = om.decode(ref, toks, want_partials=True)
     err = float(np.max(np.abs(parts - want_parts)))
     assert err <= 1e-2, err
-    check_logits(np.stack([o.logits for o in outs]), want, "C4 shard logits")
+    got = np.stack([o.logits for o in outs])
+    check_logits(got, want, "C4 shard logits")
+    assert _drift(got, om.decode(ref32, toks), "C4 shard") <= 1e-2
     for i in (0, 17, 63):  # KV pages: prior rows bit-exact, the appended row within one bf16 step
         snap = dev[i].export_kv_cache()
         for layer in (0, 31):

@@ -71,6 +71,71 @@ def test_stage_rejects_pages_outside_pool():
     ctx.close()
 
 
+# ------------------------------------------------------------------ RoPE --
+@pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("heads,kv_heads,D,base", [(32, 4, 64, 1e4), (32, 8, 128, 5e5)])
+def test_rope_kv_write_rotates_q_and_k_at_large_positions(kv_dtype, heads, kv_heads, D, base):
+    """RoPE + KV append (the RopeKvWrite stage) with the rotation on, against
+    the oracle's apply_rope (tensor_ops.rs:509-560) and the fp64 closed form,
+    at positions 0, 1, 517, 4095 and 8191.  Both sides form theta = f32(pos) *
+    inv_freq[i] in f32 from the same host powf table (runtime.rs:282-301), so
+    only the cos / sin rounding differs from the oracle: 2e-5 of the row's
+    scale.  Against fp64 the f32 theta itself moves by up to pos * 2^-24 rad
+    (the position-scaled bound).  The rotated K rows are read back from their
+    pages, V rows must be copied bit for bit."""
+    positions = [0, 1, 517, 4095, 8191]
+    Q, KV = heads * D, kv_heads * D
+    geo = ModelGeometry(hidden=Q, num_heads=heads, num_kv_heads=kv_heads, num_layers=1, vocab=64, ffn=64,
+                        rope_base=base)
+    ctx = DeviceContext(geo, kv_dtype=kv_dtype, max_tokens=16, max_seqs=8, max_pages_per_seq=8)
+    ctx.create_kv_pool(64)
+    rng = np.random.default_rng(D)
+    backends = []
+    for p in positions:
+        b = ctx.new_backend(8192 + 16)
+        if p:  # a short window ending at position p - 1: the new row lands at p
+            rows = min(p, 5)
+            k = rng.standard_normal((1, rows, KV), dtype=np.float32)
+            from mesh_amd import KVCacheSnapshot
+
+            b.import_kv_cache(KVCacheSnapshot(p, rows, k, k.copy()))
+        backends.append(b)
+    st = stage_mixed(ctx, backends, [1] * len(positions))
+    qkv = rng.standard_normal((len(positions), Q + 2 * KV), dtype=np.float32)
+    d_qkv = DeviceBuffer.from_numpy(ctx, qkv)
+    d_q = DeviceBuffer(ctx, 4 * len(positions) * Q)
+    ctx.check(ctx.lib.zr_rope_kv_write(ctx.h, st, 0, d_qkv.ptr, d_q.ptr, 1))
+    q_dev = d_q.download(np.float32, (len(positions), Q))
+    ctx.lib.zr_staged_destroy(st)
+    pos = np.asarray(positions, np.uint32)
+    want_q = O.apply_rope(qkv[:, :Q], pos, D, base)
+    want_k = O.apply_rope(qkv[:, Q:Q + KV], pos, D, base)
+    k_dev = np.stack([b.export_kv_cache().keys[0, -1] for b in backends])
+    v_dev = np.stack([b.export_kv_cache().values[0, -1] for b in backends])
+    np.testing.assert_array_equal(q_dev[0], qkv[0, :Q])  # position 0 is the identity
+    for r in range(len(positions)):
+        scale = float(np.abs(qkv[r]).max())
+        assert np.max(np.abs(q_dev[r] - want_q[r])) <= 2e-5 * scale, (positions[r], "q")
+        if kv_dtype == "f32":
+            assert np.max(np.abs(k_dev[r] - want_k[r])) <= 2e-5 * scale, (positions[r], "k")
+            np.testing.assert_array_equal(v_dev[r], qkv[r, Q + KV:])
+        else:  # the pool rounds to bf16: within one bf16 step (2^-7 relative) of the oracle's rounded row
+            wk = O.round_bf16(want_k[r])
+            assert np.all(np.abs(k_dev[r] - wk) <= 2.0 ** -7 * np.abs(wk) + 2e-5 * scale), (positions[r], "k")
+            np.testing.assert_array_equal(v_dev[r], O.round_bf16(qkv[r, Q + KV:]))
+        # the fp64 closed form, rotate-half pairing per head
+        half = D // 2
+        inv = 1.0 / (np.float64(base) ** (np.arange(half) * 2.0 / D))
+        th = positions[r] * inv
+        for h in range(heads):
+            a = qkv[r, h * D:h * D + half].astype(np.float64)
+            bb = qkv[r, h * D + half:(h + 1) * D].astype(np.float64)
+            ref = np.concatenate([a * np.cos(th) - bb * np.sin(th), a * np.sin(th) + bb * np.cos(th)])
+            bound = (3e-6 + 4e-7 * positions[r] * 8) * scale
+            assert np.max(np.abs(q_dev[r, h * D:(h + 1) * D] - ref)) <= bound, (positions[r], h)
+    ctx.close()
+
+
 # ------------------------------------------------ C1: attention + append --
 def c1_inputs(seed=0xC1):
     rng = np.random.default_rng(seed)
@@ -396,7 +461,8 @@ def test_argmax_first_index_on_ties_and_large_vocab():
 
 
 # -------------------------------- the benchmarked launch: 256 sessions --
-def test_c5_shape_attention_256_sessions_matches_oracle():
+@pytest.mark.parametrize("rope", [0, 1])
+def test_c5_shape_attention_256_sessions_matches_oracle(rope):
     # The attention launch of the 256-session decode benchmark: Llama-3-8B
     # attention shape (32 q heads, 8 kv heads, head_dim 128), bf16 pool, the
     # benchmark's lognormal contexts (seed 0xC5: median 1024, sigma 1, clipped
@@ -407,7 +473,7 @@ def test_c5_shape_attention_256_sessions_matches_oracle():
     ctxlens = np.clip(np.round(np.random.default_rng(0xC5).lognormal(math.log(1024), 1.0, 256)), 64,
                       8192).astype(np.int64)
     B, H, KVC, D = 256, 4096, 1024, 128
-    geo = ModelGeometry(hidden=H, num_heads=32, num_kv_heads=8, num_layers=1, vocab=64, ffn=64)
+    geo = ModelGeometry(hidden=H, num_heads=32, num_kv_heads=8, num_layers=1, vocab=64, ffn=64, rope_base=500000.0)
     ctx = DeviceContext(geo, kv_dtype="bf16", max_tokens=B, max_seqs=B, max_pages_per_seq=520)
     ctx.create_kv_pool(int(((ctxlens + 15) // 16).sum()) + B)
     rng = np.random.default_rng(0xA5)
@@ -424,11 +490,16 @@ def test_c5_shape_attention_256_sessions_matches_oracle():
     d_qkv = DeviceBuffer.from_numpy(ctx, qkv)
     d_q = DeviceBuffer(ctx, 4 * B * H)
     d_o = DeviceBuffer(ctx, 4 * B * H)
-    ctx.check(ctx.lib.zr_rope_kv_write(ctx.h, st, 0, d_qkv.ptr, d_q.ptr, 0))
+    ctx.check(ctx.lib.zr_rope_kv_write(ctx.h, st, 0, d_qkv.ptr, d_q.ptr, rope))
     ctx.check(ctx.lib.zr_attention(ctx.h, st, 0, d_q.ptr, d_o.ptr))
     out = d_o.download(np.float32, (B, H))
     ctx.lib.zr_staged_destroy(st)
     assert np.isfinite(out).all()
+    if rope:  # the new row of session s sits at position L - 1 (rope base 500000)
+        pos = (ctxlens - 1).astype(np.uint32)
+        qkv = qkv.copy()
+        qkv[:, :H] = O.apply_rope(qkv[:, :H], pos, D, 500000.0)
+        qkv[:, H:H + KVC] = O.apply_rope(qkv[:, H:H + KVC], pos, D, 500000.0)
     sample = sorted({int(np.argmax(ctxlens)), int(np.argmin(ctxlens))} |
                     {int(x) for x in np.random.default_rng(7).choice(B, 6, replace=False)})
     for s in sample:

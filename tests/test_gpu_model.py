@@ -343,3 +343,75 @@ def test_pool_exhaustion_reports_oom_and_keeps_state():
     assert e.value.status == -2
     assert b.sequence_position() == 48 and b.cache_seq_len() == 48
     ctx.close()
+
+
+def test_device_fed_token_out_of_vocabulary_is_an_error():
+    """Ids fed from device memory (zr_forward_staged_async) are checked on the
+    device: the first bad one is reported by zr_synchronize with the
+    reference's embed_tokens message (tensor_ops.rs:482-490), the same text
+    the oracle gives, and a later step with valid ids succeeds."""
+    import ctypes as C
+
+    from mesh_amd import DeviceBuffer
+    from tests.gpu_util import stage_mixed
+
+    cfg = SMALL
+    geo = geometry(cfg)
+    weights = random_weights(cfg, geo, seed=3, std=0.05)
+    ctx, om = make(cfg, geo, weights, "bf16", True)
+    dev = [ctx.new_backend() for _ in range(4)]
+    for b in dev:
+        b.prefill([1, 2, 3])
+    bad = np.array([5, 7, cfg["vocab"] + 9, cfg["vocab"] + 1], np.uint32)
+    st = stage_mixed(ctx, dev, [1] * 4)
+    d_tok, d_out = DeviceBuffer.from_numpy(ctx, bad), DeviceBuffer(ctx, 16)
+    assert ctx.lib.zr_forward_staged_async(ctx.h, st, d_tok.ptr, d_out.ptr, None) == 0
+    rc = ctx.lib.zr_synchronize(ctx.h)
+    msg = ctx.lib.zr_last_error(ctx.h).decode()
+    assert rc == -1 and msg == f"Token {cfg['vocab'] + 9} out of vocabulary bounds {cfg['vocab']}", msg
+    s = O.Session(cfg["num_layers"], geo["kv_cols"])
+    om.prefill(s, [1, 2, 3])
+    with pytest.raises(O.OracleError) as e:
+        om.decode([s], [cfg["vocab"] + 9])
+    assert str(e.value) == msg
+    ctx.lib.zr_staged_destroy(st)
+    # the error was reported once; valid device ids run clean
+    st = stage_mixed(ctx, dev, [1] * 4)
+    d_tok.upload(np.array([5, 7, 9, 11], np.uint32))
+    ctx.check(ctx.lib.zr_forward_staged_async(ctx.h, st, d_tok.ptr, d_out.ptr, None))
+    ctx.check(ctx.lib.zr_synchronize(ctx.h))
+    assert d_out.download(np.uint32, 4).max() < cfg["vocab"]
+    ctx.lib.zr_staged_destroy(st)
+    ctx.close()
+
+
+@pytest.mark.parametrize("cap,batches", [(8, [8]), (40, [20, 24, 40])])
+def test_split_k_workspace_covers_every_row_count(cap, batches):
+    """TinyLlama layer shape (hidden 2048, FFN 5632, vocab 32000) with the
+    microbatch capacity at 8 and 40 rows: the split-K workspace is sized for
+    every row count up to the capacity (the LM head's split plan at 8, 20, 24
+    and 40 rows needs more than any smaller count), so full batches run and
+    match the oracle."""
+    cfg = dict(hidden=2048, num_heads=32, num_kv_heads=4, num_layers=1, vocab=32000, ffn=5632, rms_norm_eps=1e-5,
+               rope_base=10000.0)
+    geo = geometry(cfg)
+    weights = random_weights(cfg, geo, seed=0x5E, std=0.02)
+    ctx, om = make(cfg, geo, weights, "bf16", True, max_tokens=cap, max_seqs=cap, pages=512, pps=16)
+    rng = np.random.default_rng(cap)
+    for n in batches:
+        dev = [ctx.new_backend() for _ in range(n)]
+        ref = [O.Session(1, geo["kv_cols"], kv_round_bf16=True) for _ in range(n)]
+        for b, s in zip(dev, ref):
+            L = int(rng.integers(1, 60))
+            k = O.round_bf16(rng.standard_normal((1, L, geo["kv_cols"]), dtype=np.float32))
+            v = O.round_bf16(rng.standard_normal((1, L, geo["kv_cols"]), dtype=np.float32))
+            snap = KVCacheSnapshot(L, L, k, v)
+            b.import_kv_cache(snap)
+            _oracle_import(s, snap)
+        toks = rng.integers(0, cfg["vocab"], n).tolist()
+        reqs = [DecodeMicrobatchRequest(str(i), t, b) for i, (t, b) in enumerate(zip(toks, dev))]
+        outs = BackendMicrobatchExecutor.decode_step_batch(reqs, want_logits=True)
+        check_logits(np.stack([o.logits for o in outs]), om.decode(ref, toks), f"{n} rows of capacity {cap}")
+        for b in dev:
+            b.close()
+    ctx.close()

@@ -406,3 +406,51 @@ def test_chunked_prefill_equals_single_prefill():
     last = m.prefill_chunk(s, toks[13:])
     np.testing.assert_allclose(last, whole, rtol=0, atol=1e-5)
     assert s.position == len(toks)
+
+
+def test_bf16_weight_model_is_bit_identical_to_f32_model():
+    """The oracle's bf16-weight form (used for full-width models) computes the
+    same f32 products as the f32 form of the same values: logits, partials and
+    KV rows must be bit-identical, not merely close."""
+    from tests.testmodels import geometry, oracle_cfg, random_weights
+
+    cfg = dict(hidden=256, num_heads=4, num_kv_heads=2, num_layers=2, vocab=300, ffn=320, rms_norm_eps=1e-5,
+               rope_base=10000.0)
+    geo = geometry(cfg)
+    w32 = random_weights(cfg, geo, seed=5, std=0.05)
+    mats = ("w_q", "w_k", "w_v", "w_o", "w_gate", "w_up", "w_down")
+    w16 = dict(embedding=O.to_bf16_bits(w32["embedding"]), final_norm=w32["final_norm"],
+               lm_head=O.to_bf16_bits(w32["lm_head"]),
+               layers=[dict({k: O.to_bf16_bits(lw[k]) for k in mats}, attn_norm=lw["attn_norm"],
+                            mlp_norm=lw["mlp_norm"]) for lw in w32["layers"]])
+    m32, m16 = O.Model(oracle_cfg(cfg, geo), w32), O.Model(oracle_cfg(cfg, geo), w16)
+    assert m16.bf16 and not m32.bf16
+    rng = np.random.default_rng(9)
+    prompts = [rng.integers(0, cfg["vocab"], n).tolist() for n in (3, 17, 40)]
+    s32 = [O.Session(2, geo["kv_cols"]) for _ in prompts]
+    s16 = [O.Session(2, geo["kv_cols"]) for _ in prompts]
+    for a, b, p in zip(s32, s16, prompts):
+        np.testing.assert_array_equal(m32.prefill(a, p), m16.prefill(b, p))
+    toks = [1, 2, 3]
+    for _ in range(3):
+        l32, p32 = m32.decode(s32, toks, want_partials=True)
+        l16, p16 = m16.decode(s16, toks, want_partials=True)
+        np.testing.assert_array_equal(l32, l16)
+        np.testing.assert_array_equal(p32, p16)
+        toks = np.argmax(l32, 1).tolist()
+    for a, b in zip(s32, s16):
+        for layer in range(2):
+            for x, y in zip(a.gather(layer), b.gather(layer)):
+                np.testing.assert_array_equal(x, y)
+    # the matmul itself, against the f32 form and against fp64
+    a = rng.standard_normal((19, 300), dtype=np.float32)
+    w = O.round_bf16(rng.standard_normal((300, 517), dtype=np.float32))
+    wb = O.to_bf16_bits(w)
+    out = np.empty((19, 517), np.float32)
+    L = O.lib()
+    import ctypes as C
+    rc = L.or_matmul_bf16w(a.ctypes.data_as(C.POINTER(C.c_float)), wb.ctypes.data_as(C.POINTER(C.c_uint16)),
+                           out.ctypes.data_as(C.POINTER(C.c_float)), 19, 300, 517)
+    assert rc == 0
+    np.testing.assert_array_equal(out, O.matmul(a, w))
+    np.testing.assert_allclose(out, a.astype(np.float64) @ w.astype(np.float64), rtol=0, atol=2e-4)
