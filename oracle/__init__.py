@@ -59,6 +59,8 @@ def lib():
         L.or_model_set_layer_bf16.argtypes = [C.c_void_p, C.c_int] + [u16p] * 7 + [f32p] * 2
         L.or_matmul_bf16w.argtypes = [f32p, u16p, f32p, C.c_int, C.c_int, C.c_int]
         L.or_decode_microbatch.argtypes = [C.c_void_p, C.POINTER(C.c_void_p), C.c_int, u32p, f32p, f32p]
+        L.or_decode_microbatch_forced.argtypes = [C.c_void_p, C.POINTER(C.c_void_p), C.c_int, u32p, f32p, f32p,
+                                                  f32p, f32p, f32p, f32p]
         L.or_prefill.argtypes = [C.c_void_p, C.c_void_p, u32p, C.c_int, f32p]
         L.or_prefill_chunk.argtypes = [C.c_void_p, C.c_void_p, u32p, C.c_int, f32p, f32p]
         L.or_matmul.argtypes = [f32p, f32p, f32p, C.c_int, C.c_int, C.c_int]
@@ -418,6 +420,24 @@ class Model:
         _check(lib().or_decode_microbatch(self.h, arr, B, _u(toks), _f(logits),
                                           _f(parts) if parts is not None else None))
         return (logits, parts) if want_partials else logits
+
+    def decode_forced(self, sessions, tokens, force_k, force_v):
+        """decode() with the appended K / V rows taken from force_k / force_v
+        [num_layers, B, kv_cols] (rows another implementation stored as
+        bf16).  Returns (logits, own_k, own_v): own_* are this oracle's own
+        f32 rows of the step, before rounding, in the same shape."""
+        B = len(sessions)
+        toks = np.ascontiguousarray(tokens, np.uint32)
+        fk, fv = f32(force_k), f32(force_v)
+        L, KV = self.cfg["num_layers"], fk.shape[-1]
+        if fk.shape != (L, B, KV) or fv.shape != (L, B, KV):
+            raise ValueError(f"forced rows must be [{L}, {B}, kv_cols], got {fk.shape} / {fv.shape}")
+        logits = np.zeros((B, self.cfg["vocab"]), np.float32)
+        own_k, own_v = np.zeros_like(fk), np.zeros_like(fv)
+        arr = (C.c_void_p * B)(*[s.h for s in sessions])
+        _check(lib().or_decode_microbatch_forced(self.h, arr, B, _u(toks), _f(logits), None, _f(fk), _f(fv),
+                                                 _f(own_k), _f(own_v)))
+        return logits, own_k, own_v
 
     def prefill(self, session, tokens):
         toks = np.ascontiguousarray(tokens, np.uint32)

@@ -886,9 +886,7 @@ int or_matmul_bf16w(const float* a, const uint16_t* b, float* c, int m, int k, i
     return 0;
 }
 
-static int mm(const float* a, wmat b, float* c, int m, int k, int n) {
-    return b.h ? or_matmul_bf16w(a, b.h, c, m, k, n) : or_matmul(a, b.f, c, m, k, n);
-}
+
 
 or_model* or_model_new(const or_model_config* cfg) {
     or_shard_layout lay;
@@ -911,6 +909,10 @@ void or_model_free(or_model* m) {
     free(m->kv_idx);
     free(m->layers);
     free(m);
+}
+
+static int mm(const float* a, wmat b, float* c, int rows, int k, int n) {
+    return b.h ? or_matmul_bf16w(a, b.h, c, rows, k, n) : or_matmul(a, b.f, c, rows, k, n);
 }
 
 int or_model_set_globals(or_model* m, const float* embedding, const float* final_norm,
@@ -1048,10 +1050,27 @@ static int mlp_block(const or_model* m, const layer_w* Lw, float* hidden, scratc
     return 0;
 }
 
+static int decode_microbatch(const or_model* m, or_session** sessions, int batch, const uint32_t* tokens,
+                             float* logits, float* partials, const float* force_k, const float* force_v,
+                             float* own_k, float* own_v);
+
 /* ForwardPass::fast_path_decode_microbatch (2143-2319) with
  * attention_output_device_batch_from_backends (2612-2740). */
 int or_decode_microbatch(const or_model* m, or_session** sessions, int batch,
                          const uint32_t* tokens, float* logits, float* partials) {
+    return decode_microbatch(m, sessions, batch, tokens, logits, partials, NULL, NULL, NULL, NULL);
+}
+
+int or_decode_microbatch_forced(const or_model* m, or_session** sessions, int batch, const uint32_t* tokens,
+                                float* logits, float* partials, const float* force_k, const float* force_v,
+                                float* own_k, float* own_v) {
+    if (!force_k || !force_v) return fail("forced decode needs the stored K and V rows");
+    return decode_microbatch(m, sessions, batch, tokens, logits, partials, force_k, force_v, own_k, own_v);
+}
+
+static int decode_microbatch(const or_model* m, or_session** sessions, int batch, const uint32_t* tokens,
+                             float* logits, float* partials, const float* force_k, const float* force_v,
+                             float* own_k, float* own_v) {
     if (batch <= 0) return fail("Decode microbatch requires at least one backend and token");
     const int H = m->cfg.hidden, Q = m->lay.q_cols, KV = m->lay.kv_cols, d = m->lay.head_dim;
     uint32_t* positions = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)batch);
@@ -1098,8 +1117,19 @@ int or_decode_microbatch(const or_model* m, or_session** sessions, int batch,
                 if (src >= 0 && (int)positions[b] != s->base_position + prefix)
                     src = fail("Non-contiguous attention positions: expected %d, got %u",
                                s->base_position + prefix, positions[b]);
-                if (src >= 0)
-                    src = or_session_append_layer(s, l, w.kr + (size_t)b * KV, w.v + (size_t)b * KV, 1);
+                const float* kr = w.kr + (size_t)b * KV;
+                const float* vr = w.v + (size_t)b * KV;
+                if (force_k) {
+                    /* the row another implementation stored is appended in
+                     * place of this oracle's own, which is handed back (f32,
+                     * before any bf16 rounding) for the caller to judge */
+                    const size_t o = ((size_t)l * batch + b) * KV;
+                    if (own_k) memcpy(own_k + o, kr, sizeof(float) * (size_t)KV);
+                    if (own_v) memcpy(own_v + o, vr, sizeof(float) * (size_t)KV);
+                    kr = force_k + o;
+                    vr = force_v + o;
+                }
+                if (src >= 0) src = or_session_append_layer(s, l, kr, vr, 1);
                 if (src >= 0)
                     src = session_attention(m, s, l, w.qr + (size_t)b * Q, Q, 1, prefix,
                                             w.attn + (size_t)b * Q);

@@ -137,6 +137,7 @@ int or_model_set_layer_bf16(or_model* m, int layer, const uint16_t* w_q, const u
 /* or_matmul with b given as bf16 bit patterns (bit-identical results). */
 int or_matmul_bf16w(const float* a, const uint16_t* b, float* c, int m, int k, int n);
 
+
 /* ForwardPass::fast_path_decode_microbatch (forward_pass.rs:2143-2319) over B
  * sessions with the same model.  logits [B, V]; partials (nullable)
  * [num_layers][2][B][H] = (o_partial, down_partial) per layer; hidden_out
@@ -145,6 +146,17 @@ int or_decode_microbatch(const or_model* m, or_session** sessions, int batch,
                          const uint32_t* tokens, float* logits, float* partials);
 /* ForwardPass::prefill (2089-2112): clears the cache, keeps the last window.
  * logits [V] of the last row. */
+/* The same step with the appended K / V row of every (layer, session) taken
+ * from force_k / force_v [num_layers][B][kv_cols]: the rows another
+ * implementation stored after rounding its own f32 values to bf16.  Two
+ * correct f32 evaluations can round a near-tie element to neighbouring bf16
+ * values; forcing the stored rows lets the rest of the step be compared
+ * without that rounding flip.  own_k / own_v (nullable, same shape) receive
+ * this oracle's own f32 rows (before rounding), so the caller can check that
+ * every forced element is a valid rounding of a value within f32 noise. */
+int or_decode_microbatch_forced(const or_model* m, or_session** sessions, int batch, const uint32_t* tokens,
+                                float* logits, float* partials, const float* force_k, const float* force_v,
+                                float* own_k, float* own_v);
 int or_prefill(const or_model* m, or_session* s, const uint32_t* tokens, int n_tokens,
                float* logits);
 /* Chunked prefill at the session's current position (forward_tokens 2456-2528

@@ -21,8 +21,17 @@ only those sessions.
   (its restored window must equal the evicted snapshot bit for bit), and the
   pool's page accounting.
 
-Bars: logits within 1e-2 absolute, greedy ids equal where the oracle's top-2
-margin exceeds 1e-3, the appended KV row within one bf16 rounding step.
+The row a step appends is rounded from f32 to bf16 by both the device and
+the oracle, each from its own f32 value; where that value sits near a bf16
+rounding tie the two can store neighbouring bf16 values (a 2^-8 relative
+jump), and 32 layers amplify such flips to ~1e-2 in the logits.  So each
+check first requires every element the device stored to be within one bf16
+step of the oracle's own rounding of its f32 value, then runs the oracle
+with the device's stored rows (Model.decode_forced) and compares the step's
+logits.  The unforced oracle's distance is printed for the record.
+
+Bars: appended K / V elements within one bf16 step, logits within 1e-2
+absolute, greedy ids equal where the oracle's top-2 margin exceeds 1e-3.
 """
 import math
 import time
@@ -74,15 +83,28 @@ def _oracle_session(g, snap, max_seq):
     return s
 
 
-def _check_appended_rows(snaps, sessions):
-    """The row each step appended: the oracle rounds its f32 K / V to bf16 as
-    the device does; the f32 inputs differ by GEMM rounding, so the stored
-    rows may differ by one bf16 step."""
-    for snap, s in zip(snaps, sessions):
-        for layer in (0, snap.keys.shape[0] - 1):
-            k, v = s.gather(layer)
-            assert np.all(np.abs(snap.keys[layer, -1] - k[-1]) <= 8e-3 * np.abs(k[-1]) + 2e-3)
-            assert np.all(np.abs(snap.values[layer, -1] - v[-1]) <= 8e-3 * np.abs(v[-1]) + 2e-3)
+def _forced_step(g, om, snaps, tokens, max_seq, label):
+    """The oracle's step over the exported sessions with the device's appended
+    rows forced.  Every element the device stored must be a bf16 rounding of
+    a value within f32 noise of the oracle's own: |stored - own| <= 2^-8 |own|
+    (half a bf16 step of the value) + 2 noise, with the noise at 1e-3 of the
+    row's largest element (the step's own f32 drift from layer to layer stays
+    far below it; a wrong row is off by O(1)).  Returns the forced logits, the
+    unforced oracle's logits and the number of elements whose rounding
+    differs from the oracle's."""
+    force_k = np.stack([snap.keys[:, -1] for snap in snaps], axis=1)
+    force_v = np.stack([snap.values[:, -1] for snap in snaps], axis=1)
+    want, own_k, own_v = om.decode_forced([_oracle_session(g, s, max_seq) for s in snaps], tokens, force_k,
+                                          force_v)
+    flips = 0
+    for stored, own in ((force_k, own_k), (force_v, own_v)):
+        noise = 1e-3 * np.abs(own).max(axis=-1, keepdims=True)
+        bound = 2.0 ** -8 * np.abs(own) + 2 * noise
+        excess = np.abs(stored - own) - bound
+        assert excess.max() <= 0, f"{label}: a stored K / V element is {excess.max():.3g} beyond a valid rounding"
+        flips += int((stored != O.round_bf16(own)).sum())
+    free = om.decode([_oracle_session(g, s, max_seq) for s in snaps], tokens)
+    return want, free, flips
 
 
 def test_benchmarked_256_session_step_matches_oracle_on_sampled_sessions(llama3):
@@ -109,14 +131,15 @@ def test_benchmarked_256_session_step_matches_oracle_on_sampled_sessions(llama3)
         while len(sample) < 16:
             sample = sorted(set(sample) | {int(np.random.default_rng(len(sample)).integers(B))})
         snaps = [b.backends[i].export_kv_cache() for i in sample]
-        for i, snap in zip(sample, snaps):
-            assert snap.cached_tokens == int(ctxlens[i]) + 1 and snap.next_position == int(ctxlens[i]) + 1
-        ref = [_oracle_session(g, snap, b.max_seq) for snap in snaps]
-        want = om.decode(ref, tokens[sample])
+        for i, snap in zip(sample, snaps):  # an 8192-row window drops its oldest row on the append
+            assert snap.next_position == int(ctxlens[i]) + 1
+            assert snap.cached_tokens == min(int(ctxlens[i]) + 1, b.max_seq)
+        want, free, flipped = _forced_step(g, om, snaps, tokens[sample], b.max_seq, "benchmarked step")
         _progress(f"oracle decoded {len(sample)} sampled sessions (contexts {sorted(int(ctxlens[i]) for i in sample)})")
         err = check_logits(logits[sample], want, "benchmarked step")
-        print(f"benchmarked step: max |logit - oracle| = {err:.3g} over {len(sample)} sessions", flush=True)
-        _check_appended_rows(snaps, ref)
+        print(f"benchmarked step: max |logit - oracle| = {err:.3g} over {len(sample)} sessions; "
+              f"{flipped} of {2 * want.shape[0] * g.num_layers * g.kv_cols} appended K / V elements round the other way; "
+              f"unforced oracle distance {float(np.max(np.abs(logits[sample] - free))):.3g}", flush=True)
     finally:
         b.close()
 
@@ -163,17 +186,17 @@ def test_c5_kv_pressure_soak_full_llama3_width(llama3):
                 assert snap.cached_tokens == rows + 1 and snap.next_position == nxt + 1, sid
                 assert digest(snap.keys[:, :rows]) == hk and digest(snap.values[:, :rows]) == hv, sid
                 checked["restored"] += 1
-        ref = [_oracle_session(g, snap, max_seq) for snap in snaps]
-        want = om.decode(ref, [sessions[i].token for i in idx])
-        err = check_logits(logits[idx], want, f"soak step {checked['steps']}")
+        label = f"soak step {checked['steps']}"
+        want, free, flipped = _forced_step(g, om, snaps, [sessions[i].token for i in idx], max_seq, label)
+        err = check_logits(logits[idx], want, label)
         ok = np.sort(want, 1)
         ok = (ok[:, -1] - ok[:, -2]) > 1e-3
         np.testing.assert_array_equal(np.asarray(toks_out)[idx][ok], np.argmax(want, 1)[ok])
-        _check_appended_rows(snaps, ref)
         checked["rows"] += len(idx)
         checked["steps"] += 1
         _progress(f"soak step {checked['steps']}: {len(sessions)} active, checked {len(idx)} "
-                  f"({len(restored)} restored), max err {err:.3g}")
+                  f"({len(restored)} restored), max err {err:.3g}, {flipped} rounding flips, "
+                  f"unforced {float(np.max(np.abs(logits[idx] - free))):.3g}")
 
     soak = KvPressureSoak(ctx, max_sessions=soak_cfg["max_sessions"], join_rate=soak_cfg["join_rate"],
                           leave_prob=soak_cfg["leave_prob"], retention=soak_cfg["retention"], max_seq_len=max_seq,

@@ -454,3 +454,46 @@ def test_bf16_weight_model_is_bit_identical_to_f32_model():
     assert rc == 0
     np.testing.assert_array_equal(out, O.matmul(a, w))
     np.testing.assert_allclose(out, a.astype(np.float64) @ w.astype(np.float64), rtol=0, atol=2e-4)
+
+
+def test_forced_kv_decode_reproduces_the_step_and_returns_its_own_rows():
+    """decode_forced appends given bf16 rows instead of its own: forced with
+    the rows the oracle itself stores (its bf16-rounded K / V), the step is
+    bit-identical to decode(), and the f32 rows it hands back round to exactly
+    those rows; a forced row moved by one bf16 step changes that session's
+    logits only."""
+    from tests.testmodels import geometry, oracle_cfg, random_weights
+
+    cfg = dict(hidden=256, num_heads=4, num_kv_heads=2, num_layers=2, vocab=300, ffn=320, rms_norm_eps=1e-5,
+               rope_base=10000.0)
+    geo = geometry(cfg)
+    m = O.Model(oracle_cfg(cfg, geo), random_weights(cfg, geo, seed=6, std=0.05))
+    rng = np.random.default_rng(4)
+    prompts = [rng.integers(0, cfg["vocab"], n).tolist() for n in (5, 18, 33)]
+
+    def sessions():
+        out = []
+        for p in prompts:
+            s = O.Session(2, geo["kv_cols"], kv_round_bf16=True)
+            m.prefill(s, p)
+            out.append(s)
+        return out
+
+    toks = [3, 1, 4]
+    a = sessions()
+    want = m.decode(a, toks)
+    rows = np.stack([np.stack([s.gather(l)[i][-1] for s in a]) for l in range(2) for i in range(2)])
+    fk, fv = rows[0::2], rows[1::2]  # [layers, B, kv_cols]
+    got, own_k, own_v = m.decode_forced(sessions(), toks, fk, fv)
+    np.testing.assert_array_equal(got, want)
+    np.testing.assert_array_equal(O.round_bf16(own_k), fk)
+    np.testing.assert_array_equal(O.round_bf16(own_v), fv)
+    assert not np.array_equal(own_k, fk)  # the own rows are the f32 values before rounding
+    fk2 = fk.copy()
+    bits = O.to_bf16_bits(fk2[1, 2, :7])
+    fk2[1, 2, :7] = O.bf16_bits_to_f32((bits + 1).astype(np.uint16))  # one bf16 step away from zero
+    got2, _, _ = m.decode_forced(sessions(), toks, fk2, fv)
+    np.testing.assert_array_equal(got2[:2], want[:2])
+    assert not np.array_equal(got2[2], want[2])
+    with pytest.raises(ValueError):
+        m.decode_forced(sessions(), toks, fk[:, :2], fv)
