@@ -208,6 +208,17 @@ zr_status zr_kv_read_pages(zr_context* ctx, int layer, const int* pages, int n_p
 /* Greedy argmax over rows of a device [rows, cols] f32 matrix (first index on
  * ties; runtime.rs:561-570). */
 zr_status zr_argmax(zr_context* ctx, const float* d_x, int rows, int cols, uint32_t* d_out);
+/* zr_argmax without allocation.  No counterpart in the reference: for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * fixed-footprint serving loops, harnesses that forbid hipMalloc).  The
+ * argmax partials go to a fixed 256 KiB device array of the library (each GPU
+ * holds its own copy for the life of the process) instead of the context's
+ * workspace, so rows * ceil(cols / 4096) <= 32768 (e.g. 256 rows of 128256
+ * logits use 8192); larger inputs return ZR_E_INVALID.  Enqueued on the
+ * context stream without synchronising (d_out is ready after
+ * zr_synchronize).  Every call on one GPU shares that array: calls that
+ * overlap on one GPU (other contexts' streams) race. */
+zr_status zr_argmax_noalloc(zr_context* ctx, const float* d_x, int rows, int cols, uint32_t* d_out);
 /* Stochastic sampling of device logits [rows, cols] f32, per row with its own
  * temperature, top_p and seed (host arrays): sample_tokens_device_with_seeds
  * (runtime.rs:534-601) as the batched decode path groups it

@@ -90,6 +90,7 @@ SIGNATURES = [
                                     C.c_void_p, C.c_size_t, C.POINTER(C.c_size_t)]),
     ("zr_kv_read_pages", C.c_int, [C.c_void_p, C.c_int, c_int_p, C.c_int, C.c_void_p]),
     ("zr_argmax", C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
+    ("zr_argmax_noalloc", C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
     ("zr_sample", C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, c_f32_p, c_f32_p, C.POINTER(C.c_uint64),
                             C.c_void_p]),
     ("zr_sample_last_logits", C.c_int, [C.c_void_p, C.c_int, c_f32_p, c_f32_p, C.POINTER(C.c_uint64), c_u32_p]),

@@ -558,6 +558,14 @@ zr_status zr_context_create(const zr_model_desc* desc, int device, zr_context** 
         inv[i] = 1.0f / powf(d.rope_base, (float)i * 2.0f / (float)ctx->head_dim);
     e = hipMemcpy(ctx->inv_freq, inv.data(), inv.size() * 4, hipMemcpyHostToDevice);
     if (e != hipSuccess) return fail(e, "hipMemcpy inv_freq");
+    if (zr_status src = noalloc_scratch_init(ctx)) {
+        const std::string why = ctx->err;
+        set_global_err(src, "%s", why.c_str());
+        free_ctx_buffers(ctx);
+        if (ctx->stream) hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return src;
+    }
     e = hipHostMalloc((void**)&ctx->h_token_err, sizeof(unsigned long long), hipHostMallocDefault);
     if (e != hipSuccess) return fail(e, "hipHostMalloc token check word");
     *ctx->h_token_err = ~0ull;
@@ -898,6 +906,12 @@ zr_status zr_argmax(zr_context* ctx, const float* d_x, int rows, int cols, uint3
     zr_status rc = launch_argmax(ctx, d_x, rows, cols, d_out);
     if (!rc) ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
     return rc;
+}
+
+zr_status zr_argmax_noalloc(zr_context* ctx, const float* d_x, int rows, int cols, uint32_t* d_out) {
+    if (!ctx || !d_x || !d_out) return set_global_err(ZR_E_INVALID, "null argument");
+    if (rows <= 0 || cols <= 0) return set_err(ctx, ZR_E_INVALID, "Device sampling received an empty logits tensor");
+    return launch_argmax_noalloc(ctx, d_x, rows, cols, d_out);
 }
 
 zr_status zr_sample(zr_context* ctx, const float* d_logits, int rows, int cols, const float* temperature,

@@ -1,4 +1,6 @@
 // Embedding gather, RMSNorm with a fused residual add, and greedy argmax.
+#include <mutex>
+
 #include "zr_internal.h"
 
 namespace zr {
@@ -314,6 +316,45 @@ static zr_status argmax_into(zr_context* ctx, const float* x, int rows, int cols
 
 zr_status launch_argmax(zr_context* ctx, const float* x, int rows, int cols, uint32_t* out) {
     return argmax_into(ctx, x, rows, cols, out, ctx->argmax_ws, ctx->argmax_ws_floats);
+}
+
+// ----------------------------------------------- argmax without allocation
+// The partials of zr_argmax_noalloc live in this fixed array of the library
+// (each device holds its own copy for the life of the process).  Host code
+// never passes `scratch` itself to a kernel: its device address is resolved
+// once per device with hipGetSymbolAddress (noalloc_scratch_init, called by
+// zr_context_create with the device current) and kept in g_scratch_dev.
+static __device__ __align__(256) float scratch[2 * kNoAllocArgmaxPairs];
+
+static std::mutex g_scratch_mu;
+static float* g_scratch_dev[kMaxDevices];
+
+zr_status noalloc_scratch_init(zr_context* ctx) {
+    if (ctx->device < 0 || ctx->device >= kMaxDevices)
+        return set_err(ctx, ZR_E_UNSUPPORTED, "device %d beyond the %d devices the library tracks", ctx->device,
+                       kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[ctx->device]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return set_err(ctx, ZR_E_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", ctx->device,
+                           hipGetErrorString(e));
+        g_scratch_dev[ctx->device] = (float*)p;
+    }
+    ctx->noalloc_scratch = g_scratch_dev[ctx->device];
+    return ZR_OK;
+}
+
+zr_status launch_argmax_noalloc(zr_context* ctx, const float* x, int rows, int cols, uint32_t* out) {
+    if (!ctx->noalloc_scratch) return set_err(ctx, ZR_E_INVARIANT, "argmax scratch not resolved for this device");
+    const size_t pairs = (size_t)rows * (size_t)((cols + kArgmaxChunk - 1) / kArgmaxChunk);
+    if (pairs > (size_t)kNoAllocArgmaxPairs)
+        return set_err(ctx, ZR_E_INVALID,
+                       "zr_argmax_noalloc: %d rows x %d columns need %zu partials; the fixed scratch holds %d "
+                       "(rows x ceil(cols / %d) <= %d)",
+                       rows, cols, pairs, kNoAllocArgmaxPairs, kArgmaxChunk, kNoAllocArgmaxPairs);
+    return argmax_into(ctx, x, rows, cols, out, ctx->noalloc_scratch, 2 * (size_t)kNoAllocArgmaxPairs);
 }
 
 }  // namespace zr

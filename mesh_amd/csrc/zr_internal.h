@@ -167,6 +167,7 @@ struct zr_context {
     unsigned long long* d_token_err = nullptr;
     unsigned long long* h_token_err = nullptr;
     bool token_check_pending = false;
+    float* noalloc_scratch = nullptr;  // device address of the library's fixed argmax scratch on this device
     zr::TimingState timing;
 };
 
@@ -272,6 +273,12 @@ zr_status launch_kv_copy(zr_context* ctx, int layer_begin, int layer_end, const 
                          int first_offset, int first_row, int n_rows, float* k, float* v,
                          int to_pool);
 zr_status launch_argmax(zr_context* ctx, const float* x, int rows, int cols, uint32_t* out);
+// The same with the partials in the library's fixed device array (no
+// allocation; rows x ceil(cols / 4096) <= kNoAllocArgmaxPairs).
+constexpr int kNoAllocArgmaxPairs = 32768;
+constexpr int kMaxDevices = 64;
+zr_status noalloc_scratch_init(zr_context* ctx);
+zr_status launch_argmax_noalloc(zr_context* ctx, const float* x, int rows, int cols, uint32_t* out);
 // sample_tokens_device_with_seeds per row (sample.hip); parameters are host arrays
 zr_status launch_sample(zr_context* ctx, const float* d_logits, int rows, int cols, const float* temperature,
                         const float* top_p, const uint64_t* seeds, uint32_t* d_out);
