@@ -15,7 +15,7 @@ device ahead of time.  Each step feeds its greedy tokens to the next step on
 the device.  The attention kernel's duration comes from HIP events recorded on
 the provider's stream around every attention launch in the timed region.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--skip-bs32]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--skip-bs32] [--skip-soak]
        python bench.py --calibrate-copy   (a plain 1 GiB device copy, for scaling
                                            rocprofv3 FETCH_SIZE / WRITE_SIZE)
 """
@@ -163,7 +163,7 @@ class GpuDecodeBench:
     `model` = (DeviceContext, ModelGeometry) reuses a model built by
     device_model (its KV pool is replaced; the caller keeps the context)."""
 
-    def __init__(self, name, steps_total, split=True, model=None):
+    def __init__(self, name, steps_total, split=True, model=None, host_steps=0):
         from mesh_amd import _lib
 
         self._lib = _lib
@@ -176,8 +176,10 @@ class GpuDecodeBench:
         self.ctx, self.geo = device_model(name, split) if model is None else model
         ctx, lib, g = self.ctx, self.ctx.lib, self.geo
         V = g.vocab
-        # KV pool: every session's context plus the benchmarked steps
-        pages = int(sum((min(int(L) + steps_total, self.max_seq) + 15) // 16 + 1 for L in self.ctxlens))
+        # KV pool: every session's context plus the benchmarked steps (staged
+        # ahead, and `host_steps` more run through the host entry point)
+        grow = steps_total + host_steps
+        pages = int(sum((min(int(L) + grow, self.max_seq) + 15) // 16 + 1 for L in self.ctxlens))
         ctx.create_kv_pool(pages)
         ctx.check(lib.zr_kv_pool_fill_normal(ctx.h, 4242, 1.0))
         self.backends = [ctx.new_backend(self.max_seq) for _ in range(self.B)]
@@ -220,6 +222,24 @@ class GpuDecodeBench:
             ctx.check(lib.zr_timing_end(ctx.h, ms, n))
         return dt, list(ms), list(n)
 
+    def run_host(self, count, tokens):
+        """`count` decode steps through zrh_decode_step_batch, the boundary's
+        host entry point (host page tables, zr_stage with its H2D copy, the
+        packing kernel, the forward pass, the token D2H), each step fed the
+        previous step's greedy tokens.  Returns (seconds, last tokens)."""
+        ctx, lib = self.ctx, self.ctx.lib
+        arr = (C.c_void_p * self.B)(*[b.h for b in self.backends])
+        ptrs = C.cast(arr, C.POINTER(C.c_void_p))
+        u32 = C.POINTER(C.c_uint32)
+        toks = np.ascontiguousarray(tokens, np.uint32)
+        out = np.zeros(self.B, np.uint32)
+        t0 = time.perf_counter()
+        for _ in range(count):
+            ctx.check(lib.zrh_decode_step_batch(ptrs, self.B, toks.ctypes.data_as(u32), out.ctypes.data_as(u32),
+                                                None, None))
+            toks, out = out, toks
+        return time.perf_counter() - t0, toks
+
     def tokens(self, i):
         out = np.zeros(self.B, np.uint32)
         self.ctx.check(self.ctx.lib.zr_memcpy_d2h(self.ctx.h, out.ctypes.data, self.tok[i % 2], out.nbytes))
@@ -246,8 +266,10 @@ BREAKDOWN_STEPS = 2
 def measure(name, steps, warmup):
     """Timed region: `steps` decode steps with HIP events around the attention
     launches only (the roofline figure).  Then BREAKDOWN_STEPS more steps with
-    events around every kernel class, for the per-class time split."""
-    bench = GpuDecodeBench(name, steps + warmup + BREAKDOWN_STEPS)
+    events around every kernel class, for the per-class time split.  Then the
+    same sessions decode `warmup` + `steps` more steps through the host entry
+    point (zrh_decode_step_batch), timed end to end with the host work."""
+    bench = GpuDecodeBench(name, steps + warmup + BREAKDOWN_STEPS, host_steps=steps + warmup)
     g, B = bench.geo, bench.B
     bench.run(0, warmup, timed=False)
     dt, ms_t, n_t = bench.run(warmup, steps, timed=True, mask=1)
@@ -283,6 +305,15 @@ def measure(name, steps, warmup):
                   weight_gbs=(gemm_flops(g, B) / B) * nb / (ms_b[1] * 1e-3) / 1e9 if ms_b[1] > 0 else 0.0),
     )
     result["kv_append"] = measure_kv_append(bench)
+    # end to end through the boundary's host entry point, host work included
+    _, last = bench.run_host(warmup, bench.tokens(warmup + steps + BREAKDOWN_STEPS))
+    dt_host, last = bench.run_host(steps, last)
+    assert last.max() < g.vocab
+    result["host_path"] = dict(
+        entry="zrh_decode_step_batch", steps=steps, ms_per_step=dt_host / steps * 1e3,
+        tokens_per_s=B * steps / dt_host,
+        includes="host page tables and window trim, zr_stage (metadata H2D), pack_kernel, the forward pass, "
+                 "greedy token D2H and the stream synchronisation, per step")
     bench.close()
     return result
 
@@ -697,7 +728,7 @@ def main():
     ap.add_argument("--skip-bs32", action="store_true")
     ap.add_argument("--workload", default="llama3_8b_b256", choices=sorted(WORKLOADS))
     ap.add_argument("--calibrate-copy", action="store_true")
-    ap.add_argument("--soak", action="store_true", help="also run the KV-pressure soak leg")
+    ap.add_argument("--skip-soak", action="store_true", help="skip the KV-pressure soak leg")
     ap.add_argument("--skip-kv-snapshot", action="store_true", help="skip the KV snapshot wire-format leg")
     ap.add_argument("--skip-sampling", action="store_true", help="skip the device sampling leg")
     ap.add_argument("--skip-mixed", action="store_true", help="skip the mixed prefill + decode microbatch leg")
@@ -726,8 +757,9 @@ def main():
         bs32 = dict(value=r["tokens_per_s"], unit="tokens/s", ms_per_step=r["ms_per_step"],
                     workload=r["workload"], step_roofline_frac=r["step_roofline_frac"],
                     attention_gbs=r["attention"]["achieved_gbs"], kernel_ms_per_step=r["kernel_ms_per_step"],
-                    gemm_tflops=r["gemm"]["achieved_tflops"], gemm_weight_gbs=r["gemm"]["weight_gbs"])
-    soak = measure_soak(max(4, a.steps // 2), 2) if a.soak else None
+                    gemm_tflops=r["gemm"]["achieved_tflops"], gemm_weight_gbs=r["gemm"]["weight_gbs"],
+                    host_path=r["host_path"])
+    soak = None if a.skip_soak else measure_soak(max(4, a.steps // 2), 2)
     kv_snapshot = None if a.skip_kv_snapshot else measure_kv_snapshot()
     sampling = None if a.skip_sampling else measure_sampling()
     mixed = None if a.skip_mixed else measure_mixed()
@@ -750,6 +782,7 @@ def main():
         "step_roofline": {"tokens_per_s": main_r["step_roofline_tokens_per_s"], "frac": main_r["step_roofline_frac"],
                           "bytes_per_step": main_r["step_bytes"]},
         "kernel_ms_per_step": main_r["kernel_ms_per_step"],
+        "host_path": main_r["host_path"],
         "kv_append": main_r["kv_append"],
         "gemm_mfma": {"achieved": main_r["gemm"]["achieved_tflops"], "peak": MFMA_BF16_PEAK_TFLOPS,
                       "unit": "TFLOP/s", "frac": main_r["gemm"]["frac"], "mfma_ops_per_flop": 2,

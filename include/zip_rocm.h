@@ -259,6 +259,34 @@ zr_status zr_fill_normal_bf16(zr_context* ctx, uint16_t* d_dst, size_t n, uint64
 /* Fills every page of the KV pool with N(0, std) values in the pool dtype. */
 zr_status zr_kv_pool_fill_normal(zr_context* ctx, uint64_t seed, float std);
 
+/* ------------------------------------------------------------ contract --- */
+/* The rocm arm of LocalExecutorContract::for_provider (engine.rs:171-273;
+ * fields of LocalExecutorContract 159-169, ExecutorPhasePlan 141-148,
+ * KvRuntimeContract 150-156) and of BackendContractDescriptor::for_provider
+ * (provider/mod.rs:88-150), as snake_case strings the reference serialises
+ * (engine.rs:102-139).  stage_kernels[i] lists, comma-separated, the kernels
+ * of this library that implement fused_stages[i].  All strings are static. */
+typedef struct {
+    const char* executor_class;          /* "fast_path" (LocalExecutorClass) */
+    const char* optimization_profile;    /* "rocm_fused" (BackendOptimizationProfile) */
+    int n_host_kernels;
+    const char* const* host_kernels;     /* HostKernel */
+    int n_fused_stages;
+    const char* const* fused_stages;     /* FusedKernelStage, contract order */
+    const char* const* stage_kernels;
+    const char* collective_residency;    /* "staged_runtime" */
+    int prefill_supports_microbatch, prefill_requires_static_workspace, prefill_uses_device_sampling;
+    int decode_supports_microbatch, decode_requires_static_workspace, decode_uses_device_sampling;
+    int kv_requires_paged_cache, kv_append_only_decode, kv_supports_prefill, kv_supports_decode;
+    int collective_tensors_per_layer;
+    const char* provider;                /* "rocm" (ExecutionProviderKind) */
+    const char* compatibility_class;     /* "rocm_fast_path" (ProviderCompatibilityClass) */
+    const char* memory_model;            /* "discrete_vram" (MemoryModel) */
+    int supports_decode_microbatch, supports_paged_kv, supports_checkpoint_handoff, supports_device_sampling;
+    int fast_path_eligible;
+} zr_executor_contract;
+zr_status zr_get_executor_contract(zr_executor_contract* out);
+
 /* ---------------------------------------------------------- profiling --- */
 /* Per-kernel-class timing with HIP events on the context stream (enabled
  * between begin/end) around the launches of the classes set in class_mask

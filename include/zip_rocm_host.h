@@ -111,6 +111,52 @@ void zrh_clear(zrh_backend* b);
  * back to the pool; the session restarts empty at position 0. */
 zr_status zrh_release_pages(zrh_backend* b);
 
+/* ------------------------------------------------------ fast-path planner --- */
+/* FastPathBackendContext (fast_path.rs:102-108) of one session, as
+ * ProviderRuntimeCore::fast_path_context builds it (backend.rs:748-755).  The
+ * provider ("rocm") and profile ("rocm_fused") are the contract's
+ * (zr_get_executor_contract); the model id is the caller's. */
+typedef struct {
+    int logical_kv_tokens;     /* ForwardPass::logical_kv_tokens */
+    int position;              /* next absolute position (DecodeSlotState.position) */
+    int cached_tokens;         /* rows in the live window (DecodeSlotState::sequence_len) */
+    int decode_token_ceiling;  /* FastPathPlanner::decode_token_ceiling_for_context (676-683); -1: none */
+} zrh_fast_path_context;
+zr_status zrh_get_fast_path_context(const zrh_backend* b, zrh_fast_path_context* out);
+
+/* FastPathPlanner::plan_decode (fast_path.rs:644-669) for the rocm_fused
+ * profile: the first bucket of DECODE_BUCKET_BATCHES x DECODE_BUCKET_KV_TOKENS
+ * (15-16) that holds batch_size and total_kv_tokens, with the metadata layout
+ * of metadata_fields (839-867): four u32 fields back to back,
+ * slot_sequence_lengths[B], slot_positions[B], slot_block_tables[B][page_slots]
+ * and slot_mapping[B] (B = batch_size_ceiling, page_slots =
+ * ceil(token_ceiling / 16)), and workspace_requirements (869-890) with the
+ * fused-profile constants.  A batch no bucket holds is ZR_E_UNSUPPORTED with
+ * FastPathInvariantError::UnsupportedBucket's text (146-157); the 256-session
+ * step is such a batch and runs without a plan (backend.rs:116-126). */
+typedef struct {
+    int batch_size_ceiling, token_ceiling;
+    int actual_batch_size, actual_token_count, max_sequence_len;
+    int page_slots;
+    size_t field_offset[4], field_bytes[4]; /* the four metadata fields, in order */
+    size_t metadata_bytes;
+    size_t workspace_bytes, workspace_alignment;
+    char bucket_label[64];                  /* "decode-b{B}-kv{T}-rocm" */
+} zrh_fast_path_plan;
+zr_status zrh_fast_path_plan_decode(int batch_size, int total_kv_tokens, int max_sequence_len,
+                                    zrh_fast_path_plan* out);
+
+/* DecodeWorkspaceLease::stage (fast_path.rs:263-338) over the slot states of
+ * n sessions (DeviceKVCache::decode_slot_state, forward_pass.rs:1065-1074):
+ * resets `metadata` (plan->metadata_bytes) and writes the sequence lengths,
+ * positions, live block tables (session page ids; unused slots u32::MAX) and
+ * slot indices (unused slots u32::MAX); token_ids / positions (nullable,
+ * batch_size_ceiling words each) receive the lease's token and position
+ * buffers (zero beyond n).  Errors carry the CaptureUnsafe texts (158-164). */
+zr_status zrh_fast_path_stage_decode(const zrh_fast_path_plan* plan, zrh_backend* const* backends, int n,
+                                     const uint32_t* tokens, uint32_t* metadata, uint32_t* token_ids,
+                                     uint32_t* positions);
+
 /* Page-table state machine without compute, for allocator checks:
  * DeviceKVCache::append_layer over all layers (rows appended, window trim
  * included) and DeviceKVCache::retain_suffix. */

@@ -5,10 +5,11 @@ include/zip_rocm.h); this package is its Python mirror of zip's provider
 interface (mesh_amd.provider).
 """
 from .provider import (BackendMicrobatchExecutor, DecodeMicrobatchOutput, DecodeMicrobatchRequest,
-                       DeviceBuffer, DeviceContext, ExecutionProviderKind, KVCacheBlob, KVCacheSnapshot,
-                       KVCacheWireSnapshot, KVSequenceState, ModelGeometry, RocmExecutionBackend, bf16_bits,
-                       device_info, probe_provider)
+                       DeviceBuffer, DeviceContext, ExecutionProviderKind, FastPathPlanner, KVCacheBlob,
+                       KVCacheSnapshot, KVCacheWireSnapshot, KVSequenceState, ModelGeometry, RocmExecutionBackend,
+                       bf16_bits, device_info, executor_contract, probe_provider)
 
 __all__ = ["BackendMicrobatchExecutor", "DecodeMicrobatchOutput", "DecodeMicrobatchRequest", "DeviceBuffer",
-           "DeviceContext", "ExecutionProviderKind", "KVCacheBlob", "KVCacheSnapshot", "KVCacheWireSnapshot",
-           "KVSequenceState", "ModelGeometry", "RocmExecutionBackend", "bf16_bits", "device_info", "probe_provider"]
+           "DeviceContext", "ExecutionProviderKind", "FastPathPlanner", "KVCacheBlob", "KVCacheSnapshot",
+           "KVCacheWireSnapshot", "KVSequenceState", "ModelGeometry", "RocmExecutionBackend", "bf16_bits",
+           "device_info", "executor_contract", "probe_provider"]

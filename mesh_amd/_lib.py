@@ -62,6 +62,36 @@ class Microbatch(C.Structure):
                 ("block_table_stride", C.c_int), ("tokens", c_u32_p)]
 
 
+class ExecutorContract(C.Structure):
+    _fields_ = [("executor_class", C.c_char_p), ("optimization_profile", C.c_char_p),
+                ("n_host_kernels", C.c_int), ("host_kernels", C.POINTER(C.c_char_p)),
+                ("n_fused_stages", C.c_int), ("fused_stages", C.POINTER(C.c_char_p)),
+                ("stage_kernels", C.POINTER(C.c_char_p)), ("collective_residency", C.c_char_p),
+                ("prefill_supports_microbatch", C.c_int), ("prefill_requires_static_workspace", C.c_int),
+                ("prefill_uses_device_sampling", C.c_int), ("decode_supports_microbatch", C.c_int),
+                ("decode_requires_static_workspace", C.c_int), ("decode_uses_device_sampling", C.c_int),
+                ("kv_requires_paged_cache", C.c_int), ("kv_append_only_decode", C.c_int),
+                ("kv_supports_prefill", C.c_int), ("kv_supports_decode", C.c_int),
+                ("collective_tensors_per_layer", C.c_int), ("provider", C.c_char_p),
+                ("compatibility_class", C.c_char_p), ("memory_model", C.c_char_p),
+                ("supports_decode_microbatch", C.c_int), ("supports_paged_kv", C.c_int),
+                ("supports_checkpoint_handoff", C.c_int), ("supports_device_sampling", C.c_int),
+                ("fast_path_eligible", C.c_int)]
+
+
+class FastPathContext(C.Structure):
+    _fields_ = [("logical_kv_tokens", C.c_int), ("position", C.c_int), ("cached_tokens", C.c_int),
+                ("decode_token_ceiling", C.c_int)]
+
+
+class FastPathPlan(C.Structure):
+    _fields_ = [("batch_size_ceiling", C.c_int), ("token_ceiling", C.c_int), ("actual_batch_size", C.c_int),
+                ("actual_token_count", C.c_int), ("max_sequence_len", C.c_int), ("page_slots", C.c_int),
+                ("field_offset", C.c_size_t * 4), ("field_bytes", C.c_size_t * 4), ("metadata_bytes", C.c_size_t),
+                ("workspace_bytes", C.c_size_t), ("workspace_alignment", C.c_size_t),
+                ("bucket_label", C.c_char * 64)]
+
+
 # (name, restype, argtypes) for every exported symbol declared in include/*.h
 SIGNATURES = [
     # zip_rocm.h
@@ -104,6 +134,7 @@ SIGNATURES = [
     ("zr_memcpy_d2h", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]),
     ("zr_fill_normal_bf16", C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_uint64, C.c_float]),
     ("zr_kv_pool_fill_normal", C.c_int, [C.c_void_p, C.c_uint64, C.c_float]),
+    ("zr_get_executor_contract", C.c_int, [C.POINTER(ExecutorContract)]),
     ("zr_timing_begin", C.c_int, [C.c_void_p, C.c_uint]),
     ("zr_timing_end", C.c_int, [C.c_void_p, C.POINTER(C.c_double), c_int_p]),
     # zip_rocm_host.h
@@ -133,6 +164,10 @@ SIGNATURES = [
     ("zrh_import_kv_cbor", C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_int]),
     ("zrh_clear", None, [C.c_void_p]),
     ("zrh_release_pages", C.c_int, [C.c_void_p]),
+    ("zrh_get_fast_path_context", C.c_int, [C.c_void_p, C.POINTER(FastPathContext)]),
+    ("zrh_fast_path_plan_decode", C.c_int, [C.c_int, C.c_int, C.c_int, C.POINTER(FastPathPlan)]),
+    ("zrh_fast_path_stage_decode", C.c_int, [C.POINTER(FastPathPlan), c_void_pp, C.c_int, c_u32_p, c_u32_p,
+                                             c_u32_p, c_u32_p]),
     ("zrh_kv_reserve", C.c_int, [C.c_void_p, C.c_int]),
     ("zrh_retain_suffix", C.c_int, [C.c_void_p, C.c_int]),
 ]

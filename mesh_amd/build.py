@@ -17,7 +17,7 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libzip_rocm.so")
 
-SOURCES = ["api.cpp", "pack_kv.hip", "attention.hip", "norm_sample.hip", "gemm.hip", "kv_cbor.hip", "sample.hip", "provider.cpp"]
+SOURCES = ["api.cpp", "pack_kv.hip", "attention.hip", "norm_sample.hip", "gemm.hip", "kv_cbor.hip", "sample.hip", "provider.cpp", "contract.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc" if os.path.exists("/opt/rocm/bin/hipcc") else "hipcc")
 # Packed FP32 instructions are disabled for every device pass.

@@ -1,6 +1,7 @@
 // Host-side rocm execution backend (include/zip_rocm_host.h): the session page
 // tables, positions and microbatch assembly that the reference keeps in its
 // Rust provider host (forward_pass.rs:303-1243, 2089-2319; backend.rs:110-151).
+#include <stdio.h>
 #include <string.h>
 
 #include <algorithm>
@@ -686,6 +687,112 @@ zr_status zrh_release_pages(zrh_backend* b) {
         if (p.global >= 0) b->pool->free_list.push_back(p.global);
     b->kv = SessionKV();
     b->position = 0;
+    return ZR_OK;
+}
+
+// ------------------------------------------------------------ fast path
+// Buckets of fast_path.rs:15-16 (decode), in the planner's search order.
+static const int kDecodeBucketBatches[] = {1, 2, 4, 8};
+static const int kDecodeBucketKvTokens[] = {2048, 8192, 16384, 32768, 65536};
+
+zr_status zrh_get_fast_path_context(const zrh_backend* b, zrh_fast_path_context* out) {
+    if (!b || !out) return set_global_err(ZR_E_INVALID, "null argument");
+    out->logical_kv_tokens = b->position - b->kv.base_position;
+    out->position = b->position;
+    out->cached_tokens = b->kv.seq_len;
+    out->decode_token_ceiling = -1;
+    for (int t : kDecodeBucketKvTokens)
+        if (out->logical_kv_tokens <= t) {
+            out->decode_token_ceiling = t;
+            break;
+        }
+    return ZR_OK;
+}
+
+zr_status zrh_fast_path_plan_decode(int batch_size, int total_kv_tokens, int max_sequence_len,
+                                    zrh_fast_path_plan* out) {
+    if (!out) return set_global_err(ZR_E_INVALID, "null argument");
+    if (batch_size < 0 || total_kv_tokens < 0 || max_sequence_len < 0)
+        return set_global_err(ZR_E_INVALID, "negative batch size or token count");
+    memset(out, 0, sizeof *out);
+    int bb = -1, bt = -1;
+    for (int b : kDecodeBucketBatches) {
+        for (int t : kDecodeBucketKvTokens)
+            if (batch_size <= b && total_kv_tokens <= t) {
+                bb = b;
+                bt = t;
+                break;
+            }
+        if (bb >= 0) break;
+    }
+    if (bb < 0)
+        return set_global_err(ZR_E_UNSUPPORTED, "no stable Decode bucket supports batch_size=%d token_count=%d for RocmFused",
+                              batch_size, total_kv_tokens);
+    out->batch_size_ceiling = bb;
+    out->token_ceiling = bt;
+    out->actual_batch_size = batch_size;
+    out->actual_token_count = total_kv_tokens;
+    out->max_sequence_len = max_sequence_len;
+    out->page_slots = (bt + kPageRows - 1) / kPageRows;
+    const size_t widths[4] = {(size_t)bb, (size_t)bb, (size_t)bb * out->page_slots, (size_t)bb};
+    size_t off = 0;
+    for (int f = 0; f < 4; ++f) {
+        out->field_offset[f] = off;
+        out->field_bytes[f] = widths[f] * sizeof(uint32_t);
+        off += out->field_bytes[f];
+    }
+    out->metadata_bytes = off;
+    // workspace_requirements: the fused profile's 96 B per token and 32 KiB per slot
+    out->workspace_bytes = off + (size_t)bt * 96 + (size_t)bb * 32 * 1024;
+    out->workspace_alignment = 256;
+    snprintf(out->bucket_label, sizeof out->bucket_label, "decode-b%d-kv%d-rocm", bb, bt);
+    return ZR_OK;
+}
+
+zr_status zrh_fast_path_stage_decode(const zrh_fast_path_plan* plan, zrh_backend* const* backends, int n,
+                                     const uint32_t* tokens, uint32_t* metadata, uint32_t* token_ids,
+                                     uint32_t* positions) {
+    if (!plan || !metadata || (n > 0 && (!backends || !tokens))) return set_global_err(ZR_E_INVALID, "null argument");
+    const int B = plan->batch_size_ceiling, slots = plan->page_slots;
+    zr_context* ctx = n > 0 && backends[0] ? backends[0]->ctx : nullptr;
+    if (n > B)
+        return set_err(ctx, ZR_E_INVALID, "fast-path capture invariant failed for %s: runtime batch size %d exceeds bucket ceiling %d",
+                       plan->bucket_label, n, B);
+    // reset (DecodeWorkspaceBuffers::reset): lengths and positions 0, tables and mapping u32::MAX
+    uint32_t* seq_lens = metadata + plan->field_offset[0] / 4;
+    uint32_t* slot_pos = metadata + plan->field_offset[1] / 4;
+    uint32_t* tables = metadata + plan->field_offset[2] / 4;
+    uint32_t* mapping = metadata + plan->field_offset[3] / 4;
+    std::fill(seq_lens, seq_lens + B, 0u);
+    std::fill(slot_pos, slot_pos + B, 0u);
+    std::fill(tables, tables + (size_t)B * slots, 0xFFFFFFFFu);
+    std::fill(mapping, mapping + B, 0xFFFFFFFFu);
+    if (token_ids) std::fill(token_ids, token_ids + B, 0u);
+    if (positions) std::fill(positions, positions + B, 0u);
+    if (token_ids) std::copy(tokens, tokens + n, token_ids);
+    for (int i = 0; i < n; ++i) {
+        const zrh_backend* b = backends[i];
+        if (!b) return set_global_err(ZR_E_INVALID, "null backend in slot %d", i);
+        // decode_slot_state (forward_pass.rs:1065-1074)
+        if (b->kv.base_position + b->kv.seq_len != b->position)
+            return set_err(b->ctx, ZR_E_INVARIANT, "Forward pass position %d diverged from KV cache next position %d",
+                           b->position, b->kv.base_position + b->kv.seq_len);
+        const int seq = b->kv.seq_len;
+        if (seq > plan->token_ceiling)
+            return set_err(b->ctx, ZR_E_INVALID,
+                           "fast-path capture invariant failed for %s: slot %d sequence length %d exceeds bucket token ceiling %d",
+                           plan->bucket_label, i, seq, plan->token_ceiling);
+        if ((int)b->kv.spans.size() > slots)
+            return set_err(b->ctx, ZR_E_INVALID,
+                           "fast-path capture invariant failed for %s: slot %d block table length %d exceeds workspace capacity %d",
+                           plan->bucket_label, i, (int)b->kv.spans.size(), slots);
+        if (positions) positions[i] = (uint32_t)b->position;
+        seq_lens[i] = (uint32_t)seq;
+        slot_pos[i] = (uint32_t)b->position;
+        mapping[i] = (uint32_t)i;
+        for (size_t p = 0; p < b->kv.spans.size(); ++p)
+            tables[(size_t)i * slots + p] = (uint32_t)b->kv.spans[p].page_index;
+    }
     return ZR_OK;
 }
 

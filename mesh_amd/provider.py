@@ -50,6 +50,55 @@ FUSED_KERNEL_STAGES = {
 }
 
 
+def executor_contract() -> dict:
+    """LocalExecutorContract + BackendContractDescriptor of the rocm arm
+    (engine.rs:171-273, provider/mod.rs:88-150) as the library reports it
+    (zr_get_executor_contract); "stage_kernels" maps each fused stage to the
+    kernels that implement it."""
+    lib = _lib.load()
+    c = _lib.ExecutorContract()
+    check(lib.zr_get_executor_contract(C.byref(c)))
+    out = {name: getattr(c, name) for name, _ in _lib.ExecutorContract._fields_
+           if not name.startswith("n_") and name not in ("host_kernels", "fused_stages", "stage_kernels")}
+    out = {k: (v.decode() if isinstance(v, bytes) else v) for k, v in out.items()}
+    out["host_kernels"] = [c.host_kernels[i].decode() for i in range(c.n_host_kernels)]
+    out["fused_stages"] = [c.fused_stages[i].decode() for i in range(c.n_fused_stages)]
+    out["stage_kernels"] = {c.fused_stages[i].decode(): c.stage_kernels[i].decode().split(",")
+                            for i in range(c.n_fused_stages)}
+    return out
+
+
+class FastPathPlanner:
+    """FastPathPlanner (fast_path.rs:604-890) for the rocm_fused profile and the
+    DecodeWorkspaceLease staging (263-338), through the C-ABI."""
+
+    @staticmethod
+    def plan_decode(batch_size: int, total_kv_tokens: int, max_sequence_len: int) -> "_lib.FastPathPlan":
+        plan = _lib.FastPathPlan()
+        check(_lib.load().zrh_fast_path_plan_decode(batch_size, total_kv_tokens, max_sequence_len, C.byref(plan)))
+        return plan
+
+    @staticmethod
+    def stage_decode(plan, backends: Sequence["RocmExecutionBackend"], tokens: Sequence[int]) -> dict:
+        lib = _lib.load()
+        B = plan.batch_size_ceiling
+        meta = np.zeros(plan.metadata_bytes // 4, np.uint32)
+        token_ids = np.zeros(B, np.uint32)
+        positions = np.zeros(B, np.uint32)
+        toks = np.ascontiguousarray(tokens, np.uint32)
+        arr = (C.c_void_p * max(len(backends), 1))(*[b.h for b in backends])
+        ctx = getattr(getattr(backends[0], "ctx", None), "h", None) if backends else None
+        check(lib.zrh_fast_path_stage_decode(C.byref(plan), C.cast(arr, C.POINTER(C.c_void_p)), len(backends),
+                                             _ptr(toks, C.c_uint32), _ptr(meta, C.c_uint32),
+                                             _ptr(token_ids, C.c_uint32), _ptr(positions, C.c_uint32)), ctx)
+        names = ("slot_sequence_lengths", "slot_positions", "slot_block_tables", "slot_mapping")
+        out = {"token_ids": token_ids, "positions": positions}
+        for f, name in enumerate(names):
+            o, n = plan.field_offset[f] // 4, plan.field_bytes[f] // 4
+            out[name] = meta[o:o + n]
+        return out
+
+
 def probe_provider(device: int = 0):
     """runtime.rs:335-385: (available, error message)."""
     try:
@@ -378,6 +427,15 @@ class RocmExecutionBackend:
         if temperature <= 0.0 or (temperature == 1.0 and top_p >= 1.0):
             return self.last_greedy
         return sample_device(self.ctx, np.asarray(logits, np.float32)[None], [temperature], [top_p], [seed])[0]
+
+    def fast_path_context(self) -> dict:
+        """FastPathBackendContext (fast_path.rs:102-108, backend.rs:748-755)."""
+        c = _lib.FastPathContext()
+        self.ctx.check(self.lib.zrh_get_fast_path_context(self.h, C.byref(c)))
+        return {"provider": ExecutionProviderKind.ROCM.value, "optimization_profile": self.optimization_profile,
+                "logical_kv_tokens": c.logical_kv_tokens, "position": c.position,
+                "cached_tokens": c.cached_tokens,
+                "decode_token_ceiling": None if c.decode_token_ceiling < 0 else c.decode_token_ceiling}
 
     def cache_seq_len(self) -> int:
         return self.lib.zrh_cache_seq_len(self.h)

@@ -453,3 +453,58 @@ class Model:
         _check(lib().or_prefill_chunk(self.h, session.h, _u(toks), toks.size, _f(logits),
                                       _f(parts) if parts is not None else None))
         return (logits, parts) if want_partials else logits
+
+
+# ------------------------------------------------------- fast-path planner --
+# FastPathPlanner / DecodeWorkspaceLease restated in Python (the planner is
+# host bookkeeping): agent/src/inference/fast_path.rs.
+DECODE_BUCKET_BATCHES = (1, 2, 4, 8)                         # fast_path.rs:15
+DECODE_BUCKET_KV_TOKENS = (2048, 8192, 16384, 32768, 65536)  # fast_path.rs:16
+U32_MAX = 0xFFFFFFFF
+
+
+def fast_path_plan_decode(batch_size, total_kv_tokens, profile="RocmFused"):
+    """FastPathPlanner::plan_decode (fast_path.rs:644-669): the first bucket of
+    supported_decode_buckets (batch outer, kv tokens inner; 606-623) holding
+    the batch, and the metadata layout of metadata_fields (839-867): field
+    name -> (element count, stride bytes) with u32 elements."""
+    for b in DECODE_BUCKET_BATCHES:
+        for t in DECODE_BUCKET_KV_TOKENS:
+            if batch_size <= b and total_kv_tokens <= t:
+                slots = -(-t // 16)
+                fields = [("slot_sequence_lengths", b), ("slot_positions", b), ("slot_block_tables", b * slots),
+                          ("slot_mapping", b)]
+                return dict(batch_size_ceiling=b, token_ceiling=t, page_slots=slots,
+                            fields=[(name, n, 4 * n) for name, n in fields],
+                            bucket_label=f"decode-b{b}-kv{t}-rocm")
+    raise OracleError(f"no stable Decode bucket supports batch_size={batch_size} token_count={total_kv_tokens} "
+                      f"for {profile}")
+
+
+def fast_path_stage_decode(plan, tokens, slots):
+    """DecodeWorkspaceLease::stage_with_slot_reader (fast_path.rs:263-338) after
+    DecodeWorkspaceBuffers::reset (227-235).  slots: (position, sequence_len,
+    page_ids) per slot, the DecodeSlotState of each session.  Returns the
+    token / position buffers and the four metadata fields."""
+    B, T, S = plan["batch_size_ceiling"], plan["token_ceiling"], plan["page_slots"]
+    label = plan["bucket_label"]
+    if len(tokens) > B:
+        raise OracleError(f"fast-path capture invariant failed for {label}: runtime batch size {len(tokens)} "
+                          f"exceeds bucket ceiling {B}")
+    out = dict(token_ids=np.zeros(B, np.uint32), positions=np.zeros(B, np.uint32),
+               slot_sequence_lengths=np.zeros(B, np.uint32), slot_positions=np.zeros(B, np.uint32),
+               slot_block_tables=np.full(B * S, U32_MAX, np.uint32), slot_mapping=np.full(B, U32_MAX, np.uint32))
+    out["token_ids"][:len(tokens)] = tokens
+    for i, (position, seq_len, page_ids) in enumerate(slots[:len(tokens)]):
+        if seq_len > T:
+            raise OracleError(f"fast-path capture invariant failed for {label}: slot {i} sequence length {seq_len} "
+                              f"exceeds bucket token ceiling {T}")
+        if len(page_ids) > S:
+            raise OracleError(f"fast-path capture invariant failed for {label}: slot {i} block table length "
+                              f"{len(page_ids)} exceeds workspace capacity {S}")
+        out["positions"][i] = position
+        out["slot_sequence_lengths"][i] = seq_len
+        out["slot_positions"][i] = position
+        out["slot_mapping"][i] = i
+        out["slot_block_tables"][i * S:i * S + len(page_ids)] = page_ids
+    return out
