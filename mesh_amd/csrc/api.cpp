@@ -105,10 +105,17 @@ static zr_status resolve_geometry(zr_context* ctx) {
                            gk);
         ctx->kv_head_map.push_back((uint32_t)(gk - ctx->kv_head_start));
     }
-    if (head_dim != 64 && head_dim != 128)
-        return set_err(ctx, ZR_E_UNSUPPORTED, "head_dim %d not supported (64 or 128)", head_dim);
-    if (qpk > 16) return set_err(ctx, ZR_E_UNSUPPORTED, "more than 16 q heads per kv head (%d)", qpk);
-    if (16 % qpk != 0) return set_err(ctx, ZR_E_UNSUPPORTED, "q heads per kv head (%d) must divide 16", qpk);
+    // RoPE's rotate-half pairs dims (i, i + d / 2): an even head_dim
+    // (tensor_ops.rs:509-520); the generic attention kernel holds up to 256
+    // dims per lane group
+    if (head_dim % 2 != 0 || head_dim > 256)
+        return set_err(ctx, ZR_E_UNSUPPORTED, "head_dim %d not supported (even, at most 256)", head_dim);
+    if (ctx->kv_cols % 4 != 0)
+        return set_err(ctx, ZR_E_UNSUPPORTED, "kv columns %d not a multiple of 4", ctx->kv_cols);
+    if (ctx->q_cols % 32 != 0)
+        return set_err(ctx, ZR_E_UNSUPPORTED, "q columns %d not a multiple of 32 (the O projection operand)",
+                       ctx->q_cols);
+    ctx->plain_kv = !((head_dim == 64 || head_dim == 128) && qpk <= 16 && 16 % qpk == 0);
     return ZR_OK;
 }
 
@@ -180,8 +187,9 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     st->stride = stride;
     st->max_kv = max_kv;
 
-    // attention tiles / split items
-    const int G = ctx->q_per_kv, qpt = 16 / G;
+    // attention tiles / split items (the generic kernel of plain-layout pools
+    // takes one workgroup per (row, q head) and needs none)
+    const int G = ctx->q_per_kv, qpt = ctx->plain_kv ? 0 : 16 / G;
     st->h_tiles.clear();
     st->h_items.clear();
     st->h_pblocks.clear();
@@ -189,15 +197,13 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     // sequences with >= 128 / G rows (prefill chunks) go to the prefill kernel
     // as blocks of 128 / G rows (bf16 pools, G dividing 32)
     int prows = 0;
-    if (ctx->desc.kv_dtype == ZR_DTYPE_BF16 && G <= 32 && 32 % G == 0 &&
-        (ctx->head_dim == 64 || ctx->head_dim == 128))
-        prows = 128 / G;
+    if (!ctx->plain_kv && ctx->desc.kv_dtype == ZR_DTYPE_BF16 && G <= 32 && 32 % G == 0) prows = 128 / G;
     if (const char* env = getenv("ZR_ATTN_PREFILL"))
         if (atoi(env) == 0) prows = 0;
     std::vector<int> tile_pages;
     std::vector<int4> pblk;  // prefill blocks {seq, r0, nrows, pages}
     long total_pages = 0, total_ktiles = 0;
-    for (int s = 0; s < S; ++s) {
+    for (int s = 0; s < S && qpt > 0; ++s) {
         const int ql = mb->q_len[s], kb = mb->kv_before[s], fo = mb->first_offset[s];
         if (prows && ql >= prows) {
             for (int r0 = 0; r0 < ql; r0 += prows) {

@@ -800,8 +800,149 @@ static zr_status launch_attn_t(zr_context* ctx, StagedMeta* st, int layer, const
     return ZR_OK;
 }
 
+// ------------------------------------------------------- any head_dim
+// Pools in the plain layout (head_dim other than 64 / 128, or q heads per kv
+// head not dividing 16): one wave per (query row, q head).  The wave walks
+// the visible keys 64 at a time (a key per lane: the lane's score over D from
+// its K row; rows of a page are contiguous), keeps an online softmax across
+// the wave and accumulates P.V with lanes over the dims (up to 4 per lane).
+// Row i of a sequence with `prefix` cached rows sees keys [0, prefix + i]: a
+// decode row sees its whole window, a prefill chunk the causal prefix
+// (forward_pass.rs:2764-2895, 1317-1372).
+struct GenericAttnArgs {
+    const float* q;
+    int q_cols;
+    const void* pool;          // layer base of the pool
+    size_t page_elems;
+    const int* block_tables;
+    int stride;
+    const int* first_offset;
+    const int* kv_before;
+    const int* cu_q;
+    const int* seq_ids;
+    int D, G, kv_heads;
+    float scale;               // 1 / sqrt(D)
+    float* out_f32;
+    uint16_t* out_bf16;
+    size_t out_lo_offset;
+};
+
+__device__ inline float load_kv(const float* p) { return *p; }
+__device__ inline float load_kv(const uint16_t* p) { return bf16_bits_to_f32(*p); }
+
+__device__ inline float wave_max64(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+__device__ inline float wave_sum64(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+template <typename KV>
+__global__ __launch_bounds__(64) void paged_attention_generic_kernel(GenericAttnArgs a) {
+    __shared__ float qs[256];
+    const int t = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const int D = a.D;
+    const int s = a.seq_ids[t];
+    const int i = t - a.cu_q[s];
+    const int L = a.kv_before[s] + i + 1;
+    const int fo = a.first_offset[s];
+    const int* bt = a.block_tables + (size_t)s * a.stride;
+    const int kvh = h / a.G;
+    const KV* pool = (const KV*)a.pool;
+    const size_t k_head = (size_t)kvh * kPageRows * D;
+    const size_t v_head = (size_t)a.kv_heads * kPageRows * D + k_head;
+    for (int d = lane; d < D; d += 64) qs[d] = a.q[(size_t)t * a.q_cols + h * D + d];
+    __syncthreads();
+    float m = -INFINITY, l = 0.0f, o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k0 = 0; k0 < L; k0 += 64) {
+        const int key = k0 + lane;
+        float sc = -INFINITY;
+        if (key < L) {
+            const int row = fo + key;
+            const KV* kr = pool + (size_t)bt[row / kPageRows] * a.page_elems + k_head + (size_t)(row % kPageRows) * D;
+            float acc = 0.0f;
+            for (int d = 0; d < D; ++d) acc += qs[d] * load_kv(kr + d);
+            sc = acc * a.scale;
+        }
+        const float mn = fmaxf(m, wave_max64(sc));  // finite: key k0 is visible
+        const float alpha = expf(m - mn);           // 0 on the first chunk (m = -inf)
+        const float p = key < L ? expf(sc - mn) : 0.0f;
+        l = l * alpha + wave_sum64(p);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] *= alpha;
+        const int nk = min(64, L - k0);
+        for (int kk = 0; kk < nk; ++kk) {
+            const float pk = __shfl(p, kk, 64);
+            const int row = fo + k0 + kk;
+            const KV* vr = pool + (size_t)bt[row / kPageRows] * a.page_elems + v_head + (size_t)(row % kPageRows) * D;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (lane + 64 * j < D) o[j] += pk * load_kv(vr + lane + 64 * j);
+        }
+        m = mn;
+    }
+    const float inv_l = 1.0f / l;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int d = lane + 64 * j;
+        if (d >= D) continue;
+        const float y = o[j] * inv_l;
+        const int c = h * D + d;
+        if (a.out_bf16) {
+            uint16_t hi, lo;
+            split_bf16(y, hi, lo);
+            const size_t idx = a_pack_index(t, c, a.q_cols);
+            a.out_bf16[idx] = hi;
+            if (a.out_lo_offset) a.out_bf16[a.out_lo_offset + idx] = lo;
+        } else {
+            a.out_f32[(size_t)t * a.q_cols + c] = y;
+        }
+    }
+}
+
+template <typename KV>
+static zr_status launch_attn_generic(zr_context* ctx, StagedMeta* st, int layer, const float* q, float* out,
+                                     uint16_t* out_bf16) {
+    GenericAttnArgs a;
+    a.q = q;
+    a.q_cols = ctx->q_cols;
+    a.page_elems = (size_t)2 * ctx->kv_cols * kPageRows;
+    a.pool = (const KV*)ctx->kv_pool + (size_t)layer * ctx->n_pages * a.page_elems;
+    a.block_tables = st->block_tables;
+    a.stride = st->stride;
+    a.first_offset = st->first_offset;
+    a.kv_before = st->kv_before;
+    a.cu_q = st->cu_q;
+    a.seq_ids = st->seq_ids;
+    a.D = ctx->head_dim;
+    a.G = ctx->q_per_kv;
+    a.kv_heads = ctx->local_kv_heads;
+    a.scale = 1.0f / sqrtf((float)ctx->head_dim);
+    a.out_f32 = out;
+    a.out_bf16 = out_bf16;
+    a.out_lo_offset = (ctx->desc.flags & ZR_FLAG_SPLIT_ACTIVATIONS) ? a_plane(st->total_q, ctx->q_cols) : 0;
+    hipEvent_t ev;
+    timing_mark_begin(ctx, kClassAttention, &ev);
+    hipLaunchKernelGGL(paged_attention_generic_kernel<KV>, dim3(st->total_q, ctx->local_q_heads), dim3(64), 0,
+                       ctx->stream, a);
+    ZR_LAUNCH_CHECK(ctx);
+    timing_mark_end(ctx, kClassAttention, ev);
+    return ZR_OK;
+}
+
 zr_status launch_attention(zr_context* ctx, StagedMeta* st, int layer, const float* q, float* out,
                            uint16_t* out_bf16) {
+    if (st->total_q == 0) return ZR_OK;
+    if (ctx->plain_kv) {
+        if (ctx->head_dim > 256) return set_err(ctx, ZR_E_UNSUPPORTED, "head_dim %d above 256", ctx->head_dim);
+        return ctx->desc.kv_dtype == ZR_DTYPE_BF16
+                   ? launch_attn_generic<uint16_t>(ctx, st, layer, q, out, out_bf16)
+                   : launch_attn_generic<float>(ctx, st, layer, q, out, out_bf16);
+    }
     if (st->n_attn_items == 0 && st->n_pblocks == 0) return ZR_OK;
     const size_t need = (size_t)st->n_part_items * ctx->local_kv_heads * 16 * (ctx->head_dim + 2);
     if (need > ctx->attn_part_floats)

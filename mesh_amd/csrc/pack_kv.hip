@@ -20,6 +20,10 @@ __device__ inline size_t k_off(int t, int d) { return ((size_t)(d >> 3) * kPageR
 __device__ inline size_t v_off(int t, int d, int) {
     return (((((size_t)(d >> 5) * 4 + (t >> 2)) * 16 + (d & 15)) * 2 + ((d >> 4) & 1)) * 4) + (t & 3);
 }
+// Plain layout (pools whose head_dim the MFMA kernels do not take): both
+// tiles row-major [16 rows][D].
+__device__ inline size_t k_off_of(int t, int d, int D, int plain) { return plain ? (size_t)t * D + d : k_off(t, d); }
+__device__ inline size_t v_off_of(int t, int d, int D, int plain) { return plain ? (size_t)t * D + d : v_off(t, d, D); }
 
 template <typename T> __device__ inline void store_elem(T* p, float x);
 template <> __device__ inline void store_elem<float>(float* p, float x) { *p = x; }
@@ -110,7 +114,7 @@ __global__ __launch_bounds__(256) void rope_kv_write_kernel(
     const float* __restrict__ qkv, int qkv_n, size_t qkv_slab, int qkv_stride, float* __restrict__ q_out,
     int q_cols, int kv_cols,
     int D, const int* __restrict__ positions, const int* __restrict__ slot,
-    const float* __restrict__ inv_freq, KV* __restrict__ layer_pool, size_t page_elems, int rope) {
+    const float* __restrict__ inv_freq, KV* __restrict__ layer_pool, size_t page_elems, int rope, int plain) {
 #pragma clang fp contract(off)
     const int t = blockIdx.x;
     const int half = D / 2;
@@ -148,8 +152,8 @@ __global__ __launch_bounds__(256) void rope_kv_write_kernel(
                 q_out[(size_t)t * q_cols + head * D + i + half] = b;
             } else {
                 KV* kt = kpage + (size_t)head * kPageRows * D;
-                store_elem(kt + k_off(r, i), a);
-                store_elem(kt + k_off(r, i + half), b);
+                store_elem(kt + k_off_of(r, i, D, plain), a);
+                store_elem(kt + k_off_of(r, i + half, D, plain), b);
             }
         } else {
             const int c = j - nq - nk;
@@ -158,7 +162,7 @@ __global__ __launch_bounds__(256) void rope_kv_write_kernel(
             float vv = row[q_cols + kv_cols + c];
 #pragma unroll 4
             for (int sl = 1; sl < qkv_n; ++sl) vv += row[sl * qkv_slab + q_cols + kv_cols + c];
-            store_elem(vt + v_off(r, d, D), vv);
+            store_elem(vt + v_off_of(r, d, D, plain), vv);
         }
     }
 }
@@ -181,12 +185,12 @@ zr_status launch_rope_kv_write(zr_context* ctx, StagedMeta* st, int layer, const
         uint16_t* pool = (uint16_t*)ctx->kv_pool + (size_t)layer * ctx->n_pages * pe;
         hipLaunchKernelGGL(rope_kv_write_kernel<uint16_t>, grid, dim3(256), 0, ctx->stream,
                            qkv.ptr, qkv.n, qkv.stride, stride, q_out, ctx->q_cols, ctx->kv_cols, ctx->head_dim, st->positions,
-                           st->slot_mapping, ctx->inv_freq, pool, pe, rope);
+                           st->slot_mapping, ctx->inv_freq, pool, pe, rope, ctx->plain_kv ? 1 : 0);
     } else {
         float* pool = (float*)ctx->kv_pool + (size_t)layer * ctx->n_pages * pe;
         hipLaunchKernelGGL(rope_kv_write_kernel<float>, grid, dim3(256), 0, ctx->stream,
                            qkv.ptr, qkv.n, qkv.stride, stride, q_out, ctx->q_cols, ctx->kv_cols, ctx->head_dim, st->positions,
-                           st->slot_mapping, ctx->inv_freq, pool, pe, rope);
+                           st->slot_mapping, ctx->inv_freq, pool, pe, rope, ctx->plain_kv ? 1 : 0);
     }
     ZR_LAUNCH_CHECK(ctx);
     timing_mark_end(ctx, kClassNormRopeKv, ev);
@@ -196,140 +200,202 @@ zr_status launch_rope_kv_write(zr_context* ctx, StagedMeta* st, int layer, const
 // ------------------------------------------------------ gather / scatter
 // Logical window row j of a sequence lives at physical row first_offset + j of
 // its page list (interior spans are full pages; only the first span may start
-// mid-page after retain_suffix).  One workgroup per (page of the range, layer);
-// its threads sweep the page's 8-element groups, which are contiguous in the
-// pool layout (16 B in bf16 pools):
-//   K group (g, r):    row r, dims 8 g .. 8 g + 7 of one head;
-//   V group (q, dd):   rows 4 q .. 4 q + 3 of dims d and d + 16, d = 32 (g / 4) + dd.
-// Consecutive threads take consecutive groups, so the page side is read or
-// written in whole 1 KiB wave segments and each row side in 128 B runs.  Only
-// rows [first_row, first_row + n_rows) are copied: a scatter writes the other
-// rows of a boundary V group element by element, leaving them untouched.
+// mid-page after retain_suffix).  One workgroup per (page of the range, layer)
+// moves the page's K block, then its V block, through an LDS tile that holds
+// the page's 16 rows row-major in the pool dtype, each row padded by 16 B:
+//   row side:  whole rows as float4 runs (the block's 16 rows are contiguous
+//              in the [layers][rows][kv_cols] f32 arrays);
+//   page side: the block's 8-element groups, contiguous in the pool layout
+//              (16 B in bf16 pools), consecutive threads on consecutive
+//              groups, so a wave moves 1 KiB segments;
+//     K group (g, r):  row r, dims 8 g .. 8 g + 7 of one head (a thread reads
+//                      them from one LDS row; consecutive rows are 16 B apart
+//                      modulo 256 B, so a wave's group reads do not conflict);
+//     V groups:        a thread takes 4 consecutive groups (rows 4 q .. 4 q + 3
+//                      of dims d .. d + 3 and d + 16 .. d + 19, one 64 B run).
+// Only rows [first_row, first_row + n_rows) are copied.  A scatter loads only
+// those rows into LDS and writes the V quads cut by the range element by
+// element, leaving the page's other rows untouched.
 template <typename KV>
 struct alignas(8 * sizeof(KV)) Group8 {
     KV x[8];
 };
 
 template <typename KV>
+__device__ inline void store4(KV* p, f32x4 x);
+template <>
+__device__ inline void store4<float>(float* p, f32x4 x) {
+    *(f32x4*)p = x;
+}
+template <>
+__device__ inline void store4<uint16_t>(uint16_t* p, f32x4 x) {
+    ushort4 h;
+    h.x = f32_to_bf16_bits(x[0]);
+    h.y = f32_to_bf16_bits(x[1]);
+    h.z = f32_to_bf16_bits(x[2]);
+    h.w = f32_to_bf16_bits(x[3]);
+    *(ushort4*)p = h;
+}
+template <typename KV>
+__device__ inline f32x4 load4(const KV* p);
+template <>
+__device__ inline f32x4 load4<float>(const float* p) {
+    return *(const f32x4*)p;
+}
+template <>
+__device__ inline f32x4 load4<uint16_t>(const uint16_t* p) {
+    const ushort4 h = *(const ushort4*)p;
+    return f32x4{bf16_bits_to_f32(h.x), bf16_bits_to_f32(h.y), bf16_bits_to_f32(h.z), bf16_bits_to_f32(h.w)};
+}
+
+template <typename KV>
+constexpr int kv_tile_pitch(int kv_cols) {
+    return kv_cols + 16 / (int)sizeof(KV);  // elements: 16 B of padding per row
+}
+
+template <typename KV>
 __global__ __launch_bounds__(256) void kv_copy_kernel(KV* __restrict__ pool, size_t page_elems, int n_pages_pool,
                                                       int layer_begin, const int* __restrict__ table,
                                                       int first_offset, int first_row, int n_rows, int kv_heads,
                                                       int D, float* __restrict__ k, float* __restrict__ v,
-                                                      int to_pool) {
+                                                      int to_pool, int plain) {
+    extern __shared__ __align__(16) unsigned char kv_lds[];
+    KV* tile = (KV*)kv_lds;
     const int slot = blockIdx.x, l = blockIdx.y;
     const int p0 = (first_offset + first_row) / kPageRows;
     const int page = table[p0 + slot];
     const int rbase = (p0 + slot) * kPageRows - first_offset - first_row;  // output row of page row 0
     const int r_lo = max(0, -rbase), r_hi = min(kPageRows, n_rows - rbase);
-    const size_t kv_cols = (size_t)kv_heads * D;
-    const int tile = kPageRows * D;           // elements of one head's K (or V) tile
-    const int groups = kv_heads * tile / 8;   // 8-element groups per K (or V) block
-    Group8<KV>* kp = (Group8<KV>*)(pool + ((size_t)(layer_begin + l) * n_pages_pool + page) * page_elems);
-    Group8<KV>* vp = kp + groups;
-    // output row of page row r (r_lo <= r < r_hi, so rbase + r >= 0)
-    auto krow = [&](int r) { return k + ((size_t)l * n_rows + (rbase + r)) * kv_cols; };
-    auto vrow = [&](int r) { return v + ((size_t)l * n_rows + (rbase + r)) * kv_cols; };
-    for (int gi = threadIdx.x; gi < groups; gi += blockDim.x) {
-        const int h = gi / (tile / 8), cg = gi - h * (tile / 8);
-        // K: group cg = g * 16 + r
-        {
-            const int g = cg >> 4, r = cg & 15;
-            if (r >= r_lo && r < r_hi) {
-                float* row = krow(r) + (size_t)h * D + 8 * g;
-                if (to_pool) {
-                    Group8<KV> gr;
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) store_elem(&gr.x[j], row[j]);
-                    kp[gi] = gr;
-                } else {
-                    const Group8<KV> gr = kp[gi];
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) row[j] = load_elem(&gr.x[j]);
-                }
+    const int kv_cols = kv_heads * D;
+    const int pitch = kv_tile_pitch<KV>(kv_cols);
+    const int c4 = kv_cols / 4;
+    const int tile8 = kPageRows * D / 8;      // 8-element groups of one head's K (or V) tile
+    KV* kblk = pool + ((size_t)(layer_begin + l) * n_pages_pool + page) * page_elems;
+    if (plain) {
+        // row-major [kv_head][16 rows][D] tiles: element by element, page side in order
+        for (int which = 0; which < 2; ++which) {
+            KV* blk = kblk + (size_t)which * kv_cols * kPageRows;
+            float* rows = (which ? v : k) + (size_t)l * n_rows * kv_cols;
+            for (int e = threadIdx.x; e < kv_cols * kPageRows; e += blockDim.x) {
+                const int h = e / (kPageRows * D), rem = e - h * (kPageRows * D);
+                const int r = rem / D, d = rem - r * D;
+                if (r < r_lo || r >= r_hi) continue;
+                float* x = rows + (size_t)(rbase + r) * kv_cols + h * D + d;
+                if (to_pool)
+                    store_elem(blk + e, *x);
+                else
+                    *x = load_elem(blk + e);
             }
         }
+        return;
     }
-    // V: group cg = ((d / 32) * 4 + q) * 16 + dd holds rows 4 q + i of dims d (i)
-    // and d + 16 (4 + i).  A thread takes 4 consecutive groups (dims d .. d + 3,
-    // one 64 B run of the page) and moves the 4 rows as float4 runs of dims
-    // d .. d + 3 and d + 16 .. d + 19; a quad cut by the row range goes element
-    // by element.
-    const int quads = kv_heads * D / 2;
-    for (int qi = threadIdx.x; qi < quads; qi += blockDim.x) {
-        const int h = qi / (D / 2), cg0 = (qi - h * (D / 2)) * 4;
-        const int q = (cg0 >> 4) & 3, d0 = (cg0 >> 6) * 32 + (cg0 & 15);
-        const int r0 = 4 * q;
-        if (r0 + 3 < r_lo || r0 >= r_hi) continue;
-        Group8<KV>* gp = vp + (size_t)h * (tile / 8) + cg0;
-        const size_t c0 = (size_t)h * D + d0;  // column of dim d0
-        if (r0 >= r_lo && r0 + 3 < r_hi) {
-            if (to_pool) {
-                f32x4 lo4[4], hi4[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    lo4[i] = *(const f32x4*)(vrow(r0 + i) + c0);
-                    hi4[i] = *(const f32x4*)(vrow(r0 + i) + c0 + 16);
-                }
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    Group8<KV> gr;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        store_elem(&gr.x[i], lo4[i][j]);
-                        store_elem(&gr.x[4 + i], hi4[i][j]);
-                    }
-                    gp[j] = gr;
-                }
-            } else {
-                Group8<KV> gr[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) gr[j] = gp[j];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    *(f32x4*)(vrow(r0 + i) + c0) = f32x4{load_elem(&gr[0].x[i]), load_elem(&gr[1].x[i]),
-                                                        load_elem(&gr[2].x[i]), load_elem(&gr[3].x[i])};
-                    *(f32x4*)(vrow(r0 + i) + c0 + 16) =
-                        f32x4{load_elem(&gr[0].x[4 + i]), load_elem(&gr[1].x[4 + i]), load_elem(&gr[2].x[4 + i]),
-                              load_elem(&gr[3].x[4 + i])};
+    for (int which = 0; which < 2; ++which) {
+        KV* blk = kblk + (size_t)which * kv_cols * kPageRows;
+        Group8<KV>* gp0 = (Group8<KV>*)blk;
+        // row r of the page is row rbase + r >= 0 of layer l's f32 rows (r_lo <= r < r_hi)
+        float* rows = (which ? v : k) + (size_t)l * n_rows * kv_cols;
+        if (which) __syncthreads();  // the K block's LDS reads are done
+        if (to_pool) {
+            for (int i = threadIdx.x; i < (r_hi - r_lo) * c4; i += blockDim.x) {
+                const int r = r_lo + i / c4, c = (i - (i / c4) * c4) * 4;
+                store4(tile + r * pitch + c, *(const f32x4*)(rows + (size_t)(rbase + r) * kv_cols + c));
+            }
+            __syncthreads();
+        }
+        if (!which) {
+            for (int gi = threadIdx.x; gi < kv_heads * tile8; gi += blockDim.x) {
+                const int h = gi / tile8, cg = gi - h * tile8;
+                const int g = cg >> 4, r = cg & 15;  // K group cg = g * 16 + r
+                KV* t = tile + r * pitch + h * D + 8 * g;
+                if (to_pool) {
+                    if (r >= r_lo && r < r_hi) gp0[gi] = *(const Group8<KV>*)t;
+                } else {
+                    *(Group8<KV>*)t = gp0[gi];
                 }
             }
         } else {
-            for (int j = 0; j < 4; ++j) {
-                KV* e = gp[j].x;
-                for (int i = 0; i < 4; ++i) {
-                    if (r0 + i < r_lo || r0 + i >= r_hi) continue;
-                    if (to_pool) {
-                        store_elem(&e[i], vrow(r0 + i)[c0 + j]);
-                        store_elem(&e[4 + i], vrow(r0 + i)[c0 + 16 + j]);
-                    } else {
-                        vrow(r0 + i)[c0 + j] = load_elem(&e[i]);
-                        vrow(r0 + i)[c0 + 16 + j] = load_elem(&e[4 + i]);
-                    }
+            // V group cg = ((d / 32) * 4 + q) * 16 + dd holds rows 4 q + i of dims d (i) and d + 16 (4 + i)
+            for (int qi = threadIdx.x; qi < kv_heads * D / 2; qi += blockDim.x) {
+                const int h = qi / (D / 2), cg0 = (qi - h * (D / 2)) * 4;
+                const int q = (cg0 >> 4) & 3, d0 = (cg0 >> 6) * 32 + (cg0 & 15);
+                const int r0 = 4 * q;
+                Group8<KV>* gp = gp0 + (size_t)h * tile8 + cg0;
+                KV* t = tile + r0 * pitch + h * D + d0;
+                if (!to_pool) {
+                    Group8<KV> gr[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) gr[j] = gp[j];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            t[i * pitch + j] = gr[j].x[i];
+                            t[i * pitch + 16 + j] = gr[j].x[4 + i];
+                        }
+                } else if (r0 >= r_lo && r0 + 3 < r_hi) {
+                    Group8<KV> gr[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            gr[j].x[i] = t[i * pitch + j];
+                            gr[j].x[4 + i] = t[i * pitch + 16 + j];
+                        }
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) gp[j] = gr[j];
+                } else if (r0 + 3 >= r_lo && r0 < r_hi) {
+                    for (int j = 0; j < 4; ++j)
+                        for (int i = 0; i < 4; ++i) {
+                            if (r0 + i < r_lo || r0 + i >= r_hi) continue;
+                            gp[j].x[i] = t[i * pitch + j];
+                            gp[j].x[4 + i] = t[i * pitch + 16 + j];
+                        }
                 }
+            }
+        }
+        if (!to_pool) {
+            __syncthreads();
+            for (int i = threadIdx.x; i < (r_hi - r_lo) * c4; i += blockDim.x) {
+                const int r = r_lo + i / c4, c = (i - (i / c4) * c4) * 4;
+                *(f32x4*)(rows + (size_t)(rbase + r) * kv_cols + c) = load4(tile + r * pitch + c);
             }
         }
     }
 }
 
+template <typename KV>
+static zr_status kv_copy_launch(zr_context* ctx, dim3 grid, int layer_begin, const int* d_table, int first_offset,
+                                int first_row, int n_rows, float* k, float* v, int to_pool) {
+    const size_t lds = ctx->plain_kv ? 0 : (size_t)kPageRows * kv_tile_pitch<KV>(ctx->kv_cols) * sizeof(KV);
+    if (lds > 160 * 1024)
+        return set_err(ctx, ZR_E_UNSUPPORTED, "KV copy tile of %zu bytes exceeds LDS (%d kv columns)", lds,
+                       ctx->kv_cols);
+    if (lds > 64 * 1024) {
+        const hipError_t e =
+            hipFuncSetAttribute((const void*)kv_copy_kernel<KV>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return set_err(ctx, ZR_E_HIP, "KV copy LDS attribute: %s", hipGetErrorString(e));
+    }
+    hipLaunchKernelGGL(kv_copy_kernel<KV>, grid, dim3(256), lds, ctx->stream, (KV*)ctx->kv_pool, page_elems_of(ctx),
+                       ctx->n_pages, layer_begin, d_table, first_offset, first_row, n_rows,
+                       ctx->kv_cols / ctx->head_dim, ctx->head_dim, k, v, to_pool, ctx->plain_kv ? 1 : 0);
+    ZR_LAUNCH_CHECK(ctx);
+    return ZR_OK;
+}
+
 zr_status launch_kv_copy(zr_context* ctx, int layer_begin, int layer_end, const int* d_table,
                          int first_offset, int first_row, int n_rows, float* k, float* v, int to_pool) {
     if (n_rows <= 0 || layer_end <= layer_begin) return ZR_OK;
-    const size_t pe = page_elems_of(ctx);
+    if (ctx->kv_cols % 4 != 0) return set_err(ctx, ZR_E_UNSUPPORTED, "kv columns %d not a multiple of 4", ctx->kv_cols);
     const int p0 = (first_offset + first_row) / kPageRows;
     const int p1 = (first_offset + first_row + n_rows - 1) / kPageRows;
     dim3 grid(p1 - p0 + 1, layer_end - layer_begin);
-    const int kvh = ctx->kv_cols / ctx->head_dim;
     hipEvent_t ev;
     timing_mark_begin(ctx, kClassOther, &ev);  // not on the decode path: class "other" holds it alone there
-    if (ctx->desc.kv_dtype == ZR_DTYPE_BF16)
-        hipLaunchKernelGGL(kv_copy_kernel<uint16_t>, grid, dim3(256), 0, ctx->stream,
-                           (uint16_t*)ctx->kv_pool, pe, ctx->n_pages, layer_begin, d_table, first_offset,
-                           first_row, n_rows, kvh, ctx->head_dim, k, v, to_pool);
-    else
-        hipLaunchKernelGGL(kv_copy_kernel<float>, grid, dim3(256), 0, ctx->stream, (float*)ctx->kv_pool,
-                           pe, ctx->n_pages, layer_begin, d_table, first_offset, first_row, n_rows, kvh,
-                           ctx->head_dim, k, v, to_pool);
-    ZR_LAUNCH_CHECK(ctx);
+    const zr_status rc =
+        ctx->desc.kv_dtype == ZR_DTYPE_BF16
+            ? kv_copy_launch<uint16_t>(ctx, grid, layer_begin, d_table, first_offset, first_row, n_rows, k, v, to_pool)
+            : kv_copy_launch<float>(ctx, grid, layer_begin, d_table, first_offset, first_row, n_rows, k, v, to_pool);
+    if (rc) return rc;
     timing_mark_end(ctx, kClassOther, ev);
     return ZR_OK;
 }

@@ -118,6 +118,12 @@ struct zr_context {
     int head_dim = 0, q_cols = 0, kv_cols = 0, local_q_heads = 0, local_kv_heads = 0;
     int q_per_kv = 0, q_head_start = 0, kv_head_start = 0;
     std::vector<uint32_t> kv_head_map;
+    // Page layout of the KV pool.  false: the MFMA fragment layout of the
+    // decode / prefill attention kernels (head_dim 64 or 128, q heads per kv
+    // head dividing 16).  true (any other even head_dim up to 256, any group):
+    // each kv head's K and V tiles are row-major [16 rows][head_dim], read by
+    // the generic attention kernel.
+    bool plain_kv = false;
 
     // weights
     std::vector<zr::LayerDev> layers;

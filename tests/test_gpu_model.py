@@ -415,3 +415,67 @@ def test_split_k_workspace_covers_every_row_count(cap, batches):
         for b in dev:
             b.close()
     ctx.close()
+
+
+# ------------------------------------------- head_dim outside the MFMA kernels --
+def test_reference_test_model_sliding_window_decode_kat():
+    """The reference's own test model (create_test_config / create_test_weights,
+    forward_pass.rs:3163-3202: hidden 64, 4 heads of head_dim 16, constant
+    weights) through the HIP path, with the sliding-window known answer of
+    test_decode_microbatch_respects_sliding_device_kv_window (3824-3907):
+    max_seq_len 2, prefill [1, 2, 3] then a decode microbatch [7, 8]; logits
+    against the oracle."""
+    cfg = TEST_CONFIG
+    geo = geometry(cfg)
+    assert geo["head_dim"] == 16
+    weights = constant_weights(cfg, geo)
+    ctx, om = make(cfg, geo, weights, "f32", True, max_tokens=16, max_seqs=4, pages=16, pps=4)
+    dev = [ctx.new_backend(max_seq_len=2) for _ in range(2)]
+    ref = [O.Session(cfg["num_layers"], geo["kv_cols"], 16, 2) for _ in range(2)]
+    for b, s in zip(dev, ref):
+        check_logits(b.prefill([1, 2, 3]), om.prefill(s, [1, 2, 3]), "prefill")
+        assert b.sequence_position() == 3 and b.cache_seq_len() == 2
+        assert b.base_position() + b.cache_seq_len() == 3
+    reqs = [DecodeMicrobatchRequest(str(i), t, b) for i, (t, b) in enumerate(zip([7, 8], dev))]
+    outs = BackendMicrobatchExecutor.decode_step_batch(reqs, want_logits=True)
+    got = np.stack([o.logits for o in outs])
+    assert got.shape == (2, cfg["vocab"])
+    check_logits(got, om.decode(ref, [7, 8]), "decode")
+    for b in dev:
+        assert b.sequence_position() == 4 and b.cache_seq_len() == 2 and b.base_position() == 2
+    ctx.close()
+
+
+@pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("hidden,heads,kv_heads", [(256, 16, 4), (384, 4, 2), (512, 16, 16), (576, 9, 3)])
+def test_generic_head_dim_models_match_oracle(kv_dtype, hidden, heads, kv_heads):
+    """Head dims 16, 96, 32 and a 64-dim model whose 3 q heads per kv head do
+    not divide 16: the plain page layout and the generic attention kernel.
+    Prompts of 1 to 40 tokens (prefill chunks with causal masking), then
+    decode microbatches."""
+    cfg = dict(hidden=hidden, num_heads=heads, num_kv_heads=kv_heads, num_layers=2, vocab=300, ffn=512,
+               rms_norm_eps=1e-5, rope_base=10000.0)
+    geo = geometry(cfg)
+    weights = random_weights(cfg, geo, seed=hidden + heads, std=0.05)
+    ctx, om = make(cfg, geo, weights, kv_dtype, True, max_tokens=64, max_seqs=8, pages=256, pps=16)
+    rng = np.random.default_rng(heads)
+    prompts = [rng.integers(0, cfg["vocab"], n).tolist() for n in (1, 7, 16, 17, 40)]
+    dev = [ctx.new_backend() for _ in prompts]
+    ref = [O.Session(cfg["num_layers"], geo["kv_cols"], kv_round_bf16=(kv_dtype == "bf16")) for _ in prompts]
+    toks = []
+    for b, s, p in zip(dev, ref, prompts):
+        want = om.prefill(s, p)
+        check_logits(b.prefill(p), want, f"D={geo['head_dim']} prefill of {len(p)}")
+        toks.append(int(np.argmax(want)))
+    for step in range(3):
+        reqs = [DecodeMicrobatchRequest(str(i), t, b) for i, (t, b) in enumerate(zip(toks, dev))]
+        outs = BackendMicrobatchExecutor.decode_step_batch(reqs, want_logits=True)
+        want = om.decode(ref, toks)
+        check_logits(np.stack([o.logits for o in outs]), want, f"D={geo['head_dim']} step {step}")
+        toks = np.argmax(want, 1).tolist()
+    for b, s in zip(dev, ref):  # the plain-layout pages hold the oracle's cache
+        snap = b.export_kv_cache()
+        for layer in range(cfg["num_layers"]):
+            k, v = s.gather(layer)
+            assert np.abs(snap.keys[layer] - k).max() <= 2e-2 * max(1.0, np.abs(k).max())
+    ctx.close()
