@@ -168,7 +168,9 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_kernel(
     if (g >= col_blocks * splits) return;  // padding block of the XCD mapping
     const int cb = g / splits, split = g - cb * splits;
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // the wave index is uniform: readfirstlane keeps it (and every copy
+    // offset derived from it) in scalar registers
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int wm_idx = wave / WAVES_N, wn_idx = wave - wm_idx * WAVES_N;
     const int m0 = rb * BMT * 32;
     const int nt_blk = cb * BNT;
@@ -177,23 +179,30 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_kernel(
     const int kt_begin = split * kt_per_split;
     const int nsteps = min(KT, kt_begin + kt_per_split) - kt_begin;
 
+    // Copies are buffer loads into LDS: the lane's 16 B of a 1 KiB fragment
+    // is a constant vector offset, the fragment's byte offset a scalar, so
+    // the per-step address arithmetic stays in the scalar unit.  Offsets are
+    // 32-bit: packed operands stay below 4 GiB (launch_gemm checks).
+    const __amdgpu_buffer_rsrc_t rsrc_a = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsrc_w = __builtin_amdgcn_make_buffer_rsrc((void*)Wp, 0, 0x7fffffff, 0x00020000);
+    const int voff = lane * 16;
     auto issue = [&](int slot, int kt) {
 #pragma unroll
         for (int i = 0; i < PW; ++i) {
             int f = i * NW + wave;
             const int fs = f < FS ? f : f - FS;  // padding rows repeat a real fragment
-            const void* src;
             if (fs < FA) {
                 // fragment-packed A: row tile (clamped into the operand), k-slice 2 kt + kh
                 const int kh = fs & 1, r = fs >> 1;
                 const int hl = r / BMT, mt = min(m0 / 32 + (r - hl * BMT), MT - 1);
-                src = (const bf16x8*)A + (((size_t)hl * MT + mt) * KT16 + 2 * kt + kh) * 64 + lane;
+                const int off = (((hl * MT + mt) * KT16 + 2 * kt + kh) << 10);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (lds_void*)&lds[slot][f][0], 16, voff, off, 0, 0);
             } else {
                 const int fb = fs - FA;
                 const int nt = min(nt_blk + (fb >> 1), NT - 1);
-                src = Wp + ((size_t)nt * KT16 + 2 * kt + (fb & 1)) * 64 + lane;
+                const int off = ((nt * KT16 + 2 * kt + (fb & 1)) << 10);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_w, (lds_void*)&lds[slot][f][0], 16, voff, off, 0, 0);
             }
-            __builtin_amdgcn_global_load_lds(src, (lds_void*)&lds[slot][f][0], 16, 0, 0);
         }
     };
 
@@ -453,6 +462,10 @@ zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_pack
         return set_err(ctx, ZR_E_INVARIANT, "deferred split-K needs an f32 store epilogue");
     if (m <= 0) return ZR_OK;
     if (k % 32 != 0) return set_err(ctx, ZR_E_UNSUPPORTED, "GEMM K=%d must be a multiple of 32", k);
+    // the kernel addresses its operands with 32-bit buffer offsets
+    const size_t a_bytes = 2 * 2 * a_plane(m, k), w_bytes = 2 * packed_weight_elems(k, n);
+    if (a_bytes > 0x7fffffffull || w_bytes > 0x7fffffffull)
+        return set_err(ctx, ZR_E_UNSUPPORTED, "GEMM operands of %zu / %zu bytes exceed 2 GiB", a_bytes, w_bytes);
     const GemmPlan p = gemm_plan(m, n, k, epilogue);
     const GemmCfg cfg = pick_cfg(m, n, k, epilogue);
     if (swiglu_fused(m, epilogue) && (!c_bf16 || c_f32 || n % 64 != 0))
