@@ -242,6 +242,13 @@ zr_status zr_rms_norm(zr_context* ctx, const float* d_x, const float* d_gamma, f
  * layout), A/C device f32 -- the shard projection GEMM on MFMA. */
 zr_status zr_gemm(zr_context* ctx, const float* d_a, const uint16_t* w, float* d_c, int m, int n,
                   int k);
+/* H[M,F] = silu(A @ Wg) * (A @ Wu) (runtime.rs:927-929 silu_device and the
+ * broadcast_mul at forward_pass.rs:2286-2289; host form tensor_ops.rs:268-278)
+ * with Wg, Wu bf16 [K,F] (host or device, reference layout), A / H device f32:
+ * the gate / up product with SwiGLU in its epilogue exactly as the decode step
+ * runs it (F % 32 == 0).  H is the next product's operand expanded to f32. */
+zr_status zr_gemm_swiglu(zr_context* ctx, const float* d_a, const uint16_t* w_gate, const uint16_t* w_up,
+                         float* d_h, int m, int f, int k);
 
 /* --------------------------------------------------------- device memory --- */
 zr_status zr_device_alloc(zr_context* ctx, size_t bytes, void** out);

@@ -126,6 +126,7 @@ SIGNATURES = [
     ("zr_sample_last_logits", C.c_int, [C.c_void_p, C.c_int, c_f32_p, c_f32_p, C.POINTER(C.c_uint64), c_u32_p]),
     ("zr_rms_norm", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int]),
     ("zr_gemm", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),
+    ("zr_gemm_swiglu", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),
     ("zr_device_alloc", C.c_int, [C.c_void_p, C.c_size_t, c_void_pp]),
     ("zr_device_free", C.c_int, [C.c_void_p, C.c_void_p]),
     ("zr_host_alloc", C.c_int, [C.c_void_p, C.c_size_t, C.POINTER(C.c_void_p)]),

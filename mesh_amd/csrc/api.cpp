@@ -950,23 +950,26 @@ zr_status zr_rms_norm(zr_context* ctx, const float* d_x, const float* d_gamma, f
     return rc;
 }
 
-zr_status zr_gemm(zr_context* ctx, const float* d_a, const uint16_t* w, float* d_c, int m, int n, int k) {
-    if (!ctx || !d_a || !w || !d_c) return set_global_err(ZR_E_INVALID, "null argument");
-    if (m <= 0 || n <= 0 || k <= 0) return set_err(ctx, ZR_E_INVALID, "Matmul shape mismatch: %dx%d @ %dx%d", m, k, k, n);
-    ZR_HIP(ctx, hipSetDevice(ctx->device));
-    uint16_t* packed = nullptr;
-    zr_status rc = pack_weight(ctx, w, k, n, &packed);
-    if (rc) return rc;
+// Op-level product of a packed weight with a device f32 A [m, k]: A is padded
+// to the packed K (a multiple of 32; the packed weights are zero beyond k) and
+// converted to the bf16 (hi + lo) operand.  kEpiStore writes C [m, n] to d_out;
+// kEpiSwiGLU writes its bf16 operand and expands it to f32 [m, n / 2] in d_out.
+// Takes ownership of `packed`.
+static zr_status run_gemm_op(zr_context* ctx, const float* d_a, uint16_t* packed, float* d_out, int m, int n, int k,
+                             int epilogue) {
     const int lo = (ctx->desc.flags & ZR_FLAG_SPLIT_ACTIVATIONS) ? 1 : 0;
-    const int kp = (k + 31) / 32 * 32;  // the packed weights are zero beyond k
-    const size_t need = gemm_ws_floats(m, n, kp, kEpiStore);
+    const int kp = (k + 31) / 32 * 32;
+    const size_t need = gemm_ws_floats(m, n, kp, epilogue);
     float* saved_ws = ctx->splitk_ws;
     size_t saved_n = ctx->splitk_ws_floats;
     float* tmp_ws = nullptr;
     float* a_pad = nullptr;
     uint16_t* a16 = nullptr;
+    uint16_t* h16 = nullptr;
+    zr_status rc = ZR_OK;
     hipError_t e = hipMalloc(&a16, (size_t)2 * 2 * a_plane(m, kp));
     if (e == hipSuccess) e = hipMalloc(&a_pad, (size_t)4 * m * kp);
+    if (e == hipSuccess && epilogue == kEpiSwiGLU) e = hipMalloc(&h16, (size_t)2 * 2 * a_plane(m, n / 2));
     if (e == hipSuccess) e = hipMemsetAsync(a_pad, 0, (size_t)4 * m * kp, ctx->stream);
     if (e == hipSuccess)
         e = hipMemcpy2DAsync(a_pad, 4 * (size_t)kp, d_a, 4 * (size_t)k, 4 * (size_t)k, m, hipMemcpyDeviceToDevice,
@@ -980,16 +983,44 @@ zr_status zr_gemm(zr_context* ctx, const float* d_a, const uint16_t* w, float* d
     }
     if (e != hipSuccess) rc = set_err(ctx, ZR_E_OOM, "gemm workspace: %s", hipGetErrorString(e));
     if (!rc) rc = launch_to_bf16_pair(ctx, a_pad, m, kp, a16, lo);
-    if (!rc) rc = launch_gemm(ctx, a16, packed, d_c, nullptr, m, n, kp, kEpiStore);
+    if (!rc && epilogue == kEpiSwiGLU) {
+        rc = launch_gemm(ctx, a16, packed, nullptr, h16, m, n, kp, kEpiSwiGLU);
+        if (!rc) rc = launch_from_bf16_pair(ctx, h16, m, n / 2, lo, d_out);
+    } else if (!rc) {
+        rc = launch_gemm(ctx, a16, packed, d_out, nullptr, m, n, kp, kEpiStore);
+    }
     e = hipStreamSynchronize(ctx->stream);
     if (!rc && e != hipSuccess) rc = set_err(ctx, ZR_E_HIP, "gemm: %s", hipGetErrorString(e));
     ctx->splitk_ws = saved_ws;
     ctx->splitk_ws_floats = saved_n;
     if (tmp_ws) (void)hipFree(tmp_ws);
+    if (h16) (void)hipFree(h16);
     if (a_pad) (void)hipFree(a_pad);
     if (a16) (void)hipFree(a16);
     (void)hipFree(packed);
     return rc;
+}
+
+zr_status zr_gemm(zr_context* ctx, const float* d_a, const uint16_t* w, float* d_c, int m, int n, int k) {
+    if (!ctx || !d_a || !w || !d_c) return set_global_err(ZR_E_INVALID, "null argument");
+    if (m <= 0 || n <= 0 || k <= 0) return set_err(ctx, ZR_E_INVALID, "Matmul shape mismatch: %dx%d @ %dx%d", m, k, k, n);
+    ZR_HIP(ctx, hipSetDevice(ctx->device));
+    uint16_t* packed = nullptr;
+    zr_status rc = pack_weight(ctx, w, k, n, &packed);
+    if (rc) return rc;
+    return run_gemm_op(ctx, d_a, packed, d_c, m, n, k, kEpiStore);
+}
+
+zr_status zr_gemm_swiglu(zr_context* ctx, const float* d_a, const uint16_t* w_gate, const uint16_t* w_up, float* d_h,
+                         int m, int f, int k) {
+    if (!ctx || !d_a || !w_gate || !w_up || !d_h) return set_global_err(ZR_E_INVALID, "null argument");
+    if (m <= 0 || f <= 0 || k <= 0)
+        return set_err(ctx, ZR_E_INVALID, "Matmul shape mismatch: %dx%d @ %dx%d", m, k, k, 2 * f);
+    ZR_HIP(ctx, hipSetDevice(ctx->device));
+    uint16_t* packed = nullptr;
+    zr_status rc = pack_weight_gate_up(ctx, w_gate, w_up, k, f, &packed);
+    if (rc) return rc;
+    return run_gemm_op(ctx, d_a, packed, d_h, m, 2 * f, k, kEpiSwiGLU);
 }
 
 zr_status zr_device_alloc(zr_context* ctx, size_t bytes, void** out) {

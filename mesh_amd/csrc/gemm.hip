@@ -125,14 +125,16 @@ __device__ inline float swiglu(float g, float u) {
 // + j]; the product lane l, element i is C[8 (i / 4) + 4 (l / 32) + i % 4][l % 32].
 // Block tile BM x BN = (32 WAVES_M WM) x (32 WAVES_N WN); wave tile
 // (32 WM) x (32 WN); a k-step covers 32 of K (two MFMA k-halves).
-// Both operands go global -> LDS with `global_load_lds_dwordx4` (no
+// Both operands go global -> LDS with `buffer_load_dwordx4 ... lds` (no
 // registers): every 1 KiB MFMA fragment of a k-step -- A rows (hi, then lo)
 // and weight tiles -- is one wave instruction, spread evenly over the
 // block's waves.  STAGES-deep ring: halfway through step i a wave waits
 // (vmcnt) for its own copies of stage i + 1, the block barrier publishes that
 // stage to every wave and retires slot i (all of its reads have returned),
 // and the copies of stage i + STAGES go into slot i.  The compiler does not
-// order LDS reads after these copies, hence the explicit waits.  (Measured on
+// order LDS reads after these copies, hence the explicit waits; on gfx950 a
+// copy into LDS retires with vmcnt only (an lgkmcnt(0) wait does not cover
+// it, measured), so the ring waits on vmcnt.  (Measured on
 // the decode shapes: 4 or 5 stages instead of 3, streaming the weights into
 // per-wave registers, staging both operands through registers + ds_write,
 // or two k-steps per stage, are each no faster; the per-half register
@@ -359,6 +361,27 @@ __global__ __launch_bounds__(256) void to_bf16_pair_kernel(const float* __restri
     }
 }
 
+// fragment-packed bf16 hi (+ lo) [rows, K] -> f32 hi + lo (the value a GEMM
+// operand stands for)
+__global__ __launch_bounds__(256) void from_bf16_pair_kernel(const uint16_t* __restrict__ in, int rows, int K,
+                                                             int with_lo, float* __restrict__ y) {
+    const size_t n = (size_t)rows * K, plane = a_plane(rows, K);
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t o = a_pack_index((int)(i / K), (int)(i % K), K);
+        const float hi = __uint_as_float((uint32_t)in[o] << 16);
+        y[i] = with_lo ? hi + __uint_as_float((uint32_t)in[plane + o] << 16) : hi;
+    }
+}
+
+zr_status launch_from_bf16_pair(zr_context* ctx, const uint16_t* in, int rows, int K, int with_lo, float* y) {
+    if (K % 32 != 0) return set_err(ctx, ZR_E_UNSUPPORTED, "GEMM operand width %d is not a multiple of 32", K);
+    const size_t n = (size_t)rows * K;
+    const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 16384);
+    hipLaunchKernelGGL(from_bf16_pair_kernel, dim3(blocks), dim3(256), 0, ctx->stream, in, rows, K, with_lo, y);
+    ZR_LAUNCH_CHECK(ctx);
+    return ZR_OK;
+}
+
 zr_status launch_to_bf16_pair(zr_context* ctx, const float* x, int rows, int K, uint16_t* out, int with_lo) {
     if (K % 32 != 0) return set_err(ctx, ZR_E_UNSUPPORTED, "GEMM operand width %d is not a multiple of 32", K);
     const size_t n = (size_t)rows * K;
@@ -389,6 +412,13 @@ static int device_cus() {
 // (split activations): 32 x 128 tiles for <= 32 rows; 128-row tiles with
 // 256 columns, or 512 for wide / deep products and the LM head.
 static GemmCfg pick_cfg(int m, int n, int k, int epilogue = kEpiStore) {
+    // A vocabulary-wide head over 129-256 rows (the 256-session decode step):
+    // 256 x 256 tiles in 16-wave blocks, four waves per SIMD (128256 columns,
+    // weights streamed from HBM: 319 us against 339 us with 8-wave 256 x 256
+    // blocks).  The same blocks for the other decode products measured no
+    // faster (gate / up) or slower; 64-row tiles, two blocks per CU, are
+    // faster only while the weights sit in the last-level cache.
+    if (m > 128 && m <= 256 && epilogue == kEpiStore && n >= 65536) return {2, 2, 4, 4, 3, false};
     // SwiGLU fused into the GEMM (one split, gate / up tile pairs in a wave) once
     // 128-row tiles fill the CUs; small row counts reduce split-K slabs instead.
     // 128 x 512 tiles once they alone fill two passes over the CUs (prefill-sized
@@ -480,22 +510,21 @@ zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_pack
     hipEvent_t ev;
     timing_mark_begin(ctx, kClassGemm, &ev);
     bool launched = false;
-    if (fused && cfg.wn == 4) {
-        if (split_act)
-            gemm_launch<2, 4, 2, 4, 3, 2, 1>(p, ctx->stream, a, m, k, w_packed, nullptr, n, 0, c_bf16, 1);
-        else
-            gemm_launch<2, 4, 2, 4, 3, 1, 1>(p, ctx->stream, a, m, k, w_packed, nullptr, n, 0, c_bf16, 0);
-        launched = true;
-    } else if (fused) {
-        if (split_act)
-            gemm_launch<2, 2, 2, 4, 3, 2, 1>(p, ctx->stream, a, m, k, w_packed, nullptr, n, 0, c_bf16, 1);
-        else
-            gemm_launch<2, 2, 2, 4, 3, 1, 1>(p, ctx->stream, a, m, k, w_packed, nullptr, n, 0, c_bf16, 0);
-        launched = true;
+#define ZR_GEMM_FUSED_CASE(WMV, WNV, WAM, WAN, ST)                                                     \
+    if (fused && !launched && cfg.wm == WMV && cfg.wn == WNV && cfg.waves_m == WAM &&                  \
+        cfg.waves_n == WAN && cfg.stages == ST) {                                                      \
+        if (split_act)                                                                                 \
+            gemm_launch<WMV, WNV, WAM, WAN, ST, 2, 1>(p, ctx->stream, a, m, k, w_packed, nullptr, n, 0, c_bf16, 1); \
+        else                                                                                           \
+            gemm_launch<WMV, WNV, WAM, WAN, ST, 1, 1>(p, ctx->stream, a, m, k, w_packed, nullptr, n, 0, c_bf16, 0); \
+        launched = true;                                                                               \
     }
+    ZR_GEMM_FUSED_CASE(2, 4, 2, 4, 3)
+    ZR_GEMM_FUSED_CASE(2, 2, 2, 4, 3)
+#undef ZR_GEMM_FUSED_CASE
 #define ZR_GEMM_CASE(WMV, WNV, WAM, WAN, ST)                                                           \
-    if (!launched && cfg.wm == WMV && cfg.wn == WNV && cfg.waves_m == WAM && cfg.waves_n == WAN &&      \
-        cfg.stages == ST) {                                                                            \
+    if (!fused && !launched && cfg.wm == WMV && cfg.wn == WNV && cfg.waves_m == WAM &&                 \
+        cfg.waves_n == WAN && cfg.stages == ST) {                                                      \
         if (split_act)                                                                                 \
             gemm_launch<WMV, WNV, WAM, WAN, ST, 2>(p, ctx->stream, a, m, k, w_packed, dst, n, split_stride); \
         else                                                                                           \
@@ -504,6 +533,7 @@ zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_pack
     }
     ZR_GEMM_CASE(1, 1, 1, 4, 3)
     ZR_GEMM_CASE(2, 1, 1, 4, 3)
+    ZR_GEMM_CASE(2, 2, 4, 4, 3)
     ZR_GEMM_CASE(2, 4, 4, 2, 3)
     ZR_GEMM_CASE(2, 4, 2, 4, 3)
     ZR_GEMM_CASE(2, 2, 2, 4, 3)

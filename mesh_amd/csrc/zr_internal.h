@@ -56,9 +56,10 @@ __host__ __device__ inline size_t a_plane(int rows, int K) { return (size_t)((ro
 // --------------------------------------------------------------- context
 typedef __attribute__((address_space(3))) void lds_void;
 
-// LDS rings fed by global_load_lds (GEMM operands, prefill K/V pages).
+// LDS rings fed by copies into LDS (GEMM operands: buffer_load ... lds;
+// prefill K/V pages: global_load_lds).
 // Block barrier for the LDS ring: wait until at most N of this wave's vector
-// memory ops (its global_load_lds copies of later stages) are outstanding and
+// memory ops (its copies of later stages) are outstanding and
 // all of its LDS reads have returned, then s_barrier.  __syncthreads() would
 // also wait for the later stages' copies (its fence drains vmcnt), which
 // serialises the ring.  The empty asm statements keep the compiler from
@@ -305,6 +306,8 @@ zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_pack
                       uint16_t* c_bf16, int m, int n, int k, int epilogue, Slabs* deferred = nullptr);
 // f32 [rows, K] -> fragment-packed bf16 hi (+ lo) A operand (K % 32 == 0)
 zr_status launch_to_bf16_pair(zr_context* ctx, const float* x, int rows, int K, uint16_t* out, int with_lo);
+// fragment-packed bf16 hi (+ lo) [rows, K] -> f32 hi + lo [rows, K]
+zr_status launch_from_bf16_pair(zr_context* ctx, const uint16_t* in, int rows, int K, int with_lo, float* y);
 zr_status pack_weight(zr_context* ctx, const uint16_t* src /* [K,N] host or device */,
                       int k, int n, uint16_t** out_packed);
 // Packs [K, n1] | [K, n2] | ... (column concatenation) into one packed matrix.

@@ -406,7 +406,10 @@ def test_kv_gather_scatter_round_trip_with_partial_first_page(kv_dtype):
 @pytest.mark.parametrize("m,k,n", [(1, 64, 100), (7, 256, 4112), (32, 2048, 2048), (100, 512, 1000),
                                    (256, 4096, 1024), (300, 128, 64), (128, 4104, 4112), (130, 520, 66000),
                                    # more 128 x 256 tiles than CUs: K split 3 and 4 ways to fill the last pass
-                                   (2108, 4096, 4096), (2108, 14336, 4096)])
+                                   (2108, 4096, 4096), (2108, 14336, 4096),
+                                   # the 256-row decode products (QKV, O, down) and a head over
+                                   # 16-wave 256 x 256 tiles
+                                   (256, 4096, 6144), (256, 4096, 4096), (256, 14336, 4096), (200, 4096, 66000)])
 def test_gemm_matches_fp64(split, m, k, n):
     geo = ModelGeometry(hidden=256, num_heads=4, num_kv_heads=4, num_layers=1, vocab=64, ffn=256)
     ctx = DeviceContext(geo, kv_dtype="f32", max_tokens=16, max_seqs=4, max_pages_per_seq=4, split_activations=split)
@@ -425,6 +428,41 @@ def test_gemm_matches_fp64(split, m, k, n):
     # hi+lo activations: ~2^-16 relative per product; bf16 activations: ~2^-8
     tol = 2e-5 * scale if split else 1.5e-2 * scale
     assert np.max(np.abs(got - ref)) <= tol, np.max(np.abs(got - ref)) / scale
+    ctx.close()
+
+
+@pytest.mark.parametrize("split", [True, False])
+@pytest.mark.parametrize("m,k,f", [(40, 320, 512),       # <= 64 rows: split-K slabs, SwiGLU in the reduce
+                                   (100, 256, 512),      # 65-128 rows: fused, 8-wave 128 x 256 tiles
+                                   (130, 200, 96),       # fused, 128 x 256 tiles, K padded to 224
+                                   (256, 4096, 14336),   # the Llama-3-8B gate / up product of the decode step
+                                   (2108, 1024, 2048)])  # prefill-sized: fused 128 x 512 tiles
+def test_gemm_swiglu_matches_fp64(split, m, k, f):
+    # h = silu(A @ Wg) * (A @ Wu) (tensor_ops.rs:268-278, forward_pass.rs:2286-2289)
+    geo = ModelGeometry(hidden=256, num_heads=4, num_kv_heads=4, num_layers=1, vocab=64, ffn=256)
+    ctx = DeviceContext(geo, kv_dtype="f32", max_tokens=16, max_seqs=4, max_pages_per_seq=4, split_activations=split)
+    rng = np.random.default_rng(m + k + f)
+    a = rng.standard_normal((m, k), dtype=np.float32)
+    wg = O.round_bf16(rng.standard_normal((k, f), dtype=np.float32) * 0.02)
+    wu = O.round_bf16(rng.standard_normal((k, f), dtype=np.float32) * 0.02)
+    from mesh_amd import bf16_bits
+
+    d_a, d_h = DeviceBuffer.from_numpy(ctx, a), DeviceBuffer(ctx, m * f * 4)
+    wgb, wub = bf16_bits(wg), bf16_bits(wu)  # held until the call returns
+    ctx.check(ctx.lib.zr_gemm_swiglu(ctx.h, d_a.ptr, wgb.ctypes.data, wub.ctypes.data, d_h.ptr, m, f, k))
+    got = d_h.download(np.float32, (m, f))
+    a64 = a.astype(np.float64)
+    g, u = a64 @ wg.astype(np.float64), a64 @ wu.astype(np.float64)
+    ref = g / (1.0 + np.exp(-g)) * u
+    scale = np.sqrt(k) * 0.02  # typical |g|, |u|
+    # g and u carry the product's error (the bar of test_gemm_matches_fp64:
+    # 2e-5 scale with hi+lo activations, 1.5e-2 scale with bf16 ones), which
+    # silu(g) * u scales by |silu'(g)| <= 1.1 and |u|, |silu(g)| <= |g|; h
+    # is stored as hi + lo (2^-16 relative) or bf16 (2^-8)
+    eps, rel = (2e-5, 2.0 ** -15) if split else (1.5e-2, 2.0 ** -8)
+    bound = eps * scale * (1.1 * np.abs(u) + np.abs(g) + scale) + rel * np.abs(ref)
+    excess = np.abs(got - ref) - bound
+    assert excess.max() <= 0, (excess.max(), np.abs(got - ref).max())
     ctx.close()
 
 
