@@ -167,6 +167,119 @@ __global__ __launch_bounds__(256) void rope_kv_write_kernel(
     }
 }
 
+// The same stage for head_dim % 8 == 0 in float4 runs, one item per lane of
+// one-wave workgroups (row, y): 4 consecutive rotation pairs of one q / k
+// head -- float4 loads of both halves from every split-K slab, issued 8 slabs
+// at a time and summed in slab order, and the lane's own 4 angles (theta =
+// position * inv_freq[i], cosf / sinf, as above) computed while they are in
+// flight -- or 4 consecutive V elements.  Bit-identical to the scalar kernel.
+template <typename KV>
+__global__ __launch_bounds__(64) void rope_kv_write_vec_kernel(
+    const float* __restrict__ qkv, int qkv_n, size_t qkv_slab, int qkv_stride, float* __restrict__ q_out,
+    int q_cols, int kv_cols,
+    int D, const int* __restrict__ positions, const int* __restrict__ slot,
+    const float* __restrict__ inv_freq, KV* __restrict__ layer_pool, size_t page_elems, int rope, int plain) {
+#pragma clang fp contract(off)
+    const int t = blockIdx.x;
+    const int half = D / 2, g4 = half / 4;
+    const int kv_heads = kv_cols / D, q_heads = q_cols / D;
+    const int n_rot = (q_heads + kv_heads) * g4, n_v = kv_cols / 4;
+    const int j = blockIdx.y * blockDim.x + threadIdx.x;
+    if (j >= n_rot + n_v) return;
+    const float* row = qkv + (size_t)t * qkv_stride;
+    const int s = slot[t];
+    const int page = s / kPageRows, r = s % kPageRows;
+    KV* kpage = layer_pool + (size_t)page * page_elems;
+    KV* vpage = kpage + (size_t)kv_heads * kPageRows * D;
+    auto add4 = [](float4& x, const float4& y) {
+        x.x += y.x;
+        x.y += y.y;
+        x.z += y.z;
+        x.w += y.w;
+    };
+    if (j < n_rot) {
+        const int head = j / g4, i0 = (j - head * g4) * 4;
+        const bool is_q = head < q_heads;
+        const int hh = is_q ? head : head - q_heads;
+        const float* src = row + (is_q ? 0 : q_cols) + hh * D + i0;
+        float4 a4 = *(const float4*)src, b4 = *(const float4*)(src + half);
+        float c[4] = {1.f, 1.f, 1.f, 1.f}, sv[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int s0 = 1; s0 < qkv_n; s0 += 8) {
+            float4 qa[8], qb[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const bool ok = s0 + u < qkv_n;
+                qa[u] = ok ? *(const float4*)(src + (s0 + u) * qkv_slab) : make_float4(0.f, 0.f, 0.f, 0.f);
+                qb[u] = ok ? *(const float4*)(src + (s0 + u) * qkv_slab + half) : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+            if (rope && s0 == 1) {
+                const float pos = (float)positions[t];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const float theta = pos * inv_freq[i0 + u];
+                    c[u] = cosf(theta);
+                    sv[u] = sinf(theta);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (s0 + u < qkv_n) {
+                    add4(a4, qa[u]);
+                    add4(b4, qb[u]);
+                }
+        }
+        if (rope && qkv_n == 1) {
+            const float pos = (float)positions[t];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float theta = pos * inv_freq[i0 + u];
+                c[u] = cosf(theta);
+                sv[u] = sinf(theta);
+            }
+        }
+        float a[4] = {a4.x, a4.y, a4.z, a4.w}, b[4] = {b4.x, b4.y, b4.z, b4.w};
+        if (rope) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float na = a[u] * c[u] - b[u] * sv[u];
+                const float nb = a[u] * sv[u] + b[u] * c[u];
+                a[u] = na;
+                b[u] = nb;
+            }
+        }
+        if (is_q) {
+            float* qo = q_out + (size_t)t * q_cols + hh * D + i0;
+            *(float4*)qo = make_float4(a[0], a[1], a[2], a[3]);
+            *(float4*)(qo + half) = make_float4(b[0], b[1], b[2], b[3]);
+        } else {
+            KV* kt = kpage + (size_t)hh * kPageRows * D;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                store_elem(kt + k_off_of(r, i0 + u, D, plain), a[u]);
+                store_elem(kt + k_off_of(r, half + i0 + u, D, plain), b[u]);
+            }
+        }
+    } else {
+        const int cidx = (j - n_rot) * 4;
+        const int head = cidx / D, d = cidx - head * D;
+        KV* vt = vpage + (size_t)head * kPageRows * D;
+        const float* src = row + q_cols + kv_cols + cidx;
+        float4 v4 = *(const float4*)src;
+        for (int s0 = 1; s0 < qkv_n; s0 += 8) {
+            float4 q[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                q[u] = s0 + u < qkv_n ? *(const float4*)(src + (s0 + u) * qkv_slab) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (s0 + u < qkv_n) add4(v4, q[u]);
+        }
+        const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) store_elem(vt + v_off_of(r, d + u, D, plain), vv[u]);
+    }
+}
+
 static inline size_t page_elems_of(const zr_context* ctx) {
     return (size_t)2 * ctx->kv_cols * kPageRows;
 }
@@ -181,7 +294,29 @@ zr_status launch_rope_kv_write(zr_context* ctx, StagedMeta* st, int layer, const
     const dim3 grid(st->total_q, (items + 255) / 256);
     hipEvent_t ev;
     timing_mark_begin(ctx, kClassNormRopeKv, &ev);
-    if (ctx->desc.kv_dtype == ZR_DTYPE_BF16) {
+    // float4 runs need 4 | D / 2 and 16 B aligned rows and slabs.  Measured
+    // on the decode steps: at 256 rows the float4 kernel takes 4 % off the
+    // norm / RoPE class; at 32 rows (16 split-K slabs) one pair per thread,
+    // spread over 4x more waves, is 2 % faster per step.
+    const bool vec = ctx->head_dim % 8 == 0 && stride % 4 == 0 && qkv.stride % 4 == 0 && st->total_q >= 128;
+    if (vec) {
+        // one float4 item per lane: (q + kv heads) x D / 8 rotations + kv_cols / 4 V runs per row,
+        // one-wave workgroups so that small batches still spread over the CUs
+        const int vitems = (ctx->q_cols + ctx->kv_cols) / 8 + ctx->kv_cols / 4;
+        const dim3 vgrid(st->total_q, (vitems + 63) / 64);
+        if (ctx->desc.kv_dtype == ZR_DTYPE_BF16)
+            hipLaunchKernelGGL(rope_kv_write_vec_kernel<uint16_t>, vgrid, dim3(64), 0, ctx->stream,
+                               qkv.ptr, qkv.n, qkv.stride, stride, q_out, ctx->q_cols, ctx->kv_cols, ctx->head_dim,
+                               st->positions, st->slot_mapping, ctx->inv_freq,
+                               (uint16_t*)ctx->kv_pool + (size_t)layer * ctx->n_pages * pe, pe, rope,
+                               ctx->plain_kv ? 1 : 0);
+        else
+            hipLaunchKernelGGL(rope_kv_write_vec_kernel<float>, vgrid, dim3(64), 0, ctx->stream,
+                               qkv.ptr, qkv.n, qkv.stride, stride, q_out, ctx->q_cols, ctx->kv_cols, ctx->head_dim,
+                               st->positions, st->slot_mapping, ctx->inv_freq,
+                               (float*)ctx->kv_pool + (size_t)layer * ctx->n_pages * pe, pe, rope,
+                               ctx->plain_kv ? 1 : 0);
+    } else if (ctx->desc.kv_dtype == ZR_DTYPE_BF16) {
         uint16_t* pool = (uint16_t*)ctx->kv_pool + (size_t)layer * ctx->n_pages * pe;
         hipLaunchKernelGGL(rope_kv_write_kernel<uint16_t>, grid, dim3(256), 0, ctx->stream,
                            qkv.ptr, qkv.n, qkv.stride, stride, q_out, ctx->q_cols, ctx->kv_cols, ctx->head_dim, st->positions,

@@ -136,6 +136,59 @@ def test_rope_kv_write_rotates_q_and_k_at_large_positions(kv_dtype, heads, kv_he
     ctx.close()
 
 
+@pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("heads,kv_heads,D,base", [(32, 4, 64, 1e4), (32, 8, 128, 5e5)])
+def test_rope_kv_write_float4_path_matches_scalar_path_bit_exact(kv_dtype, heads, kv_heads, D, base):
+    """From 128 rows the stage runs its float4 kernel, which must reproduce the
+    scalar kernel bit for bit (same angles, same slab order).  The same 160 rows
+    (4 sessions x 40, positions from 1000 k + 7) run as one launch and as two
+    80-row launches on identically prepared sessions: q and the appended K / V
+    rows must be equal, and q within the oracle's RoPE bound."""
+    from mesh_amd import KVCacheSnapshot
+
+    Q, KV = heads * D, kv_heads * D
+    geo = ModelGeometry(hidden=Q, num_heads=heads, num_kv_heads=kv_heads, num_layers=1, vocab=64, ffn=64,
+                        rope_base=base)
+    ctx = DeviceContext(geo, kv_dtype=kv_dtype, max_tokens=256, max_seqs=8, max_pages_per_seq=64)
+    ctx.create_kv_pool(256)
+    rng = np.random.default_rng(D + 1)
+    rows, prefix = 40, [1000 * k + 7 for k in range(4)]
+    qkv = rng.standard_normal((4 * rows, Q + 2 * KV), dtype=np.float32)
+
+    def prepared():
+        out = []
+        for p in prefix:  # a 3-row window ending at position p - 1: the new rows land at p ..
+            b = ctx.new_backend(8192)
+            k = rng.standard_normal((1, 3, KV), dtype=np.float32)
+            b.import_kv_cache(KVCacheSnapshot(p, 3, k, k.copy()))
+            out.append(b)
+        return out
+
+    def run(backends, qkv_rows):
+        st = stage_mixed(ctx, backends, [rows] * len(backends))
+        d_qkv = DeviceBuffer.from_numpy(ctx, qkv_rows)
+        d_q = DeviceBuffer(ctx, 4 * qkv_rows.shape[0] * Q)
+        ctx.check(ctx.lib.zr_rope_kv_write(ctx.h, st, 0, d_qkv.ptr, d_q.ptr, 1))
+        ctx.lib.zr_staged_destroy(st)
+        return d_q.download(np.float32, (qkv_rows.shape[0], Q))
+
+    one = prepared()
+    q_vec = run(one, qkv)
+    two = prepared()
+    q_scalar = np.concatenate([run(two[:2], qkv[:2 * rows]), run(two[2:], qkv[2 * rows:])])
+    np.testing.assert_array_equal(q_vec, q_scalar)
+    for b1, b2 in zip(one, two):
+        s1, s2 = b1.export_kv_cache(), b2.export_kv_cache()
+        assert s1.next_position == s2.next_position and s1.cached_tokens == 3 + rows
+        np.testing.assert_array_equal(s1.keys[:, -rows:], s2.keys[:, -rows:])
+        np.testing.assert_array_equal(s1.values[:, -rows:], s2.values[:, -rows:])
+    pos = np.concatenate([np.arange(p, p + rows) for p in prefix]).astype(np.uint32)
+    want_q = O.apply_rope(qkv[:, :Q], pos, D, base)
+    scale = np.abs(qkv).max(1, keepdims=True)
+    assert np.all(np.abs(q_vec - want_q) <= 2e-5 * scale)
+    ctx.close()
+
+
 # ------------------------------------------------ C1: attention + append --
 def c1_inputs(seed=0xC1):
     rng = np.random.default_rng(seed)
