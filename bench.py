@@ -12,8 +12,12 @@ bf16 N(0, 0.02) generated on the device, the KV pages of every session's
 context are filled with N(0, 1) bf16 (standing in for prefill output), and the
 per-step metadata (page tables after each step's append) is staged on the
 device ahead of time.  Each step feeds its greedy tokens to the next step on
-the device.  The attention kernel's duration comes from HIP events recorded on
-the provider's stream around every attention launch in the timed region.
+the device.  Each timed step is replayed from a HIP graph of its staged launch
+sequence, captured before the timing (the fused profile's ReplayPreferred
+strategy); as many further steps launched kernel by kernel are reported as
+"eager".  The attention kernel's duration (the roofline) comes from HIP events
+recorded on the provider's stream around every attention launch of the eager
+steps (events recorded by graph nodes do not time).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--skip-bs32] [--skip-soak]
        python bench.py --calibrate-copy   (a plain 1 GiB device copy, for scaling
@@ -240,6 +244,31 @@ class GpuDecodeBench:
             toks, out = out, toks
         return time.perf_counter() - t0, toks
 
+    def run_graphs(self, first, count):
+        """Runs staged steps [first, first + count), each replayed from a HIP
+        graph of its launch sequence (zr_graph_capture_staged), the way the
+        fused profile executes a step (ReplayPreferred).  The graphs are
+        captured before the timing and the first is replayed once untimed.
+        Returns seconds."""
+        ctx, lib = self.ctx, self.ctx.lib
+        graphs = []
+        try:
+            for i in range(first, first + count):
+                gph = C.c_void_p()
+                ctx.check(lib.zr_graph_capture_staged(ctx.h, self.staged[i], self.tok[i % 2], self.tok[(i + 1) % 2],
+                                                      None, C.byref(gph)))
+                graphs.append(gph)
+            ctx.check(lib.zr_graph_launch(ctx.h, graphs[0]))
+            ctx.check(lib.zr_synchronize(ctx.h))
+            t0 = time.perf_counter()
+            for gph in graphs:
+                ctx.check(lib.zr_graph_launch(ctx.h, gph))
+            ctx.check(lib.zr_synchronize(ctx.h))
+            return time.perf_counter() - t0
+        finally:
+            for gph in graphs:
+                lib.zr_graph_destroy(gph)
+
     def tokens(self, i):
         out = np.zeros(self.B, np.uint32)
         self.ctx.check(self.ctx.lib.zr_memcpy_d2h(self.ctx.h, out.ctypes.data, self.tok[i % 2], out.nbytes))
@@ -264,23 +293,29 @@ BREAKDOWN_STEPS = 2
 
 
 def measure(name, steps, warmup):
-    """Timed region: `steps` decode steps with HIP events around the attention
-    launches only (the roofline figure).  Then BREAKDOWN_STEPS more steps with
-    events around every kernel class, for the per-class time split.  Then the
-    same sessions decode `warmup` + `steps` more steps through the host entry
-    point (zrh_decode_step_batch), timed end to end with the host work."""
-    bench = GpuDecodeBench(name, steps + warmup + BREAKDOWN_STEPS, host_steps=steps + warmup)
+    """Timed region: `steps` decode steps, each replayed from the HIP graph of
+    its staged launch sequence.  Then `steps` more steps launched kernel by
+    kernel (zr_forward_staged_async) with HIP events around the attention
+    launches only (the roofline figure: events recorded by graph nodes do not
+    time), then BREAKDOWN_STEPS with events around every kernel class, for the
+    per-class time split.  Then the same sessions decode `warmup` + `steps`
+    more steps through the host entry point (zrh_decode_step_batch), timed
+    end to end with the host work."""
+    bench = GpuDecodeBench(name, warmup + 2 * steps + BREAKDOWN_STEPS, host_steps=steps + warmup)
     g, B = bench.geo, bench.B
     bench.run(0, warmup, timed=False)
-    dt, ms_t, n_t = bench.run(warmup, steps, timed=True, mask=1)
+    dt = bench.run_graphs(warmup, steps)
     toks = bench.tokens(warmup + steps)
-    _, ms_b, n_b = bench.run(warmup + steps, BREAKDOWN_STEPS, timed=True, mask=0xF)
     assert toks.max() < g.vocab
+    dt_eager, ms_t, n_t = bench.run(warmup + steps, steps, timed=True, mask=1)
+    assert bench.tokens(warmup + 2 * steps).max() < g.vocab
+    _, ms_b, n_b = bench.run(warmup + 2 * steps, BREAKDOWN_STEPS, timed=True, mask=0xF)
     ms_per_step = dt / steps * 1000.0
     # attention: algorithmic bytes per launch (K+V of every attended row, bf16;
-    # Q in and the output out, f32), averaged over the timed launches
+    # Q in and the output out, f32), averaged over the eager steps' launches
     timed_rows = bench.kv_rows[warmup:warmup + steps]
-    kv_bytes = sum(timed_rows) * g.num_layers * g.kv_cols * 2 * 2
+    eager_rows = bench.kv_rows[warmup + steps:warmup + 2 * steps]
+    kv_bytes = sum(eager_rows) * g.num_layers * g.kv_cols * 2 * 2
     qo_bytes = steps * g.num_layers * B * g.q_cols * 4 * 2
     attn_launches = n_t[0]
     attn_bytes_per_launch = (kv_bytes + qo_bytes) / max(attn_launches, 1)
@@ -304,6 +339,10 @@ def measure(name, steps, warmup):
                   frac=gemm_tflops / MFMA_BF16_PEAK_TFLOPS,
                   weight_gbs=(gemm_flops(g, B) / B) * nb / (ms_b[1] * 1e-3) / 1e9 if ms_b[1] > 0 else 0.0),
     )
+    result["eager"] = dict(entry="zr_forward_staged_async", steps=steps, ms_per_step=dt_eager / steps * 1e3,
+                           tokens_per_s=B * steps / dt_eager,
+                           includes="the same decode step launched kernel by kernel instead of replayed, "
+                                    "HIP events around its attention launches")
     result["kv_append"] = measure_kv_append(bench)
     # end to end through the boundary's host entry point, host work included
     _, last = bench.run_host(warmup, bench.tokens(warmup + steps + BREAKDOWN_STEPS))
@@ -762,7 +801,7 @@ def main():
                     workload=r["workload"], step_roofline_frac=r["step_roofline_frac"],
                     attention_gbs=r["attention"]["achieved_gbs"], kernel_ms_per_step=r["kernel_ms_per_step"],
                     gemm_tflops=r["gemm"]["achieved_tflops"], gemm_weight_gbs=r["gemm"]["weight_gbs"],
-                    host_path=r["host_path"])
+                    host_path=r["host_path"], eager=r["eager"])
     soak = None if a.skip_soak else measure_soak(max(4, a.steps // 2), 2)
     kv_snapshot = None if a.skip_kv_snapshot else measure_kv_snapshot()
     sampling = None if a.skip_sampling else measure_sampling()
@@ -778,6 +817,8 @@ def main():
         "config": {"workload": main_r["workload"], "sessions": main_r["batch"], "layers": main_r["layers"],
                    "context_tokens": main_r["context_tokens"], "context_max": main_r["context_max"],
                    "parallelism": "one worker shard (1 of 1) on one GPU",
+                   "step_launch": "each step replayed from a HIP graph of its staged launch sequence "
+                                  "(zr_graph_launch); kernel-by-kernel launch under eager",
                    "gemm_a_operand": "bf16 hi + lo pair (activation = hi + lo to 2^-16), fp32 accumulation"},
         "roofline": {"bound": "hbm", "kernel": "paged_attention_kernel", "achieved": att["achieved_gbs"],
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": att["frac"], "traffic": measured_traffic(),
@@ -787,6 +828,7 @@ def main():
                           "bytes_per_step": main_r["step_bytes"]},
         "kernel_ms_per_step": main_r["kernel_ms_per_step"],
         "host_path": main_r["host_path"],
+        "eager": main_r["eager"],
         "kv_append": main_r["kv_append"],
         "gemm_mfma": {"achieved": main_r["gemm"]["achieved_tflops"], "peak": MFMA_BF16_PEAK_TFLOPS,
                       "unit": "TFLOP/s", "frac": main_r["gemm"]["frac"], "mfma_ops_per_flop": 2,

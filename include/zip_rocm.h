@@ -164,6 +164,20 @@ zr_status zr_forward_staged_async(zr_context* ctx, zr_staged* st, const uint32_t
                                   uint32_t* d_out_tokens, float* d_out_logits);
 /* Waits for the context stream; reports a device-fed id error (above). */
 zr_status zr_synchronize(zr_context* ctx);
+/* Replay of a staged step (GraphCaptureStrategy::ReplayPreferred, the fused
+ * profile's capture strategy, fast_path.rs:831-837): records exactly what
+ * zr_forward_staged_async(ctx, st, d_tokens, d_out_tokens, d_out_logits)
+ * enqueues -- kernels and, for device-fed ids, the id-check copy; no memset
+ * or allocation -- into a HIP graph on the context stream.  zr_graph_launch
+ * enqueues the recorded step again (same staged metadata and buffers, which
+ * must stay alive), with the same id check at the next zr_synchronize.
+ * Capture is refused while per-class timing is on (events recorded by graph
+ * nodes do not time).  Destroy a graph before its context. */
+typedef struct zr_graph zr_graph;
+zr_status zr_graph_capture_staged(zr_context* ctx, zr_staged* st, const uint32_t* d_tokens,
+                                  uint32_t* d_out_tokens, float* d_out_logits, zr_graph** out);
+zr_status zr_graph_launch(zr_context* ctx, zr_graph* g);
+void zr_graph_destroy(zr_graph* g);
 
 /* ------------------------------------------------------ op-level entries --- */
 /* Ragged packing on the GPU: device outputs cu_q/cu_k [num_seqs+1],

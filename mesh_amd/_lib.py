@@ -111,6 +111,9 @@ SIGNATURES = [
     ("zr_staged_destroy", None, [C.c_void_p]),
     ("zr_forward_staged_async", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
     ("zr_synchronize", C.c_int, [C.c_void_p]),
+    ("zr_graph_capture_staged", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, c_void_pp]),
+    ("zr_graph_launch", C.c_int, [C.c_void_p, C.c_void_p]),
+    ("zr_graph_destroy", None, [C.c_void_p]),
     ("zr_pack", C.c_int, [C.c_void_p, C.POINTER(Microbatch), c_int_p, c_int_p, c_int_p, c_int_p, c_int_p]),
     ("zr_rope_kv_write", C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int]),
     ("zr_attention", C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]),

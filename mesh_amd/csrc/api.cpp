@@ -752,6 +752,66 @@ zr_status zr_synchronize(zr_context* ctx) {
     return ZR_OK;
 }
 
+struct zr_graph {
+    zr_context* ctx = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    bool token_check = false;  // the step copies the device id-check word to the host
+};
+
+zr_status zr_graph_capture_staged(zr_context* ctx, zr_staged* s, const uint32_t* d_tokens, uint32_t* d_out_tokens,
+                                  float* d_out_logits, zr_graph** out) {
+    StagedMeta* st = (StagedMeta*)s;
+    if (!ctx || !st || !out) return set_global_err(ZR_E_INVALID, "null argument");
+    if (st->ctx != ctx) return set_err(ctx, ZR_E_INVALID, "staged microbatch of another context");
+    // HIP events recorded by graph nodes do not time (hipEventElapsedTime
+    // reports an invalid handle for them), so timing stays eager-only
+    if (ctx->timing.enabled) return set_err(ctx, ZR_E_INVALID, "graph capture with per-class timing on");
+    ZR_HIP(ctx, hipSetDevice(ctx->device));
+    // a step pending on the stream finishes first; its id check stays pending
+    ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    const bool pending = ctx->token_check_pending;
+    ZR_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    zr_status rc = run_forward(ctx, st, d_tokens, d_out_tokens, d_out_logits, nullptr);
+    hipGraph_t graph = nullptr;
+    const hipError_t e_end = hipStreamEndCapture(ctx->stream, &graph);
+    ctx->token_check_pending = pending;  // nothing ran yet
+    if (!rc && e_end != hipSuccess) rc = set_err(ctx, ZR_E_HIP, "graph capture: %s", hipGetErrorString(e_end));
+    hipGraphExec_t exec = nullptr;
+    if (!rc) {
+        const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        if (e != hipSuccess) rc = set_err(ctx, ZR_E_HIP, "graph instantiate: %s", hipGetErrorString(e));
+    }
+    if (rc) {
+        if (graph) (void)hipGraphDestroy(graph);
+        (void)hipGetLastError();
+        return rc;
+    }
+    zr_graph* g = new zr_graph;
+    g->ctx = ctx;
+    g->graph = graph;
+    g->exec = exec;
+    g->token_check = d_tokens != nullptr;
+    *out = g;
+    return ZR_OK;
+}
+
+zr_status zr_graph_launch(zr_context* ctx, zr_graph* g) {
+    if (!ctx || !g) return set_global_err(ZR_E_INVALID, "null argument");
+    if (g->ctx != ctx) return set_err(ctx, ZR_E_INVALID, "graph of another context");
+    ZR_HIP(ctx, hipGraphLaunch(g->exec, ctx->stream));
+    if (g->token_check) ctx->token_check_pending = true;
+    return ZR_OK;
+}
+
+void zr_graph_destroy(zr_graph* g) {
+    if (!g) return;
+    if (g->ctx && g->ctx->stream) (void)hipStreamSynchronize(g->ctx->stream);
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    delete g;
+}
+
 zr_status zr_forward(zr_context* ctx, const zr_microbatch* mb, uint32_t* out_tokens, float* out_logits,
                      float* out_partials) {
     if (!ctx || !mb) return set_global_err(ZR_E_INVALID, "null argument");
