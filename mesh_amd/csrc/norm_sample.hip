@@ -121,17 +121,18 @@ __global__ __launch_bounds__(NT) void rms_norm_vec_kernel(const float* __restric
         if (i4 < n4) {
             float4 a = *(const float4*)(x + base + 4 * (size_t)i4);
             if (residual_in) {
-                // slabs summed in slab order, their loads issued 8 at a time
+                // slabs summed in slab order, their loads issued 16 at a time
+                // (one round trip for the split-K products of a decode step)
                 const float* rp = residual_in + base + 4 * (size_t)i4;
                 float4 rr = *(const float4*)rp;
-                for (int s0 = 1; s0 < res_n; s0 += 8) {
-                    float4 q[8];
+                for (int s0 = 1; s0 < res_n; s0 += 16) {
+                    float4 q[16];
 #pragma unroll
-                    for (int u = 0; u < 8; ++u)
+                    for (int u = 0; u < 16; ++u)
                         q[u] = s0 + u < res_n ? *(const float4*)(rp + (size_t)(s0 + u) * res_stride)
                                               : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-                    for (int u = 0; u < 8; ++u)
+                    for (int u = 0; u < 16; ++u)
                         if (s0 + u < res_n) {
                             rr.x += q[u].x;
                             rr.y += q[u].y;
@@ -152,6 +153,13 @@ __global__ __launch_bounds__(NT) void rms_norm_vec_kernel(const float* __restric
             ss += a.w * a.w;
         }
     }
+    // gamma is fetched while the row sum is reduced
+    float4 gv[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int i4 = threadIdx.x + j * NT;
+        gv[j] = i4 < n4 ? *(const float4*)(gamma + 4 * (size_t)i4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     ss = wave_sum(ss);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
     __syncthreads();
@@ -163,7 +171,7 @@ __global__ __launch_bounds__(NT) void rms_norm_vec_kernel(const float* __restric
     for (int j = 0; j < NV; ++j) {
         const int i4 = threadIdx.x + j * NT;
         if (i4 >= n4) continue;
-        const float4 g = *(const float4*)(gamma + 4 * (size_t)i4);
+        const float4 g = gv[j];
         float y[4] = {v[j].x * inv_rms * g.x, v[j].y * inv_rms * g.y, v[j].z * inv_rms * g.z,
                       v[j].w * inv_rms * g.w};
         if (y_bf16) {

@@ -462,7 +462,10 @@ def test_kv_gather_scatter_round_trip_with_partial_first_page(kv_dtype):
                                    (2108, 4096, 4096), (2108, 14336, 4096),
                                    # the 256-row decode products (QKV, O, down) and a head over
                                    # 16-wave 256 x 256 tiles
-                                   (256, 4096, 6144), (256, 4096, 4096), (256, 14336, 4096), (200, 4096, 66000)])
+                                   (256, 4096, 6144), (256, 4096, 4096), (256, 14336, 4096), (200, 4096, 66000),
+                                   # the 32-session TinyLlama products: QKV (11 splits), down (16), an
+                                   # unsplit vocabulary head
+                                   (32, 2048, 2560), (32, 5632, 2048), (32, 2048, 32000)])
 def test_gemm_matches_fp64(split, m, k, n):
     geo = ModelGeometry(hidden=256, num_heads=4, num_kv_heads=4, num_layers=1, vocab=64, ffn=256)
     ctx = DeviceContext(geo, kv_dtype="f32", max_tokens=16, max_seqs=4, max_pages_per_seq=4, split_activations=split)
@@ -486,6 +489,7 @@ def test_gemm_matches_fp64(split, m, k, n):
 
 @pytest.mark.parametrize("split", [True, False])
 @pytest.mark.parametrize("m,k,f", [(40, 320, 512),       # <= 64 rows: split-K slabs, SwiGLU in the reduce
+                                   (32, 2048, 5632),     # the 32-session TinyLlama gate / up: 2 slabs
                                    (100, 256, 512),      # 65-128 rows: fused, 8-wave 128 x 256 tiles
                                    (130, 200, 96),       # fused, 128 x 256 tiles, K padded to 224
                                    (256, 4096, 14336),   # the Llama-3-8B gate / up product of the decode step
