@@ -645,6 +645,62 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(const float* __res
     const size_t pstride = (size_t)kv_heads * 16 * (D + 2);
     const float* base = part + ((size_t)first * kv_heads + kvh) * 16 * (D + 2);
     const int tid = threadIdx.x;
+    if (nparts <= 16) {
+        // One round trip: thread (column tid / 16, dims D / 16 from (tid % 16) D / 16)
+        // loads (m, l) and its dims of every split at once (partial rows are
+        // 8-byte aligned), then combines them in registers -- the same
+        // operations in the same order as the general path below.
+        constexpr int DT = D / 16, P2 = DT / 2;
+        const int c = tid >> 4, d0 = (tid & 15) * DT;
+        if (c >= ncols) return;
+        const float* pc = base + (size_t)c * (D + 2);
+        float2 ml[16], ov[16][P2];
+#pragma unroll
+        for (int s = 0; s < 16; ++s)
+            if (s < nparts) {
+                ml[s] = *(const float2*)(pc + s * pstride);
+#pragma unroll
+                for (int k = 0; k < P2; ++k) ov[s][k] = *(const float2*)(pc + s * pstride + 2 + d0 + 2 * k);
+            }
+        float M = -INFINITY;
+#pragma unroll
+        for (int s = 0; s < 16; ++s)
+            if (s < nparts) M = fmaxf(M, ml[s].x);
+        float L = 0.0f;
+#pragma unroll
+        for (int s = 0; s < 16; ++s)
+            if (s < nparts && ml[s].x != -INFINITY) L = L + __fmul_rn(ml[s].y, exp2f(ml[s].x - M));
+        const float Linv = 1.0f / L;
+        float acc[DT];
+#pragma unroll
+        for (int j = 0; j < DT; ++j) acc[j] = 0.0f;
+#pragma unroll
+        for (int s = 0; s < 16; ++s)
+            if (s < nparts) {
+                const float w = ml[s].x != -INFINITY ? exp2f(ml[s].x - M) * Linv : 0.0f;
+#pragma unroll
+                for (int k = 0; k < P2; ++k) {
+                    acc[2 * k] = fmaf(ov[s][k].x, w, acc[2 * k]);
+                    acc[2 * k + 1] = fmaf(ov[s][k].y, w, acc[2 * k + 1]);
+                }
+            }
+        const int qi = c / G, g = c - qi * G;
+        const int row = cu_q[seq] + q0 + qi;
+#pragma unroll
+        for (int j = 0; j < DT; ++j) {
+            const int col = (kvh * G + g) * D + d0 + j;
+            if (out_bf16) {
+                uint16_t hi, lo;
+                split_bf16(acc[j], hi, lo);
+                const size_t o = a_pack_index(row, col, q_cols);
+                out_bf16[o] = hi;
+                if (lo_offset) out_bf16[lo_offset + o] = lo;
+            } else {
+                out[(size_t)row * q_cols + col] = acc[j];
+            }
+        }
+        return;
+    }
     // column max over splits: 16 threads per column
     {
         const int c = tid & 15, pl = tid >> 4;

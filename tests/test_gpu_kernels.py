@@ -260,6 +260,31 @@ def test_c1_paged_gqa_decode_attention_and_append(kv_dtype):
     ctx.close()
 
 
+@pytest.mark.parametrize("pages_per_split", [1, 3])
+def test_c1_decode_attention_merges_many_splits(monkeypatch, pages_per_split):
+    """Decode tiles split every 1 or 3 pages (ZR_ATTN_PAGES_PER_SPLIT): up to
+    32 splits per tile at 512 keys, so the merge runs both its one-round-trip
+    form (at most 16 splits) and its general form (more), against the
+    oracle's attention over the same pages."""
+    monkeypatch.setenv("ZR_ATTN_PAGES_PER_SPLIT", str(pages_per_split))
+    ctx, backends, (B, ctxlens, order, Q, K, V), out = run_c1("bf16")
+    pages = (ctxlens + 15) // 16
+    assert pages_per_split > 1 or (pages.max() > 16 and pages.min() <= 16)  # both merge forms
+    for s in range(B):
+        o = O.Session(1, 256, 16, 4096, kv_round_bf16=True)
+        o.append_layer(0, K[s], V[s])
+        ok, ov = o.gather(0)
+        want = np.zeros(32 * 64, np.float32)
+        for h in range(32):
+            kvh = h // 8
+            want[h * 64:(h + 1) * 64] = O.causal_attention_with_prefix(
+                Q[s, h * 64:(h + 1) * 64][None], ok[:, kvh * 64:(kvh + 1) * 64], ov[:, kvh * 64:(kvh + 1) * 64],
+                1 / math.sqrt(64), ctxlens[s] - 1)[0]
+        err = max_rel_err_rows(out[s], want, 64)
+        assert err <= ATTN_RTOL, (s, err)
+    ctx.close()
+
+
 def test_c1_raw_page_row_holds_appended_kv_in_pool_layout():
     ctx, backends, (B, ctxlens, order, Q, K, V), out = run_c1("f32")
     s = 3
