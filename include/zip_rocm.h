@@ -194,6 +194,16 @@ zr_status zr_rope_kv_write(zr_context* ctx, zr_staged* st, int layer, const floa
  * staged microbatch for `layer`: d_q device [sum q_len, q_cols] f32 (RoPE'd),
  * d_out device [sum q_len, q_cols] f32. */
 zr_status zr_attention(zr_context* ctx, zr_staged* st, int layer, const float* d_q, float* d_out);
+/* The RopeKvWrite and Attention stages in one launch, for a staged
+ * microbatch whose sequences each have one query row (decode; the MFMA page
+ * layout): d_qkv as for zr_rope_kv_write, d_out as for zr_attention.  The
+ * same q, K / V rows and outputs as zr_rope_kv_write + zr_attention, bit for
+ * bit; the forward pass takes this path for such microbatches.  Other
+ * microbatches: ZR_E_UNSUPPORTED.  (The RopeKvWrite and PagedAttention stages
+ * of FusedKernelStage, engine.rs:124-132; RoPE tensor_ops.rs:509-560, append
+ * forward_pass.rs:462-521, attention forward_pass.rs:2838-2895.) */
+zr_status zr_rope_attention(zr_context* ctx, zr_staged* st, int layer, const float* d_qkv, float* d_out,
+                            int rope);
 /* Checkpoint KV handoff gather (build_active_tensors + retain_suffix window,
  * forward_pass.rs:633-680, 1169-1204): rows [first_row, first_row + n_rows)
  * of one sequence's live window, all layers, into dst_k/dst_v

@@ -300,6 +300,17 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
         st->h_psplits.swap(s2);
     }
     st->n_pblocks = (int)st->h_pblocks.size();
+    // every sequence one query row in the MFMA page layout: the decode kernel
+    // can take RoPE + KV append too (launch_attention_rope).  The forward pass
+    // does so when splits stream >= 48 pages: the q slab loads and the last
+    // split's append then add little to a split (256 Llama-3 sessions, ~96
+    // pages per split: 17.9 -> 17.3 ms per step), where 12-page splits
+    // (32 TinyLlama sessions) lose more than the RoPE launch costs
+    // (1.49 -> 1.59 ms).  ZR_ATTN_FUSE_ROPE=1 / 0 forces either path.
+    st->pure_decode = !ctx->plain_kv && S > 0 && st->n_pblocks == 0;
+    for (int s = 0; s < S && st->pure_decode; ++s) st->pure_decode = mb->q_len[s] == 1;
+    st->fuse_rope = st->pure_decode && pps >= 48;
+    if (const char* env = getenv("ZR_ATTN_FUSE_ROPE")) st->fuse_rope = st->pure_decode && atoi(env) != 0;
 
     const size_t need_part = (size_t)st->n_part_items * ctx->local_kv_heads * 16 * (ctx->head_dim + 2);
     if (need_part > ctx->attn_part_floats) {
@@ -328,6 +339,7 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     const size_t host_bytes = off;
     const size_t o_cuq = take(4 * (S + 1)), o_cuk = take(4 * (S + 1)), o_pos = take(4 * (size_t)total_q);
     const size_t o_slot = take(4 * (size_t)total_q), o_seq = take(4 * (size_t)total_q), o_last = take(4 * S);
+    const size_t o_rcs = take(8 * (size_t)total_q * (ctx->head_dim / 2));
     const size_t total_bytes = off;
     if (total_bytes > st->cap_bytes) {
         hipStreamSynchronize(ctx->stream);
@@ -371,6 +383,7 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     st->slot_mapping = (int*)(db + o_slot);
     st->seq_ids = (int*)(db + o_seq);
     st->last_rows = (int*)(db + o_last);
+    st->rope_cs = (float2*)(db + o_rcs);
     st->h_q_len.assign(mb->q_len, mb->q_len + S);
     st->h_kv_before.assign(mb->kv_before, mb->kv_before + S);
     ZR_HIP(ctx, hipMemcpyAsync(st->dev, hb, host_bytes, hipMemcpyHostToDevice, ctx->stream));
@@ -409,8 +422,12 @@ static zr_status run_forward(zr_context* ctx, StagedMeta* st, const uint32_t* d_
             return rc;
         Slabs qkv(ctx->qkv);
         if ((rc = launch_gemm(ctx, ctx->xa, L.w_qkv, ctx->qkv, nullptr, T, QKV, H, kEpiStore, &qkv))) return rc;
-        if ((rc = launch_rope_kv_write(ctx, st, l, qkv, ctx->q_rope, 1))) return rc;
-        if ((rc = launch_attention(ctx, st, l, ctx->q_rope, nullptr, ctx->attn_a))) return rc;
+        if (st->fuse_rope) {  // RoPE + KV append inside the decode attention launch
+            if ((rc = launch_attention_rope(ctx, st, l, qkv, 1, nullptr, ctx->attn_a))) return rc;
+        } else {
+            if ((rc = launch_rope_kv_write(ctx, st, l, qkv, ctx->q_rope, 1))) return rc;
+            if ((rc = launch_attention(ctx, st, l, ctx->q_rope, nullptr, ctx->attn_a))) return rc;
+        }
         Slabs o(ctx->proj);
         if ((rc = launch_gemm(ctx, ctx->attn_a, L.w_o, ctx->proj, nullptr, T, H, ctx->q_cols, kEpiStore,
                               h_partials ? nullptr : &o)))
@@ -855,6 +872,15 @@ zr_status zr_rope_kv_write(zr_context* ctx, zr_staged* s, int layer, const float
     if (!ctx || !st || !d_qkv || !d_q_out) return set_global_err(ZR_E_INVALID, "null argument");
     if (layer < 0 || layer >= ctx->desc.num_layers) return set_err(ctx, ZR_E_INVALID, "Invalid layer index: %d", layer);
     zr_status rc = launch_rope_kv_write(ctx, st, layer, d_qkv, d_q_out, rope);
+    if (!rc) ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return rc;
+}
+
+zr_status zr_rope_attention(zr_context* ctx, zr_staged* s, int layer, const float* d_qkv, float* d_out, int rope) {
+    StagedMeta* st = (StagedMeta*)s;
+    if (!ctx || !st || !d_qkv || !d_out) return set_global_err(ZR_E_INVALID, "null argument");
+    if (layer < 0 || layer >= ctx->desc.num_layers) return set_err(ctx, ZR_E_INVALID, "Invalid layer index: %d", layer);
+    zr_status rc = launch_attention_rope(ctx, st, layer, Slabs(d_qkv), rope, d_out, nullptr);
     if (!rc) ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
     return rc;
 }

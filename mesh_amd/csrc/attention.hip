@@ -205,9 +205,19 @@ struct AttnArgs {
     float* out_f32;          // final output of single-split tiles ([T, q_cols]) ...
     uint16_t* out_bf16;      // ... or as the bf16 A operand (lo half at out_lo_offset)
     size_t out_lo_offset;
+    // FUSE (pure decode microbatches): q and the new K / V rows come from the
+    // QKV product's split-K slabs, rotated with the step's (cos, sin) table,
+    // and each tile's last split appends its kv head's K / V row to the page
+    const float* qkv;        // slab 0 of [T, qkv_stride]
+    int qkv_n;               // slabs, summed in slab order
+    size_t qkv_slab;         // floats from one slab to the next
+    int qkv_stride;          // q_cols + 2 kv_cols
+    int kv_cols;
+    const int* slot;         // [T] pool slot of each row's new K / V
+    const float2* rope_cs;   // [T][D / 2] (cos, sin), or null: no rotation
 };
 
-template <typename KV, int D, int RING>
+template <typename KV, int D, int RING, bool FUSE>
 __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
     const int lane = threadIdx.x;
     // Workgroups go to the 8 XCDs round-robin (XCD = blockIdx % 8).  Block
@@ -294,7 +304,101 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
     // Q row of this lane's column, fetched before the first pages so that its
     // wait (in-order vmcnt) does not also wait for them
     f32x4 qx[D / 32][2];
-    {
+    if constexpr (FUSE) {
+        // RoPE + KV append of the decode row (the scalar RoPE kernel's
+        // operations in its order: slabs summed in slab order, then
+        // a c - b s, a s + b c per rotate-half pair, no contraction).  A
+        // decode tile holds one query: column c < G is q head kvh G + c.
+        const int row = a.cu_q[seq] + q0;
+        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+        const float* qp = a.qkv + (size_t)row * a.qkv_stride + (size_t)(kvh * a.G + g) * D + q4 * 8;
+#pragma unroll
+        for (int kb = 0; kb < D / 32; ++kb) {
+            qx[kb][0] = col_valid ? *(const f32x4*)(qp + kb * 32) : zero;
+            qx[kb][1] = col_valid ? *(const f32x4*)(qp + kb * 32 + 4) : zero;
+        }
+        constexpr int CH = D == 64 ? 8 : 4;  // slabs per batch of loads
+        for (int s0 = 1; s0 < a.qkv_n; s0 += CH) {
+            f32x4 t[CH][D / 32][2];
+#pragma unroll
+            for (int u = 0; u < CH; ++u)
+#pragma unroll
+                for (int kb = 0; kb < D / 32; ++kb)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+                        t[u][kb][h] = (col_valid && s0 + u < a.qkv_n)
+                                          ? *(const f32x4*)(qp + (size_t)(s0 + u) * a.qkv_slab + kb * 32 + 4 * h)
+                                          : zero;
+#pragma unroll
+            for (int u = 0; u < CH; ++u)
+                if (s0 + u < a.qkv_n)
+#pragma unroll
+                    for (int kb = 0; kb < D / 32; ++kb) {
+                        qx[kb][0] += t[u][kb][0];
+                        qx[kb][1] += t[u][kb][1];
+                    }
+        }
+        if (a.rope_cs) {
+#pragma clang fp contract(off)
+            // the lane's dims 32 kb + 8 q4 + j: pair partner of kb < D / 64 is kb + D / 64
+            const float2* cs = a.rope_cs + (size_t)row * (D / 2) + q4 * 8;
+#pragma unroll
+            for (int kb = 0; kb < D / 64; ++kb) {
+                const float4* c4 = (const float4*)(cs + kb * 32);
+                float cv[8], sv[8];
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    const float4 pr = c4[w];
+                    cv[2 * w] = pr.x;
+                    sv[2 * w] = pr.y;
+                    cv[2 * w + 1] = pr.z;
+                    sv[2 * w + 1] = pr.w;
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float x = qx[kb][j >> 2][j & 3], y = qx[kb + D / 64][j >> 2][j & 3];
+                    qx[kb][j >> 2][j & 3] = x * cv[j] - y * sv[j];
+                    qx[kb + D / 64][j >> 2][j & 3] = x * sv[j] + y * cv[j];
+                }
+            }
+        }
+        if (item == a.tiles[it.x + 1].w - 1) {
+#pragma clang fp contract(off)
+            // the tile's last split holds the new row's page: append this kv
+            // head's K and V row there before any page of the split is read
+            const int sl = a.slot[row], r = sl % kPageRows;
+            KV* kt = (KV*)a.pool + (size_t)(sl / kPageRows) * a.page_elems + (size_t)kvh * kv_tile;
+            KV* vt = kt + v_block;
+            const float* kr = a.qkv + (size_t)row * a.qkv_stride + a.q_cols + (size_t)kvh * D;
+            const float* vr = kr + a.kv_cols;
+            for (int e = lane; e < D / 2 + D; e += 64) {
+                if (e < D / 2) {
+                    float x = kr[e], y = kr[e + D / 2];
+#pragma unroll 4
+                    for (int sb = 1; sb < a.qkv_n; ++sb) {
+                        x += kr[(size_t)sb * a.qkv_slab + e];
+                        y += kr[(size_t)sb * a.qkv_slab + e + D / 2];
+                    }
+                    if (a.rope_cs) {
+                        const float2 cs = a.rope_cs[(size_t)row * (D / 2) + e];
+                        const float nx = x * cs.x - y * cs.y;
+                        const float ny = x * cs.y + y * cs.x;
+                        x = nx;
+                        y = ny;
+                    }
+                    store_elem(kt + k_off(r, e), x);
+                    store_elem(kt + k_off(r, e + D / 2), y);
+                } else {
+                    const int d = e - D / 2;
+                    float v = vr[d];
+#pragma unroll 4
+                    for (int sb = 1; sb < a.qkv_n; ++sb) v += vr[(size_t)sb * a.qkv_slab + d];
+                    store_elem(vt + v_off(r, d), v);
+                }
+            }
+            ring_barrier<0>();  // the row is written before the page loads below
+        }
+    } else {
         const int row = a.cu_q[seq] + q0 + (col_valid ? qi : 0);
         const float* qp = a.q + (size_t)row * a.q_cols + (size_t)(kvh * a.G + g) * D + q4 * 8;
 #pragma unroll
@@ -784,9 +888,16 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(const float* __res
 
 template <typename KV, int D>
 static zr_status launch_attn_t(zr_context* ctx, StagedMeta* st, int layer, const float* q, float* out,
-                               uint16_t* out_bf16) {
+                               uint16_t* out_bf16, const Slabs* qkv = nullptr, int rope = 0) {
     AttnArgs a;
     a.q = q;
+    a.qkv = qkv ? qkv->ptr : nullptr;
+    a.qkv_n = qkv ? qkv->n : 1;
+    a.qkv_slab = qkv ? qkv->stride : 0;
+    a.qkv_stride = ctx->q_cols + 2 * ctx->kv_cols;
+    a.kv_cols = ctx->kv_cols;
+    a.slot = st->slot_mapping;
+    a.rope_cs = rope ? st->rope_cs : nullptr;
     a.q_cols = ctx->q_cols;
     a.page_elems = (size_t)2 * ctx->kv_cols * kPageRows;
     a.pool = (const KV*)ctx->kv_pool + (size_t)layer * ctx->n_pages * a.page_elems;
@@ -812,8 +923,12 @@ static zr_status launch_attn_t(zr_context* ctx, StagedMeta* st, int layer, const
         // bf16 pages: a 6-page ring, one wave per SIMD (measured: a 4-page ring
         // at two waves per SIMD spills and loses ~20%); f32 pages: 4 pages
         const dim3 grid(((st->n_attn_items + 7) / 8) * 8 * ctx->local_kv_heads);
-        hipLaunchKernelGGL((paged_attention_kernel<KV, D, sizeof(KV) == 4 ? 4 : 6>), grid, dim3(64), 0, ctx->stream,
-                           a);
+        if (qkv)
+            hipLaunchKernelGGL((paged_attention_kernel<KV, D, sizeof(KV) == 4 ? 4 : 6, true>), grid, dim3(64), 0,
+                               ctx->stream, a);
+        else
+            hipLaunchKernelGGL((paged_attention_kernel<KV, D, sizeof(KV) == 4 ? 4 : 6, false>), grid, dim3(64), 0,
+                               ctx->stream, a);
         ZR_LAUNCH_CHECK(ctx);
     }
     if constexpr (sizeof(KV) == 2) {
@@ -1012,6 +1127,27 @@ zr_status launch_attention(zr_context* ctx, StagedMeta* st, int layer, const flo
         default: return set_err(ctx, ZR_E_UNSUPPORTED, "head_dim %d not supported (64, 128)", ctx->head_dim);
     }
     return rc;
+}
+
+zr_status launch_attention_rope(zr_context* ctx, StagedMeta* st, int layer, const Slabs& qkv, int rope,
+                                float* out, uint16_t* out_bf16) {
+    if (!st->pure_decode)
+        return set_err(ctx, ZR_E_UNSUPPORTED, "RoPE inside attention needs a microbatch of one-row decode sequences");
+    if (st->n_attn_items == 0) return ZR_OK;
+    const size_t need = (size_t)st->n_part_items * ctx->local_kv_heads * 16 * (ctx->head_dim + 2);
+    if (need > ctx->attn_part_floats)
+        return set_err(ctx, ZR_E_OOM, "attention partial workspace too small: need %zu floats, have %zu",
+                       need, ctx->attn_part_floats);
+    const bool bf = ctx->desc.kv_dtype == ZR_DTYPE_BF16;
+    switch (ctx->head_dim) {  // pure_decode implies the MFMA page layout: head_dim 64 or 128
+        case 64:
+            return bf ? launch_attn_t<uint16_t, 64>(ctx, st, layer, nullptr, out, out_bf16, &qkv, rope)
+                      : launch_attn_t<float, 64>(ctx, st, layer, nullptr, out, out_bf16, &qkv, rope);
+        case 128:
+            return bf ? launch_attn_t<uint16_t, 128>(ctx, st, layer, nullptr, out, out_bf16, &qkv, rope)
+                      : launch_attn_t<float, 128>(ctx, st, layer, nullptr, out, out_bf16, &qkv, rope);
+        default: return set_err(ctx, ZR_E_UNSUPPORTED, "head_dim %d not supported (64, 128)", ctx->head_dim);
+    }
 }
 
 }  // namespace zr

@@ -15,7 +15,7 @@ const char* const kStageNames[] = {"norm_qkv", "rope_kv_write", "paged_attention
                                    "device_sampling"};
 const char* const kStageKernels[] = {
     "rms_norm_vec_kernel,rms_norm_kernel,gemm_kernel",
-    "rope_kv_write_kernel",
+    "rope_table_kernel,rope_kv_write_kernel,rope_kv_write_vec_kernel,paged_attention_kernel",
     "paged_attention_kernel,paged_prefill_attention_kernel,attention_merge_kernel",
     "rms_norm_vec_kernel,rms_norm_kernel,gemm_kernel,splitk_reduce_kernel",
     "argmax_partial_kernel,argmax_final_kernel,sample_kernel",

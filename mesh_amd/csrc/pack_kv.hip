@@ -1,36 +1,9 @@
 // Ragged-batch packing, fused RoPE + paged-KV append, and the KV handoff
-// gather/scatter kernels.
-//
-// KV pool layout (per layer, per global page, K block then V block, one
-// [16 x head_dim] tile per local kv head, element type = pool dtype):
-//   K tile: element (t, d) at ((d / 8) * 16 + t) * 8 + d % 8
-//           -> one 1 KiB row of 64 lanes x 16 B is exactly the MFMA A-operand
-//              fragment (token = lane % 16, 8 dims per lane) for 32 dims.
-//   V tile: element (t, d) at ((((d / 32) * 4 + t / 4) * 16 + d % 16) * 2
-//           + (d / 16) % 2) * 4 + t % 4
-//           -> 4 consecutive tokens of one dim are one P.V MFMA operand
-//              lane; dims d and d + 16 sit next to each other, so a lane
-//              loads both with one 16 B (bf16) load and a wave reads 1 KiB
-//              contiguous per 32 dims.
+// gather/scatter kernels.  The KV pool's page layouts (MFMA fragment and
+// plain) are k_off / v_off / k_off_of / v_off_of in zr_internal.h.
 #include "zr_internal.h"
 
 namespace zr {
-
-__device__ inline size_t k_off(int t, int d) { return ((size_t)(d >> 3) * kPageRows + t) * 8 + (d & 7); }
-__device__ inline size_t v_off(int t, int d, int) {
-    return (((((size_t)(d >> 5) * 4 + (t >> 2)) * 16 + (d & 15)) * 2 + ((d >> 4) & 1)) * 4) + (t & 3);
-}
-// Plain layout (pools whose head_dim the MFMA kernels do not take): both
-// tiles row-major [16 rows][D].
-__device__ inline size_t k_off_of(int t, int d, int D, int plain) { return plain ? (size_t)t * D + d : k_off(t, d); }
-__device__ inline size_t v_off_of(int t, int d, int D, int plain) { return plain ? (size_t)t * D + d : v_off(t, d, D); }
-
-template <typename T> __device__ inline void store_elem(T* p, float x);
-template <> __device__ inline void store_elem<float>(float* p, float x) { *p = x; }
-template <> __device__ inline void store_elem<uint16_t>(uint16_t* p, float x) { *p = f32_to_bf16_bits(x); }
-template <typename T> __device__ inline float load_elem(const T* p);
-template <> __device__ inline float load_elem<float>(const float* p) { return *p; }
-template <> __device__ inline float load_elem<uint16_t>(const uint16_t* p) { return bf16_bits_to_f32(*p); }
 
 // ------------------------------------------------------------------ pack
 // One workgroup: exclusive scans of q_len and kv_after, then per-token
@@ -96,29 +69,47 @@ __global__ __launch_bounds__(1024) void pack_kernel(int S, const int* __restrict
     }
 }
 
+// RoPE angles of the step, shared by every layer: (cos, sin) of
+// theta = f32(position) * inv_freq[i] in f32 (tensor_ops.rs:509-560,
+// runtime.rs:935-1005), one entry per (row, rotation pair).
+__global__ __launch_bounds__(256) void rope_table_kernel(int rows, int half, const int* __restrict__ positions,
+                                                         const float* __restrict__ inv_freq, float2* __restrict__ cs) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= rows * half) return;
+    const int t = idx / half, i = idx - t * half;
+    const float theta = (float)positions[t] * inv_freq[i];
+    cs[idx] = make_float2(cosf(theta), sinf(theta));
+}
+
 zr_status launch_pack(zr_context* ctx, StagedMeta* st) {
     hipLaunchKernelGGL(pack_kernel, dim3(1), dim3(1024), 0, ctx->stream, st->num_seqs, st->q_len,
                        st->kv_before, st->first_pos, st->first_offset, st->block_tables, st->stride,
                        st->cu_q, st->cu_k, st->positions, st->slot_mapping, st->seq_ids, st->last_rows);
     ZR_LAUNCH_CHECK(ctx);
+    const int half = ctx->head_dim / 2, n = st->total_q * half;
+    if (n > 0) {
+        hipLaunchKernelGGL(rope_table_kernel, dim3((n + 255) / 256), dim3(256), 0, ctx->stream, st->total_q, half,
+                           st->positions, ctx->inv_freq, st->rope_cs);
+        ZR_LAUNCH_CHECK(ctx);
+    }
     return ZR_OK;
 }
 
 // ---------------------------------------------------------- RoPE + append
 // One workgroup per token row.  RoPE follows tensor_ops.rs:509-560 /
-// runtime.rs:935-1005 (rotate-half, theta = position * inv_freq in f32) and
-// the KV append is DeviceLayerKVCache::append (forward_pass.rs:462-521) at the
-// slot the host reserved.
+// runtime.rs:935-1005 (rotate-half; (cos, sin) of theta = position * inv_freq
+// in f32 from the step's table, rope_table_kernel) and the KV append is
+// DeviceLayerKVCache::append (forward_pass.rs:462-521) at the slot the host
+// reserved.
 template <typename KV>
 __global__ __launch_bounds__(256) void rope_kv_write_kernel(
     const float* __restrict__ qkv, int qkv_n, size_t qkv_slab, int qkv_stride, float* __restrict__ q_out,
     int q_cols, int kv_cols,
-    int D, const int* __restrict__ positions, const int* __restrict__ slot,
-    const float* __restrict__ inv_freq, KV* __restrict__ layer_pool, size_t page_elems, int rope, int plain) {
+    int D, const int* __restrict__ slot, const float2* __restrict__ rope_cs,
+    KV* __restrict__ layer_pool, size_t page_elems, int rope, int plain) {
 #pragma clang fp contract(off)
     const int t = blockIdx.x;
     const int half = D / 2;
-    const float pos = (float)positions[t];
     const float* row = qkv + (size_t)t * qkv_stride;
     const int s = slot[t];
     const int page = s / kPageRows, r = s % kPageRows;
@@ -140,8 +131,8 @@ __global__ __launch_bounds__(256) void rope_kv_write_kernel(
                 b += src[sl * qkv_slab + i + half];
             }
             if (rope) {
-                const float theta = pos * inv_freq[i];
-                const float c = cosf(theta), sn = sinf(theta);
+                const float2 cs = rope_cs[(size_t)t * half + i];
+                const float c = cs.x, sn = cs.y;
                 const float na = a * c - b * sn;
                 const float nb = a * sn + b * c;
                 a = na;
@@ -170,15 +161,15 @@ __global__ __launch_bounds__(256) void rope_kv_write_kernel(
 // The same stage for head_dim % 8 == 0 in float4 runs, one item per lane of
 // one-wave workgroups (row, y): 4 consecutive rotation pairs of one q / k
 // head -- float4 loads of both halves from every split-K slab, issued 8 slabs
-// at a time and summed in slab order, and the lane's own 4 angles (theta =
-// position * inv_freq[i], cosf / sinf, as above) computed while they are in
-// flight -- or 4 consecutive V elements.  Bit-identical to the scalar kernel.
+// at a time and summed in slab order, and the lane's own 4 (cos, sin) pairs
+// from the table loaded while they are in flight -- or 4 consecutive V
+// elements.  Bit-identical to the scalar kernel.
 template <typename KV>
 __global__ __launch_bounds__(64) void rope_kv_write_vec_kernel(
     const float* __restrict__ qkv, int qkv_n, size_t qkv_slab, int qkv_stride, float* __restrict__ q_out,
     int q_cols, int kv_cols,
-    int D, const int* __restrict__ positions, const int* __restrict__ slot,
-    const float* __restrict__ inv_freq, KV* __restrict__ layer_pool, size_t page_elems, int rope, int plain) {
+    int D, const int* __restrict__ slot, const float2* __restrict__ rope_cs,
+    KV* __restrict__ layer_pool, size_t page_elems, int rope, int plain) {
 #pragma clang fp contract(off)
     const int t = blockIdx.x;
     const int half = D / 2, g4 = half / 4;
@@ -213,13 +204,10 @@ __global__ __launch_bounds__(64) void rope_kv_write_vec_kernel(
                 qb[u] = ok ? *(const float4*)(src + (s0 + u) * qkv_slab + half) : make_float4(0.f, 0.f, 0.f, 0.f);
             }
             if (rope && s0 == 1) {
-                const float pos = (float)positions[t];
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const float theta = pos * inv_freq[i0 + u];
-                    c[u] = cosf(theta);
-                    sv[u] = sinf(theta);
-                }
+                const float4* cs4 = (const float4*)(rope_cs + (size_t)t * half + i0);
+                const float4 p0 = cs4[0], p1 = cs4[1];
+                c[0] = p0.x, sv[0] = p0.y, c[1] = p0.z, sv[1] = p0.w;
+                c[2] = p1.x, sv[2] = p1.y, c[3] = p1.z, sv[3] = p1.w;
             }
 #pragma unroll
             for (int u = 0; u < 8; ++u)
@@ -229,13 +217,10 @@ __global__ __launch_bounds__(64) void rope_kv_write_vec_kernel(
                 }
         }
         if (rope && qkv_n == 1) {
-            const float pos = (float)positions[t];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const float theta = pos * inv_freq[i0 + u];
-                c[u] = cosf(theta);
-                sv[u] = sinf(theta);
-            }
+            const float4* cs4 = (const float4*)(rope_cs + (size_t)t * half + i0);
+            const float4 p0 = cs4[0], p1 = cs4[1];
+            c[0] = p0.x, sv[0] = p0.y, c[1] = p0.z, sv[1] = p0.w;
+            c[2] = p1.x, sv[2] = p1.y, c[3] = p1.z, sv[3] = p1.w;
         }
         float a[4] = {a4.x, a4.y, a4.z, a4.w}, b[4] = {b4.x, b4.y, b4.z, b4.w};
         if (rope) {
@@ -307,25 +292,25 @@ zr_status launch_rope_kv_write(zr_context* ctx, StagedMeta* st, int layer, const
         if (ctx->desc.kv_dtype == ZR_DTYPE_BF16)
             hipLaunchKernelGGL(rope_kv_write_vec_kernel<uint16_t>, vgrid, dim3(64), 0, ctx->stream,
                                qkv.ptr, qkv.n, qkv.stride, stride, q_out, ctx->q_cols, ctx->kv_cols, ctx->head_dim,
-                               st->positions, st->slot_mapping, ctx->inv_freq,
+                               st->slot_mapping, st->rope_cs,
                                (uint16_t*)ctx->kv_pool + (size_t)layer * ctx->n_pages * pe, pe, rope,
                                ctx->plain_kv ? 1 : 0);
         else
             hipLaunchKernelGGL(rope_kv_write_vec_kernel<float>, vgrid, dim3(64), 0, ctx->stream,
                                qkv.ptr, qkv.n, qkv.stride, stride, q_out, ctx->q_cols, ctx->kv_cols, ctx->head_dim,
-                               st->positions, st->slot_mapping, ctx->inv_freq,
+                               st->slot_mapping, st->rope_cs,
                                (float*)ctx->kv_pool + (size_t)layer * ctx->n_pages * pe, pe, rope,
                                ctx->plain_kv ? 1 : 0);
     } else if (ctx->desc.kv_dtype == ZR_DTYPE_BF16) {
         uint16_t* pool = (uint16_t*)ctx->kv_pool + (size_t)layer * ctx->n_pages * pe;
         hipLaunchKernelGGL(rope_kv_write_kernel<uint16_t>, grid, dim3(256), 0, ctx->stream,
-                           qkv.ptr, qkv.n, qkv.stride, stride, q_out, ctx->q_cols, ctx->kv_cols, ctx->head_dim, st->positions,
-                           st->slot_mapping, ctx->inv_freq, pool, pe, rope, ctx->plain_kv ? 1 : 0);
+                           qkv.ptr, qkv.n, qkv.stride, stride, q_out, ctx->q_cols, ctx->kv_cols, ctx->head_dim,
+                           st->slot_mapping, st->rope_cs, pool, pe, rope, ctx->plain_kv ? 1 : 0);
     } else {
         float* pool = (float*)ctx->kv_pool + (size_t)layer * ctx->n_pages * pe;
         hipLaunchKernelGGL(rope_kv_write_kernel<float>, grid, dim3(256), 0, ctx->stream,
-                           qkv.ptr, qkv.n, qkv.stride, stride, q_out, ctx->q_cols, ctx->kv_cols, ctx->head_dim, st->positions,
-                           st->slot_mapping, ctx->inv_freq, pool, pe, rope, ctx->plain_kv ? 1 : 0);
+                           qkv.ptr, qkv.n, qkv.stride, stride, q_out, ctx->q_cols, ctx->kv_cols, ctx->head_dim,
+                           st->slot_mapping, st->rope_cs, pool, pe, rope, ctx->plain_kv ? 1 : 0);
     }
     ZR_LAUNCH_CHECK(ctx);
     timing_mark_end(ctx, kClassNormRopeKv, ev);

@@ -90,6 +90,31 @@ __device__ __forceinline__ void ring_wait(int ahead) {
 
 struct StagedMeta;  // device copy of one microbatch's metadata
 
+// KV pool page layout (per layer, per global page: the K block, then the V
+// block, one [16 x head_dim] tile per local kv head):
+//   K tile: element (t, d) at ((d / 8) * 16 + t) * 8 + d % 8 -- one 1 KiB row of
+//           64 lanes x 16 B is the MFMA A-operand fragment (token = lane % 16,
+//           8 dims per lane) for 32 dims.
+//   V tile: element (t, d) at ((((d / 32) * 4 + t / 4) * 16 + d % 16) * 2
+//           + (d / 16) % 2) * 4 + t % 4 -- 4 consecutive tokens of one dim are
+//           one P.V MFMA operand lane; dims d and d + 16 sit side by side, so a
+//           lane loads both with one 16 B (bf16) load and a wave reads 1 KiB
+//           contiguous per 32 dims.
+// Plain layout (pools whose head_dim the MFMA kernels do not take): both tiles
+// row-major [16 rows][head_dim].
+__device__ inline size_t k_off(int t, int d) { return ((size_t)(d >> 3) * kPageRows + t) * 8 + (d & 7); }
+__device__ inline size_t v_off(int t, int d) {
+    return (((((size_t)(d >> 5) * 4 + (t >> 2)) * 16 + (d & 15)) * 2 + ((d >> 4) & 1)) * 4) + (t & 3);
+}
+__device__ inline size_t k_off_of(int t, int d, int D, int plain) { return plain ? (size_t)t * D + d : k_off(t, d); }
+__device__ inline size_t v_off_of(int t, int d, int D, int plain) { return plain ? (size_t)t * D + d : v_off(t, d); }
+template <typename T> __device__ inline void store_elem(T* p, float x);
+template <> __device__ inline void store_elem<float>(float* p, float x) { *p = x; }
+template <> __device__ inline void store_elem<uint16_t>(uint16_t* p, float x) { *p = f32_to_bf16_bits(x); }
+template <typename T> __device__ inline float load_elem(const T* p);
+template <> __device__ inline float load_elem<float>(const float* p) { return *p; }
+template <> __device__ inline float load_elem<uint16_t>(const uint16_t* p) { return bf16_bits_to_f32(*p); }
+
 struct LayerDev {
     uint16_t* w_qkv = nullptr;     // packed [K=H, N=Q+2Kc]
     uint16_t* w_o = nullptr;       // packed [K=Q, N=H]
@@ -216,6 +241,9 @@ struct StagedMeta {
     int n_merge = 0;          // tiles with more than one split
     int n_pblocks = 0;        // prefill work units (block, key split) per kv head
     int n_part_items = 0;     // partial items: decode items, then prefill (group, split) items
+    bool pure_decode = false; // every sequence has one query row (MFMA page layout): RoPE + KV append can run
+                              // inside the decode attention kernel
+    bool fuse_rope = false;   // ... and the forward pass has them do so
     bool owns = true;
     // one device allocation holding every array below
     void* dev = nullptr;
@@ -233,6 +261,7 @@ struct StagedMeta {
     int* slot_mapping = nullptr;// [T]
     int* seq_ids = nullptr;     // [T]
     int* last_rows = nullptr;   // [S] row index of each sequence's last token
+    float2* rope_cs = nullptr;  // [T][head_dim / 2] (cos, sin) of position x inv_freq (pack stage output)
     int4* attn_items = nullptr; // [n_attn_items] {tile, page_begin, page_end, part_index}
     int4* attn_tiles = nullptr; // [n_tiles] {seq, q0, nq, first_part}
     int* tile_nparts = nullptr; // [n_tiles]
@@ -276,6 +305,10 @@ zr_status launch_rope_kv_write(zr_context* ctx, StagedMeta* st, int layer, const
 // out_f32 [T, q_cols] or out_bf16 (A operand of the O projection).
 zr_status launch_attention(zr_context* ctx, StagedMeta* st, int layer, const float* q, float* out_f32,
                            uint16_t* out_bf16);
+// Pure decode microbatches (st->pure_decode): RoPE + KV append and attention in
+// one launch, q and the new K / V rows read from the QKV product's slabs.
+zr_status launch_attention_rope(zr_context* ctx, StagedMeta* st, int layer, const Slabs& qkv, int rope,
+                                float* out_f32, uint16_t* out_bf16);
 zr_status launch_kv_copy(zr_context* ctx, int layer_begin, int layer_end, const int* d_table,
                          int first_offset, int first_row, int n_rows, float* k, float* v,
                          int to_pool);

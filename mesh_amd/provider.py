@@ -43,7 +43,8 @@ class ExecutionProviderKind(str, Enum):
 # FusedKernelStage (engine.rs:124-132) -> the kernels that implement it here.
 FUSED_KERNEL_STAGES = {
     "norm_qkv": ["rms_norm_vec_kernel", "rms_norm_kernel", "gemm_kernel"],
-    "rope_kv_write": ["rope_kv_write_kernel"],
+    # one-row decode microbatches: RoPE + KV append run inside paged_attention_kernel
+    "rope_kv_write": ["rope_table_kernel", "rope_kv_write_kernel", "rope_kv_write_vec_kernel", "paged_attention_kernel"],
     "paged_attention": ["paged_attention_kernel", "paged_prefill_attention_kernel", "attention_merge_kernel"],
     "residual_mlp": ["rms_norm_vec_kernel", "rms_norm_kernel", "gemm_kernel", "splitk_reduce_kernel"],
     "device_sampling": ["argmax_partial_kernel", "argmax_final_kernel", "sample_kernel"],

@@ -136,6 +136,61 @@ def test_rope_kv_write_rotates_q_and_k_at_large_positions(kv_dtype, heads, kv_he
     ctx.close()
 
 
+@pytest.mark.parametrize("rope", [0, 1])
+@pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("heads,kv_heads,D,base", [(32, 4, 64, 1e4), (32, 8, 128, 5e5)])
+def test_rope_attention_equals_rope_kv_write_then_attention_bit_exact(monkeypatch, rope, kv_dtype, heads, kv_heads,
+                                                                      D, base):
+    """RoPE + KV append inside the decode attention launch (zr_rope_attention,
+    the forward pass's path for one-row decode microbatches) against the two
+    stages run apart (zr_rope_kv_write, then zr_attention) on identically
+    prepared sessions: the attention outputs and every KV row, the appended
+    one included, bit for bit.  Splits of 2 pages give most tiles several
+    splits (the last one appends the row) and the 1-row context a single
+    one; positions run to ~5600."""
+    from mesh_amd import KVCacheSnapshot
+
+    monkeypatch.setenv("ZR_ATTN_PAGES_PER_SPLIT", "2")
+    Q, KV = heads * D, kv_heads * D
+    geo = ModelGeometry(hidden=Q, num_heads=heads, num_kv_heads=kv_heads, num_layers=1, vocab=64, ffn=64,
+                        rope_base=base)
+    ctx = DeviceContext(geo, kv_dtype=kv_dtype, max_tokens=16, max_seqs=16, max_pages_per_seq=64)
+    ctx.create_kv_pool(600)
+    rng = np.random.default_rng(D + rope)
+    ctxlens = [0, 1, 15, 16, 17, 200, 431, 599]
+    sets = [[ctx.new_backend(8192) for _ in ctxlens] for _ in range(2)]
+    for i, L in enumerate(ctxlens):
+        if L:
+            k = rng.standard_normal((1, L, KV), dtype=np.float32)
+            v = rng.standard_normal((1, L, KV), dtype=np.float32)
+            for bs in sets:
+                bs[i].import_kv_cache(KVCacheSnapshot(5000 + L, L, k, v))
+    qkv = rng.standard_normal((len(ctxlens), Q + 2 * KV), dtype=np.float32)
+    d_qkv = DeviceBuffer.from_numpy(ctx, qkv)
+    d_q = DeviceBuffer(ctx, 4 * len(ctxlens) * Q)
+    d_a, d_b = DeviceBuffer(ctx, 4 * len(ctxlens) * Q), DeviceBuffer(ctx, 4 * len(ctxlens) * Q)
+    st_a, st_b = stage_mixed(ctx, sets[0], [1] * len(ctxlens)), stage_mixed(ctx, sets[1], [1] * len(ctxlens))
+    ctx.check(ctx.lib.zr_rope_kv_write(ctx.h, st_a, 0, d_qkv.ptr, d_q.ptr, rope))
+    ctx.check(ctx.lib.zr_attention(ctx.h, st_a, 0, d_q.ptr, d_a.ptr))
+    ctx.check(ctx.lib.zr_rope_attention(ctx.h, st_b, 0, d_qkv.ptr, d_b.ptr, rope))
+    ctx.lib.zr_staged_destroy(st_a)
+    ctx.lib.zr_staged_destroy(st_b)
+    out_a, out_b = d_a.download(np.float32, (len(ctxlens), Q)), d_b.download(np.float32, (len(ctxlens), Q))
+    assert np.isfinite(out_a).all()
+    np.testing.assert_array_equal(out_b, out_a)
+    for i, L in enumerate(ctxlens):
+        ka, kb = sets[0][i].export_kv_cache(), sets[1][i].export_kv_cache()
+        assert ka.cached_tokens == kb.cached_tokens == L + 1
+        np.testing.assert_array_equal(kb.keys, ka.keys)
+        np.testing.assert_array_equal(kb.values, ka.values)
+    # a microbatch with a two-row sequence is not a decode microbatch
+    st = stage_mixed(ctx, [ctx.new_backend(64), ctx.new_backend(64)], [1, 2])
+    assert ctx.lib.zr_rope_attention(ctx.h, st, 0, d_qkv.ptr, d_b.ptr, rope) == -5
+    assert b"one-row decode" in ctx.lib.zr_last_error(ctx.h)
+    ctx.lib.zr_staged_destroy(st)
+    ctx.close()
+
+
 @pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("heads,kv_heads,D,base", [(32, 4, 64, 1e4), (32, 8, 128, 5e5)])
 def test_rope_kv_write_float4_path_matches_scalar_path_bit_exact(kv_dtype, heads, kv_heads, D, base):
