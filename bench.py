@@ -360,7 +360,9 @@ def measure(name, steps, warmup):
 def measure_kv_append(bench, reps=5):
     """RoPE + KV append (the RopeKvWrite stage; rope_kv_write_vec_kernel at 256 rows) alone:
     one launch over a decode step's rows (layer 0, the last staged step, after
-    the timed region), HIP events of class 2.  Algorithmic bytes: the f32 QKV
+    the timed region), HIP events of class 2.  (The 256-session forward pass
+    runs this stage inside the attention launch; the separate kernel serves
+    mixed microbatches and decode steps with short splits.)  Algorithmic bytes: the f32 QKV
     row read, the rotated f32 Q written, and the new K and V rows written into
     their bf16 pages."""
     ctx, lib, g = bench.ctx, bench.ctx.lib, bench.geo
