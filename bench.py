@@ -464,7 +464,9 @@ def measure_soak(steps, warmup):
     2048-token segmented-window export and restore through import
     (mesh_amd.kv_pressure).  A joining session's context pages are reserved
     and hold the pool's synthetic values (standing in for its prefill).
-    value = decoded tokens / wall time of the steps, host path included."""
+    value = decoded tokens / wall time of the steps, host path included, with
+    the window copies overlapping the steps; `synchronous_copies` continues
+    the same soak for as many steps with each copy made before the step."""
     from mesh_amd.kv_pressure import KvPressureSoak
 
     w = WORKLOADS[SOAK["workload"]]
@@ -489,20 +491,34 @@ def measure_soak(steps, warmup):
         soak.add_session(int(L))
     for _ in range(warmup):
         soak.step()
-    st0 = dict(vars(soak.stats))
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        soak.step()
-    dt = time.perf_counter() - t0
-    st = soak.stats
-    d = lambda k: getattr(st, k) - st0[k]
-    out = dict(value=d("tokens") / dt, unit="tokens/s", steps=steps, pool_pages=pool, pool_frac_of_need=pool / need,
-               mean_active=float(np.mean(st.active_hist[-steps:])), joins=d("joins"), leaves=d("leaves"),
-               evictions=d("evictions"), restores=d("restores"), ms_per_step=dt / steps * 1e3,
-               ms_per_step_decode=d("decode_s") / steps * 1e3, ms_per_step_evict=d("evict_s") / steps * 1e3,
-               ms_per_step_restore=d("restore_s") / steps * 1e3, ms_per_step_admit=d("admit_s") / steps * 1e3,
+
+    def timed():
+        st0 = dict(vars(soak.stats))
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            soak.step()
+        dt = time.perf_counter() - t0
+        st = soak.stats
+        d = lambda k: getattr(st, k) - st0[k]
+        return dict(value=d("tokens") / dt, unit="tokens/s", steps=steps, mean_active=float(np.mean(st.active_hist[-steps:])),
+                    joins=d("joins"), leaves=d("leaves"), evictions=d("evictions"), restores=d("restores"),
+                    ms_per_step=dt / steps * 1e3, ms_per_step_decode=d("decode_s") / steps * 1e3,
+                    ms_per_step_evict=d("evict_s") / steps * 1e3, ms_per_step_restore=d("restore_s") / steps * 1e3,
+                    ms_per_step_admit=d("admit_s") / steps * 1e3)
+
+    out = timed()
+    out.update(pool_pages=pool, pool_frac_of_need=pool / need,
+               transfers="each window's PCIe copy on a stream of its own while the steps run (evict: gather into a "
+                         "device buffer, pages released at once, copy-out to pinned host memory; restore: the oldest "
+                         "evicted windows uploaded a step ahead); the evict / restore times are the host time to "
+                         "issue them",
                workload="Llama-3-8B-shape decode under KV pressure: pool 85% of 256 lognormal contexts, Poisson "
                         "joins 4/step, leave 1/64, evict/restore via 2048-token window export/import")
+    # the same soak continued with the copies made synchronously, as the reference makes them
+    soak.finish()
+    soak.async_transfers = False
+    out["synchronous_copies"] = timed()
+    soak.finish()
     ctx.close()
     return out
 

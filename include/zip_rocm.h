@@ -215,6 +215,39 @@ zr_status zr_kv_gather(zr_context* ctx, const int* block_table, int n_pages, int
  * logical rows first_row.. of the window described by block_table. */
 zr_status zr_kv_scatter(zr_context* ctx, const int* block_table, int n_pages, int first_offset,
                         int first_row, int n_rows, const float* src_k, const float* src_v);
+
+/* ---- KV windows in flight: zr_kv_gather / zr_kv_scatter with the PCIe copy
+ * on a stream of its own (one per direction), overlapping the decode steps --
+ * the eviction checkpoint and restore of the KV-pressure path (coordinator.rs
+ * 871-894, forward_pass.rs:1169-1242 export / import), whose copies the
+ * reference makes synchronously.  A transfer owns a device buffer
+ * [num_layers][n_rows][kv_cols] K, then V (reused after destroy, never freed
+ * before the context).  Host buffers should be pinned (zr_host_alloc) for the
+ * copies to overlap.  One host thread per context. */
+typedef struct zr_transfer zr_transfer;
+/* The gather of zr_kv_gather on the context's stream into the transfer's
+ * buffer, then the copy to dst_k / dst_v on the device-to-host stream.
+ * Returns at once: the window's pages may be reused as soon as this returns
+ * (later launches on the context's stream run after the gather); dst_k /
+ * dst_v are valid after zr_transfer_wait. */
+zr_status zr_kv_gather_async(zr_context* ctx, const int* block_table, int n_pages, int first_offset,
+                             int first_row, int n_rows, float* dst_k, float* dst_v, zr_transfer** out);
+/* Copies src_k / src_v [num_layers][n_rows][kv_cols] f32 into a transfer's
+ * buffer on the host-to-device stream (a restore, issued ahead of it). */
+zr_status zr_kv_upload_async(zr_context* ctx, const float* src_k, const float* src_v, int n_rows,
+                             zr_transfer** out);
+/* zr_kv_scatter from a transfer's buffer, on the context's stream: after its
+ * upload (waited for on the device), or straight from a gather's buffer (its
+ * rows are on the device; its copy to the host may still be running).
+ * n_rows must be the transfer's. */
+zr_status zr_kv_scatter_transfer(zr_context* ctx, zr_transfer* t, const int* block_table, int n_pages,
+                                 int first_offset, int first_row, int n_rows);
+/* 1 when the transfer's host copy has finished, 0 while it runs, <0 on error. */
+int zr_transfer_done(const zr_transfer* t);
+zr_status zr_transfer_wait(zr_transfer* t);
+/* Waits for the copy and the last kernel on the buffer, keeps the buffer for
+ * reuse.  Destroy every transfer before its context. */
+void zr_transfer_destroy(zr_transfer* t);
 /* KV snapshot wire format (KVCache::to_bytes, kv_cache.rs:880-887: ciborium
  * 0.2.2 CBOR of the cache DeviceKVCache::export_snapshot builds,
  * forward_pass.rs:1169-1204): gathers rows [first_row, first_row + n_rows)

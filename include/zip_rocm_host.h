@@ -90,6 +90,15 @@ zr_status zrh_export_kv(const zrh_backend* b, int max_cached_tokens, float* k, f
  * fresh pages, validates cached_tokens and base_position. */
 zr_status zrh_import_kv(zrh_backend* b, const float* k, const float* v, int rows, int base_position,
                         int next_position);
+/* zrh_export_kv with its copy to k / v in flight (zr_kv_gather_async): the
+ * session's pages may be released once this returns; k / v (pinned host
+ * memory) hold the rows after zr_transfer_wait(*out).  *out = NULL when there
+ * is no snapshot (empty cache). */
+zr_status zrh_export_kv_async(const zrh_backend* b, int max_cached_tokens, float* k, float* v, int* rows,
+                              int* base_position, int* next_position, zr_transfer** out);
+/* zrh_import_kv from a transfer's device buffer (zr_kv_scatter_transfer): an
+ * upload (zr_kv_upload_async) or a session's own in-flight export. */
+zr_status zrh_import_kv_transfer(zrh_backend* b, zr_transfer* t, int rows, int base_position, int next_position);
 /* export_kv_cache -> export_snapshot (forward_pass.rs:1169-1204) as its wire
  * bytes: the KVCacheSnapshot blob (KVCacheBlob::from_cache, kv_cache.rs:77-84,
  * encoding FullSnapshotCbor) = KVCache::to_bytes (880-887) of the newest

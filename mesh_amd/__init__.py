@@ -6,10 +6,11 @@ interface (mesh_amd.provider).
 """
 from .provider import (BackendMicrobatchExecutor, DecodeMicrobatchOutput, DecodeMicrobatchRequest,
                        DeviceBuffer, DeviceContext, ExecutionProviderKind, FastPathPlanner, KVCacheBlob,
-                       KVCacheSnapshot, KVCacheWireSnapshot, KVSequenceState, ModelGeometry, RocmExecutionBackend,
+                       KVCacheSnapshot, KVCacheWireSnapshot, KVSequenceState, KVTransfer, ModelGeometry,
+                       RocmExecutionBackend,
                        bf16_bits, device_info, executor_contract, probe_provider)
 
 __all__ = ["BackendMicrobatchExecutor", "DecodeMicrobatchOutput", "DecodeMicrobatchRequest", "DeviceBuffer",
            "DeviceContext", "ExecutionProviderKind", "FastPathPlanner", "KVCacheBlob", "KVCacheSnapshot",
-           "KVCacheWireSnapshot", "KVSequenceState", "ModelGeometry", "RocmExecutionBackend", "bf16_bits",
+           "KVCacheWireSnapshot", "KVSequenceState", "KVTransfer", "ModelGeometry", "RocmExecutionBackend", "bf16_bits",
            "device_info", "executor_contract", "probe_provider"]

@@ -120,6 +120,13 @@ SIGNATURES = [
     ("zr_rope_attention", C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int]),
     ("zr_kv_gather", C.c_int, [C.c_void_p, c_int_p, C.c_int, C.c_int, C.c_int, C.c_int, c_f32_p, c_f32_p]),
     ("zr_kv_scatter", C.c_int, [C.c_void_p, c_int_p, C.c_int, C.c_int, C.c_int, C.c_int, c_f32_p, c_f32_p]),
+    ("zr_kv_gather_async", C.c_int, [C.c_void_p, c_int_p, C.c_int, C.c_int, C.c_int, C.c_int, c_f32_p, c_f32_p,
+                                     c_void_pp]),
+    ("zr_kv_upload_async", C.c_int, [C.c_void_p, c_f32_p, c_f32_p, C.c_int, c_void_pp]),
+    ("zr_kv_scatter_transfer", C.c_int, [C.c_void_p, C.c_void_p, c_int_p, C.c_int, C.c_int, C.c_int, C.c_int]),
+    ("zr_transfer_done", C.c_int, [C.c_void_p]),
+    ("zr_transfer_wait", C.c_int, [C.c_void_p]),
+    ("zr_transfer_destroy", None, [C.c_void_p]),
     ("zr_kv_export_cbor", C.c_int, [C.c_void_p, c_int_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_longlong, C.c_int,
                                     C.c_void_p, C.c_size_t, C.POINTER(C.c_size_t)]),
     ("zr_kv_read_pages", C.c_int, [C.c_void_p, C.c_int, c_int_p, C.c_int, C.c_void_p]),
@@ -164,6 +171,8 @@ SIGNATURES = [
     ("zrh_block_table", C.c_int, [C.c_void_p, c_u32_p, c_int_p, c_int_p, c_int_p, C.c_int]),
     ("zrh_export_kv", C.c_int, [C.c_void_p, C.c_int, c_f32_p, c_f32_p, c_int_p, c_int_p, c_int_p]),
     ("zrh_import_kv", C.c_int, [C.c_void_p, c_f32_p, c_f32_p, C.c_int, C.c_int, C.c_int]),
+    ("zrh_export_kv_async", C.c_int, [C.c_void_p, C.c_int, c_f32_p, c_f32_p, c_int_p, c_int_p, c_int_p, c_void_pp]),
+    ("zrh_import_kv_transfer", C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),
     ("zrh_export_kv_cbor", C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_size_t, C.POINTER(C.c_size_t), c_int_p,
                                      c_int_p]),
     ("zrh_import_kv_cbor", C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_int]),

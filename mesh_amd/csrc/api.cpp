@@ -122,6 +122,14 @@ static zr_status resolve_geometry(zr_context* ctx) {
 // Split-K workspace of one GEMM shape (same plan as launch_gemm).
 static size_t gemm_ws_floats(int m, int n, int k, int epilogue) { return gemm_plan(m, n, k, epilogue).ws_floats; }
 
+static void destroy_streams(zr_context* ctx) {
+    for (hipStream_t* st : {&ctx->stream, &ctx->d2h_stream, &ctx->h2d_stream})
+        if (*st) {
+            (void)hipStreamDestroy(*st);
+            *st = nullptr;
+        }
+}
+
 static void free_ctx_buffers(zr_context* ctx) {
     void* bufs[] = {ctx->hidden, ctx->xa, ctx->qkv, ctx->q_rope, ctx->attn_a, ctx->proj, ctx->ffn_a,
                     ctx->logits, ctx->final_a, ctx->tokens_out, ctx->splitk_ws, ctx->attn_part,
@@ -526,13 +534,15 @@ zr_status zr_context_create(const zr_model_desc* desc, int device, zr_context** 
     auto fail = [&](hipError_t e, const char* what) {
         set_global_err(ZR_E_HIP, "%s: %s", what, hipGetErrorString(e));
         free_ctx_buffers(ctx);
-        if (ctx->stream) hipStreamDestroy(ctx->stream);
+        destroy_streams(ctx);
         delete ctx;
         return e == hipErrorOutOfMemory ? ZR_E_OOM : ZR_E_HIP;
     };
     hipError_t e = hipSetDevice(device);
     if (e != hipSuccess) return fail(e, "hipSetDevice");
     e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->d2h_stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->h2d_stream, hipStreamNonBlocking);
     if (e != hipSuccess) return fail(e, "hipStreamCreate");
     const size_t T = d.max_tokens, S = d.max_seqs, H = d.hidden, Q = ctx->q_cols, KV = ctx->kv_cols, F = d.ffn_cols;
     struct {
@@ -585,7 +595,7 @@ zr_status zr_context_create(const zr_model_desc* desc, int device, zr_context** 
         const std::string why = ctx->err;
         set_global_err(src, "%s", why.c_str());
         free_ctx_buffers(ctx);
-        if (ctx->stream) hipStreamDestroy(ctx->stream);
+        destroy_streams(ctx);
         delete ctx;
         return src;
     }
@@ -603,7 +613,10 @@ zr_status zr_context_create(const zr_model_desc* desc, int device, zr_context** 
 void zr_context_destroy(zr_context* ctx) {
     if (!ctx) return;
     hipSetDevice(ctx->device);
-    if (ctx->stream) hipStreamSynchronize(ctx->stream);
+    for (hipStream_t st : {ctx->stream, ctx->d2h_stream, ctx->h2d_stream})
+        if (st) hipStreamSynchronize(st);
+    for (auto& fb : ctx->xfer_free) (void)hipFree(fb.first);
+    ctx->xfer_free.clear();
     if (ctx->scratch_stage) {
         if (ctx->scratch_stage->dev) hipFree(ctx->scratch_stage->dev);
         delete ctx->scratch_stage;
@@ -614,7 +627,7 @@ void zr_context_destroy(zr_context* ctx) {
     if (ctx->cbor_out) (void)hipFree(ctx->cbor_out);
     if (ctx->sample_ws) (void)hipFree(ctx->sample_ws);
     free_ctx_buffers(ctx);
-    if (ctx->stream) hipStreamDestroy(ctx->stream);
+    destroy_streams(ctx);
     delete ctx;
 }
 
@@ -894,11 +907,10 @@ zr_status zr_attention(zr_context* ctx, zr_staged* s, int layer, const float* d_
     return rc;
 }
 
-static zr_status kv_copy_entry(zr_context* ctx, const int* block_table, int n_pages, int first_offset, int first_row,
-                               int n_rows, float* k, float* v, int to_pool, float** d_rows = nullptr) {
-    if (!ctx || !block_table || (!d_rows && (!k || !v))) return set_global_err(ZR_E_INVALID, "null argument");
+// the page window of a gather / scatter lies inside the table and the pool
+static zr_status kv_copy_check(zr_context* ctx, const int* block_table, int n_pages, int first_offset, int first_row,
+                               int n_rows) {
     if (!ctx->kv_pool) return set_err(ctx, ZR_E_INVALID, "KV pool not created");
-    if (n_rows <= 0) return ZR_OK;
     if (first_offset < 0 || first_offset >= kPageRows || first_row < 0)
         return set_err(ctx, ZR_E_INVALID, "first_offset %d first_row %d", first_offset, first_row);
     const long last = (long)first_offset + first_row + n_rows - 1;
@@ -908,6 +920,15 @@ static zr_status kv_copy_entry(zr_context* ctx, const int* block_table, int n_pa
         if (block_table[p] < 0 || block_table[p] >= ctx->n_pages)
             return set_err(ctx, ZR_E_INVARIANT, "page slot %ld holds page %d outside pool of %d", p, block_table[p],
                            ctx->n_pages);
+    return ZR_OK;
+}
+
+static zr_status kv_copy_entry(zr_context* ctx, const int* block_table, int n_pages, int first_offset, int first_row,
+                               int n_rows, float* k, float* v, int to_pool, float** d_rows = nullptr) {
+    if (!ctx || !block_table || (!d_rows && (!k || !v))) return set_global_err(ZR_E_INVALID, "null argument");
+    if (!ctx->kv_pool) return set_err(ctx, ZR_E_INVALID, "KV pool not created");
+    if (n_rows <= 0) return ZR_OK;
+    if (zr_status rc = kv_copy_check(ctx, block_table, n_pages, first_offset, first_row, n_rows)) return rc;
     ZR_HIP(ctx, hipSetDevice(ctx->device));
     const int L = ctx->desc.num_layers;
     const size_t elems = (size_t)L * n_rows * ctx->kv_cols;
@@ -941,6 +962,170 @@ static zr_status kv_copy_entry(zr_context* ctx, const int* block_table, int n_pa
     e = hipStreamSynchronize(ctx->stream);
     if (!rc && e != hipSuccess) rc = set_err(ctx, ZR_E_HIP, "kv copy: %s", hipGetErrorString(e));
     return rc;
+}
+
+}  // extern "C"
+
+// One session window's KV in a device buffer of its own, on its way to or
+// from host memory on a copy stream: K [layers][rows][kv_cols], then V, then
+// room for a page table.  `used` is recorded after the last compute-stream
+// kernel on the buffer; `copied` after the host copy.
+struct zr_transfer {
+    zr_context* ctx = nullptr;
+    float* buf = nullptr;
+    size_t floats = 0;
+    int rows = 0;
+    bool to_host = false;
+    hipEvent_t copied = nullptr;
+    hipEvent_t used = nullptr;
+};
+
+namespace zr {
+
+// a transfer with a buffer of >= floats: the smallest finished one that fits, else a new allocation
+static zr_status xfer_new(zr_context* ctx, size_t floats, zr_transfer** out) {
+    zr_transfer* t = new zr_transfer();
+    t->ctx = ctx;
+    int best = -1;
+    for (int i = 0; i < (int)ctx->xfer_free.size(); ++i)
+        if (ctx->xfer_free[i].second >= floats && (best < 0 || ctx->xfer_free[i].second < ctx->xfer_free[best].second))
+            best = i;
+    hipError_t e = hipSuccess;
+    if (best >= 0) {
+        t->buf = ctx->xfer_free[best].first;
+        t->floats = ctx->xfer_free[best].second;
+        ctx->xfer_free.erase(ctx->xfer_free.begin() + best);
+    } else {
+        e = hipMalloc(&t->buf, floats * sizeof(float));
+        t->floats = floats;
+    }
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&t->copied, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&t->used, hipEventDisableTiming);
+    if (e != hipSuccess) {
+        if (t->buf && best < 0) (void)hipFree(t->buf);
+        else if (t->buf) ctx->xfer_free.emplace_back(t->buf, t->floats);
+        if (t->copied) (void)hipEventDestroy(t->copied);
+        if (t->used) (void)hipEventDestroy(t->used);
+        delete t;
+        return set_err(ctx, e == hipErrorOutOfMemory ? ZR_E_OOM : ZR_E_HIP, "KV transfer buffer: %s",
+                       hipGetErrorString(e));
+    }
+    *out = t;
+    return ZR_OK;
+}
+
+}  // namespace zr
+
+extern "C" {
+
+zr_status zr_kv_gather_async(zr_context* ctx, const int* block_table, int n_pages, int first_offset, int first_row,
+                             int n_rows, float* dst_k, float* dst_v, zr_transfer** out) {
+    if (!ctx || !block_table || !dst_k || !dst_v || !out) return set_global_err(ZR_E_INVALID, "null argument");
+    *out = nullptr;
+    if (n_rows <= 0) return set_err(ctx, ZR_E_INVALID, "a KV transfer needs rows (%d)", n_rows);
+    if (zr_status rc = kv_copy_check(ctx, block_table, n_pages, first_offset, first_row, n_rows)) return rc;
+    ZR_HIP(ctx, hipSetDevice(ctx->device));
+    const int L = ctx->desc.num_layers;
+    const size_t elems = (size_t)L * n_rows * ctx->kv_cols;
+    zr_transfer* t = nullptr;
+    if (zr_status rc = xfer_new(ctx, 2 * elems + (size_t)n_pages, &t)) return rc;
+    t->rows = n_rows;
+    t->to_host = true;
+    float* d_k = t->buf;
+    float* d_v = d_k + elems;
+    int* d_table = (int*)(d_v + elems);
+    // the gather on the compute stream (the session's pages may be handed out
+    // right after this call: later kernels run after it), the copy-out on the
+    // device-to-host stream once the gather is done
+    hipError_t e = hipMemcpyAsync(d_table, block_table, 4 * (size_t)n_pages, hipMemcpyHostToDevice, ctx->stream);
+    zr_status rc = e == hipSuccess ? ZR_OK : set_err(ctx, ZR_E_HIP, "kv transfer table: %s", hipGetErrorString(e));
+    if (!rc) rc = launch_kv_copy(ctx, 0, L, d_table, first_offset, first_row, n_rows, d_k, d_v, 0);
+    if (!rc) {
+        e = hipEventRecord(t->used, ctx->stream);
+        if (e == hipSuccess) e = hipStreamWaitEvent(ctx->d2h_stream, t->used, 0);
+        if (e == hipSuccess) e = hipMemcpyAsync(dst_k, d_k, 4 * elems, hipMemcpyDeviceToHost, ctx->d2h_stream);
+        if (e == hipSuccess) e = hipMemcpyAsync(dst_v, d_v, 4 * elems, hipMemcpyDeviceToHost, ctx->d2h_stream);
+        if (e == hipSuccess) e = hipEventRecord(t->copied, ctx->d2h_stream);
+        if (e != hipSuccess) rc = set_err(ctx, ZR_E_HIP, "kv transfer copy-out: %s", hipGetErrorString(e));
+    }
+    if (rc) {
+        zr_transfer_destroy(t);
+        return rc;
+    }
+    *out = t;
+    return ZR_OK;
+}
+
+zr_status zr_kv_upload_async(zr_context* ctx, const float* src_k, const float* src_v, int n_rows, zr_transfer** out) {
+    if (!ctx || !src_k || !src_v || !out) return set_global_err(ZR_E_INVALID, "null argument");
+    *out = nullptr;
+    if (n_rows <= 0) return set_err(ctx, ZR_E_INVALID, "a KV transfer needs rows (%d)", n_rows);
+    ZR_HIP(ctx, hipSetDevice(ctx->device));
+    const size_t elems = (size_t)ctx->desc.num_layers * n_rows * ctx->kv_cols;
+    zr_transfer* t = nullptr;
+    // room for the page table of any placement of the rows (a partial first page)
+    if (zr_status rc = xfer_new(ctx, 2 * elems + (size_t)n_rows / kPageRows + 2, &t)) return rc;
+    t->rows = n_rows;
+    hipError_t e = hipMemcpyAsync(t->buf, src_k, 4 * elems, hipMemcpyHostToDevice, ctx->h2d_stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(t->buf + elems, src_v, 4 * elems, hipMemcpyHostToDevice, ctx->h2d_stream);
+    if (e == hipSuccess) e = hipEventRecord(t->copied, ctx->h2d_stream);
+    if (e == hipSuccess) e = hipEventRecord(t->used, ctx->h2d_stream);
+    if (e != hipSuccess) {
+        zr_status rc = set_err(ctx, ZR_E_HIP, "kv transfer upload: %s", hipGetErrorString(e));
+        zr_transfer_destroy(t);
+        return rc;
+    }
+    *out = t;
+    return ZR_OK;
+}
+
+zr_status zr_kv_scatter_transfer(zr_context* ctx, zr_transfer* t, const int* block_table, int n_pages,
+                                 int first_offset, int first_row, int n_rows) {
+    if (!ctx || !t || !block_table) return set_global_err(ZR_E_INVALID, "null argument");
+    if (t->ctx != ctx) return set_err(ctx, ZR_E_INVALID, "KV transfer of another context");
+    if (n_rows != t->rows) return set_err(ctx, ZR_E_INVALID, "KV transfer holds %d rows, not %d", t->rows, n_rows);
+    if (zr_status rc = kv_copy_check(ctx, block_table, n_pages, first_offset, first_row, n_rows)) return rc;
+    const int L = ctx->desc.num_layers;
+    const size_t elems = (size_t)L * n_rows * ctx->kv_cols;
+    if (2 * elems + (size_t)n_pages > t->floats)
+        return set_err(ctx, ZR_E_INVALID, "page table of %d pages does not fit the KV transfer", n_pages);
+    ZR_HIP(ctx, hipSetDevice(ctx->device));
+    float* d_k = t->buf;
+    float* d_v = d_k + elems;
+    int* d_table = (int*)(d_v + elems);
+    // an upload is waited for; a gather's rows are on the device already (an
+    // earlier launch on this stream), its copy-out only reads them
+    hipError_t e = hipMemcpyAsync(d_table, block_table, 4 * (size_t)n_pages, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess && !t->to_host) e = hipStreamWaitEvent(ctx->stream, t->copied, 0);
+    if (e != hipSuccess) return set_err(ctx, ZR_E_HIP, "kv transfer scatter: %s", hipGetErrorString(e));
+    if (zr_status rc = launch_kv_copy(ctx, 0, L, d_table, first_offset, first_row, n_rows, d_k, d_v, 1)) return rc;
+    ZR_HIP(ctx, hipEventRecord(t->used, ctx->stream));
+    return ZR_OK;
+}
+
+int zr_transfer_done(const zr_transfer* t) {
+    if (!t) return set_global_err(ZR_E_INVALID, "null argument");
+    const hipError_t e = hipEventQuery(t->copied);
+    if (e == hipSuccess) return 1;
+    if (e == hipErrorNotReady) return 0;
+    return set_err(t->ctx, ZR_E_HIP, "KV transfer: %s", hipGetErrorString(e));
+}
+
+zr_status zr_transfer_wait(zr_transfer* t) {
+    if (!t) return set_global_err(ZR_E_INVALID, "null argument");
+    ZR_HIP(t->ctx, hipEventSynchronize(t->copied));
+    return ZR_OK;
+}
+
+void zr_transfer_destroy(zr_transfer* t) {
+    if (!t) return;
+    // the buffer is reused once its host copy and its last kernel are done
+    (void)hipEventSynchronize(t->copied);
+    (void)hipEventSynchronize(t->used);
+    if (t->buf) t->ctx->xfer_free.emplace_back(t->buf, t->floats);
+    (void)hipEventDestroy(t->copied);
+    (void)hipEventDestroy(t->used);
+    delete t;
 }
 
 zr_status zr_kv_gather(zr_context* ctx, const int* block_table, int n_pages, int first_offset, int first_row,

@@ -547,10 +547,11 @@ int zrh_block_table(const zrh_backend* b, uint32_t* page_ids, int* start_tokens,
     return n;
 }
 
-zr_status zrh_export_kv(const zrh_backend* cb, int max_cached_tokens, float* k, float* v, int* rows,
-                        int* base_position, int* next_position) {
-    zrh_backend* b = (zrh_backend*)cb;
-    if (!b || !rows) return set_global_err(ZR_E_INVALID, "null argument");
+extern "C++" {
+// export_kv_cache's checks and window; `gather` copies rows [first, first + keep)
+template <typename Gather>
+static zr_status export_rows(zrh_backend* b, int max_cached_tokens, int* rows, int* base_position,
+                             int* next_position, bool have_buffers, Gather gather) {
     const SessionKV& kv = b->kv;
     if (kv.base_position + kv.seq_len != b->position)
         return set_err(b->ctx, ZR_E_INVARIANT, "Device KV export next_position %d does not match cache next position %d",
@@ -561,21 +562,46 @@ zr_status zrh_export_kv(const zrh_backend* cb, int max_cached_tokens, float* k, 
     if (kv.seq_len == 0) return ZR_OK;
     int keep = kv.seq_len;
     if (max_cached_tokens >= 0) keep = std::min(keep, std::max(max_cached_tokens, 1));
-    if (!k || !v) return set_err(b->ctx, ZR_E_INVALID, "null export buffers");
+    if (!have_buffers) return set_err(b->ctx, ZR_E_INVALID, "null export buffers");
     if (!b->ctx) return set_global_err(ZR_E_INVALID, "bookkeeping-only pool has no device context");
     std::vector<int> table;
     int foff = 0;
     zr_status rc = device_table(b, table, &foff);
-    if (!rc) rc = zr_kv_gather(b->ctx, table.data(), (int)table.size(), foff, kv.seq_len - keep, keep, k, v);
+    if (!rc) rc = gather(table, foff, kv.seq_len - keep, keep);
     if (rc) return rc;
     *rows = keep;
     if (base_position) *base_position = kv.base_position + (kv.seq_len - keep);
     return ZR_OK;
 }
+}  // extern "C++"
 
-zr_status zrh_import_kv(zrh_backend* b, const float* k, const float* v, int rows, int base_position,
-                        int next_position) {
-    if (!b) return set_global_err(ZR_E_INVALID, "null argument");
+zr_status zrh_export_kv_async(const zrh_backend* cb, int max_cached_tokens, float* k, float* v, int* rows,
+                              int* base_position, int* next_position, zr_transfer** out) {
+    zrh_backend* b = (zrh_backend*)cb;
+    if (!b || !rows || !out) return set_global_err(ZR_E_INVALID, "null argument");
+    *out = nullptr;
+    return export_rows(b, max_cached_tokens, rows, base_position, next_position, k && v,
+                       [&](const std::vector<int>& table, int foff, int first, int keep) {
+                           return zr_kv_gather_async(b->ctx, table.data(), (int)table.size(), foff, first, keep, k, v,
+                                                     out);
+                       });
+}
+
+zr_status zrh_export_kv(const zrh_backend* cb, int max_cached_tokens, float* k, float* v, int* rows,
+                        int* base_position, int* next_position) {
+    zrh_backend* b = (zrh_backend*)cb;
+    if (!b || !rows) return set_global_err(ZR_E_INVALID, "null argument");
+    return export_rows(b, max_cached_tokens, rows, base_position, next_position, k && v,
+                       [&](const std::vector<int>& table, int foff, int first, int keep) {
+                           return zr_kv_gather(b->ctx, table.data(), (int)table.size(), foff, first, keep, k, v);
+                       });
+}
+
+extern "C++" {
+// import_kv_cache's checks, page binding and rollback; `scatter` writes the rows
+template <typename Scatter>
+static zr_status import_rows(zrh_backend* b, int rows, int base_position, int next_position, bool have_rows,
+                             Scatter scatter) {
     if (rows < 0 || rows > next_position)
         return set_err(b->ctx, ZR_E_INVALID, "KV sequence state is invalid: cached_tokens %d exceeds next_position %d",
                        rows, next_position);
@@ -589,7 +615,7 @@ zr_status zrh_import_kv(zrh_backend* b, const float* k, const float* v, int rows
     b->kv.base_position = base_position;
     zr_status rc = ZR_OK;
     if (rows > 0) {
-        if (!k || !v) rc = set_err(b->ctx, ZR_E_INVALID, "null import buffers");
+        if (!have_rows) rc = set_err(b->ctx, ZR_E_INVALID, "null import buffers");
         const int max_seq = std::max(b->max_seq_len, 1);
         const int keep = std::min(rows, max_seq);
         if (!rc) rc = append_rows(b, keep);
@@ -601,7 +627,7 @@ zr_status zrh_import_kv(zrh_backend* b, const float* k, const float* v, int rows
         std::vector<int> table;
         int foff = 0;
         if (!rc) rc = device_table(b, table, &foff);
-        if (!rc) rc = zr_kv_scatter(b->ctx, table.data(), (int)table.size(), foff, 0, rows, k, v);
+        if (!rc) rc = scatter(table, foff);
     }
     if (!rc && b->kv.base_position != next_position - rows)
         rc = set_err(b->ctx, ZR_E_INVARIANT, "Recovered device KV cache base position %d does not match snapshot first cached position %d",
@@ -614,6 +640,22 @@ zr_status zrh_import_kv(zrh_backend* b, const float* k, const float* v, int rows
     }
     b->position = next_position;
     return ZR_OK;
+}
+}  // extern "C++"
+
+zr_status zrh_import_kv(zrh_backend* b, const float* k, const float* v, int rows, int base_position,
+                        int next_position) {
+    if (!b) return set_global_err(ZR_E_INVALID, "null argument");
+    return import_rows(b, rows, base_position, next_position, k && v, [&](const std::vector<int>& table, int foff) {
+        return zr_kv_scatter(b->ctx, table.data(), (int)table.size(), foff, 0, rows, k, v);
+    });
+}
+
+zr_status zrh_import_kv_transfer(zrh_backend* b, zr_transfer* t, int rows, int base_position, int next_position) {
+    if (!b || !t) return set_global_err(ZR_E_INVALID, "null argument");
+    return import_rows(b, rows, base_position, next_position, true, [&](const std::vector<int>& table, int foff) {
+        return zr_kv_scatter_transfer(b->ctx, t, table.data(), (int)table.size(), foff, 0, rows);
+    });
 }
 
 zr_status zrh_export_kv_cbor(const zrh_backend* cb, int max_cached_tokens, uint8_t* out, size_t capacity,

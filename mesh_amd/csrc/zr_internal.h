@@ -186,6 +186,12 @@ struct zr_context {
     zr::StagedMeta* scratch_stage = nullptr;  // reused by zr_forward
     float* kv_stage = nullptr;      // KV gather / scatter staging (rows + table)
     size_t kv_stage_floats = 0;
+    // KV window copies between HBM and host memory that overlap the compute
+    // stream (zr_transfer): one stream per direction, default priority, and
+    // the device buffers of finished transfers, kept for reuse (hipFree
+    // would synchronise the device)
+    hipStream_t d2h_stream = nullptr, h2d_stream = nullptr;
+    std::vector<std::pair<float*, size_t>> xfer_free;
     void* cbor_ws = nullptr;        // KV snapshot encoder: chunk sizes / offsets / header tables
     size_t cbor_ws_bytes = 0;
     void* cbor_out = nullptr;       // KV snapshot encoder: the document on the device

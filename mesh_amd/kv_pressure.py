@@ -16,6 +16,14 @@ restores them when pages free up.
   larger KV footprint.
 * Restore = import_kv_cache (forward_pass.rs:2450-2454 -> 1206-1242): clear,
   scatter the window into fresh pages, continue at the saved position.
+
+The reference makes these copies synchronously.  Here (async_transfers, the
+default) each moves over PCIe on a stream of its own while decode steps run
+(KVTransfer): an eviction gathers the window into a device buffer and returns
+its pages at once, the copy to pinned host memory follows on the
+device-to-host stream; the oldest evicted windows are uploaded ahead of their
+restore on the host-to-device stream, and a session restored before its
+eviction copy finished is scattered straight from that device buffer.
 """
 from __future__ import annotations
 
@@ -35,6 +43,7 @@ class SoakSession:
     backend: object = None              # RocmExecutionBackend while resident
     snapshot: Optional[KVCacheSnapshot] = None  # while evicted
     steps_served: int = 0
+    transfer: object = None             # KVTransfer of the evicted window: its export or its upload
 
 
 @dataclass
@@ -66,7 +75,8 @@ class KvPressureSoak:
                  retention: int, max_seq_len: int, context_sampler: Callable[[np.random.Generator], int],
                  admit: Callable[[SoakSession, int, np.random.Generator], int], seed: int,
                  on_step: Optional[Callable[[List[SoakSession], List[int], np.ndarray], None]] = None,
-                 on_evict: Optional[Callable[[SoakSession], None]] = None):
+                 on_evict: Optional[Callable[[SoakSession], None]] = None, async_transfers: bool = True,
+                 prefetch: int = 2):
         self.ctx = ctx
         self.max_sessions = max_sessions
         self.join_rate = join_rate
@@ -81,6 +91,9 @@ class KvPressureSoak:
         self.active: List[SoakSession] = []
         self.evicted: List[SoakSession] = []   # FIFO
         self.free_pinned: list = []             # snapshot buffers of restored sessions, reused
+        self.async_transfers = async_transfers
+        self.prefetch = prefetch                # evicted windows uploaded ahead of their restore
+        self.retiring: list = []                # (KVTransfer, pinned buffer to reuse once it is done)
         self.next_sid = 0
         self.stats = SoakStats()
 
@@ -99,13 +112,18 @@ class KvPressureSoak:
         victim = min(cands, key=lambda s: (s.steps_served, -s.backend.live_kv_cache_bytes(), s.sid))
         t0 = time.perf_counter()
         buf = self.free_pinned.pop() if self.free_pinned else None
-        victim.snapshot = victim.backend.export_kv_cache(self.retention, pinned=True, into=buf)
+        if self.async_transfers:
+            victim.snapshot, victim.transfer = victim.backend.export_kv_cache_async(self.retention, into=buf)
+        else:
+            victim.snapshot = victim.backend.export_kv_cache(self.retention, pinned=True, into=buf)
         if buf is not None and (victim.snapshot is None or victim.snapshot.storage is not buf):
             self.free_pinned.append(buf)
         victim.backend.close()  # pages back to the pool
         victim.backend = None
         self.stats.evict_s += time.perf_counter() - t0
         if self.on_evict is not None:
+            if victim.transfer is not None:
+                victim.transfer.wait()  # the callback reads the snapshot
             self.on_evict(victim)
         self.active.remove(victim)
         self.evicted.append(victim)
@@ -139,6 +157,9 @@ class KvPressureSoak:
         for s in list(self.evicted):
             if self.rng.random() < self.leave_prob:
                 self.evicted.remove(s)
+                if s.transfer is not None:
+                    self._retire(s.transfer, s.snapshot.storage)
+                    s.transfer = None
                 self.stats.leaves += 1
 
     def _joins(self):
@@ -159,7 +180,14 @@ class KvPressureSoak:
                 break
             t0 = time.perf_counter()
             b = self.ctx.new_backend(self.max_seq_len)
-            if s.snapshot is not None:
+            if s.snapshot is not None and self.async_transfers:
+                # from the window's device buffer: its own export still in flight, its upload
+                # (issued a step ahead), or an upload issued now that the scatter waits for on the device
+                t = s.transfer if s.transfer is not None else self.ctx.upload_kv_async(s.snapshot)
+                b.import_kv_cache_transfer(s.snapshot, t)
+                self._retire(t, s.snapshot.storage)
+                s.transfer = None
+            elif s.snapshot is not None:
                 b.import_kv_cache(s.snapshot)
                 if s.snapshot.storage is not None:
                     self.free_pinned.append(s.snapshot.storage)
@@ -169,14 +197,54 @@ class KvPressureSoak:
             self.active.append(s)
             self.stats.restores += 1
 
+    # -- transfers ----------------------------------------------------------------------
+    def _retire(self, t, pinned):
+        self.retiring.append((t, pinned))
+
+    def _reap(self, block: bool = False):
+        """Closes finished transfers (their device buffers go back to the context) and
+        recycles their pinned buffers; an evicted window whose export has landed in host
+        memory gives up its device buffer."""
+        keep = []
+        for t, pinned in self.retiring:
+            if block or t.done():
+                t.close()
+                if pinned is not None:
+                    self.free_pinned.append(pinned)
+            else:
+                keep.append((t, pinned))
+        self.retiring = keep
+        for s in self.evicted[self.prefetch:]:
+            if s.transfer is not None and (block or s.transfer.done()):
+                s.transfer.close()
+                s.transfer = None
+
+    def _prefetch(self):
+        """Uploads the oldest evicted windows (the next restores) while the coming step runs."""
+        for s in self.evicted[:self.prefetch]:
+            if s.transfer is None and s.snapshot is not None:
+                s.transfer = self.ctx.upload_kv_async(s.snapshot)
+
+    def finish(self):
+        """Waits for every copy in flight and releases the device buffers."""
+        self._reap(block=True)
+        for s in self.evicted:
+            if s.transfer is not None:
+                s.transfer.close()
+                s.transfer = None
+
     # -- one decode step ----------------------------------------------------------------
     def step(self, want_logits: bool = False):
         t_start = time.perf_counter()
+        if self.async_transfers:
+            self._reap()
         self._leaves()
         self._restores()  # evicted sessions resume before new ones are admitted
         self._joins()
         # every resident session may open a new page this step
         self._make_room(len(self.active))
+        if self.async_transfers:
+            self._prefetch()
         if not self.active:
             return None
         reqs = [DecodeMicrobatchRequest(str(s.sid), s.token, s.backend) for s in self.active]

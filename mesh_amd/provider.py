@@ -131,6 +131,39 @@ def bf16_bits(x: np.ndarray) -> np.ndarray:
     return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
 
 
+class KVTransfer:
+    """A session's KV window between HBM and host memory, its PCIe copy on a
+    stream of its own (zr_transfer): from zrh_export_kv_async (to the host) or
+    zr_kv_upload_async (from the host)."""
+
+    def __init__(self, ctx: "DeviceContext", handle: int):
+        self.ctx = ctx
+        self.h = handle
+        ctx._transfers.add(self)
+
+    def done(self) -> bool:
+        """The host copy has finished."""
+        r = self.ctx.lib.zr_transfer_done(self.h)
+        if r < 0:
+            self.ctx.check(r)
+        return r == 1
+
+    def wait(self):
+        self.ctx.check(self.ctx.lib.zr_transfer_wait(self.h))
+
+    def close(self):
+        """Waits for the copy and for the last kernel on the device buffer, which the context keeps for reuse."""
+        if getattr(self, "h", None) and self.ctx.h:
+            self.ctx.lib.zr_transfer_destroy(self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class PinnedBuffer:
     """Pinned host memory of a context (zr_host_alloc), viewed as numpy."""
 
@@ -260,10 +293,13 @@ class DeviceContext:
         self.pool = None
         self._backends = weakref.WeakSet()
         self._pinned = weakref.WeakSet()
+        self._transfers = weakref.WeakSet()
 
     def close(self):
         for b in list(getattr(self, "_backends", ())):
             b.close()
+        for t in list(getattr(self, "_transfers", ())):  # before the pinned buffers they copy into
+            t.close()
         for p in list(getattr(self, "_pinned", ())):
             p.free()
         if getattr(self, "pool", None) is not None:
@@ -331,6 +367,16 @@ class DeviceContext:
         out = np.zeros(max(self.geo.num_heads, 1), np.uint32)
         self.check(self.lib.zr_kv_head_map(self.h, _ptr(out, C.c_uint32), out.size, C.byref(n)))
         return out[: n.value].tolist()
+
+    def upload_kv_async(self, snap: "KVCacheSnapshot") -> KVTransfer:
+        """Starts copying a snapshot's rows into a device buffer (zr_kv_upload_async) for a
+        later import_kv_cache_transfer; the arrays must stay untouched until the transfer is done."""
+        k, v = snap.keys, snap.values
+        assert k.dtype == np.float32 and v.dtype == np.float32 and k.flags.c_contiguous and v.flags.c_contiguous
+        t = C.c_void_p()
+        self.check(self.lib.zr_kv_upload_async(self.h, _ptr(k, C.c_float), _ptr(v, C.c_float), snap.cached_tokens,
+                                               C.byref(t)))
+        return KVTransfer(self, t.value)
 
     def new_backend(self, max_seq_len: int = 4096) -> "RocmExecutionBackend":
         b = RocmExecutionBackend(self, max_seq_len)
@@ -489,6 +535,38 @@ class RocmExecutionBackend:
         if owner is not None:
             return KVCacheSnapshot(nxt.value, r, k, v, owner)
         return KVCacheSnapshot(nxt.value, r, k, v)
+
+    def export_kv_cache_async(self, max_cached_tokens: Optional[int] = None,
+                              into: Optional[PinnedBuffer] = None):
+        """export_kv_cache with the copy to pinned host memory in flight
+        (zrh_export_kv_async): returns (snapshot, transfer), (None, None) for
+        an empty cache.  The session's pages may be released at once; the
+        snapshot's arrays hold the rows after transfer.wait() (or done())."""
+        geo = self.ctx.geo
+        n = self.cache_seq_len()
+        if max_cached_tokens is not None:
+            n = min(n, max(int(max_cached_tokens), 1))
+        shape = (geo.num_layers, max(n, 1), geo.kv_cols)
+        need = 2 * 4 * int(np.prod(shape))
+        owner = into if into is not None and into.ptr and into.nbytes >= need else PinnedBuffer(self.ctx, need)
+        both = owner.array(np.float32, (2,) + shape)
+        k, v = both[0], both[1]
+        rows, base, nxt, t = C.c_int(), C.c_int(), C.c_int(), C.c_void_p()
+        self.ctx.check(self.lib.zrh_export_kv_async(self.h, -1 if max_cached_tokens is None else int(max_cached_tokens),
+                                                    _ptr(k, C.c_float), _ptr(v, C.c_float), C.byref(rows),
+                                                    C.byref(base), C.byref(nxt), C.byref(t)))
+        if rows.value == 0:
+            if owner is not into:
+                owner.free()
+            return None, None
+        assert rows.value == n and t.value
+        return KVCacheSnapshot(nxt.value, rows.value, k, v, owner), KVTransfer(self.ctx, t.value)
+
+    def import_kv_cache_transfer(self, snap: KVCacheSnapshot, transfer: KVTransfer):
+        """import_kv_cache from a transfer's device buffer (zrh_import_kv_transfer): an upload of
+        `snap`, or the in-flight export that produced it."""
+        self.ctx.check(self.lib.zrh_import_kv_transfer(self.h, transfer.h, snap.cached_tokens,
+                                                       snap.first_cached_position(), snap.next_position))
 
     def import_kv_cache(self, snap: KVCacheSnapshot):
         k = np.ascontiguousarray(snap.keys, np.float32)
