@@ -453,8 +453,10 @@ def cpu_baseline(name):
                        f"f32 weights/KV as the reference CPU provider")
 
 
+# pinned_windows: eviction buffers (2048-row windows, 0.54 GB each) pinned before the steps, about the
+# number of sessions the 85% pool keeps evicted at a time
 SOAK = dict(workload="llama3_8b_b256", pool_frac=0.85, join_rate=4.0, leave_prob=1 / 64, retention=2048,
-            max_sessions=256, seed=0xC5)
+            max_sessions=256, seed=0xC5, pinned_windows=40, prefetch=4)
 
 
 def measure_soak(steps, warmup):
@@ -486,7 +488,9 @@ def measure_soak(steps, warmup):
 
     soak = KvPressureSoak(ctx, max_sessions=SOAK["max_sessions"], join_rate=SOAK["join_rate"],
                           leave_prob=SOAK["leave_prob"], retention=SOAK["retention"],
-                          max_seq_len=w["max_seq_len"], context_sampler=sample_len, admit=admit, seed=SOAK["seed"])
+                          max_seq_len=w["max_seq_len"], context_sampler=sample_len, admit=admit, seed=SOAK["seed"],
+                          prefetch=SOAK["prefetch"])
+    soak.reserve_pinned(SOAK["pinned_windows"])
     for L in ctxlens:
         soak.add_session(int(L))
     for _ in range(warmup):

@@ -33,7 +33,8 @@ from typing import Callable, List, Optional
 
 import numpy as np
 
-from .provider import BackendMicrobatchExecutor, DecodeMicrobatchRequest, DeviceContext, KVCacheSnapshot
+from .provider import (BackendMicrobatchExecutor, DecodeMicrobatchRequest, DeviceContext, KVCacheSnapshot,
+                       PinnedBuffer)
 
 
 @dataclass
@@ -97,6 +98,23 @@ class KvPressureSoak:
         self.next_sid = 0
         self.stats = SoakStats()
 
+    # -- pinned snapshot buffers --------------------------------------------------------
+    def _window_bytes(self) -> int:
+        g = self.ctx.geo
+        return 2 * 4 * g.num_layers * self.retention * g.kv_cols
+
+    def _pinned(self):
+        """A pinned buffer for one eviction window: a recycled one, else a new one of the
+        full window's size (any window fits any buffer, so they keep circulating)."""
+        if self.free_pinned:
+            return self.free_pinned.pop()
+        return PinnedBuffer(self.ctx, self._window_bytes())
+
+    def reserve_pinned(self, n: int):
+        """Pins n window buffers ahead (pinning 0.5 GB takes ~10 ms of host time)."""
+        for _ in range(n):
+            self.free_pinned.append(PinnedBuffer(self.ctx, self._window_bytes()))
+
     # -- pages --------------------------------------------------------------------------
     @staticmethod
     def pages_for(rows: int) -> int:
@@ -111,7 +129,7 @@ class KvPressureSoak:
             return False
         victim = min(cands, key=lambda s: (s.steps_served, -s.backend.live_kv_cache_bytes(), s.sid))
         t0 = time.perf_counter()
-        buf = self.free_pinned.pop() if self.free_pinned else None
+        buf = self._pinned()
         if self.async_transfers:
             victim.snapshot, victim.transfer = victim.backend.export_kv_cache_async(self.retention, into=buf)
         else:
