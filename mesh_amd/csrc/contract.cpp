@@ -17,7 +17,7 @@ const char* const kStageKernels[] = {
     "rms_norm_vec_kernel,rms_norm_kernel,gemm_kernel",
     "rope_table_kernel,rope_kv_write_kernel,rope_kv_write_vec_kernel,paged_attention_kernel",
     "paged_attention_kernel,paged_prefill_attention_kernel,attention_merge_kernel",
-    "rms_norm_vec_kernel,rms_norm_kernel,gemm_kernel,splitk_reduce_kernel",
+    "rms_norm_vec_kernel,rms_norm_kernel,gemm_kernel,gemm_swiglu_ksplit_kernel,splitk_reduce_kernel",
     "argmax_partial_kernel,argmax_final_kernel,sample_kernel",
 };
 const char* const kHostKernels[] = {"host_assisted_sampling"};

@@ -309,6 +309,128 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_kernel(
     }
 }
 
+// gate/up + SwiGLU for at most 32 rows in one launch: K split over the 4
+// waves of a workgroup instead of over workgroups (no slabs, no reduce
+// kernel).  A workgroup owns one gate / up tile pair (64 columns of the
+// interleaved product, 32 columns of H); wave w takes k-steps w, w + 4, ...
+// through a ring of its own in LDS: it copies a step's 8 fragments (A hi / lo
+// and both weight tiles, two k-halves each) with `buffer_load ... lds` and
+// reads only what it copied, so its own vmcnt wait orders the ring and the
+// waves never wait for one another until the end.  Each wave accumulates its
+// steps in k order ((kh 0, hi), (kh 0, lo), (kh 1, hi), (kh 1, lo) per step);
+// the four partial sums then meet in LDS and are added in wave order, and
+// silu(g) * u goes to H as the next GEMM's fragment-packed bf16 hi (+ lo).
+// Requires M <= 32 and KT % 4 == 0 (every wave the same number of steps).
+// ring_wait without the block barrier: only this wave's copies order its ring
+template <int N>
+__device__ __forceinline__ void wave_copies_wait() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));  // vmcnt(N), expcnt(7), lgkmcnt(0)
+    asm volatile("" ::: "memory");
+}
+template <int VM, int MAXA>
+__device__ __forceinline__ void wave_ring_wait(int ahead) {
+    if constexpr (MAXA > 0) {
+        if (ahead >= MAXA) {
+            wave_copies_wait<VM * MAXA>();
+            return;
+        }
+        wave_ring_wait<VM, MAXA - 1>(ahead);
+    } else {
+        wave_copies_wait<0>();
+    }
+}
+
+template <int STAGES, int HL>
+__global__ __launch_bounds__(256) void gemm_swiglu_ksplit_kernel(const uint16_t* __restrict__ A, int M, int K,
+                                                                const bf16x8* __restrict__ Wp, int KT, int N,
+                                                                uint16_t* __restrict__ H, int h_lo) {
+    constexpr int FW = 2 * HL + 4;  // fragments per k-step: A (hl, kh), then weights (tile, kh)
+    typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+    __shared__ bf16x8 lds[4][STAGES][FW][64];
+    const int pair = blockIdx.x;  // weight tiles 2 pair (gate), 2 pair + 1 (up)
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int KT16 = 2 * KT;
+    const int nsteps = KT / 4;
+    const __amdgpu_buffer_rsrc_t rsrc_a = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsrc_w = __builtin_amdgcn_make_buffer_rsrc((void*)Wp, 0, 0x7fffffff, 0x00020000);
+    const int voff = lane * 16;
+    auto issue = [&](int slot, int step) {
+        const int kt = step * 4 + wave;
+#pragma unroll
+        for (int hl = 0; hl < HL; ++hl)
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh)  // row tile 0 of the packed A operand (hi plane, then lo)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (lds_void*)&lds[wave][slot][hl * 2 + kh][0], 16, voff,
+                                                         ((hl * KT16 + 2 * kt + kh) << 10), 0, 0);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_w, (lds_void*)&lds[wave][slot][2 * HL + t * 2 + kh][0],
+                                                         16, voff, (((2 * pair + t) * KT16 + 2 * kt + kh) << 10), 0, 0);
+    };
+    f32x16 acc[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s)
+        if (s < nsteps) issue(s, s);
+    for (int i0 = 0; i0 < nsteps; i0 += STAGES) {
+#pragma unroll
+        for (int u = 0; u < STAGES; ++u) {
+            const int i = i0 + u;
+            if (i >= nsteps) break;
+            // this wave's copies of step i have landed (later steps may still be in flight)
+            wave_ring_wait<FW, STAGES - 2>(max(0, min(STAGES - 2, nsteps - 1 - i)));
+            if (i + STAGES - 1 < nsteps) issue((u + STAGES - 1) % STAGES, i + STAGES - 1);
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh) {
+                const bf16x8 bg = lds[wave][u][2 * HL + kh][lane], bu = lds[wave][u][2 * HL + 2 + kh][lane];
+#pragma unroll
+                for (int hl = 0; hl < HL; ++hl) {
+                    const bf16x8 a = lds[wave][u][hl * 2 + kh][lane];
+                    acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bg, acc[0], 0, 0, 0);
+                    acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bu, acc[1], 0, 0, 0);
+                }
+            }
+        }
+    }
+    // the four partial sums meet in LDS (the ring is free once every wave is past its last step)
+    __syncthreads();
+    float* red = (float*)&lds[0][0][0][0];  // [wave][tile][i][lane]
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) red[((wave * 2 + t) * 16 + i) * 64 + lane] = acc[t][i];
+    __syncthreads();
+    // thread (i-group tid / 64, lane): elements i = 4 (tid / 64) .. + 3 of the accumulators
+    const int F = N / 2;
+    const size_t plane = a_plane(M, F);
+    const int j = pair * 32 + (lane & 31);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int i = 4 * wave + q;
+        const int m = 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+        float g = red[((0 * 2 + 0) * 16 + i) * 64 + lane], up = red[((0 * 2 + 1) * 16 + i) * 64 + lane];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) {
+            g += red[((w * 2 + 0) * 16 + i) * 64 + lane];
+            up += red[((w * 2 + 1) * 16 + i) * 64 + lane];
+        }
+        if (m < M && j < F) {
+            uint16_t hi, lo;
+            split_bf16(swiglu(g, up), hi, lo);
+            const size_t o = a_pack_index(m, j, F);
+            H[o] = hi;
+            if (h_lo) H[plane + o] = lo;
+        }
+    }
+}
+
 // Sum of split-K slabs [S][M][N] with the epilogue.
 // kEpiStore:  out_f32[m][n] = sum
 // kEpiSwiGLU: N = 2F interleaved per 32 columns; h = silu(g) * u written as
@@ -443,8 +565,22 @@ static GemmCfg pick_cfg(int m, int n, int k, int epilogue = kEpiStore) {
 
 static bool swiglu_fused(int m, int epilogue) { return epilogue == kEpiSwiGLU && m > 64; }
 
+// <= 32 rows of gate / up: SwiGLU in one launch with K split over the waves of
+// a workgroup (gemm_swiglu_ksplit_kernel)
+static bool swiglu_ksplit(int m, int n, int k, int epilogue) {
+    return epilogue == kEpiSwiGLU && m <= 32 && n % 64 == 0 && ((k + 31) / 32) % 4 == 0;
+}
+
 GemmPlan gemm_plan(int m, int n, int k, int epilogue) {
     GemmPlan p;
+    if (swiglu_ksplit(m, n, k, epilogue)) {
+        p.KT = (k + 31) / 32;
+        p.NT = (n + 31) / 32;
+        p.row_blocks = 1;
+        p.col_blocks = p.NT / 2;
+        p.kt_per_split = p.KT;
+        return p;  // one launch, no workspace
+    }
     const GemmCfg c = pick_cfg(m, n, k, epilogue);
     p.KT = (k + 31) / 32;
     p.NT = (n + 31) / 32;
@@ -501,6 +637,21 @@ zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_pack
     const size_t a_bytes = 2 * 2 * a_plane(m, k), w_bytes = 2 * packed_weight_elems(k, n);
     if (a_bytes > 0x7fffffffull || w_bytes > 0x7fffffffull)
         return set_err(ctx, ZR_E_UNSUPPORTED, "GEMM operands of %zu / %zu bytes exceed 2 GiB", a_bytes, w_bytes);
+    const bool split_act = (ctx->desc.flags & ZR_FLAG_SPLIT_ACTIVATIONS) != 0;
+    if (swiglu_ksplit(m, n, k, epilogue) && c_bf16 && !c_f32 && !deferred) {
+        const GemmPlan p = gemm_plan(m, n, k, epilogue);
+        hipEvent_t ev;
+        timing_mark_begin(ctx, kClassGemm, &ev);
+        if (split_act)
+            hipLaunchKernelGGL((gemm_swiglu_ksplit_kernel<3, 2>), dim3(p.col_blocks), dim3(256), 0, ctx->stream, a, m,
+                               k, (const bf16x8*)w_packed, p.KT, n, c_bf16, 1);
+        else
+            hipLaunchKernelGGL((gemm_swiglu_ksplit_kernel<3, 1>), dim3(p.col_blocks), dim3(256), 0, ctx->stream, a, m,
+                               k, (const bf16x8*)w_packed, p.KT, n, c_bf16, 0);
+        ZR_LAUNCH_CHECK(ctx);
+        timing_mark_end(ctx, kClassGemm, ev);
+        return ZR_OK;
+    }
     const GemmPlan p = gemm_plan(m, n, k, epilogue);
     const GemmCfg cfg = pick_cfg(m, n, k, epilogue);
     if (swiglu_fused(m, epilogue) && (!c_bf16 || c_f32 || n % 64 != 0))
@@ -511,7 +662,6 @@ zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_pack
     if (!direct && (size_t)p.splits * split_stride > ctx->splitk_ws_floats)
         return set_err(ctx, ZR_E_OOM, "split-K workspace too small (%d x %d x %d)", p.splits, m, n);
     float* dst = direct ? c_f32 : ctx->splitk_ws;
-    const bool split_act = (ctx->desc.flags & ZR_FLAG_SPLIT_ACTIVATIONS) != 0;
     hipEvent_t ev;
     timing_mark_begin(ctx, kClassGemm, &ev);
     bool launched = false;

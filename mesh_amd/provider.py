@@ -46,7 +46,8 @@ FUSED_KERNEL_STAGES = {
     # one-row decode microbatches: RoPE + KV append run inside paged_attention_kernel
     "rope_kv_write": ["rope_table_kernel", "rope_kv_write_kernel", "rope_kv_write_vec_kernel", "paged_attention_kernel"],
     "paged_attention": ["paged_attention_kernel", "paged_prefill_attention_kernel", "attention_merge_kernel"],
-    "residual_mlp": ["rms_norm_vec_kernel", "rms_norm_kernel", "gemm_kernel", "splitk_reduce_kernel"],
+    "residual_mlp": ["rms_norm_vec_kernel", "rms_norm_kernel", "gemm_kernel", "gemm_swiglu_ksplit_kernel",
+                     "splitk_reduce_kernel"],
     "device_sampling": ["argmax_partial_kernel", "argmax_final_kernel", "sample_kernel"],
 }
 
