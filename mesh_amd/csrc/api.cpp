@@ -292,6 +292,34 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     for (int t = 0; t < st->n_tiles; ++t)
         if (t >= n_decode_tiles || st->h_tiles[t + 1].w - st->h_tiles[t].w > 1) st->h_merge.push_back(t);
     st->n_merge = (int)st->h_merge.size();
+    // Per-launch records in the order the kernels read them, so that a
+    // workgroup's first page and Q loads wait on one metadata load instead of
+    // a chain (rank -> item -> tile -> sequence arrays).
+    {
+        std::vector<int> cuq(S + 1, 0);
+        for (int s = 0; s < S; ++s) cuq[s + 1] = cuq[s] + mb->q_len[s];
+        if (st->n_part_items >= (int)kAttnSingle)
+            return set_err(ctx, ZR_E_INVALID, "%d attention items exceed the record's index field", st->n_part_items);
+        st->h_attn_rec.resize(2 * (size_t)st->n_attn_items);
+        for (int r = 0; r < st->n_attn_items; ++r) {
+            const int item = st->h_order[r];
+            const int4 it = st->h_items[item], tl = st->h_tiles[it.x];
+            const int first = tl.w, end = st->h_tiles[it.x + 1].w;
+            const int seq = tl.x;
+            unsigned meta = (unsigned)item;
+            if (end - first == 1) meta |= kAttnSingle;
+            if (item == end - 1) meta |= kAttnLast;
+            st->h_attn_rec[2 * r] = make_int4(seq, cuq[seq] + tl.y, tl.z, it.y);
+            st->h_attn_rec[2 * r + 1] =
+                make_int4(it.z, mb->kv_before[seq] + tl.y, mb->first_offset[seq], (int)meta);
+        }
+        st->h_merge_rec.resize(st->n_merge);
+        for (int i = 0; i < st->n_merge; ++i) {
+            const int t = st->h_merge[i];
+            const int4 tl = st->h_tiles[t];
+            st->h_merge_rec[i] = make_int4(tl.w, st->h_tiles[t + 1].w - tl.w, cuq[tl.x] + tl.y, tl.z);
+        }
+    }
     // prefill work units: most key tiles first
     {
         std::vector<int> ord(st->h_pblocks.size());
@@ -339,9 +367,8 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     };
     const size_t o_qlen = take(4 * S), o_kvb = take(4 * S), o_fpos = take(4 * S), o_foff = take(4 * S);
     const size_t o_bt = take(4 * (size_t)S * stride), o_tok = take(4 * (size_t)std::max(total_q, 1));
-    const size_t o_items = take(16 * (size_t)st->n_attn_items), o_tiles = take(16 * st->h_tiles.size());
-    const size_t o_merge = take(4 * (size_t)std::max(st->n_merge, 1));
-    const size_t o_order = take(4 * (size_t)std::max(st->n_attn_items, 1));
+    const size_t o_arec = take(32 * (size_t)std::max(st->n_attn_items, 1));
+    const size_t o_mrec = take(16 * (size_t)std::max(st->n_merge, 1));
     const size_t o_pblk = take(16 * (size_t)std::max(st->n_pblocks, 1));
     const size_t o_psplit = take(16 * (size_t)std::max(st->n_pblocks, 1));
     const size_t host_bytes = off;
@@ -366,10 +393,8 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     memcpy(hb + o_foff, mb->first_offset, 4 * S);
     memcpy(hb + o_bt, mb->block_tables, 4 * (size_t)S * stride);
     if (mb->tokens) memcpy(hb + o_tok, mb->tokens, 4 * (size_t)total_q);
-    memcpy(hb + o_items, st->h_items.data(), 16 * (size_t)st->n_attn_items);
-    memcpy(hb + o_tiles, st->h_tiles.data(), 16 * st->h_tiles.size());
-    if (st->n_merge) memcpy(hb + o_merge, st->h_merge.data(), 4 * (size_t)st->n_merge);
-    if (st->n_attn_items) memcpy(hb + o_order, st->h_order.data(), 4 * (size_t)st->n_attn_items);
+    if (st->n_attn_items) memcpy(hb + o_arec, st->h_attn_rec.data(), 32 * (size_t)st->n_attn_items);
+    if (st->n_merge) memcpy(hb + o_mrec, st->h_merge_rec.data(), 16 * (size_t)st->n_merge);
     if (st->n_pblocks) memcpy(hb + o_pblk, st->h_pblocks.data(), 16 * (size_t)st->n_pblocks);
     if (st->n_pblocks) memcpy(hb + o_psplit, st->h_psplits.data(), 16 * (size_t)st->n_pblocks);
     unsigned char* db = (unsigned char*)st->dev;
@@ -379,10 +404,8 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     st->first_offset = (int*)(db + o_foff);
     st->block_tables = (int*)(db + o_bt);
     st->tokens = (uint32_t*)(db + o_tok);
-    st->attn_items = (int4*)(db + o_items);
-    st->attn_tiles = (int4*)(db + o_tiles);
-    st->merge_tiles = (int*)(db + o_merge);
-    st->attn_order = (int*)(db + o_order);
+    st->attn_rec = (int4*)(db + o_arec);
+    st->merge_rec = (int4*)(db + o_mrec);
     st->pblocks = (int4*)(db + o_pblk);
     st->psplits = (int4*)(db + o_psplit);
     st->cu_q = (int*)(db + o_cuq);

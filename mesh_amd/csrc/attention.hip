@@ -191,13 +191,9 @@ struct AttnArgs {
     size_t page_elems;       // elements of one page (K + V, all kv heads)
     const int* block_tables;
     int stride;
-    const int* first_offset;
-    const int* kv_before;
-    const int* cu_q;
-    const int4* items;       // {tile, page_begin, page_end, unused}
-    const int* order;        // dispatch rank -> item (longest first)
+    const int4* rec;         // two records per dispatch rank (longest item first): {seq, first q row, nq,
+                             // page_begin}, {page_end, kv_before + q0, first_offset, item | kAttnSingle | kAttnLast}
     int n_items;
-    const int4* tiles;       // {seq, q0, nq, first_item}
     int G;                   // q heads per kv head
     int kv_heads;
     float scale_log2;        // log2(e) / sqrt(d)
@@ -229,17 +225,16 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
     const int kvh = rem >> 3;
     const int rank = (blockIdx.x / per_grp) * 8 + (rem & 7);
     if (rank >= a.n_items) return;
-    const int item = a.order[rank];
-    const int4 it = a.items[item];
-    const int4 tl = a.tiles[it.x];
-    const int seq = tl.x, q0 = tl.y, nq = tl.z;
+    // everything the workgroup needs to start its loads, in one record
+    const int4 r0 = a.rec[2 * rank], r1 = a.rec[2 * rank + 1];
+    const int seq = r0.x, row0 = r0.y, nq = r0.z, page_b = r0.w, page_e = r1.x, foff = r1.z;
+    const unsigned meta = (unsigned)r1.w;
+    const int item = (int)(meta & (kAttnSingle - 1));
     const int c = lane & 15, q4 = lane >> 4;
     const int qi = c / a.G, g = c - qi * a.G;
     const bool col_valid = qi < nq && c < (16 / a.G) * a.G;
-    const int kvb = a.kv_before[seq];
-    const int foff = a.first_offset[seq];
     // last visible logical key index of this column (causal: prefix + row)
-    const int jmax = kvb + q0 + (col_valid ? qi : 0);
+    const int jmax = r1.y + (col_valid ? qi : 0);
 
     // Q^T as the MFMA B operand (lane holds Q[c][32*kb + 8*q4 + j]) as bf16
     // hi + lo fragments, parked in LDS to keep registers for the page ring.
@@ -309,7 +304,7 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
         // operations in its order: slabs summed in slab order, then
         // a c - b s, a s + b c per rotate-half pair, no contraction).  A
         // decode tile holds one query: column c < G is q head kvh G + c.
-        const int row = a.cu_q[seq] + q0;
+        const int row = row0;
         const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
         const float* qp = a.qkv + (size_t)row * a.qkv_stride + (size_t)(kvh * a.G + g) * D + q4 * 8;
 #pragma unroll
@@ -362,7 +357,7 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
                 }
             }
         }
-        if (item == a.tiles[it.x + 1].w - 1) {
+        if (meta & kAttnLast) {
 #pragma clang fp contract(off)
             // the tile's last split holds the new row's page: append this kv
             // head's K and V row there before any page of the split is read
@@ -399,7 +394,7 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
             ring_barrier<0>();  // the row is written before the page loads below
         }
     } else {
-        const int row = a.cu_q[seq] + q0 + (col_valid ? qi : 0);
+        const int row = row0 + (col_valid ? qi : 0);
         const float* qp = a.q + (size_t)row * a.q_cols + (size_t)(kvh * a.G + g) * D + q4 * 8;
 #pragma unroll
         for (int kb = 0; kb < D / 32; ++kb) {
@@ -407,13 +402,13 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
             qx[kb][1] = col_valid ? *(const f32x4*)(qp + kb * 32 + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
         }
     }
-    const int pend = it.z;
+    const int pend = page_e;
     // Every ring slot is loaded unconditionally (past the split's end, the
     // last page again, an L2 hit): with no conditional loads the compiler
     // can wait for exactly the slot it computes on (in-order vmcnt) instead
     // of conservatively draining the newest pages' loads too.
 #pragma unroll
-    for (int r = 0; r < RING - 2; ++r) load(ring[r], min(it.y + r, pend - 1));
+    for (int r = 0; r < RING - 2; ++r) load(ring[r], min(page_b + r, pend - 1));
 #pragma unroll
     for (int kb = 0; kb < D / 32; ++kb) {
         const float x[8] = {qx[kb][0][0], qx[kb][0][1], qx[kb][0][2], qx[kb][0][3],
@@ -421,7 +416,7 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
         qs[0][kb][lane] = to_bf16x8(x, false);
         qs[1][kb][lane] = to_bf16x8(x, true);
     }
-    for (int p = it.y; p < pend; p += RING) {
+    for (int p = page_b; p < pend; p += RING) {
 #pragma unroll
         for (int r = 0; r < RING; r += 2) {
             const int pp = p + r;
@@ -436,9 +431,9 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
     lsum += shfl_xor(lsum, 32);
 
     if (!col_valid) return;
-    if (a.tiles[it.x + 1].w - tl.w == 1) {
+    if (meta & kAttnSingle) {
         // the tile has one split: normalise and write the final output here
-        const int row = a.cu_q[seq] + q0 + qi;
+        const int row = row0 + qi;
         const float inv = 1.0f / lsum;
 #pragma unroll
         for (int db = 0; db < D / 16; ++db)
@@ -731,20 +726,18 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attention_kernel(Prefill
 // output elements, consecutive threads reading consecutive columns.
 template <int D>
 __global__ __launch_bounds__(256) void attention_merge_kernel(const float* __restrict__ part,
-                                                              const int4* __restrict__ tiles,
-                                                              const int* __restrict__ merge_tiles,
-                                                              const int* __restrict__ cu_q, int G, int kv_heads,
-                                                              int q_cols, float* __restrict__ out,
+                                                              const int4* __restrict__ merge_rec, int G,
+                                                              int kv_heads, int q_cols, float* __restrict__ out,
                                                               uint16_t* __restrict__ out_bf16, size_t lo_offset) {
     constexpr int kChunk = 64;
     constexpr int kPer = 16 * D / 256;  // output elements per thread (16 columns max)
     __shared__ float sw[kChunk][16];
     __shared__ float sred[16][16];
     __shared__ float sM[16], sLinv[16];
-    const int tile = merge_tiles[blockIdx.x], kvh = blockIdx.y;
-    const int4 tl = tiles[tile];
-    const int seq = tl.x, q0 = tl.y, nq = tl.z, first = tl.w;
-    const int nparts = tiles[tile + 1].w - first;
+    // {first partial, splits, first q row, nq} of the tile
+    const int4 mr = merge_rec[blockIdx.x];
+    const int kvh = blockIdx.y;
+    const int first = mr.x, nparts = mr.y, row0 = mr.z, nq = mr.w;
     const int ncols = min(nq, 16 / G) * G;
     const size_t pstride = (size_t)kv_heads * 16 * (D + 2);
     const float* base = part + ((size_t)first * kv_heads + kvh) * 16 * (D + 2);
@@ -789,7 +782,7 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(const float* __res
                 }
             }
         const int qi = c / G, g = c - qi * G;
-        const int row = cu_q[seq] + q0 + qi;
+        const int row = row0 + qi;
 #pragma unroll
         for (int j = 0; j < DT; ++j) {
             const int col = (kvh * G + g) * D + d0 + j;
@@ -872,7 +865,7 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(const float* __res
         const int c = e / D, d = e - c * D;
         if (c >= ncols) continue;
         const int qi = c / G, g = c - qi * G;
-        const int row = cu_q[seq] + q0 + qi;
+        const int row = row0 + qi;
         const int col = (kvh * G + g) * D + d;
         if (out_bf16) {
             uint16_t hi, lo;
@@ -903,13 +896,8 @@ static zr_status launch_attn_t(zr_context* ctx, StagedMeta* st, int layer, const
     a.pool = (const KV*)ctx->kv_pool + (size_t)layer * ctx->n_pages * a.page_elems;
     a.block_tables = st->block_tables;
     a.stride = st->stride;
-    a.first_offset = st->first_offset;
-    a.kv_before = st->kv_before;
-    a.cu_q = st->cu_q;
-    a.items = st->attn_items;
-    a.order = st->attn_order;
+    a.rec = st->attn_rec;
     a.n_items = st->n_attn_items;
-    a.tiles = st->attn_tiles;
     a.G = ctx->q_per_kv;
     a.kv_heads = ctx->local_kv_heads;
     a.scale_log2 = 1.4426950408889634f / sqrtf((float)D);
@@ -939,9 +927,9 @@ static zr_status launch_attn_t(zr_context* ctx, StagedMeta* st, int layer, const
             pa.pool = (const uint16_t*)a.pool;
             pa.page_elems = a.page_elems;
             pa.stride = a.stride;
-            pa.first_offset = a.first_offset;
-            pa.kv_before = a.kv_before;
-            pa.cu_q = a.cu_q;
+            pa.first_offset = st->first_offset;
+            pa.kv_before = st->kv_before;
+            pa.cu_q = st->cu_q;
             pa.blocks = st->pblocks;
             pa.splits = st->psplits;
             pa.n_blocks = st->n_pblocks;
@@ -963,8 +951,8 @@ static zr_status launch_attn_t(zr_context* ctx, StagedMeta* st, int layer, const
     if (st->n_merge > 0) {
         timing_mark_begin(ctx, kClassOther, &ev);
         hipLaunchKernelGGL((attention_merge_kernel<D>), dim3(st->n_merge, ctx->local_kv_heads), dim3(256), 0,
-                           ctx->stream, ctx->attn_part, st->attn_tiles, st->merge_tiles, st->cu_q, ctx->q_per_kv,
-                           ctx->local_kv_heads, ctx->q_cols, out, out_bf16, a.out_lo_offset);
+                           ctx->stream, ctx->attn_part, st->merge_rec, ctx->q_per_kv, ctx->local_kv_heads,
+                           ctx->q_cols, out, out_bf16, a.out_lo_offset);
         ZR_LAUNCH_CHECK(ctx);
         timing_mark_end(ctx, kClassOther, ev);
     }

@@ -268,22 +268,25 @@ struct StagedMeta {
     int* seq_ids = nullptr;     // [T]
     int* last_rows = nullptr;   // [S] row index of each sequence's last token
     float2* rope_cs = nullptr;  // [T][head_dim / 2] (cos, sin) of position x inv_freq (pack stage output)
-    int4* attn_items = nullptr; // [n_attn_items] {tile, page_begin, page_end, part_index}
-    int4* attn_tiles = nullptr; // [n_tiles] {seq, q0, nq, first_part}
-    int* tile_nparts = nullptr; // [n_tiles]
-    int* merge_tiles = nullptr; // [n_merge] tiles the merge kernel combines
-    int* attn_order = nullptr;  // [n_attn_items] items by decreasing page count
+    // decode attention: two records per dispatch rank (items longest first),
+    //   {seq, first q row, nq, page_begin}, {page_end, kv_before + q0, first_offset, item | kAttnSingle | kAttnLast}
+    int4* attn_rec = nullptr;
+    int4* merge_rec = nullptr;  // [n_merge] tiles the merge kernel combines: {first partial, splits, first q row, nq}
     int4* pblocks = nullptr;    // [n_pblocks] {seq, r0, nrows, pages}, most key tiles first
     int4* psplits = nullptr;    // [n_pblocks] {first key tile, end key tile, item, splits}
     // host copies
     std::vector<int> h_q_len, h_kv_before, h_first_pos, h_first_offset, h_block_tables;
     std::vector<int4> h_items, h_tiles, h_pblocks, h_psplits;
-    std::vector<int> h_tile_nparts, h_merge, h_order;
+    std::vector<int> h_merge, h_order;
+    std::vector<int4> h_attn_rec, h_merge_rec;
     std::vector<uint32_t> h_tokens;
     std::vector<unsigned char> h_blob;
 };
 
 zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta* st);
+// flags of a decode attention record's last field (above them: the item index)
+constexpr unsigned kAttnSingle = 1u << 30;  // the item's tile has one split: it writes the final output
+constexpr unsigned kAttnLast = 1u << 31;    // the item is its tile's last split (holds the newest rows)
 
 // An f32 [rows, cols] operand held as n split-K slabs `stride` floats apart;
 // readers sum the slabs in order (n = 1: a plain array).
