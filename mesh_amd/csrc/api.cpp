@@ -300,7 +300,7 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
         for (int s = 0; s < S; ++s) cuq[s + 1] = cuq[s] + mb->q_len[s];
         if (st->n_part_items >= (int)kAttnSingle)
             return set_err(ctx, ZR_E_INVALID, "%d attention items exceed the record's index field", st->n_part_items);
-        st->h_attn_rec.resize(2 * (size_t)st->n_attn_items);
+        st->h_attn_rec.resize(3 * (size_t)st->n_attn_items);
         for (int r = 0; r < st->n_attn_items; ++r) {
             const int item = st->h_order[r];
             const int4 it = st->h_items[item], tl = st->h_tiles[it.x];
@@ -309,9 +309,12 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
             unsigned meta = (unsigned)item;
             if (end - first == 1) meta |= kAttnSingle;
             if (item == end - 1) meta |= kAttnLast;
-            st->h_attn_rec[2 * r] = make_int4(seq, cuq[seq] + tl.y, tl.z, it.y);
-            st->h_attn_rec[2 * r + 1] =
+            const int* bt = mb->block_tables + (size_t)seq * stride;
+            auto pid = [&](int k) { return bt[std::min(it.y + k, it.z - 1)]; };
+            st->h_attn_rec[3 * r] = make_int4(seq, cuq[seq] + tl.y, tl.z, it.y);
+            st->h_attn_rec[3 * r + 1] =
                 make_int4(it.z, mb->kv_before[seq] + tl.y, mb->first_offset[seq], (int)meta);
+            st->h_attn_rec[3 * r + 2] = make_int4(pid(0), pid(1), pid(2), pid(3));
         }
         st->h_merge_rec.resize(st->n_merge);
         for (int i = 0; i < st->n_merge; ++i) {
@@ -367,7 +370,7 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     };
     const size_t o_qlen = take(4 * S), o_kvb = take(4 * S), o_fpos = take(4 * S), o_foff = take(4 * S);
     const size_t o_bt = take(4 * (size_t)S * stride), o_tok = take(4 * (size_t)std::max(total_q, 1));
-    const size_t o_arec = take(32 * (size_t)std::max(st->n_attn_items, 1));
+    const size_t o_arec = take(48 * (size_t)std::max(st->n_attn_items, 1));
     const size_t o_mrec = take(16 * (size_t)std::max(st->n_merge, 1));
     const size_t o_pblk = take(16 * (size_t)std::max(st->n_pblocks, 1));
     const size_t o_psplit = take(16 * (size_t)std::max(st->n_pblocks, 1));
@@ -393,7 +396,7 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     memcpy(hb + o_foff, mb->first_offset, 4 * S);
     memcpy(hb + o_bt, mb->block_tables, 4 * (size_t)S * stride);
     if (mb->tokens) memcpy(hb + o_tok, mb->tokens, 4 * (size_t)total_q);
-    if (st->n_attn_items) memcpy(hb + o_arec, st->h_attn_rec.data(), 32 * (size_t)st->n_attn_items);
+    if (st->n_attn_items) memcpy(hb + o_arec, st->h_attn_rec.data(), 48 * (size_t)st->n_attn_items);
     if (st->n_merge) memcpy(hb + o_mrec, st->h_merge_rec.data(), 16 * (size_t)st->n_merge);
     if (st->n_pblocks) memcpy(hb + o_pblk, st->h_pblocks.data(), 16 * (size_t)st->n_pblocks);
     if (st->n_pblocks) memcpy(hb + o_psplit, st->h_psplits.data(), 16 * (size_t)st->n_pblocks);

@@ -191,8 +191,9 @@ struct AttnArgs {
     size_t page_elems;       // elements of one page (K + V, all kv heads)
     const int* block_tables;
     int stride;
-    const int4* rec;         // two records per dispatch rank (longest item first): {seq, first q row, nq,
-                             // page_begin}, {page_end, kv_before + q0, first_offset, item | kAttnSingle | kAttnLast}
+    const int4* rec;         // three records per dispatch rank (longest item first): {seq, first q row, nq,
+                             // page_begin}, {page_end, kv_before + q0, first_offset, item | kAttnSingle | kAttnLast},
+                             // {pool pages of the item's first 4 pages}
     int n_items;
     int G;                   // q heads per kv head
     int kv_heads;
@@ -226,7 +227,7 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
     const int rank = (blockIdx.x / per_grp) * 8 + (rem & 7);
     if (rank >= a.n_items) return;
     // everything the workgroup needs to start its loads, in one record
-    const int4 r0 = a.rec[2 * rank], r1 = a.rec[2 * rank + 1];
+    const int4 r0 = a.rec[3 * rank], r1 = a.rec[3 * rank + 1], r2 = a.rec[3 * rank + 2];
     const int seq = r0.x, row0 = r0.y, nq = r0.z, page_b = r0.w, page_e = r1.x, foff = r1.z;
     const unsigned meta = (unsigned)r1.w;
     const int item = (int)(meta & (kAttnSingle - 1));
@@ -292,10 +293,11 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
     // in flight while a pair is computed.
     static_assert(RING % 2 == 0 && RING >= 4, "ring of page pairs");
     PageRegs<KV, D> ring[RING];
-    auto load = [&](PageRegs<KV, D>& r, int p) {
-        const KV* base = pool + (size_t)bt[p] * a.page_elems + (size_t)kvh * kv_tile;
+    auto load_page = [&](PageRegs<KV, D>& r, int pool_page) {
+        const KV* base = pool + (size_t)pool_page * a.page_elems + (size_t)kvh * kv_tile;
         r.load(base, base + v_block, lane);
     };
+    auto load = [&](PageRegs<KV, D>& r, int p) { load_page(r, bt[p]); };
     // Q row of this lane's column, fetched before the first pages so that its
     // wait (in-order vmcnt) does not also wait for them
     f32x4 qx[D / 32][2];
@@ -406,9 +408,13 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
     // Every ring slot is loaded unconditionally (past the split's end, the
     // last page again, an L2 hit): with no conditional loads the compiler
     // can wait for exactly the slot it computes on (in-order vmcnt) instead
-    // of conservatively draining the newest pages' loads too.
+    // of conservatively draining the newest pages' loads too.  The pool
+    // pages of the first RING - 2 come from the record: no block-table load
+    // stands before them.
+    static_assert(RING - 2 <= 4, "the record holds the first 4 pages");
+    const int first_pages[4] = {r2.x, r2.y, r2.z, r2.w};
 #pragma unroll
-    for (int r = 0; r < RING - 2; ++r) load(ring[r], min(page_b + r, pend - 1));
+    for (int r = 0; r < RING - 2; ++r) load_page(ring[r], first_pages[r]);
 #pragma unroll
     for (int kb = 0; kb < D / 32; ++kb) {
         const float x[8] = {qx[kb][0][0], qx[kb][0][1], qx[kb][0][2], qx[kb][0][3],

@@ -268,8 +268,9 @@ struct StagedMeta {
     int* seq_ids = nullptr;     // [T]
     int* last_rows = nullptr;   // [S] row index of each sequence's last token
     float2* rope_cs = nullptr;  // [T][head_dim / 2] (cos, sin) of position x inv_freq (pack stage output)
-    // decode attention: two records per dispatch rank (items longest first),
-    //   {seq, first q row, nq, page_begin}, {page_end, kv_before + q0, first_offset, item | kAttnSingle | kAttnLast}
+    // decode attention: three records per dispatch rank (items longest first),
+    //   {seq, first q row, nq, page_begin}, {page_end, kv_before + q0, first_offset, item | kAttnSingle | kAttnLast},
+    //   {the pool pages of the item's first 4 pages (the last one repeated past its end)}
     int4* attn_rec = nullptr;
     int4* merge_rec = nullptr;  // [n_merge] tiles the merge kernel combines: {first partial, splits, first q row, nq}
     int4* pblocks = nullptr;    // [n_pblocks] {seq, r0, nrows, pages}, most key tiles first
