@@ -308,11 +308,30 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
         // decode tile holds one query: column c < G is q head kvh G + c.
         const int row = row0;
         const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+        // Every column reads a q head of the row (g < G), so the loads need
+        // no guard: columns past the tile are zeroed after the sums.
         const float* qp = a.qkv + (size_t)row * a.qkv_stride + (size_t)(kvh * a.G + g) * D + q4 * 8;
+        // (cos, sin) of the lane's dims 32 kb + 8 q4 + j for kb < D / 64 (the
+        // rotate-half partner of block kb is kb + D / 64), fetched together
+        // with the slabs: one round trip for both
+        float cv[D / 64][8], sv[D / 64][8];
+        if (a.rope_cs) {
+            const float2* cs = a.rope_cs + (size_t)row * (D / 2) + q4 * 8;
+#pragma unroll
+            for (int kb = 0; kb < D / 64; ++kb)
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    const float4 pr = ((const float4*)(cs + kb * 32))[w];
+                    cv[kb][2 * w] = pr.x;
+                    sv[kb][2 * w] = pr.y;
+                    cv[kb][2 * w + 1] = pr.z;
+                    sv[kb][2 * w + 1] = pr.w;
+                }
+        }
 #pragma unroll
         for (int kb = 0; kb < D / 32; ++kb) {
-            qx[kb][0] = col_valid ? *(const f32x4*)(qp + kb * 32) : zero;
-            qx[kb][1] = col_valid ? *(const f32x4*)(qp + kb * 32 + 4) : zero;
+            qx[kb][0] = *(const f32x4*)(qp + kb * 32);
+            qx[kb][1] = *(const f32x4*)(qp + kb * 32 + 4);
         }
         constexpr int CH = D == 64 ? 8 : 4;  // slabs per batch of loads
         for (int s0 = 1; s0 < a.qkv_n; s0 += CH) {
@@ -323,7 +342,7 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
                 for (int kb = 0; kb < D / 32; ++kb)
 #pragma unroll
                     for (int h = 0; h < 2; ++h)
-                        t[u][kb][h] = (col_valid && s0 + u < a.qkv_n)
+                        t[u][kb][h] = s0 + u < a.qkv_n
                                           ? *(const f32x4*)(qp + (size_t)(s0 + u) * a.qkv_slab + kb * 32 + 4 * h)
                                           : zero;
 #pragma unroll
@@ -335,29 +354,19 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
                         qx[kb][1] += t[u][kb][1];
                     }
         }
+        if (!col_valid)
+#pragma unroll
+            for (int kb = 0; kb < D / 32; ++kb) qx[kb][0] = qx[kb][1] = zero;
         if (a.rope_cs) {
 #pragma clang fp contract(off)
-            // the lane's dims 32 kb + 8 q4 + j: pair partner of kb < D / 64 is kb + D / 64
-            const float2* cs = a.rope_cs + (size_t)row * (D / 2) + q4 * 8;
 #pragma unroll
-            for (int kb = 0; kb < D / 64; ++kb) {
-                const float4* c4 = (const float4*)(cs + kb * 32);
-                float cv[8], sv[8];
-#pragma unroll
-                for (int w = 0; w < 4; ++w) {
-                    const float4 pr = c4[w];
-                    cv[2 * w] = pr.x;
-                    sv[2 * w] = pr.y;
-                    cv[2 * w + 1] = pr.z;
-                    sv[2 * w + 1] = pr.w;
-                }
+            for (int kb = 0; kb < D / 64; ++kb)
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const float x = qx[kb][j >> 2][j & 3], y = qx[kb + D / 64][j >> 2][j & 3];
-                    qx[kb][j >> 2][j & 3] = x * cv[j] - y * sv[j];
-                    qx[kb + D / 64][j >> 2][j & 3] = x * sv[j] + y * cv[j];
+                    qx[kb][j >> 2][j & 3] = x * cv[kb][j] - y * sv[kb][j];
+                    qx[kb + D / 64][j >> 2][j & 3] = x * sv[kb][j] + y * cv[kb][j];
                 }
-            }
         }
         if (meta & kAttnLast) {
 #pragma clang fp contract(off)
