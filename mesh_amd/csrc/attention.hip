@@ -298,6 +298,18 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
         r.load(base, base + v_block, lane);
     };
     auto load = [&](PageRegs<KV, D>& r, int p) { load_page(r, bt[p]); };
+    // Every ring slot is loaded unconditionally (past the split's end, the
+    // last page again, an L2 hit): with no conditional loads the compiler
+    // can wait for exactly the slot it computes on (in-order vmcnt) instead
+    // of conservatively draining the newest pages' loads too.  The pool
+    // pages of the first RING - 2 come from the record: no block-table load
+    // stands before them.
+    static_assert(RING - 2 <= 4, "the record holds the first 4 pages");
+    const int first_pages[4] = {r2.x, r2.y, r2.z, r2.w};
+    auto load_first_pages = [&]() {
+#pragma unroll
+        for (int r = 0; r < RING - 2; ++r) load_page(ring[r], first_pages[r]);
+    };
     // Q row of this lane's column, fetched before the first pages so that its
     // wait (in-order vmcnt) does not also wait for them
     f32x4 qx[D / 32][2];
@@ -334,6 +346,35 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
             qx[kb][1] = *(const f32x4*)(qp + kb * 32 + 4);
         }
         constexpr int CH = D == 64 ? 8 : 4;  // slabs per batch of loads
+        // The tile's last split appends the new row.  Lane e (and e + 64 ...)
+        // handles K pair (e, e + D / 2) for e < D / 2, else V dim e - D / 2;
+        // its values of the first NB slabs, K's (cos, sin) and the row's
+        // slot come in the same round trip as q's slabs.
+        const bool last = meta & kAttnLast;
+        constexpr int NE = (D / 2 + D + 63) / 64, NB = 1 + CH;
+        const float* kr = a.qkv + (size_t)row * a.qkv_stride + a.q_cols + (size_t)kvh * D;
+        const float* vr = kr + a.kv_cols;
+        float ax[NE][NB], ay[NE][NB];
+        float2 kcs = make_float2(1.f, 0.f);
+        int sl = 0;
+        if (last) {
+            sl = a.slot[row];
+#pragma unroll
+            for (int i = 0; i < NE; ++i) {
+                const int e = lane + 64 * i;
+#pragma unroll
+                for (int u = 0; u < NB; ++u)
+                    if (u < a.qkv_n) {
+                        if (e < D / 2) {
+                            ax[i][u] = kr[(size_t)u * a.qkv_slab + e];
+                            ay[i][u] = kr[(size_t)u * a.qkv_slab + e + D / 2];
+                        } else if (e < D / 2 + D) {
+                            ax[i][u] = vr[(size_t)u * a.qkv_slab + e - D / 2];
+                        }
+                    }
+            }
+            if (a.rope_cs && lane < D / 2) kcs = a.rope_cs[(size_t)row * (D / 2) + lane];
+        }
         for (int s0 = 1; s0 < a.qkv_n; s0 += CH) {
             f32x4 t[CH][D / 32][2];
 #pragma unroll
@@ -368,42 +409,61 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
                     qx[kb + D / 64][j >> 2][j & 3] = x * sv[kb][j] + y * cv[kb][j];
                 }
         }
-        if (meta & kAttnLast) {
+        // the appended row's values, complete before any page load goes out
+        // (the same operations in the same order as the RoPE kernel: slabs
+        // summed in slab order, then x c - y s, x s + y c)
+        float av[NE][2];
+        if (last) {
 #pragma clang fp contract(off)
-            // the tile's last split holds the new row's page: append this kv
-            // head's K and V row there before any page of the split is read
-            const int sl = a.slot[row], r = sl % kPageRows;
+#pragma unroll
+            for (int i = 0; i < NE; ++i) {
+                const int e = lane + 64 * i;
+                float x = ax[i][0], y = ay[i][0];
+#pragma unroll
+                for (int u = 1; u < NB; ++u)
+                    if (u < a.qkv_n) {
+                        x += ax[i][u];
+                        if (e < D / 2) y += ay[i][u];
+                    }
+                for (int u = NB; u < a.qkv_n; ++u) {
+                    if (e < D / 2) {
+                        x += kr[(size_t)u * a.qkv_slab + e];
+                        y += kr[(size_t)u * a.qkv_slab + e + D / 2];
+                    } else if (e < D / 2 + D) {
+                        x += vr[(size_t)u * a.qkv_slab + e - D / 2];
+                    }
+                }
+                if (e < D / 2 && a.rope_cs) {
+                    const float nx = x * kcs.x - y * kcs.y;
+                    const float ny = x * kcs.y + y * kcs.x;
+                    x = nx;
+                    y = ny;
+                }
+                av[i][0] = x;
+                av[i][1] = y;
+            }
+        }
+        // the first ring pages go out before the append's wait when none of
+        // them can hold the new row (it sits in the split's last page)
+        const bool early = !last || page_e - page_b > RING - 2;
+        if (early) load_first_pages();
+        if (last) {
+            const int r = sl % kPageRows;
             KV* kt = (KV*)a.pool + (size_t)(sl / kPageRows) * a.page_elems + (size_t)kvh * kv_tile;
             KV* vt = kt + v_block;
-            const float* kr = a.qkv + (size_t)row * a.qkv_stride + a.q_cols + (size_t)kvh * D;
-            const float* vr = kr + a.kv_cols;
-            for (int e = lane; e < D / 2 + D; e += 64) {
+#pragma unroll
+            for (int i = 0; i < NE; ++i) {
+                const int e = lane + 64 * i;
                 if (e < D / 2) {
-                    float x = kr[e], y = kr[e + D / 2];
-#pragma unroll 4
-                    for (int sb = 1; sb < a.qkv_n; ++sb) {
-                        x += kr[(size_t)sb * a.qkv_slab + e];
-                        y += kr[(size_t)sb * a.qkv_slab + e + D / 2];
-                    }
-                    if (a.rope_cs) {
-                        const float2 cs = a.rope_cs[(size_t)row * (D / 2) + e];
-                        const float nx = x * cs.x - y * cs.y;
-                        const float ny = x * cs.y + y * cs.x;
-                        x = nx;
-                        y = ny;
-                    }
-                    store_elem(kt + k_off(r, e), x);
-                    store_elem(kt + k_off(r, e + D / 2), y);
-                } else {
-                    const int d = e - D / 2;
-                    float v = vr[d];
-#pragma unroll 4
-                    for (int sb = 1; sb < a.qkv_n; ++sb) v += vr[(size_t)sb * a.qkv_slab + d];
-                    store_elem(vt + v_off(r, d), v);
+                    store_elem(kt + k_off(r, e), av[i][0]);
+                    store_elem(kt + k_off(r, e + D / 2), av[i][1]);
+                } else if (e < D / 2 + D) {
+                    store_elem(vt + v_off(r, e - D / 2), av[i][0]);
                 }
             }
-            ring_barrier<0>();  // the row is written before the page loads below
+            ring_barrier<0>();  // the row is written before its page is read
         }
+        if (!early) load_first_pages();
     } else {
         const int row = row0 + (col_valid ? qi : 0);
         const float* qp = a.q + (size_t)row * a.q_cols + (size_t)(kvh * a.G + g) * D + q4 * 8;
@@ -412,18 +472,9 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
             qx[kb][0] = col_valid ? *(const f32x4*)(qp + kb * 32) : f32x4{0.f, 0.f, 0.f, 0.f};
             qx[kb][1] = col_valid ? *(const f32x4*)(qp + kb * 32 + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
         }
+        load_first_pages();
     }
     const int pend = page_e;
-    // Every ring slot is loaded unconditionally (past the split's end, the
-    // last page again, an L2 hit): with no conditional loads the compiler
-    // can wait for exactly the slot it computes on (in-order vmcnt) instead
-    // of conservatively draining the newest pages' loads too.  The pool
-    // pages of the first RING - 2 come from the record: no block-table load
-    // stands before them.
-    static_assert(RING - 2 <= 4, "the record holds the first 4 pages");
-    const int first_pages[4] = {r2.x, r2.y, r2.z, r2.w};
-#pragma unroll
-    for (int r = 0; r < RING - 2; ++r) load_page(ring[r], first_pages[r]);
 #pragma unroll
     for (int kb = 0; kb < D / 32; ++kb) {
         const float x[8] = {qx[kb][0][0], qx[kb][0][1], qx[kb][0][2], qx[kb][0][3],
