@@ -101,6 +101,8 @@ zr_status launch_pack(zr_context* ctx, StagedMeta* st) {
 // in f32 from the step's table, rope_table_kernel) and the KV append is
 // DeviceLayerKVCache::append (forward_pass.rs:462-521) at the slot the host
 // reserved.
+constexpr int kSlabsAhead = 16;  // split-K slabs whose loads go out together (the GEMM splits at most 16 ways)
+
 template <typename KV>
 __global__ __launch_bounds__(256) void rope_kv_write_kernel(
     const float* __restrict__ qkv, int qkv_n, size_t qkv_slab, int qkv_stride, float* __restrict__ q_out,
@@ -124,14 +126,28 @@ __global__ __launch_bounds__(256) void rope_kv_write_kernel(
             const int jj = is_q ? j : j - nq;
             const int head = jj / half, i = jj % half;
             const float* src = row + (is_q ? 0 : q_cols) + head * D;
-            float a = src[i], b = src[i + half];
-#pragma unroll 4
-            for (int sl = 1; sl < qkv_n; ++sl) {
+            // every slab's pair (up to kSlabsAhead) and the (cos, sin) are
+            // loaded before the first add: one round trip, summed in slab order
+            const float2 cs = rope ? rope_cs[(size_t)t * half + i] : make_float2(1.f, 0.f);
+            float la[kSlabsAhead], lb[kSlabsAhead];
+#pragma unroll
+            for (int sl = 0; sl < kSlabsAhead; ++sl)
+                if (sl < qkv_n) {
+                    la[sl] = src[sl * qkv_slab + i];
+                    lb[sl] = src[sl * qkv_slab + i + half];
+                }
+            float a = la[0], b = lb[0];
+#pragma unroll
+            for (int sl = 1; sl < kSlabsAhead; ++sl)
+                if (sl < qkv_n) {
+                    a += la[sl];
+                    b += lb[sl];
+                }
+            for (int sl = kSlabsAhead; sl < qkv_n; ++sl) {
                 a += src[sl * qkv_slab + i];
                 b += src[sl * qkv_slab + i + half];
             }
             if (rope) {
-                const float2 cs = rope_cs[(size_t)t * half + i];
                 const float c = cs.x, sn = cs.y;
                 const float na = a * c - b * sn;
                 const float nb = a * sn + b * c;
@@ -150,9 +166,16 @@ __global__ __launch_bounds__(256) void rope_kv_write_kernel(
             const int c = j - nq - nk;
             const int head = c / D, d = c % D;
             KV* vt = vpage + (size_t)head * kPageRows * D;
-            float vv = row[q_cols + kv_cols + c];
-#pragma unroll 4
-            for (int sl = 1; sl < qkv_n; ++sl) vv += row[sl * qkv_slab + q_cols + kv_cols + c];
+            const float* src = row + q_cols + kv_cols + c;
+            float lv[kSlabsAhead];
+#pragma unroll
+            for (int sl = 0; sl < kSlabsAhead; ++sl)
+                if (sl < qkv_n) lv[sl] = src[sl * qkv_slab];
+            float vv = lv[0];
+#pragma unroll
+            for (int sl = 1; sl < kSlabsAhead; ++sl)
+                if (sl < qkv_n) vv += lv[sl];
+            for (int sl = kSlabsAhead; sl < qkv_n; ++sl) vv += src[sl * qkv_slab];
             store_elem(vt + v_off_of(r, d, D, plain), vv);
         }
     }
