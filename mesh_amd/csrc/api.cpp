@@ -233,11 +233,11 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
         }
     }
     // ~96 pages per split at 256 sessions x 8 kv heads x ~1.5k tokens (measured
-    // best on MI355X with longest-first dispatch); at least 12 pages, which
-    // measured best at 32 sessions (fewer merges: 6, 8, 16 and 24 pages are
-    // 0.3-3 % slower there)
+    // best on MI355X with longest-first dispatch: 64 and 144 tie); at least 8
+    // pages, which measured best at 32 sessions (a launch there costs ~8 us
+    // plus ~0.45 us per page of a split: 12 pages 0.4 % slower, 16 1.2 %, 24 6 %)
     const long target_wgs = 2048;
-    int pps = (int)std::min<long>(4096, std::max<long>(12, (total_pages * ctx->local_kv_heads + target_wgs - 1) / target_wgs));
+    int pps = (int)std::min<long>(4096, std::max<long>(8, (total_pages * ctx->local_kv_heads + target_wgs - 1) / target_wgs));
     if (const char* env = getenv("ZR_ATTN_PAGES_PER_SPLIT")) pps = std::max(1, atoi(env));
     for (size_t t = 0; t < st->h_tiles.size(); ++t) {
         st->h_tiles[t].w = (int)st->h_items.size();
@@ -343,7 +343,7 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     // can take RoPE + KV append too (launch_attention_rope).  The forward pass
     // does so when splits stream >= 48 pages: the q slab loads and the last
     // split's append then add little to a split (256 Llama-3 sessions, ~96
-    // pages per split: 17.9 -> 17.3 ms per step), where 12-page splits
+    // pages per split: 17.9 -> 17.3 ms per step), where 8- to 12-page splits
     // (32 TinyLlama sessions) lose more than the RoPE launch costs
     // (1.49 -> 1.59 ms).  ZR_ATTN_FUSE_ROPE=1 / 0 forces either path.
     st->pure_decode = !ctx->plain_kv && S > 0 && st->n_pblocks == 0;

@@ -36,7 +36,7 @@ def _two_steps(b):
 
 
 def test_decode_step_with_rope_inside_attention_equals_separate_rope_kernel(monkeypatch):
-    monkeypatch.setenv("ZR_ATTN_FUSE_ROPE", "1")  # 12-page splits would keep the RoPE kernel
+    monkeypatch.setenv("ZR_ATTN_FUSE_ROPE", "1")  # short splits would keep the RoPE kernel
     fused = bench.GpuDecodeBench("tinyllama_b32", 2)
     try:
         got = _two_steps(fused)
