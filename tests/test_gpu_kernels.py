@@ -139,18 +139,21 @@ def test_rope_kv_write_rotates_q_and_k_at_large_positions(kv_dtype, heads, kv_he
 @pytest.mark.parametrize("rope", [0, 1])
 @pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("heads,kv_heads,D,base", [(32, 4, 64, 1e4), (32, 8, 128, 5e5)])
+@pytest.mark.parametrize("pages_per_split", [2, 9])
 def test_rope_attention_equals_rope_kv_write_then_attention_bit_exact(monkeypatch, rope, kv_dtype, heads, kv_heads,
-                                                                      D, base):
+                                                                      D, base, pages_per_split):
     """RoPE + KV append inside the decode attention launch (zr_rope_attention,
     the forward pass's path for one-row decode microbatches) against the two
     stages run apart (zr_rope_kv_write, then zr_attention) on identically
     prepared sessions: the attention outputs and every KV row, the appended
     one included, bit for bit.  Splits of 2 pages give most tiles several
     splits (the last one appends the row) and the 1-row context a single
-    one; positions run to ~5600."""
+    one; positions run to ~5600.  Splits of 9 pages give last splits of 2 to
+    9 pages: those of more than 4 issue their first pages before the append
+    (which cannot touch them), the others after it."""
     from mesh_amd import KVCacheSnapshot
 
-    monkeypatch.setenv("ZR_ATTN_PAGES_PER_SPLIT", "2")
+    monkeypatch.setenv("ZR_ATTN_PAGES_PER_SPLIT", str(pages_per_split))
     Q, KV = heads * D, kv_heads * D
     geo = ModelGeometry(hidden=Q, num_heads=heads, num_kv_heads=kv_heads, num_layers=1, vocab=64, ffn=64,
                         rope_base=base)
