@@ -178,6 +178,8 @@ class KvPressureSoak:
                 if s.transfer is not None:
                     self._retire(s.transfer, s.snapshot.storage)
                     s.transfer = None
+                elif s.snapshot is not None and s.snapshot.storage is not None:
+                    self.free_pinned.append(s.snapshot.storage)  # no copy uses it any more
                 self.stats.leaves += 1
 
     def _joins(self):

@@ -175,6 +175,10 @@ def test_soak_transfer_bookkeeping(monkeypatch, lag, prefetch):
     assert all(s.transfer is None for s in soak.evicted)
     # buffers circulate: far fewer pinned allocations than evictions
     assert FakePinned.count < st.evictions
+    # and none is lost: each is free or holds an evicted window (also after evicted sessions left)
+    held = [s.snapshot.storage for s in soak.evicted if s.snapshot is not None and s.snapshot.storage is not None]
+    assert len({id(b) for b in held} | {id(b) for b in soak.free_pinned}) == len(held) + len(soak.free_pinned)
+    assert len(held) + len(soak.free_pinned) == FakePinned.count
 
 
 def test_synchronous_copies_keep_the_reference_order(monkeypatch):
