@@ -172,7 +172,11 @@ zr_status zr_synchronize(zr_context* ctx);
  * enqueues the recorded step again (same staged metadata and buffers, which
  * must stay alive), with the same id check at the next zr_synchronize.
  * Capture is refused while per-class timing is on (events recorded by graph
- * nodes do not time).  Destroy a graph before its context. */
+ * nodes do not time).  A graph holds the addresses of the context's buffers
+ * too: once one of them has been reallocated (a workspace grown for a larger
+ * microbatch, the KV pool re-created, weights uploaded again), zr_graph_launch
+ * returns ZR_E_INVALID for graphs captured before; capture again.  Destroy a
+ * graph before its context. */
 typedef struct zr_graph zr_graph;
 zr_status zr_graph_capture_staged(zr_context* ctx, zr_staged* st, const uint32_t* d_tokens,
                                   uint32_t* d_out_tokens, float* d_out_logits, zr_graph** out);

@@ -355,6 +355,7 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     if (need_part > ctx->attn_part_floats) {
         hipStreamSynchronize(ctx->stream);
         if (ctx->attn_part) hipFree(ctx->attn_part);
+        ++ctx->buffer_epoch;
         ctx->attn_part = nullptr;
         ctx->attn_part_floats = 0;
         ZR_HIP(ctx, hipMalloc(&ctx->attn_part, need_part * sizeof(float)));
@@ -699,6 +700,7 @@ zr_status zr_upload_layer(zr_context* ctx, int layer, const zr_layer_weights* w)
     void* old[] = {L.w_qkv, L.w_o, L.w_gate_up, L.w_down, L.attn_norm, L.mlp_norm};
     for (void* b : old)
         if (b) hipFree(b);
+    if (L.w_qkv) ++ctx->buffer_epoch;
     L = fresh;
     return ZR_OK;
 }
@@ -723,6 +725,7 @@ zr_status zr_upload_globals(zr_context* ctx, const uint16_t* embedding, const fl
         if (head) hipFree(head);
         return rc;
     }
+    if (ctx->embedding) ++ctx->buffer_epoch;
     if (ctx->embedding) hipFree(ctx->embedding);
     if (ctx->final_norm) hipFree(ctx->final_norm);
     if (ctx->lm_head) hipFree(ctx->lm_head);
@@ -742,6 +745,7 @@ zr_status zr_kv_pool_create(zr_context* ctx, int n_pages) {
     if (ctx->kv_pool) {
         hipStreamSynchronize(ctx->stream);
         hipFree(ctx->kv_pool);
+        ++ctx->buffer_epoch;
         ctx->kv_pool = nullptr;
         ctx->n_pages = 0;
     }
@@ -813,6 +817,7 @@ struct zr_graph {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     bool token_check = false;  // the step copies the device id-check word to the host
+    uint64_t buffer_epoch = 0; // the context's buffer epoch at capture
 };
 
 zr_status zr_graph_capture_staged(zr_context* ctx, zr_staged* s, const uint32_t* d_tokens, uint32_t* d_out_tokens,
@@ -848,6 +853,7 @@ zr_status zr_graph_capture_staged(zr_context* ctx, zr_staged* s, const uint32_t*
     g->graph = graph;
     g->exec = exec;
     g->token_check = d_tokens != nullptr;
+    g->buffer_epoch = ctx->buffer_epoch;
     *out = g;
     return ZR_OK;
 }
@@ -855,6 +861,9 @@ zr_status zr_graph_capture_staged(zr_context* ctx, zr_staged* s, const uint32_t*
 zr_status zr_graph_launch(zr_context* ctx, zr_graph* g) {
     if (!ctx || !g) return set_global_err(ZR_E_INVALID, "null argument");
     if (g->ctx != ctx) return set_err(ctx, ZR_E_INVALID, "graph of another context");
+    if (g->buffer_epoch != ctx->buffer_epoch)
+        return set_err(ctx, ZR_E_INVALID,
+                       "graph captured before a workspace, the KV pool or weights were reallocated: capture it again");
     ZR_HIP(ctx, hipGraphLaunch(g->exec, ctx->stream));
     if (g->token_check) ctx->token_check_pending = true;
     return ZR_OK;
@@ -1201,6 +1210,7 @@ zr_status zr_argmax(zr_context* ctx, const float* d_x, int rows, int cols, uint3
     if (need > ctx->argmax_ws_floats) {
         hipStreamSynchronize(ctx->stream);
         hipFree(ctx->argmax_ws);
+        ++ctx->buffer_epoch;
         ctx->argmax_ws = nullptr;
         ctx->argmax_ws_floats = 0;
         ZR_HIP(ctx, hipMalloc(&ctx->argmax_ws, need * 4));

@@ -182,6 +182,10 @@ struct zr_context {
     size_t attn_part_floats = 0;
     float* argmax_ws = nullptr;     // argmax partials
     size_t argmax_ws_floats = 0;
+    // bumped whenever a buffer the forward pass reads is freed or moved (a
+    // workspace regrown, the KV pool or weights replaced): graphs captured
+    // before hold its old address and are refused at launch
+    uint64_t buffer_epoch = 0;
 
     zr::StagedMeta* scratch_stage = nullptr;  // reused by zr_forward
     float* kv_stage = nullptr;      // KV gather / scatter staging (rows + table)

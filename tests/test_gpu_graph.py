@@ -121,3 +121,40 @@ def test_capture_is_refused_while_timing_is_on(tiny):
     ctx.check(lib.zr_timing_end(ctx.h, ms, n))
     assert rc == -1 and not g.value
     assert b"timing" in lib.zr_last_error(ctx.h)
+
+
+def test_a_graph_is_refused_once_a_buffer_it_reads_was_reallocated(tiny):
+    """The step reads the context's argmax workspace; zr_argmax over more rows
+    than the context was sized for reallocates it.  A graph captured before
+    is refused (it would replay with the freed address); one captured again
+    runs and equals the eager step."""
+    b = tiny
+    ctx, lib = b.ctx, b.ctx.lib
+    rows = 2 * b.B
+    d_logits, d_out = b._dev(4 * b.B * b.geo.vocab), b._dev(4 * b.B)
+    d_x, d_am = b._dev(4 * rows * b.geo.vocab), b._dev(4 * rows)
+    g = C.c_void_p()
+    try:
+        _upload(b, d_x, np.zeros(rows * b.geo.vocab, np.float32))
+        ctx.check(lib.zr_forward_staged_async(ctx.h, b.staged[0], b.tok[0], d_out, d_logits))
+        ctx.check(lib.zr_synchronize(ctx.h))
+        want_logits, want_toks = _read(b, d_logits, d_out)
+        ctx.check(lib.zr_graph_capture_staged(ctx.h, b.staged[0], b.tok[0], d_out, d_logits, C.byref(g)))
+        ctx.check(lib.zr_argmax(ctx.h, d_x, rows, b.geo.vocab, d_am))  # regrows the argmax workspace
+        rc = lib.zr_graph_launch(ctx.h, g)
+        assert rc == -1, rc
+        assert b"capture it again" in lib.zr_last_error(ctx.h)
+        lib.zr_graph_destroy(g)
+        g = C.c_void_p()
+        ctx.check(lib.zr_graph_capture_staged(ctx.h, b.staged[0], b.tok[0], d_out, d_logits, C.byref(g)))
+        _clobber(b, d_logits, d_out)
+        ctx.check(lib.zr_graph_launch(ctx.h, g))
+        ctx.check(lib.zr_synchronize(ctx.h))
+        got_logits, got_toks = _read(b, d_logits, d_out)
+        np.testing.assert_array_equal(got_logits, want_logits)
+        np.testing.assert_array_equal(got_toks, want_toks)
+    finally:
+        if g.value:
+            lib.zr_graph_destroy(g)
+        for p in (d_logits, d_out, d_x, d_am):
+            lib.zr_device_free(ctx.h, p)
