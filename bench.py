@@ -62,6 +62,15 @@ WORKLOADS = {
         contexts=lambda: contexts_lognormal(0xC5, 256, 1024, 1.0, 64, 8192),
         desc="Llama-3-8B-shape decode step, 256 sessions, lognormal contexts (median 1024, sigma 1, "
              "clip [64, 8192]), page 16, bf16 weights + bf16 KV, 32 layers, greedy"),
+    "llama3_8b_tp2_b64": dict(
+        geo=dict(hidden=4096, num_heads=32, num_kv_heads=8, num_layers=32, vocab=128256, ffn=14336,
+                 rope_base=500000.0, shard_start=0, shard_end=2048, ffn_cols=7168),
+        batch=64, max_seq_len=8192,
+        contexts=lambda: contexts_lognormal(0xC4, 64, 1024, 1.0, 64, 8192),
+        desc="Llama-3-8B tensor-parallel shard 0 of 2 (q columns 0-2047 = 16 q / 4 kv heads, FFN columns "
+             "0-7167), decode step, 64 sessions, lognormal contexts (median 1024, sigma 1, clip [64, 8192]), "
+             "page 16, bf16 weights + bf16 KV, 32 layers, greedy; O and down give the pre-all-reduce partials "
+             "(the all-reduce is the identity on one worker)"),
     "tinyllama_b32": dict(
         geo=dict(hidden=2048, num_heads=32, num_kv_heads=4, num_layers=22, vocab=32000, ffn=5632,
                  rope_base=10000.0),
@@ -797,6 +806,7 @@ def main():
     ap.add_argument("--skip-kv-snapshot", action="store_true", help="skip the KV snapshot wire-format leg")
     ap.add_argument("--skip-sampling", action="store_true", help="skip the device sampling leg")
     ap.add_argument("--skip-mixed", action="store_true", help="skip the mixed prefill + decode microbatch leg")
+    ap.add_argument("--skip-tp-shard", action="store_true", help="skip the tensor-parallel shard decode leg")
     ap.add_argument("--mixed-only", action="store_true",
                     help="run only the mixed prefill + decode microbatch leg (for profiling its kernels)")
     a = ap.parse_args()
@@ -824,6 +834,14 @@ def main():
                     attention_gbs=r["attention"]["achieved_gbs"], kernel_ms_per_step=r["kernel_ms_per_step"],
                     gemm_tflops=r["gemm"]["achieved_tflops"], gemm_weight_gbs=r["gemm"]["weight_gbs"],
                     host_path=r["host_path"], eager=r["eager"])
+    tp_shard = None
+    if not a.skip_tp_shard and a.workload != "llama3_8b_tp2_b64":
+        r = measure("llama3_8b_tp2_b64", max(4, a.steps // 2), 2)
+        tp_shard = dict(value=r["tokens_per_s"], unit="tokens/s (one shard's step)", ms_per_step=r["ms_per_step"],
+                        workload=r["workload"], step_roofline_frac=r["step_roofline_frac"],
+                        attention_gbs=r["attention"]["achieved_gbs"], kernel_ms_per_step=r["kernel_ms_per_step"],
+                        gemm_tflops=r["gemm"]["achieved_tflops"], gemm_weight_gbs=r["gemm"]["weight_gbs"],
+                        host_path=r["host_path"])
     soak = None if a.skip_soak else measure_soak(max(4, a.steps // 2), 2)
     kv_snapshot = None if a.skip_kv_snapshot else measure_kv_snapshot()
     sampling = None if a.skip_sampling else measure_sampling()
@@ -856,6 +874,7 @@ def main():
                       "unit": "TFLOP/s", "frac": main_r["gemm"]["frac"], "mfma_ops_per_flop": 2,
                       "weight_stream_gbs": main_r["gemm"]["weight_gbs"]},
         "bs32": bs32,
+        "tp_shard": tp_shard,
         "soak": soak,
         "kv_snapshot": kv_snapshot,
         "sampling": sampling,

@@ -342,11 +342,11 @@ __device__ __forceinline__ void wave_ring_wait(int ahead) {
     }
 }
 
-template <int STAGES, int HL>
+template <int STAGES, int HL, int MT>
 __global__ __launch_bounds__(256) void gemm_swiglu_ksplit_kernel(const uint16_t* __restrict__ A, int M, int K,
                                                                 const bf16x8* __restrict__ Wp, int KT, int N,
                                                                 uint16_t* __restrict__ H, int h_lo) {
-    constexpr int FW = 2 * HL + 4;  // fragments per k-step: A (hl, kh), then weights (tile, kh)
+    constexpr int FW = 2 * HL * MT + 4;  // fragments per k-step: A (hl, row tile, kh), then weights (tile, kh)
     typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
     __shared__ bf16x8 lds[4][STAGES][FW][64];
     const int pair = blockIdx.x;  // weight tiles 2 pair (gate), 2 pair + 1 (up)
@@ -361,21 +361,27 @@ __global__ __launch_bounds__(256) void gemm_swiglu_ksplit_kernel(const uint16_t*
 #pragma unroll
         for (int hl = 0; hl < HL; ++hl)
 #pragma unroll
-            for (int kh = 0; kh < 2; ++kh)  // row tile 0 of the packed A operand (hi plane, then lo)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (lds_void*)&lds[wave][slot][hl * 2 + kh][0], 16, voff,
-                                                         ((hl * KT16 + 2 * kt + kh) << 10), 0, 0);
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int kh = 0; kh < 2; ++kh)  // row tile mt of the packed A operand (hi plane, then lo)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (lds_void*)&lds[wave][slot][(hl * MT + mt) * 2 + kh][0],
+                                                             16, voff, (((hl * MT + mt) * KT16 + 2 * kt + kh) << 10), 0,
+                                                             0);
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int kh = 0; kh < 2; ++kh)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_w, (lds_void*)&lds[wave][slot][2 * HL + t * 2 + kh][0],
-                                                         16, voff, (((2 * pair + t) * KT16 + 2 * kt + kh) << 10), 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_w,
+                                                         (lds_void*)&lds[wave][slot][2 * HL * MT + t * 2 + kh][0], 16,
+                                                         voff, (((2 * pair + t) * KT16 + 2 * kt + kh) << 10), 0, 0);
     };
-    f32x16 acc[2];
+    f32x16 acc[MT][2];
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[mt][t][i] = 0.0f;
 #pragma unroll
     for (int s = 0; s < STAGES - 1; ++s)
         if (s < nsteps) issue(s, s);
@@ -389,46 +395,52 @@ __global__ __launch_bounds__(256) void gemm_swiglu_ksplit_kernel(const uint16_t*
             if (i + STAGES - 1 < nsteps) issue((u + STAGES - 1) % STAGES, i + STAGES - 1);
 #pragma unroll
             for (int kh = 0; kh < 2; ++kh) {
-                const bf16x8 bg = lds[wave][u][2 * HL + kh][lane], bu = lds[wave][u][2 * HL + 2 + kh][lane];
+                const bf16x8 bg = lds[wave][u][2 * HL * MT + kh][lane], bu = lds[wave][u][2 * HL * MT + 2 + kh][lane];
 #pragma unroll
-                for (int hl = 0; hl < HL; ++hl) {
-                    const bf16x8 a = lds[wave][u][hl * 2 + kh][lane];
-                    acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bg, acc[0], 0, 0, 0);
-                    acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bu, acc[1], 0, 0, 0);
-                }
+                for (int hl = 0; hl < HL; ++hl)
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        const bf16x8 a = lds[wave][u][(hl * MT + mt) * 2 + kh][lane];
+                        acc[mt][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bg, acc[mt][0], 0, 0, 0);
+                        acc[mt][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bu, acc[mt][1], 0, 0, 0);
+                    }
             }
         }
     }
     // the four partial sums meet in LDS (the ring is free once every wave is past its last step)
     __syncthreads();
-    float* red = (float*)&lds[0][0][0][0];  // [wave][tile][i][lane]
+    float* red = (float*)&lds[0][0][0][0];  // [wave][row tile][tile][i][lane]
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) red[((wave * 2 + t) * 16 + i) * 64 + lane] = acc[t][i];
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) red[(((wave * MT + mt) * 2 + t) * 16 + i) * 64 + lane] = acc[mt][t][i];
     __syncthreads();
-    // thread (i-group tid / 64, lane): elements i = 4 (tid / 64) .. + 3 of the accumulators
+    // thread (i-group tid / 64, lane): elements i = 4 (tid / 64) .. + 3 of each row tile's accumulators
     const int F = N / 2;
     const size_t plane = a_plane(M, F);
     const int j = pair * 32 + (lane & 31);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int i = 4 * wave + q;
-        const int m = 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-        float g = red[((0 * 2 + 0) * 16 + i) * 64 + lane], up = red[((0 * 2 + 1) * 16 + i) * 64 + lane];
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int w = 1; w < 4; ++w) {
-            g += red[((w * 2 + 0) * 16 + i) * 64 + lane];
-            up += red[((w * 2 + 1) * 16 + i) * 64 + lane];
+        for (int q = 0; q < 4; ++q) {
+            const int i = 4 * wave + q;
+            const int m = 32 * mt + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+            float g = red[((mt * 2 + 0) * 16 + i) * 64 + lane], up = red[((mt * 2 + 1) * 16 + i) * 64 + lane];
+#pragma unroll
+            for (int w = 1; w < 4; ++w) {
+                g += red[(((w * MT + mt) * 2 + 0) * 16 + i) * 64 + lane];
+                up += red[(((w * MT + mt) * 2 + 1) * 16 + i) * 64 + lane];
+            }
+            if (m < M && j < F) {
+                uint16_t hi, lo;
+                split_bf16(swiglu(g, up), hi, lo);
+                const size_t o = a_pack_index(m, j, F);
+                H[o] = hi;
+                if (h_lo) H[plane + o] = lo;
+            }
         }
-        if (m < M && j < F) {
-            uint16_t hi, lo;
-            split_bf16(swiglu(g, up), hi, lo);
-            const size_t o = a_pack_index(m, j, F);
-            H[o] = hi;
-            if (h_lo) H[plane + o] = lo;
-        }
-    }
 }
 
 // Sum of split-K slabs [S][M][N] with the epilogue.
@@ -565,10 +577,10 @@ static GemmCfg pick_cfg(int m, int n, int k, int epilogue = kEpiStore) {
 
 static bool swiglu_fused(int m, int epilogue) { return epilogue == kEpiSwiGLU && m > 64; }
 
-// <= 32 rows of gate / up: SwiGLU in one launch with K split over the waves of
-// a workgroup (gemm_swiglu_ksplit_kernel)
+// <= 64 rows of gate / up: SwiGLU in one launch with K split over the waves of
+// a workgroup (gemm_swiglu_ksplit_kernel; two 32-row tiles above 32 rows)
 static bool swiglu_ksplit(int m, int n, int k, int epilogue) {
-    return epilogue == kEpiSwiGLU && m <= 32 && n % 64 == 0 && ((k + 31) / 32) % 4 == 0;
+    return epilogue == kEpiSwiGLU && m <= 64 && n % 64 == 0 && ((k + 31) / 32) % 4 == 0;
 }
 
 GemmPlan gemm_plan(int m, int n, int k, int epilogue) {
@@ -642,12 +654,21 @@ zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_pack
         const GemmPlan p = gemm_plan(m, n, k, epilogue);
         hipEvent_t ev;
         timing_mark_begin(ctx, kClassGemm, &ev);
-        if (split_act)
-            hipLaunchKernelGGL((gemm_swiglu_ksplit_kernel<3, 2>), dim3(p.col_blocks), dim3(256), 0, ctx->stream, a, m,
-                               k, (const bf16x8*)w_packed, p.KT, n, c_bf16, 1);
-        else
-            hipLaunchKernelGGL((gemm_swiglu_ksplit_kernel<3, 1>), dim3(p.col_blocks), dim3(256), 0, ctx->stream, a, m,
-                               k, (const bf16x8*)w_packed, p.KT, n, c_bf16, 0);
+#define ZR_KSPLIT(HLV, MTV)                                                                                     \
+    hipLaunchKernelGGL((gemm_swiglu_ksplit_kernel<3, HLV, MTV>), dim3(p.col_blocks), dim3(256), 0, ctx->stream, a, \
+                       m, k, (const bf16x8*)w_packed, p.KT, n, c_bf16, HLV - 1)
+        if (split_act) {
+            if (m > 32)
+                ZR_KSPLIT(2, 2);
+            else
+                ZR_KSPLIT(2, 1);
+        } else {
+            if (m > 32)
+                ZR_KSPLIT(1, 2);
+            else
+                ZR_KSPLIT(1, 1);
+        }
+#undef ZR_KSPLIT
         ZR_LAUNCH_CHECK(ctx);
         timing_mark_end(ctx, kClassGemm, ev);
         return ZR_OK;

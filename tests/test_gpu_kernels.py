@@ -571,7 +571,9 @@ def test_gemm_matches_fp64(split, m, k, n):
 
 
 @pytest.mark.parametrize("split", [True, False])
-@pytest.mark.parametrize("m,k,f", [(40, 320, 512),       # <= 64 rows: split-K slabs, SwiGLU in the reduce
+@pytest.mark.parametrize("m,k,f", [(40, 320, 512),       # <= 64 rows, K = 10 steps: split-K slabs, the reduce
+                                   (40, 512, 512), (33, 256, 96),  # 33-64 rows: K over 4 waves, two row tiles
+                                   (64, 4096, 7168),     # the tensor-parallel shard's gate / up at 64 sessions
                                    (32, 2048, 5632),     # the 32-session TinyLlama gate / up: K over 4 waves
                                    (1, 128, 64), (7, 256, 96),  # <= 32 rows, K over 4 waves of 1 / 2 steps
                                    (5, 96, 64),          # K = 3 steps: split-K slabs and the reduce
