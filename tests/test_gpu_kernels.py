@@ -548,7 +548,10 @@ def test_kv_gather_scatter_round_trip_with_partial_first_page(kv_dtype):
                                    (256, 4096, 6144), (256, 4096, 4096), (256, 14336, 4096), (200, 4096, 66000),
                                    # the 32-session TinyLlama products: QKV (11 splits), down (16), an
                                    # unsplit vocabulary head
-                                   (32, 2048, 2560), (32, 5632, 2048), (32, 2048, 32000)])
+                                   (32, 2048, 2560), (32, 5632, 2048), (32, 2048, 32000),
+                                   # 33-64 rows on 64-row tiles (a 4-deep ring, one pass of splits): the
+                                   # 64-session shard's QKV, O and down products, and a ragged one
+                                   (64, 4096, 3072), (64, 2048, 4096), (64, 7168, 4096), (40, 512, 1000)])
 def test_gemm_matches_fp64(split, m, k, n):
     geo = ModelGeometry(hidden=256, num_heads=4, num_kv_heads=4, num_layers=1, vocab=64, ffn=256)
     ctx = DeviceContext(geo, kv_dtype="f32", max_tokens=16, max_seqs=4, max_pages_per_seq=4, split_activations=split)
