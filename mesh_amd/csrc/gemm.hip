@@ -572,6 +572,12 @@ static GemmCfg pick_cfg(int m, int n, int k, int epilogue = kEpiStore) {
     // at 64 sessions: 12.6k -> 13.4k tokens/s against ~3 blocks per CU and 3
     // stages, whose 16 slabs each consumer read back)
     if (m <= 64) return {2, 1, 1, 4, 4, false};
+    // and the 65-128-row store products (QKV, O, down) on two or more 64-row
+    // tiles: fewer split-K slabs for their consumers (decode steps at 96 / 128
+    // sessions 10.5 -> 10.2 / 12.4 -> 11.3 ms; at 128 sessions the attention,
+    // with RoPE inside, sums q from 2 QKV slabs instead of 10).  At 256 rows
+    // the same plan costs the GEMMs what it saves their consumers.
+    if (m <= 128 && epilogue == kEpiStore && n < 65536) return {2, 1, 1, 4, 4, false};
     // vocabulary-wide heads: 256-row tiles read each weight tile once
     if (n >= 65536) return m > 128 ? GemmCfg{2, 4, 4, 2, 3, false} : GemmCfg{2, 4, 2, 4, 3, false};
     if (n >= 16384) return {2, 4, 2, 4, 3, false};
