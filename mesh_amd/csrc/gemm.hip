@@ -560,6 +560,11 @@ static GemmCfg pick_cfg(int m, int n, int k, int epilogue = kEpiStore) {
     if (epilogue == kEpiSwiGLU && m > 64) {
         const int wide_tiles = ((m + 127) / 128) * ((n + 511) / 512);
         if (wide_tiles >= 2 * device_cus()) return {2, 4, 2, 4, 3, false};
+        // 65-128 rows: 64 x 256 tiles (two row blocks share each weight tile)
+        // fill twice the CUs of one 128-row block (decode steps at 96 / 128
+        // sessions -4.7 / -4.2 %); at 256 rows they are slower (GEMMs 7.5
+        // against 6.8 ms per step)
+        if (m <= 128) return {2, 2, 1, 4, 3, false};
         return {2, 2, 2, 4, 3, false};
     }
     // <= 32 rows: a 4-deep ring and one pass of splits over the CUs (TinyLlama
@@ -706,6 +711,7 @@ zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_pack
     }
     ZR_GEMM_FUSED_CASE(2, 4, 2, 4, 3)
     ZR_GEMM_FUSED_CASE(2, 2, 2, 4, 3)
+    ZR_GEMM_FUSED_CASE(2, 2, 1, 4, 3)
 #undef ZR_GEMM_FUSED_CASE
 #define ZR_GEMM_CASE(WMV, WNV, WAM, WAN, ST)                                                           \
     if (!fused && !launched && cfg.wm == WMV && cfg.wn == WNV && cfg.waves_m == WAM &&                 \
