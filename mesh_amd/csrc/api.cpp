@@ -318,7 +318,7 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
             if (end - first == 1) meta |= kAttnSingle;
             if (item == end - 1) meta |= kAttnLast;
             const int* bt = mb->block_tables + (size_t)seq * stride;
-            auto pid = [&](int k) { return bt[std::min(it.y + k, it.z - 1)]; };
+            auto pid = [&](int k) { return it.y + k < it.z ? bt[it.y + k] : 0; };
             st->h_attn_rec[3 * r] = make_int4(seq, cuq[seq] + tl.y, tl.z, it.y);
             st->h_attn_rec[3 * r + 1] =
                 make_int4(it.z, mb->kv_before[seq] + tl.y, mb->first_offset[seq], (int)meta);

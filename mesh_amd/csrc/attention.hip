@@ -302,10 +302,16 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
         const KV* base = pool + (size_t)pool_page * a.page_elems + (size_t)kvh * kv_tile;
         r.load(base, base + v_block, lane);
     };
-    auto load = [&](PageRegs<KV, D>& r, int p) { load_page(r, bt[p]); };
-    // Every ring slot is loaded unconditionally (past the split's end, the
-    // last page again; with the nontemporal hint not always an L2 hit, ~1.5%
-    // of the launch's traffic at 256 sessions): with no conditional loads the compiler
+    auto load_or_shared = [&](PageRegs<KV, D>& r, int p) {
+        const int pg = bt[min(p, page_e - 1)];
+        load_page(r, p < page_e ? pg : 0);
+    };
+    // Every ring slot is loaded unconditionally (past the split's end, and in
+    // the record past a short item's end, pool page 0, which every wave
+    // shares, so those loads hit L2; the values are never used: 32-session
+    // TinyLlama step attention -1.4% against reloading the split's last page,
+    // a third of whose loads fall past the end of an 8-page split with this
+    // ring): with no conditional loads the compiler
     // can wait for exactly the slot it computes on (in-order vmcnt) instead
     // of conservatively draining the newest pages' loads too.  The pool
     // pages of the first RING - 2 come from the record: no block-table load
@@ -493,8 +499,8 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
         for (int r = 0; r < RING; r += 2) {
             const int pp = p + r;
             if (pp >= pend) break;
-            load(ring[(r + RING - 2) % RING], min(pp + RING - 2, pend - 1));
-            load(ring[(r + RING - 1) % RING], min(pp + RING - 1, pend - 1));
+            load_or_shared(ring[(r + RING - 2) % RING], pp + RING - 2);
+            load_or_shared(ring[(r + RING - 1) % RING], pp + RING - 1);
             const bool has_b = pp + 1 < pend;
             process2(ring[r], has_b ? ring[r + 1] : ring[r], pp, has_b);
         }
