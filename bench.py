@@ -99,20 +99,22 @@ def measured_traffic():
     return None
 
 
-def step_bytes(geo, batch, kv_rows_total):
+def step_bytes(geo, batch, kv_rows_total, kv_bytes=2):
     """Algorithmic HBM bytes of one decode step: every weight once (bf16), the
-    embedding rows, every cached K/V row of every layer once (bf16), the new
-    K/V rows written, and the per-row activations in and out of each kernel."""
+    embedding rows, every cached K/V row of every layer once (`kv_bytes` per
+    element: 2 bf16, 4 f32), the new K/V rows written, and the per-row
+    activations in and out of each kernel."""
     H, Q, KV, F, V, L = geo.hidden, geo.q_cols, geo.kv_cols, geo.ffn_cols, geo.vocab, geo.num_layers
     weights = 2 * (L * (H * (Q + 2 * KV) + Q * H + H * 2 * F + F * H) + H * V) + 4 * (2 * L + 1) * H
-    kv = L * kv_rows_total * KV * 2 * 2 + L * batch * KV * 2 * 2
+    kv = L * kv_rows_total * KV * 2 * kv_bytes + L * batch * KV * 2 * kv_bytes
     act = 4 * batch * (L * (3 * H + 2 * (Q + 2 * KV) + 2 * Q + 2 * H + 3 * F + 2 * H) + V)
     return weights + 2 * batch * H + kv + act
 
 
-def device_model(name, split=True, max_tokens=None, max_seqs=None, host_weights=None):
+def device_model(name, split=True, max_tokens=None, max_seqs=None, host_weights=None, kv_dtype="bf16"):
     """A DeviceContext holding the workload's model with random-init bf16
-    N(0, 0.02) weights generated on the device (RMSNorm gains 1).  A dict
+    N(0, 0.02) weights generated on the device (RMSNorm gains 1) and a KV
+    pool of `kv_dtype` ("bf16", or "f32" as the reference stores it).  A dict
     passed as `host_weights` receives host copies of the generated weights as
     bf16 bit patterns in the reference [in, out] layout (embedding, lm_head,
     final_norm, layers), e.g. for a parity check of the same model."""
@@ -121,7 +123,7 @@ def device_model(name, split=True, max_tokens=None, max_seqs=None, host_weights=
     w = WORKLOADS[name]
     g = ModelGeometry(**w["geo"])
     B = w["batch"]
-    ctx = DeviceContext(g, kv_dtype="bf16", max_tokens=max_tokens or B, max_seqs=max_seqs or B,
+    ctx = DeviceContext(g, kv_dtype=kv_dtype, max_tokens=max_tokens or B, max_seqs=max_seqs or B,
                         max_pages_per_seq=w["max_seq_len"] // 16 + 2, split_activations=split)
     lib = ctx.lib
 
@@ -176,7 +178,7 @@ class GpuDecodeBench:
     `model` = (DeviceContext, ModelGeometry) reuses a model built by
     device_model (its KV pool is replaced; the caller keeps the context)."""
 
-    def __init__(self, name, steps_total, split=True, model=None, host_steps=0):
+    def __init__(self, name, steps_total, split=True, model=None, host_steps=0, kv_dtype="bf16"):
         from mesh_amd import _lib
 
         self._lib = _lib
@@ -186,7 +188,7 @@ class GpuDecodeBench:
         self.ctxlens = w["contexts"]()
         self.max_seq = w["max_seq_len"]
         self.owns_ctx = model is None
-        self.ctx, self.geo = device_model(name, split) if model is None else model
+        self.ctx, self.geo = device_model(name, split, kv_dtype=kv_dtype) if model is None else model
         ctx, lib, g = self.ctx, self.ctx.lib, self.geo
         V = g.vocab
         # KV pool: every session's context plus the benchmarked steps (staged
@@ -301,7 +303,7 @@ class GpuDecodeBench:
 BREAKDOWN_STEPS = 2
 
 
-def measure(name, steps, warmup):
+def measure(name, steps, warmup, kv_dtype="bf16"):
     """Timed region: `steps` decode steps, each replayed from the HIP graph of
     its staged launch sequence.  Then `steps` more steps launched kernel by
     kernel (zr_forward_staged_async) with HIP events around the attention
@@ -310,8 +312,9 @@ def measure(name, steps, warmup):
     per-class time split.  Then the same sessions decode `warmup` + `steps`
     more steps through the host entry point (zrh_decode_step_batch), timed
     end to end with the host work."""
-    bench = GpuDecodeBench(name, warmup + 2 * steps + BREAKDOWN_STEPS, host_steps=steps + warmup)
+    bench = GpuDecodeBench(name, warmup + 2 * steps + BREAKDOWN_STEPS, host_steps=steps + warmup, kv_dtype=kv_dtype)
     g, B = bench.geo, bench.B
+    kv_size = 2 if kv_dtype == "bf16" else 4
     bench.run(0, warmup, timed=False)
     dt = bench.run_graphs(warmup, steps)
     toks = bench.tokens(warmup + steps)
@@ -320,17 +323,18 @@ def measure(name, steps, warmup):
     assert bench.tokens(warmup + 2 * steps).max() < g.vocab
     _, ms_b, n_b = bench.run(warmup + 2 * steps, BREAKDOWN_STEPS, timed=True, mask=0xF)
     ms_per_step = dt / steps * 1000.0
-    # attention: algorithmic bytes per launch (K+V of every attended row, bf16;
-    # Q in and the output out, f32), averaged over the eager steps' launches
+    # attention: algorithmic bytes per launch (K+V of every attended row in the
+    # pool's dtype; Q in and the output out, f32), averaged over the eager
+    # steps' launches
     timed_rows = bench.kv_rows[warmup:warmup + steps]
     eager_rows = bench.kv_rows[warmup + steps:warmup + 2 * steps]
-    kv_bytes = sum(eager_rows) * g.num_layers * g.kv_cols * 2 * 2
+    kv_bytes = sum(eager_rows) * g.num_layers * g.kv_cols * 2 * kv_size
     qo_bytes = steps * g.num_layers * B * g.q_cols * 4 * 2
     attn_launches = n_t[0]
     attn_bytes_per_launch = (kv_bytes + qo_bytes) / max(attn_launches, 1)
     attn_ms_per_launch = ms_t[0] / max(attn_launches, 1)
     attn_gbs = attn_bytes_per_launch / (attn_ms_per_launch * 1e-3) / 1e9
-    sb = np.mean([step_bytes(g, B, r) for r in timed_rows])
+    sb = np.mean([step_bytes(g, B, r, kv_size) for r in timed_rows])
     nb = BREAKDOWN_STEPS
     gemm_tflops = gemm_flops(g, B) * nb / (ms_b[1] * 1e-3) / 1e12 if ms_b[1] > 0 else 0.0
     roof_tps = B / (sb / (HBM_PEAK_GBS * 1e9))
@@ -352,7 +356,7 @@ def measure(name, steps, warmup):
                            tokens_per_s=B * steps / dt_eager,
                            includes="the same decode step launched kernel by kernel instead of replayed, "
                                     "HIP events around its attention launches")
-    result["kv_append"] = measure_kv_append(bench)
+    result["kv_append"] = measure_kv_append(bench, kv_size)
     # end to end through the boundary's host entry point, host work included
     _, last = bench.run_host(warmup, bench.tokens(warmup + steps + BREAKDOWN_STEPS))
     dt_host, last = bench.run_host(steps, last)
@@ -366,7 +370,7 @@ def measure(name, steps, warmup):
     return result
 
 
-def measure_kv_append(bench, reps=5):
+def measure_kv_append(bench, kv_size=2, reps=5):
     """RoPE + KV append (the RopeKvWrite stage; rope_kv_write_vec_kernel at 256 rows) alone:
     one launch over a decode step's rows (layer 0, the last staged step, after
     the timed region), HIP events of class 2.  (The 256-session forward pass
@@ -393,7 +397,7 @@ def measure_kv_append(bench, reps=5):
     lib.zr_device_free(ctx.h, d_qkv)
     lib.zr_device_free(ctx.h, d_q)
     k_ms = float(np.median(times))
-    alg = T * width * 4 + T * g.q_cols * 4 + T * 2 * g.kv_cols * 2
+    alg = T * width * 4 + T * g.q_cols * 4 + T * 2 * g.kv_cols * kv_size
     return dict(kernel="rope_kv_write_vec_kernel" if T >= 128 else "rope_kv_write_kernel", rows=T, kernel_ms=k_ms, algorithmic_bytes=alg,
                 achieved_gbs=alg / (k_ms * 1e6), frac=alg / (k_ms * 1e6) / HBM_PEAK_GBS,
                 note="one launch is a few MB, so it is launch/latency-bound rather than HBM-bound")
@@ -807,6 +811,7 @@ def main():
     ap.add_argument("--skip-sampling", action="store_true", help="skip the device sampling leg")
     ap.add_argument("--skip-mixed", action="store_true", help="skip the mixed prefill + decode microbatch leg")
     ap.add_argument("--skip-tp-shard", action="store_true", help="skip the tensor-parallel shard decode leg")
+    ap.add_argument("--skip-f32-kv", action="store_true", help="skip the headline step with an f32 KV pool")
     ap.add_argument("--mixed-only", action="store_true",
                     help="run only the mixed prefill + decode microbatch leg (for profiling its kernels)")
     a = ap.parse_args()
@@ -842,6 +847,19 @@ def main():
                         attention_gbs=r["attention"]["achieved_gbs"], kernel_ms_per_step=r["kernel_ms_per_step"],
                         gemm_tflops=r["gemm"]["achieved_tflops"], gemm_weight_gbs=r["gemm"]["weight_gbs"],
                         host_path=r["host_path"])
+    f32_kv = None
+    if not a.skip_f32_kv and a.workload == "llama3_8b_b256":
+        r = measure(a.workload, max(4, a.steps // 2), 2, kv_dtype="f32")
+        att32 = r["attention"]
+        f32_kv = dict(value=r["tokens_per_s"], unit="tokens/s", ms_per_step=r["ms_per_step"],
+                      workload=r["workload"].replace("bf16 KV", "f32 KV (the reference's page dtype)"),
+                      step_roofline_frac=r["step_roofline_frac"],
+                      step_roofline_tokens_per_s=r["step_roofline_tokens_per_s"],
+                      kernel_ms_per_step=r["kernel_ms_per_step"], host_path=r["host_path"], eager=r["eager"],
+                      roofline={"bound": "hbm", "kernel": "paged_attention_kernel<float>",
+                                "achieved": att32["achieved_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                "frac": att32["frac"], "bytes_per_launch": att32["bytes_per_launch"],
+                                "avg_ms": att32["avg_ms"], "launches": att32["launches"], "sizeof_kv": 4})
     soak = None if a.skip_soak else measure_soak(max(4, a.steps // 2), 2)
     kv_snapshot = None if a.skip_kv_snapshot else measure_kv_snapshot()
     sampling = None if a.skip_sampling else measure_sampling()
@@ -875,6 +893,7 @@ def main():
                       "weight_stream_gbs": main_r["gemm"]["weight_gbs"]},
         "bs32": bs32,
         "tp_shard": tp_shard,
+        "f32_kv": f32_kv,
         "soak": soak,
         "kv_snapshot": kv_snapshot,
         "sampling": sampling,

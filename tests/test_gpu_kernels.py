@@ -646,20 +646,23 @@ def test_argmax_first_index_on_ties_and_large_vocab():
 
 
 # -------------------------------- the benchmarked launch: 256 sessions --
+@pytest.mark.parametrize("kv_dtype", ["bf16", "f32"])
 @pytest.mark.parametrize("rope", [0, 1])
-def test_c5_shape_attention_256_sessions_matches_oracle(rope):
+def test_c5_shape_attention_256_sessions_matches_oracle(rope, kv_dtype):
     # The attention launch of the 256-session decode benchmark: Llama-3-8B
-    # attention shape (32 q heads, 8 kv heads, head_dim 128), bf16 pool, the
-    # benchmark's lognormal contexts (seed 0xC5: median 1024, sigma 1, clipped
-    # to [64, 8192]; sum ~395k keys) with the launch's own split sizing (~96
+    # attention shape (32 q heads, 8 kv heads, head_dim 128), the benchmark's
+    # lognormal contexts (seed 0xC5: median 1024, sigma 1, clipped to
+    # [64, 8192]; sum ~395k keys) with the launch's own split sizing (~96
     # pages per split, so long sessions merge several splits).  All 32 heads
     # of a sample of sessions (the longest, the shortest and six more) are
-    # checked against the oracle; every output must be finite.
+    # checked against the oracle; every output must be finite.  The bf16 pool
+    # is the benchmark's; the f32 pool is the reference's own KV precision
+    # (forward_pass.rs:255-262), checked against unrounded K / V.
     ctxlens = np.clip(np.round(np.random.default_rng(0xC5).lognormal(math.log(1024), 1.0, 256)), 64,
                       8192).astype(np.int64)
     B, H, KVC, D = 256, 4096, 1024, 128
     geo = ModelGeometry(hidden=H, num_heads=32, num_kv_heads=8, num_layers=1, vocab=64, ffn=64, rope_base=500000.0)
-    ctx = DeviceContext(geo, kv_dtype="bf16", max_tokens=B, max_seqs=B, max_pages_per_seq=520)
+    ctx = DeviceContext(geo, kv_dtype=kv_dtype, max_tokens=B, max_seqs=B, max_pages_per_seq=520)
     ctx.create_kv_pool(int(((ctxlens + 15) // 16).sum()) + B)
     rng = np.random.default_rng(0xA5)
     rows = 1 << 16
@@ -689,8 +692,10 @@ def test_c5_shape_attention_256_sessions_matches_oracle(rope):
                     {int(x) for x in np.random.default_rng(7).choice(B, 6, replace=False)})
     for s in sample:
         L = int(ctxlens[s])
-        k = O.round_bf16(np.concatenate([big[koff[s]:koff[s] + L - 1], qkv[s:s + 1, H:H + KVC]]))
-        v = O.round_bf16(np.concatenate([big[voff[s]:voff[s] + L - 1], qkv[s:s + 1, H + KVC:]]))
+        k = np.concatenate([big[koff[s]:koff[s] + L - 1], qkv[s:s + 1, H:H + KVC]])
+        v = np.concatenate([big[voff[s]:voff[s] + L - 1], qkv[s:s + 1, H + KVC:]])
+        if kv_dtype == "bf16":
+            k, v = O.round_bf16(k), O.round_bf16(v)
         want = np.zeros(H, np.float32)
         for h in range(32):
             kvh = h // 4
