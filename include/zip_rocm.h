@@ -352,6 +352,10 @@ typedef struct {
     const char* memory_model;            /* "discrete_vram" (MemoryModel) */
     int supports_decode_microbatch, supports_paged_kv, supports_checkpoint_handoff, supports_device_sampling;
     int fast_path_eligible;
+    /* FastPathPlanner::capture_strategy (fast_path.rs:831-837) of the rocm_fused
+     * profile: "replay_preferred", as the CudaFused arm; served by
+     * zr_graph_capture_staged / zr_step_graph_* (GraphCaptureStrategy). */
+    const char* capture_strategy;
 } zr_executor_contract;
 zr_status zr_get_executor_contract(zr_executor_contract* out);
 

@@ -150,10 +150,58 @@ typedef struct {
     size_t field_offset[4], field_bytes[4]; /* the four metadata fields, in order */
     size_t metadata_bytes;
     size_t workspace_bytes, workspace_alignment;
-    char bucket_label[64];                  /* "decode-b{B}-kv{T}-rocm" */
+    char bucket_label[64];                  /* "decode-b{B}-kv{T}-rocm" / "prefill-t{T}-rocm" */
+    int phase;                              /* ExecutionPhase: 0 decode, 1 prefill */
+    char capture_strategy[24];              /* FastPathPlanner::capture_strategy (831-837): "replay_preferred" */
+    char prefill_strategy[32];              /* "single_sequence_buckets" (prefill plans), "" (decode) */
+    /* BucketMetadataLayout::layout_hash (892-902) of the bucket key (phase,
+     * provider "rocm", profile "rocm_fused", both ceilings) and the fields
+     * (name, element size, count, stride).  The reference hashes with Rust's
+     * DefaultHasher, a process-local value that never leaves the process; this
+     * library hashes the same items with FNV-1a 64 (each integer as 8
+     * little-endian bytes, each name's bytes then 0xff).  The value only has
+     * to match the plan it was computed for (the drift check). */
+    uint64_t layout_hash;
 } zrh_fast_path_plan;
 zr_status zrh_fast_path_plan_decode(int batch_size, int total_kv_tokens, int max_sequence_len,
                                     zrh_fast_path_plan* out);
+/* FastPathPlanner::plan_prefill (fast_path.rs:680-702): the first bucket of
+ * PREFILL_BUCKET_TOKENS (17: 128, 512, 2048, 8192, 16384; batch ceiling 1)
+ * holding prompt_tokens, built as plan_decode builds its plan (metadata
+ * fields over one slot, workspace_requirements, capture strategy) with
+ * prefill_strategy SingleSequenceBuckets.  A prompt longer than every bucket
+ * is ZR_E_UNSUPPORTED with UnsupportedBucket's text; the coordinator plans
+ * a prefill so when the request permits the fast path (coordinator.rs:2164-2172). */
+zr_status zrh_fast_path_plan_prefill(int prompt_tokens, zrh_fast_path_plan* out);
+/* PrefillWorkspaceLease::stage_positions (fast_path.rs:409-445), which
+ * ForwardPass::forward_tokens calls for a leased prefill (forward_pass.rs:2470-2476):
+ * resets the lease's positions (plan->token_ceiling words) and writes
+ * absolute_position_start + i for i < token_count.  A count beyond the ceiling
+ * is CaptureUnsafe ("prefill token count {n} exceeds bucket ceiling {T}"), a
+ * position beyond u32 "prefill absolute position exceeded u32 addressable
+ * range" (ZR_E_INVALID). */
+zr_status zrh_fast_path_stage_prefill_positions(const zrh_fast_path_plan* plan, uint64_t absolute_position_start,
+                                                int token_count, uint32_t* positions);
+/* FastPathBackendContext (fast_path.rs:102-108) of any provider's backend,
+ * as ExecutionBackend::fast_path_context reports it (backend.rs:748-755):
+ * ExecutionProviderKind and BackendOptimizationProfile as the reference
+ * serialises them ("rocm" / "rocm_fused", "cpu" / "cpu_serial", "cuda" /
+ * "cuda_fused", "metal" / "metal_vectorized"), the model id (nullable). */
+typedef struct {
+    const char* provider;
+    const char* optimization_profile;
+    const char* model_id;
+    int logical_kv_tokens;
+} zrh_fast_path_backend_context;
+/* FastPathPlanner::validate_decode_contexts (fast_path.rs:704-778), which
+ * BackendMicrobatchExecutor::decode_step_batch runs before a planned batch
+ * (backend.rs:116-123): the request count equals the plan's batch, every
+ * context is the plan's provider and profile, fits the bucket's token
+ * ceiling and shares one model id, and the plan's layout hash matches its
+ * bucket and fields.  Errors carry CaptureUnsafe / MetadataDrift texts
+ * (ZR_E_INVALID). */
+zr_status zrh_fast_path_validate_decode_contexts(const zrh_fast_path_plan* plan,
+                                                 const zrh_fast_path_backend_context* contexts, int n);
 
 /* DecodeWorkspaceLease::stage (fast_path.rs:263-338) over the slot states of
  * n sessions (DeviceKVCache::decode_slot_state, forward_pass.rs:1065-1074):

@@ -76,7 +76,7 @@ class ExecutorContract(C.Structure):
                 ("compatibility_class", C.c_char_p), ("memory_model", C.c_char_p),
                 ("supports_decode_microbatch", C.c_int), ("supports_paged_kv", C.c_int),
                 ("supports_checkpoint_handoff", C.c_int), ("supports_device_sampling", C.c_int),
-                ("fast_path_eligible", C.c_int)]
+                ("fast_path_eligible", C.c_int), ("capture_strategy", C.c_char_p)]
 
 
 class FastPathContext(C.Structure):
@@ -89,7 +89,13 @@ class FastPathPlan(C.Structure):
                 ("actual_token_count", C.c_int), ("max_sequence_len", C.c_int), ("page_slots", C.c_int),
                 ("field_offset", C.c_size_t * 4), ("field_bytes", C.c_size_t * 4), ("metadata_bytes", C.c_size_t),
                 ("workspace_bytes", C.c_size_t), ("workspace_alignment", C.c_size_t),
-                ("bucket_label", C.c_char * 64)]
+                ("bucket_label", C.c_char * 64), ("phase", C.c_int), ("capture_strategy", C.c_char * 24),
+                ("prefill_strategy", C.c_char * 32), ("layout_hash", C.c_uint64)]
+
+
+class FastPathBackendContext(C.Structure):
+    _fields_ = [("provider", C.c_char_p), ("optimization_profile", C.c_char_p), ("model_id", C.c_char_p),
+                ("logical_kv_tokens", C.c_int)]
 
 
 # (name, restype, argtypes) for every exported symbol declared in include/*.h
@@ -182,6 +188,10 @@ SIGNATURES = [
     ("zrh_fast_path_plan_decode", C.c_int, [C.c_int, C.c_int, C.c_int, C.POINTER(FastPathPlan)]),
     ("zrh_fast_path_stage_decode", C.c_int, [C.POINTER(FastPathPlan), c_void_pp, C.c_int, c_u32_p, c_u32_p,
                                              c_u32_p, c_u32_p]),
+    ("zrh_fast_path_plan_prefill", C.c_int, [C.c_int, C.POINTER(FastPathPlan)]),
+    ("zrh_fast_path_stage_prefill_positions", C.c_int, [C.POINTER(FastPathPlan), C.c_uint64, C.c_int, c_u32_p]),
+    ("zrh_fast_path_validate_decode_contexts", C.c_int, [C.POINTER(FastPathPlan), C.POINTER(FastPathBackendContext),
+                                                         C.c_int]),
     ("zrh_kv_reserve", C.c_int, [C.c_void_p, C.c_int]),
     ("zrh_retain_suffix", C.c_int, [C.c_void_p, C.c_int]),
 ]

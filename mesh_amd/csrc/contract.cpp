@@ -58,5 +58,7 @@ extern "C" zr_status zr_get_executor_contract(zr_executor_contract* out) {
     out->supports_checkpoint_handoff = 1;
     out->supports_device_sampling = 1;
     out->fast_path_eligible = 1;
+    // FastPathPlanner::capture_strategy (fast_path.rs:831-837): the fused profile replays
+    out->capture_strategy = "replay_preferred";
     return ZR_OK;
 }

@@ -751,12 +751,81 @@ zr_status zrh_get_fast_path_context(const zrh_backend* b, zrh_fast_path_context*
     return ZR_OK;
 }
 
+}  // extern "C"
+
+// FNV-1a 64 over the layout's items (zrh_fast_path_plan.layout_hash).
+struct LayoutHasher {
+    uint64_t h = 0xcbf29ce484222325ull;
+    void byte(uint8_t b) { h = (h ^ b) * 0x100000001b3ull; }
+    void u64(uint64_t v) {
+        for (int i = 0; i < 8; ++i) byte((uint8_t)(v >> (8 * i)));
+    }
+    void str(const char* s) {
+        for (; *s; ++s) byte((uint8_t)*s);
+        byte(0xff);
+    }
+};
+
+static const char* const kMetadataFieldNames[4] = {"slot_sequence_lengths", "slot_positions", "slot_block_tables",
+                                                   "slot_mapping"};
+
+static uint64_t plan_layout_hash(const zrh_fast_path_plan* p) {
+    LayoutHasher h;
+    h.u64((uint64_t)p->phase);
+    h.str("rocm");
+    h.str("rocm_fused");
+    h.u64((uint64_t)p->batch_size_ceiling);
+    h.u64((uint64_t)p->token_ceiling);
+    for (int f = 0; f < 4; ++f) {
+        h.str(kMetadataFieldNames[f]);
+        h.u64(sizeof(uint32_t));
+        h.u64(p->field_bytes[f] / sizeof(uint32_t));
+        h.u64(p->field_bytes[f]);
+    }
+    return h.h;
+}
+
+// FastPathPlanner::build_plan (fast_path.rs:780-829) for the rocm_fused profile.
+static void build_plan(int phase, int bb, int bt, int batch, int tokens, int max_seq, zrh_fast_path_plan* out) {
+    memset(out, 0, sizeof *out);
+    out->phase = phase;
+    out->batch_size_ceiling = bb;
+    out->token_ceiling = bt;
+    out->actual_batch_size = batch;
+    out->actual_token_count = tokens;
+    out->max_sequence_len = max_seq;
+    out->page_slots = (bt + kPageRows - 1) / kPageRows;
+    // metadata_fields (839-867): the same four u32 fields for either phase
+    const size_t widths[4] = {(size_t)bb, (size_t)bb, (size_t)bb * out->page_slots, (size_t)bb};
+    size_t off = 0;
+    for (int f = 0; f < 4; ++f) {
+        out->field_offset[f] = off;
+        out->field_bytes[f] = widths[f] * sizeof(uint32_t);
+        off += out->field_bytes[f];
+    }
+    out->metadata_bytes = off;
+    // workspace_requirements (869-890): the fused profile's 96 B per token and 32 KiB per slot
+    out->workspace_bytes = off + (size_t)bt * 96 + (size_t)bb * 32 * 1024;
+    out->workspace_alignment = 256;
+    if (phase == 0)
+        snprintf(out->bucket_label, sizeof out->bucket_label, "decode-b%d-kv%d-rocm", bb, bt);
+    else
+        snprintf(out->bucket_label, sizeof out->bucket_label, "prefill-t%d-rocm", bt);
+    snprintf(out->capture_strategy, sizeof out->capture_strategy, "replay_preferred");
+    if (phase == 1) snprintf(out->prefill_strategy, sizeof out->prefill_strategy, "single_sequence_buckets");
+    out->layout_hash = plan_layout_hash(out);
+}
+
+// Buckets of fast_path.rs:17 (prefill).
+static const int kPrefillBucketTokens[] = {128, 512, 2048, 8192, 16384};
+
+extern "C" {
+
 zr_status zrh_fast_path_plan_decode(int batch_size, int total_kv_tokens, int max_sequence_len,
                                     zrh_fast_path_plan* out) {
     if (!out) return set_global_err(ZR_E_INVALID, "null argument");
     if (batch_size < 0 || total_kv_tokens < 0 || max_sequence_len < 0)
         return set_global_err(ZR_E_INVALID, "negative batch size or token count");
-    memset(out, 0, sizeof *out);
     int bb = -1, bt = -1;
     for (int b : kDecodeBucketBatches) {
         for (int t : kDecodeBucketKvTokens)
@@ -770,24 +839,74 @@ zr_status zrh_fast_path_plan_decode(int batch_size, int total_kv_tokens, int max
     if (bb < 0)
         return set_global_err(ZR_E_UNSUPPORTED, "no stable Decode bucket supports batch_size=%d token_count=%d for RocmFused",
                               batch_size, total_kv_tokens);
-    out->batch_size_ceiling = bb;
-    out->token_ceiling = bt;
-    out->actual_batch_size = batch_size;
-    out->actual_token_count = total_kv_tokens;
-    out->max_sequence_len = max_sequence_len;
-    out->page_slots = (bt + kPageRows - 1) / kPageRows;
-    const size_t widths[4] = {(size_t)bb, (size_t)bb, (size_t)bb * out->page_slots, (size_t)bb};
-    size_t off = 0;
-    for (int f = 0; f < 4; ++f) {
-        out->field_offset[f] = off;
-        out->field_bytes[f] = widths[f] * sizeof(uint32_t);
-        off += out->field_bytes[f];
+    build_plan(0, bb, bt, batch_size, total_kv_tokens, max_sequence_len, out);
+    return ZR_OK;
+}
+
+zr_status zrh_fast_path_plan_prefill(int prompt_tokens, zrh_fast_path_plan* out) {
+    if (!out) return set_global_err(ZR_E_INVALID, "null argument");
+    if (prompt_tokens < 0) return set_global_err(ZR_E_INVALID, "negative token count");
+    for (int t : kPrefillBucketTokens)
+        if (prompt_tokens <= t) {
+            build_plan(1, 1, t, 1, prompt_tokens, prompt_tokens, out);
+            return ZR_OK;
+        }
+    return set_global_err(ZR_E_UNSUPPORTED, "no stable Prefill bucket supports batch_size=1 token_count=%d for RocmFused",
+                          prompt_tokens);
+}
+
+zr_status zrh_fast_path_stage_prefill_positions(const zrh_fast_path_plan* plan, uint64_t absolute_position_start,
+                                                int token_count, uint32_t* positions) {
+    if (!plan || !positions || token_count < 0) return set_global_err(ZR_E_INVALID, "null argument or negative count");
+    if (plan->phase != 1)
+        return set_global_err(ZR_E_INVALID, "prefill workspace checkout requires prefill plan, got Decode");
+    if (token_count > plan->token_ceiling)
+        return set_global_err(ZR_E_INVALID,
+                              "fast-path capture invariant failed for prefill-t%d-rocm: prefill token count %d exceeds "
+                              "bucket ceiling %d",
+                              plan->token_ceiling, token_count, plan->token_ceiling);
+    std::fill(positions, positions + plan->token_ceiling, 0u);  // PrefillWorkspaceBuffers::reset
+    for (int i = 0; i < token_count; ++i) {
+        const uint64_t p = absolute_position_start + (uint64_t)i;
+        if (p < absolute_position_start || p > 0xFFFFFFFFull)
+            return set_global_err(ZR_E_INVALID, "prefill absolute position exceeded u32 addressable range");
+        positions[i] = (uint32_t)p;
     }
-    out->metadata_bytes = off;
-    // workspace_requirements: the fused profile's 96 B per token and 32 KiB per slot
-    out->workspace_bytes = off + (size_t)bt * 96 + (size_t)bb * 32 * 1024;
-    out->workspace_alignment = 256;
-    snprintf(out->bucket_label, sizeof out->bucket_label, "decode-b%d-kv%d-rocm", bb, bt);
+    return ZR_OK;
+}
+
+zr_status zrh_fast_path_validate_decode_contexts(const zrh_fast_path_plan* plan,
+                                                 const zrh_fast_path_backend_context* contexts, int n) {
+    if (!plan || (n > 0 && !contexts) || n < 0) return set_global_err(ZR_E_INVALID, "null argument");
+    const char* label = plan->bucket_label;
+    auto unsafe = [&](const char* fmt, auto... args) {
+        char detail[256];
+        snprintf(detail, sizeof detail, fmt, args...);
+        return set_global_err(ZR_E_INVALID, "fast-path capture invariant failed for %s: %s", label, detail);
+    };
+    if (n != plan->actual_batch_size)
+        return unsafe("planned batch size %d but executor received %d requests", plan->actual_batch_size, n);
+    if (n == 0) return ZR_OK;
+    auto is_plan_kind = [](const zrh_fast_path_backend_context& c) {
+        return c.provider && c.optimization_profile && strcmp(c.provider, "rocm") == 0 &&
+               strcmp(c.optimization_profile, "rocm_fused") == 0;
+    };
+    if (!is_plan_kind(contexts[0])) return unsafe("%s", "primary backend context does not match planned provider/profile");
+    const char* primary_model = contexts[0].model_id;
+    for (int i = 0; i < n; ++i) {
+        const zrh_fast_path_backend_context& c = contexts[i];
+        if (!is_plan_kind(c))
+            return unsafe("%s", "mixed provider/profile contexts cannot reuse a single fast-path bucket");
+        if (c.logical_kv_tokens > plan->token_ceiling)
+            return unsafe("session KV footprint %d exceeds bucket token ceiling %d", c.logical_kv_tokens,
+                          plan->token_ceiling);
+        if (primary_model && c.model_id && strcmp(primary_model, c.model_id) != 0)
+            return unsafe("%s", "mixed model residencies cannot share one replay-valid bucket");
+    }
+    const uint64_t observed = plan_layout_hash(plan);
+    if (observed != plan->layout_hash)
+        return set_global_err(ZR_E_INVALID, "fast-path metadata drift for %s: expected layout hash %llu, observed %llu",
+                              label, (unsigned long long)plan->layout_hash, (unsigned long long)observed);
     return ZR_OK;
 }
 

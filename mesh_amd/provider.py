@@ -71,14 +71,44 @@ def executor_contract() -> dict:
 
 
 class FastPathPlanner:
-    """FastPathPlanner (fast_path.rs:604-890) for the rocm_fused profile and the
-    DecodeWorkspaceLease staging (263-338), through the C-ABI."""
+    """FastPathPlanner (fast_path.rs:604-890) for the rocm_fused profile, the
+    DecodeWorkspaceLease staging (263-338) and PrefillWorkspaceLease
+    positions (409-445), through the C-ABI."""
 
     @staticmethod
     def plan_decode(batch_size: int, total_kv_tokens: int, max_sequence_len: int) -> "_lib.FastPathPlan":
         plan = _lib.FastPathPlan()
         check(_lib.load().zrh_fast_path_plan_decode(batch_size, total_kv_tokens, max_sequence_len, C.byref(plan)))
         return plan
+
+    @staticmethod
+    def plan_prefill(prompt_tokens: int) -> "_lib.FastPathPlan":
+        """plan_prefill (680-702): SingleSequenceBuckets over 128 ... 16384 tokens."""
+        plan = _lib.FastPathPlan()
+        check(_lib.load().zrh_fast_path_plan_prefill(prompt_tokens, C.byref(plan)))
+        return plan
+
+    @staticmethod
+    def stage_prefill_positions(plan, absolute_position_start: int, token_count: int) -> np.ndarray:
+        """PrefillWorkspaceLease::stage_positions (409-445): the staged
+        positions (token_count words of the lease's token_ceiling)."""
+        out = np.zeros(max(plan.token_ceiling, 1), np.uint32)
+        check(_lib.load().zrh_fast_path_stage_prefill_positions(C.byref(plan), absolute_position_start, token_count,
+                                                                _ptr(out, C.c_uint32)))
+        return out[:token_count]
+
+    @staticmethod
+    def validate_decode_contexts(plan, contexts: Sequence[dict]) -> None:
+        """validate_decode_contexts (704-778) over FastPathBackendContext dicts
+        (provider, optimization_profile, model_id, logical_kv_tokens)."""
+        arr = (_lib.FastPathBackendContext * max(len(contexts), 1))()
+        keep = []
+        for i, c in enumerate(contexts):
+            enc = [None if c.get(k) is None else str(c[k]).encode() for k in
+                   ("provider", "optimization_profile", "model_id")]
+            keep.append(enc)
+            arr[i] = _lib.FastPathBackendContext(enc[0], enc[1], enc[2], int(c["logical_kv_tokens"]))
+        check(_lib.load().zrh_fast_path_validate_decode_contexts(C.byref(plan), arr, len(contexts)))
 
     @staticmethod
     def stage_decode(plan, backends: Sequence["RocmExecutionBackend"], tokens: Sequence[int]) -> dict:
@@ -274,9 +304,10 @@ class DeviceContext:
 
     def __init__(self, geo: ModelGeometry, *, kv_dtype: str = "bf16", max_tokens: int = 256,
                  max_seqs: int = 256, max_pages_per_seq: int = 512, split_activations: bool = False,
-                 device: int = 0):
+                 device: int = 0, model_id: Optional[str] = None):
         self.lib = _lib.load()
         self.geo = geo
+        self.model_id = model_id  # SharedModelResidency's model id (FastPathBackendContext.model_id)
         d = _lib.ModelDesc()
         d.hidden, d.num_heads, d.num_kv_heads = geo.hidden, geo.num_heads, geo.num_kv_heads
         d.num_layers, d.vocab, d.ffn_cols = geo.num_layers, geo.vocab, geo.ffn_cols
@@ -481,7 +512,7 @@ class RocmExecutionBackend:
         c = _lib.FastPathContext()
         self.ctx.check(self.lib.zrh_get_fast_path_context(self.h, C.byref(c)))
         return {"provider": ExecutionProviderKind.ROCM.value, "optimization_profile": self.optimization_profile,
-                "logical_kv_tokens": c.logical_kv_tokens, "position": c.position,
+                "model_id": self.ctx.model_id, "logical_kv_tokens": c.logical_kv_tokens, "position": c.position,
                 "cached_tokens": c.cached_tokens,
                 "decode_token_ceiling": None if c.decode_token_ceiling < 0 else c.decode_token_ceiling}
 
@@ -689,9 +720,13 @@ def _backend_array(backends):
 class BackendMicrobatchExecutor:
     @staticmethod
     def decode_step_batch(requests: List[DecodeMicrobatchRequest], want_logits: bool = False,
-                          partials: Optional[np.ndarray] = None) -> List[DecodeMicrobatchOutput]:
+                          partials: Optional[np.ndarray] = None, plan=None) -> List[DecodeMicrobatchOutput]:
         """backend.rs:110-151 fast path: one fused microbatch over every session.
+        A `plan` (FastPathPlanner.plan_decode) is validated against the
+        requests' backend contexts first (validate_decode_contexts, 116-123).
         Greedy requests get `sampled_token` from the device argmax (backend.rs:537-553)."""
+        if plan is not None:
+            FastPathPlanner.validate_decode_contexts(plan, [r.backend.fast_path_context() for r in requests])
         if not requests:
             raise ZrError(-1, "Decode microbatch requires at least one backend and token")
         ctx = requests[0].backend.ctx

@@ -463,6 +463,60 @@ DECODE_BUCKET_KV_TOKENS = (2048, 8192, 16384, 32768, 65536)  # fast_path.rs:16
 U32_MAX = 0xFFFFFFFF
 
 
+PREFILL_BUCKET_TOKENS = (128, 512, 2048, 8192, 16384)        # fast_path.rs:17
+
+
+def fast_path_layout_hash(phase, batch_size_ceiling, token_ceiling, fields):
+    """The layout hash of a bucket key (phase 0 decode / 1 prefill, provider
+    rocm, profile rocm_fused, both ceilings) and its metadata fields, hashed
+    in the order of FastPathPlanner::layout_hash (fast_path.rs:892-902).  The
+    reference's hasher (Rust's DefaultHasher) is process-local; the library
+    uses FNV-1a 64 over the same items (integers as 8 little-endian bytes,
+    names as their bytes then 0xff), restated here."""
+    h = 0xcbf29ce484222325
+
+    def byte(b):
+        nonlocal h
+        h = ((h ^ b) * 0x100000001b3) & 0xFFFFFFFFFFFFFFFF
+
+    def u64(v):
+        for i in range(8):
+            byte((v >> (8 * i)) & 0xFF)
+
+    def name(s):
+        for c in s.encode():
+            byte(c)
+        byte(0xFF)
+
+    u64(phase)
+    name("rocm")
+    name("rocm_fused")
+    u64(batch_size_ceiling)
+    u64(token_ceiling)
+    for field, count, stride in fields:
+        name(field)
+        u64(4)
+        u64(count)
+        u64(stride)
+    return h
+
+
+def _fast_path_plan(phase, b, t, actual_batch, actual_tokens):
+    """FastPathPlanner::build_plan (fast_path.rs:780-829) for the rocm_fused
+    profile: metadata_fields (839-867), capture_strategy (831-837: the fused
+    profile replays), the prefill strategy of plan_prefill (697)."""
+    slots = -(-t // 16)
+    fields = [(name, n, 4 * n) for name, n in (("slot_sequence_lengths", b), ("slot_positions", b),
+                                               ("slot_block_tables", b * slots), ("slot_mapping", b))]
+    label = f"decode-b{b}-kv{t}-rocm" if phase == 0 else f"prefill-t{t}-rocm"
+    return dict(phase=phase, batch_size_ceiling=b, token_ceiling=t, page_slots=slots, fields=fields,
+                bucket_label=label, actual_batch_size=actual_batch, actual_token_count=actual_tokens,
+                capture_strategy="replay_preferred",
+                prefill_strategy="single_sequence_buckets" if phase == 1 else "",
+                workspace_bytes=sum(f[2] for f in fields) + 96 * t + 32 * 1024 * b,
+                layout_hash=fast_path_layout_hash(phase, b, t, fields))
+
+
 def fast_path_plan_decode(batch_size, total_kv_tokens, profile="RocmFused"):
     """FastPathPlanner::plan_decode (fast_path.rs:644-669): the first bucket of
     supported_decode_buckets (batch outer, kv tokens inner; 606-623) holding
@@ -471,14 +525,69 @@ def fast_path_plan_decode(batch_size, total_kv_tokens, profile="RocmFused"):
     for b in DECODE_BUCKET_BATCHES:
         for t in DECODE_BUCKET_KV_TOKENS:
             if batch_size <= b and total_kv_tokens <= t:
-                slots = -(-t // 16)
-                fields = [("slot_sequence_lengths", b), ("slot_positions", b), ("slot_block_tables", b * slots),
-                          ("slot_mapping", b)]
-                return dict(batch_size_ceiling=b, token_ceiling=t, page_slots=slots,
-                            fields=[(name, n, 4 * n) for name, n in fields],
-                            bucket_label=f"decode-b{b}-kv{t}-rocm")
+                return _fast_path_plan(0, b, t, batch_size, total_kv_tokens)
     raise OracleError(f"no stable Decode bucket supports batch_size={batch_size} token_count={total_kv_tokens} "
                       f"for {profile}")
+
+
+def fast_path_plan_prefill(prompt_tokens, profile="RocmFused"):
+    """FastPathPlanner::plan_prefill (fast_path.rs:680-702): the first bucket of
+    supported_prefill_buckets (625-642: batch ceiling 1) holding the prompt."""
+    for t in PREFILL_BUCKET_TOKENS:
+        if prompt_tokens <= t:
+            return _fast_path_plan(1, 1, t, 1, prompt_tokens)
+    raise OracleError(f"no stable Prefill bucket supports batch_size=1 token_count={prompt_tokens} for {profile}")
+
+
+def fast_path_stage_prefill_positions(plan, absolute_position_start, token_count):
+    """PrefillWorkspaceLease::stage_positions (fast_path.rs:409-445) after
+    PrefillWorkspaceBuffers::reset (207-210): the lease's positions buffer."""
+    T = plan["token_ceiling"]
+    if token_count > T:
+        raise OracleError(f"fast-path capture invariant failed for prefill-t{T}-rocm: prefill token count "
+                          f"{token_count} exceeds bucket ceiling {T}")
+    out = np.zeros(T, np.uint32)
+    for i in range(token_count):
+        p = absolute_position_start + i
+        if p > U32_MAX:
+            raise OracleError("prefill absolute position exceeded u32 addressable range")
+        out[i] = p
+    return out
+
+
+def fast_path_validate_decode_contexts(plan, contexts):
+    """FastPathPlanner::validate_decode_contexts (fast_path.rs:704-778).
+    contexts: dicts of FastPathBackendContext (provider, optimization_profile,
+    model_id or None, logical_kv_tokens); the plan's bucket is rocm /
+    rocm_fused."""
+    label = plan["bucket_label"]
+
+    def unsafe(detail):
+        return OracleError(f"fast-path capture invariant failed for {label}: {detail}")
+
+    if len(contexts) != plan["actual_batch_size"]:
+        raise unsafe(f"planned batch size {plan['actual_batch_size']} but executor received {len(contexts)} requests")
+    if not contexts:
+        return
+
+    def same_kind(c):
+        return c["provider"] == "rocm" and c["optimization_profile"] == "rocm_fused"
+
+    if not same_kind(contexts[0]):
+        raise unsafe("primary backend context does not match planned provider/profile")
+    primary = contexts[0].get("model_id")
+    for c in contexts:
+        if not same_kind(c):
+            raise unsafe("mixed provider/profile contexts cannot reuse a single fast-path bucket")
+        if c["logical_kv_tokens"] > plan["token_ceiling"]:
+            raise unsafe(f"session KV footprint {c['logical_kv_tokens']} exceeds bucket token ceiling "
+                         f"{plan['token_ceiling']}")
+        if primary is not None and c.get("model_id") is not None and c["model_id"] != primary:
+            raise unsafe("mixed model residencies cannot share one replay-valid bucket")
+    observed = fast_path_layout_hash(plan["phase"], plan["batch_size_ceiling"], plan["token_ceiling"], plan["fields"])
+    if observed != plan["layout_hash"]:
+        raise OracleError(f"fast-path metadata drift for {label}: expected layout hash {plan['layout_hash']}, "
+                          f"observed {observed}")
 
 
 def fast_path_stage_decode(plan, tokens, slots):

@@ -41,6 +41,30 @@ def test_oracle_staging_reproduces_the_reference_known_answers():
         O.fast_path_plan_decode(9, 10)
 
 
+def test_oracle_prefill_plan_positions_and_validation_reproduce_the_reference_known_answers():
+    # decode_plan_selects_smallest_supported_bucket (935-942): the fused profile replays
+    assert O.fast_path_plan_decode(3, 5000)["capture_strategy"] == "replay_preferred"
+    # prefill_plan_uses_explicit_single_sequence_strategy (944-955)
+    plan = O.fast_path_plan_prefill(400)
+    assert plan["phase"] == 1 and plan["batch_size_ceiling"] == 1 and plan["token_ceiling"] == 512
+    assert plan["prefill_strategy"] == "single_sequence_buckets"
+    # prefill_workspace_lease_stages_positions_and_reuses_bucket_pool (1058-1080)
+    assert O.fast_path_stage_prefill_positions(plan, 64, 4)[:4].tolist() == [64, 65, 66, 67]
+    again = O.fast_path_stage_prefill_positions(plan, 128, 3)
+    assert again[:3].tolist() == [128, 129, 130] and not again[3:].any()  # the restage reset the buffer
+    # validate_decode_contexts_rejects_provider_drift (959-972)
+    plan = O.fast_path_plan_decode(1, 1024)
+    cpu = dict(provider="cpu", optimization_profile="cpu_serial", model_id="llama-70b", logical_kv_tokens=1024)
+    with pytest.raises(O.OracleError, match="does not match planned provider/profile"):
+        O.fast_path_validate_decode_contexts(plan, [cpu])
+    # the same context from the plan's own provider passes
+    O.fast_path_validate_decode_contexts(plan, [dict(cpu, provider="rocm", optimization_profile="rocm_fused")])
+    # a changed field no longer hashes to the plan's layout hash
+    bad = dict(plan, fields=[plan["fields"][0], plan["fields"][1], ("slot_block_tables", 1, 4), plan["fields"][3]])
+    with pytest.raises(O.OracleError, match="fast-path metadata drift for decode-b1-kv2048-rocm"):
+        O.fast_path_validate_decode_contexts(bad, [dict(cpu, provider="rocm", optimization_profile="rocm_fused")])
+
+
 # ----------------------------------------------------------- the planner --
 @pytest.mark.parametrize("batch,tokens", [(1, 0), (1, 2048), (1, 2049), (3, 5000), (4, 8192), (5, 100),
                                           (8, 65536), (2, 16385)])
@@ -68,6 +92,108 @@ def test_plan_decode_rejects_batches_no_bucket_holds(batch, tokens):
     with pytest.raises(O.OracleError) as w:
         O.fast_path_plan_decode(batch, tokens)
     assert str(e.value).endswith(str(w.value))
+
+
+@pytest.mark.parametrize("tokens", [0, 1, 128, 129, 400, 512, 2049, 8192, 16384])
+def test_plan_prefill_matches_the_oracle(tokens):
+    plan = FastPathPlanner.plan_prefill(tokens)
+    want = O.fast_path_plan_prefill(tokens)
+    assert (plan.phase, plan.batch_size_ceiling, plan.token_ceiling, plan.page_slots) == (
+        want["phase"], want["batch_size_ceiling"], want["token_ceiling"], want["page_slots"])
+    assert (plan.actual_batch_size, plan.actual_token_count, plan.max_sequence_len) == (1, tokens, tokens)
+    assert plan.bucket_label.decode() == want["bucket_label"]
+    assert plan.capture_strategy.decode() == "replay_preferred"
+    assert plan.prefill_strategy.decode() == "single_sequence_buckets"
+    assert [plan.field_bytes[f] for f in range(4)] == [stride for _, _, stride in want["fields"]]
+    assert plan.workspace_bytes == want["workspace_bytes"] and plan.layout_hash == want["layout_hash"]
+
+
+def test_plan_decode_carries_capture_strategy_and_layout_hash():
+    for batch, tokens in ((1, 0), (3, 5000), (8, 65536)):
+        plan = FastPathPlanner.plan_decode(batch, tokens, 2048)
+        want = O.fast_path_plan_decode(batch, tokens)
+        assert plan.phase == 0 and plan.capture_strategy.decode() == "replay_preferred"
+        assert plan.prefill_strategy.decode() == "" and plan.layout_hash == want["layout_hash"]
+    hashes = {FastPathPlanner.plan_decode(b, t, 1).layout_hash for b in O.DECODE_BUCKET_BATCHES
+              for t in O.DECODE_BUCKET_KV_TOKENS}
+    hashes |= {FastPathPlanner.plan_prefill(t).layout_hash for t in O.PREFILL_BUCKET_TOKENS}
+    assert len(hashes) == 25  # every bucket has its own layout
+
+
+def test_plan_prefill_rejects_prompts_no_bucket_holds():
+    with pytest.raises(_lib.ZrError) as e:
+        FastPathPlanner.plan_prefill(16385)
+    with pytest.raises(O.OracleError) as w:
+        O.fast_path_plan_prefill(16385)
+    assert str(e.value).endswith(str(w.value))
+    assert "no stable Prefill bucket supports batch_size=1 token_count=16385 for RocmFused" in str(e.value)
+
+
+@pytest.mark.parametrize("start,count", [(64, 4), (128, 3), (0, 0), (0, 512), (4095, 400),
+                                         (0xFFFFFFFF - 3, 4)])
+def test_stage_prefill_positions_matches_the_oracle(start, count):
+    plan = FastPathPlanner.plan_prefill(400)
+    got = FastPathPlanner.stage_prefill_positions(plan, start, count)
+    want = O.fast_path_stage_prefill_positions(O.fast_path_plan_prefill(400), start, count)
+    np.testing.assert_array_equal(got, want[:count])
+
+
+def test_stage_prefill_positions_errors_carry_the_reference_text():
+    plan = FastPathPlanner.plan_prefill(400)
+    for start, count in ((0, 513), (0xFFFFFFFF - 2, 4)):
+        with pytest.raises(_lib.ZrError) as e:
+            FastPathPlanner.stage_prefill_positions(plan, start, count)
+        with pytest.raises(O.OracleError) as w:
+            O.fast_path_stage_prefill_positions(O.fast_path_plan_prefill(400), start, count)
+        assert str(e.value).endswith(str(w.value))
+    with pytest.raises(_lib.ZrError, match="requires prefill plan"):
+        FastPathPlanner.stage_prefill_positions(FastPathPlanner.plan_decode(1, 10, 10), 0, 1)
+
+
+def _ctx(provider="rocm", profile="rocm_fused", model="llama-3-8b", tokens=1024):
+    return dict(provider=provider, optimization_profile=profile, model_id=model, logical_kv_tokens=tokens)
+
+
+@pytest.mark.parametrize("case", ["ok", "count", "primary", "mixed", "footprint", "model", "model_none", "empty"])
+def test_validate_decode_contexts_matches_the_oracle(case):
+    batch = 0 if case == "empty" else 3
+    plan = FastPathPlanner.plan_decode(batch, 5000, 2048)
+    want_plan = O.fast_path_plan_decode(batch, 5000)
+    ctxs = [_ctx(), _ctx(tokens=7000), _ctx(tokens=10)]
+    if case == "count":
+        ctxs = ctxs[:2]
+    elif case == "primary":
+        ctxs[0] = _ctx("cpu", "cpu_serial")
+    elif case == "mixed":
+        ctxs[2] = _ctx("cuda", "cuda_fused")
+    elif case == "footprint":
+        ctxs[1] = _ctx(tokens=8193)
+    elif case == "model":
+        ctxs[2] = _ctx(model="llama-70b")
+    elif case == "model_none":
+        ctxs[1] = _ctx(model=None)  # a backend without a model id shares any residency
+    elif case == "empty":
+        ctxs = []
+    if case in ("ok", "model_none", "empty"):
+        FastPathPlanner.validate_decode_contexts(plan, ctxs)
+        O.fast_path_validate_decode_contexts(want_plan, ctxs)
+        return
+    with pytest.raises(_lib.ZrError) as e:
+        FastPathPlanner.validate_decode_contexts(plan, ctxs)
+    with pytest.raises(O.OracleError) as w:
+        O.fast_path_validate_decode_contexts(want_plan, ctxs)
+    assert str(e.value).endswith(str(w.value))
+    assert "fast-path capture invariant failed for decode-b4-kv8192-rocm: " in str(e.value)
+
+
+def test_validate_decode_contexts_detects_metadata_drift():
+    plan = FastPathPlanner.plan_decode(1, 100, 100)
+    ctxs = [_ctx(tokens=100)]
+    FastPathPlanner.validate_decode_contexts(plan, ctxs)
+    plan.field_bytes[2] += 4  # a slot table one entry longer than the bucket's layout
+    with pytest.raises(_lib.ZrError, match=f"fast-path metadata drift for decode-b1-kv2048-rocm: expected layout "
+                                           f"hash {plan.layout_hash}, observed "):
+        FastPathPlanner.validate_decode_contexts(plan, ctxs)
 
 
 # ------------------------------------------------------------ the staging --
@@ -165,6 +291,8 @@ def test_executor_contract_is_the_rocm_arm_and_names_real_kernels():
     assert c["collective_residency"] == "staged_runtime" and c["collective_tensors_per_layer"] == 2
     assert c["decode_supports_microbatch"] and c["decode_uses_device_sampling"] and c["kv_requires_paged_cache"]
     assert c["supports_device_sampling"] and c["supports_checkpoint_handoff"] and c["fast_path_eligible"]
+    # FastPathPlanner::capture_strategy (fast_path.rs:831-837), as the CudaFused arm
+    assert c["capture_strategy"] == "replay_preferred"
     src = "".join(open(f).read() for f in glob.glob(os.path.join(ROOT, "mesh_amd", "csrc", "*.hip")))
     defined = set(re.findall(r"__global__\s+(?:__launch_bounds__\([^)]*\)\s*)?void\s+(\w+)\s*\(", src))
     for stage, kernels in c["stage_kernels"].items():
