@@ -8,16 +8,17 @@ TinyLlama-shape step (22 layers, contexts U[128, 2048]) is measured in the same
 run and reported under "bs32".
 
 Inputs are resident in HBM before the timed region: weights are random-init
-bf16 N(0, 0.02) generated on the device, the KV pages of every session's
-context are filled with N(0, 1) bf16 (standing in for prefill output), and the
-per-step metadata (page tables after each step's append) is staged on the
-device ahead of time.  Each step feeds its greedy tokens to the next step on
-the device.  Each timed step is replayed from a HIP graph of its staged launch
-sequence, captured before the timing (the fused profile's ReplayPreferred
-strategy); as many further steps launched kernel by kernel are reported as
-"eager".  The attention kernel's duration (the roofline) comes from HIP events
-recorded on the provider's stream around every attention launch of the eager
-steps (events recorded by graph nodes do not time).
+bf16 N(0, 0.02) generated on the device and the KV pages of every session's
+context are filled with N(0, 1) bf16 (standing in for prefill output).  The
+timed region is the serving loop (zrh_decode_pipeline): every step does its
+host page-table work, stages its metadata, copies it to the device, replays
+the bucket's captured step graph (the fused profile's ReplayPreferred
+strategy, one capture per bucket, before the timing) and copies its greedy ids
+back, which the host reads while the next step runs; the ids are fed to the
+next step on the device.  The attention kernel's duration (the roofline)
+comes from HIP events recorded on the provider's stream around every
+attention launch of as many pre-staged steps launched kernel by kernel
+("eager"; events recorded by graph nodes do not time).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--skip-bs32] [--skip-soak]
        python bench.py --calibrate-copy   (a plain 1 GiB device copy, for scaling
@@ -255,30 +256,30 @@ class GpuDecodeBench:
             toks, out = out, toks
         return time.perf_counter() - t0, toks
 
-    def run_graphs(self, first, count):
-        """Runs staged steps [first, first + count), each replayed from a HIP
-        graph of its launch sequence (zr_graph_capture_staged), the way the
-        fused profile executes a step (ReplayPreferred).  The graphs are
-        captured before the timing and the first is replayed once untimed.
-        Returns seconds."""
-        ctx, lib = self.ctx, self.ctx.lib
-        graphs = []
+    def run_pipeline(self, warmup, count, tokens):
+        """The serving loop (zrh_decode_pipeline through mesh_amd.DecodePipeline):
+        every step does its host page-table work (window trim, page
+        reservation), stages its metadata into pinned memory, copies it to the
+        device on a copy stream, replays the bucket's captured step graph and
+        copies its greedy ids back; the host reads each step's ids while the
+        next step runs.  `warmup` steps (the bucket's captures among them),
+        then `count` timed steps, synchronised on both sides.  Returns
+        (seconds, last ids, pipeline info)."""
+        from mesh_amd import DecodePipeline
+
+        pipe = DecodePipeline(self.backends, tokens)
         try:
-            for i in range(first, first + count):
-                gph = C.c_void_p()
-                ctx.check(lib.zr_graph_capture_staged(ctx.h, self.staged[i], self.tok[i % 2], self.tok[(i + 1) % 2],
-                                                      None, C.byref(gph)))
-                graphs.append(gph)
-            ctx.check(lib.zr_graph_launch(ctx.h, graphs[0]))
-            ctx.check(lib.zr_synchronize(ctx.h))
+            for _ in range(warmup):
+                pipe.step()
+            pipe.finish()
             t0 = time.perf_counter()
-            for gph in graphs:
-                ctx.check(lib.zr_graph_launch(ctx.h, gph))
-            ctx.check(lib.zr_synchronize(ctx.h))
-            return time.perf_counter() - t0
+            for _ in range(count):
+                pipe.step()
+            last = pipe.finish()
+            dt = time.perf_counter() - t0
+            return dt, last, pipe.info()
         finally:
-            for gph in graphs:
-                lib.zr_graph_destroy(gph)
+            pipe.close()
 
     def tokens(self, i):
         out = np.zeros(self.B, np.uint32)
@@ -304,30 +305,33 @@ BREAKDOWN_STEPS = 2
 
 
 def measure(name, steps, warmup, kv_dtype="bf16"):
-    """Timed region: `steps` decode steps, each replayed from the HIP graph of
-    its staged launch sequence.  Then `steps` more steps launched kernel by
+    """Pre-staged steps first: `warmup` untimed, `steps` launched kernel by
     kernel (zr_forward_staged_async) with HIP events around the attention
-    launches only (the roofline figure: events recorded by graph nodes do not
-    time), then BREAKDOWN_STEPS with events around every kernel class, for the
-    per-class time split.  Then the same sessions decode `warmup` + `steps`
-    more steps through the host entry point (zrh_decode_step_batch), timed
-    end to end with the host work."""
-    bench = GpuDecodeBench(name, warmup + 2 * steps + BREAKDOWN_STEPS, host_steps=steps + warmup, kv_dtype=kv_dtype)
+    launches only (the roofline figure), then BREAKDOWN_STEPS with events
+    around every kernel class, for the per-class time split.  Then the timed
+    region, the headline: `steps` decode steps of the same sessions through the
+    pipelined serving loop (GpuDecodeBench.run_pipeline: host page tables,
+    metadata staging and copy, the replayed step graph and the id copy-back of
+    every step inside the timing), after `warmup` untimed ones.  Then as many
+    steps through the synchronous host entry point (zrh_decode_step_batch),
+    timed end to end."""
+    bench = GpuDecodeBench(name, warmup + steps + BREAKDOWN_STEPS, host_steps=2 * (steps + warmup), kv_dtype=kv_dtype)
     g, B = bench.geo, bench.B
     kv_size = 2 if kv_dtype == "bf16" else 4
     bench.run(0, warmup, timed=False)
-    dt = bench.run_graphs(warmup, steps)
-    toks = bench.tokens(warmup + steps)
-    assert toks.max() < g.vocab
-    dt_eager, ms_t, n_t = bench.run(warmup + steps, steps, timed=True, mask=1)
-    assert bench.tokens(warmup + 2 * steps).max() < g.vocab
-    _, ms_b, n_b = bench.run(warmup + 2 * steps, BREAKDOWN_STEPS, timed=True, mask=0xF)
+    dt_eager, ms_t, n_t = bench.run(warmup, steps, timed=True, mask=1)
+    assert bench.tokens(warmup + steps).max() < g.vocab
+    _, ms_b, n_b = bench.run(warmup + steps, BREAKDOWN_STEPS, timed=True, mask=0xF)
+    cached = [b.cache_seq_len() for b in bench.backends]
+    dt, last, pinfo = bench.run_pipeline(warmup, steps, bench.tokens(warmup + steps + BREAKDOWN_STEPS))
+    assert last.max() < g.vocab
     ms_per_step = dt / steps * 1000.0
     # attention: algorithmic bytes per launch (K+V of every attended row in the
     # pool's dtype; Q in and the output out, f32), averaged over the eager
     # steps' launches
-    timed_rows = bench.kv_rows[warmup:warmup + steps]
-    eager_rows = bench.kv_rows[warmup + steps:warmup + 2 * steps]
+    # rows the pipeline's timed steps attend (every window capped at max_seq_len)
+    timed_rows = [sum(min(c + warmup + k + 1, bench.max_seq) for c in cached) for k in range(steps)]
+    eager_rows = bench.kv_rows[warmup:warmup + steps]
     kv_bytes = sum(eager_rows) * g.num_layers * g.kv_cols * 2 * kv_size
     qo_bytes = steps * g.num_layers * B * g.q_cols * 4 * 2
     attn_launches = n_t[0]
@@ -352,13 +356,21 @@ def measure(name, steps, warmup, kv_dtype="bf16"):
                   frac=gemm_tflops / MFMA_BF16_PEAK_TFLOPS,
                   weight_gbs=(gemm_flops(g, B) / B) * nb / (ms_b[1] * 1e-3) / 1e9 if ms_b[1] > 0 else 0.0),
     )
+    result["pipeline"] = dict(entry="zrh_decode_pipeline_step", steps=steps, captures=pinfo["captures"],
+                              buckets=pinfo["buckets"], attention_items_capacity=pinfo["items_capacity"],
+                              metadata_bytes_per_step=pinfo["metadata_bytes"],
+                              includes="per step: host page tables and window trim, attention work list and "
+                                       "metadata staged into pinned memory, its H2D copy on a copy stream, "
+                                       "pack_kernel + rope_table_kernel and the forward pass replayed from the "
+                                       "bucket's captured graph, greedy ids copied back and read by the host "
+                                       "(one step behind)")
     result["eager"] = dict(entry="zr_forward_staged_async", steps=steps, ms_per_step=dt_eager / steps * 1e3,
                            tokens_per_s=B * steps / dt_eager,
-                           includes="the same decode step launched kernel by kernel instead of replayed, "
-                                    "HIP events around its attention launches")
+                           includes="pre-staged steps launched kernel by kernel (metadata staged before the "
+                                    "timing), HIP events around their attention launches")
     result["kv_append"] = measure_kv_append(bench, kv_size)
-    # end to end through the boundary's host entry point, host work included
-    _, last = bench.run_host(warmup, bench.tokens(warmup + steps + BREAKDOWN_STEPS))
+    # end to end through the boundary's synchronous host entry point
+    _, last = bench.run_host(warmup, last)
     dt_host, last = bench.run_host(steps, last)
     assert last.max() < g.vocab
     result["host_path"] = dict(
@@ -838,7 +850,7 @@ def main():
                     workload=r["workload"], step_roofline_frac=r["step_roofline_frac"],
                     attention_gbs=r["attention"]["achieved_gbs"], kernel_ms_per_step=r["kernel_ms_per_step"],
                     gemm_tflops=r["gemm"]["achieved_tflops"], gemm_weight_gbs=r["gemm"]["weight_gbs"],
-                    host_path=r["host_path"], eager=r["eager"])
+                    host_path=r["host_path"], eager=r["eager"], pipeline=r["pipeline"])
     tp_shard = None
     if not a.skip_tp_shard and a.workload != "llama3_8b_tp2_b64":
         r = measure("llama3_8b_tp2_b64", max(4, a.steps // 2), 2)
@@ -875,8 +887,10 @@ def main():
         "config": {"workload": main_r["workload"], "sessions": main_r["batch"], "layers": main_r["layers"],
                    "context_tokens": main_r["context_tokens"], "context_max": main_r["context_max"],
                    "parallelism": "one worker shard (1 of 1) on one GPU",
-                   "step_launch": "each step replayed from a HIP graph of its staged launch sequence "
-                                  "(zr_graph_launch); kernel-by-kernel launch under eager",
+                   "step_launch": "serving loop: each step staged (host page tables, metadata H2D) and "
+                                  "replayed from the bucket's captured step graph, ids copied back "
+                                  "(zrh_decode_pipeline_step); kernel-by-kernel launch of pre-staged steps "
+                                  "under eager",
                    "gemm_a_operand": "bf16 hi + lo pair (activation = hi + lo to 2^-16), fp32 accumulation"},
         "roofline": {"bound": "hbm", "kernel": "paged_attention_kernel", "achieved": att["achieved_gbs"],
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": att["frac"], "traffic": measured_traffic(),
@@ -885,6 +899,7 @@ def main():
         "step_roofline": {"tokens_per_s": main_r["step_roofline_tokens_per_s"], "frac": main_r["step_roofline_frac"],
                           "bytes_per_step": main_r["step_bytes"]},
         "kernel_ms_per_step": main_r["kernel_ms_per_step"],
+        "pipeline": main_r["pipeline"],
         "host_path": main_r["host_path"],
         "eager": main_r["eager"],
         "kv_append": main_r["kv_append"],

@@ -183,6 +183,37 @@ zr_status zr_graph_capture_staged(zr_context* ctx, zr_staged* st, const uint32_t
 zr_status zr_graph_launch(zr_context* ctx, zr_graph* g);
 void zr_graph_destroy(zr_graph* g);
 
+/* A decode step replayed across steps: the fused profile's ReplayPreferred
+ * capture (fast_path.rs:831-837) over a bucket workspace that is re-staged
+ * every step (DecodeWorkspaceLease, fast_path.rs:263-338, 542-571).  One HIP
+ * graph (the pack stage and the forward pass) is captured per bucket -- the
+ * sequence count and room for the step's attention work list -- and replayed
+ * for every later step that fits it, each launch carrying that step's
+ * metadata.  A launch stages the microbatch into a pinned host buffer, copies
+ * it into the graph's own device buffers on a copy stream of its own, replays
+ * the graph on the context stream and, with h_out_tokens (pinned host memory,
+ * nullable), copies the step's greedy ids back.  Two buffer sets alternate, so
+ * the host staging of the next step overlaps this one on the device; nothing
+ * is allocated per step and no graph holds a memset.  Only decode microbatches
+ * of one row per sequence (MFMA page layout); a microbatch that outgrows its
+ * bucket gets a new one (synchronously).  d_tokens / d_out_tokens: device
+ * [num_seqs] ids in and out (a captured graph per pair; the ids are checked
+ * as in zr_forward_staged_async, at the next zr_synchronize).  The outputs
+ * are ready after zr_synchronize (or an event the caller records on the
+ * stream).  Not with per-class timing on. */
+typedef struct zr_step_graph zr_step_graph;
+typedef struct {
+    uint64_t launches;
+    int captures, buckets, sequences;
+    int items_capacity, merge_capacity, fused_rope;
+    size_t metadata_bytes;   /* staged per step (H2D) */
+} zr_step_graph_stats;
+zr_status zr_step_graph_create(zr_context* ctx, zr_step_graph** out);
+zr_status zr_step_graph_launch(zr_step_graph* g, const zr_microbatch* mb, const uint32_t* d_tokens,
+                               uint32_t* d_out_tokens, uint32_t* h_out_tokens);
+zr_status zr_step_graph_info(const zr_step_graph* g, zr_step_graph_stats* out);
+void zr_step_graph_destroy(zr_step_graph* g);
+
 /* ------------------------------------------------------ op-level entries --- */
 /* Ragged packing on the GPU: device outputs cu_q/cu_k [num_seqs+1],
  * positions/slot_mapping/seq_ids [sum q_len] (host arrays, copied back). */

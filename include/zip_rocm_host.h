@@ -214,6 +214,28 @@ zr_status zrh_fast_path_stage_decode(const zrh_fast_path_plan* plan, zrh_backend
                                      const uint32_t* tokens, uint32_t* metadata, uint32_t* token_ids,
                                      uint32_t* positions);
 
+/* ---------------------------------------------------- decode pipeline --- */
+/* The serving loop of BackendMicrobatchExecutor::decode_step_batch
+ * (backend.rs:110-151) over a fixed set of n sessions, pipelined.  Each
+ * zrh_decode_pipeline_step does the step's host bookkeeping (window trim and
+ * page reservation per session, as zrh_decode_step_batch), launches it through
+ * a zr_step_graph (one captured graph per bucket, replayed with the step's
+ * metadata) and returns the greedy ids of the previous step, waiting for that
+ * step only: the host work of step k + 1 overlaps step k on the device.  Ids
+ * stay on the device between steps: step 0 reads first_tokens, step k the ids
+ * of step k - 1.  Positions advance as each step is enqueued.  A step that
+ * fails to enqueue leaves its sessions as they were (steps already enqueued
+ * run).  zrh_decode_pipeline_finish waits for the last step and returns its
+ * ids.  The sessions must not be used elsewhere while the pipeline lives. */
+typedef struct zrh_decode_pipeline zrh_decode_pipeline;
+zr_status zrh_decode_pipeline_create(zrh_backend* const* backends, int n, const uint32_t* first_tokens,
+                                     zrh_decode_pipeline** out);
+/* prev_tokens [n] (nullable) receives the previous step's ids when *prev_ready = 1. */
+zr_status zrh_decode_pipeline_step(zrh_decode_pipeline* p, uint32_t* prev_tokens, int* prev_ready);
+zr_status zrh_decode_pipeline_finish(zrh_decode_pipeline* p, uint32_t* last_tokens);
+zr_status zrh_decode_pipeline_info(const zrh_decode_pipeline* p, uint64_t* steps, zr_step_graph_stats* graph);
+void zrh_decode_pipeline_destroy(zrh_decode_pipeline* p);
+
 /* Page-table state machine without compute, for allocator checks:
  * DeviceKVCache::append_layer over all layers (rows appended, window trim
  * included) and DeviceKVCache::retain_suffix. */

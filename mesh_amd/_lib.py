@@ -62,6 +62,12 @@ class Microbatch(C.Structure):
                 ("block_table_stride", C.c_int), ("tokens", c_u32_p)]
 
 
+class StepGraphStats(C.Structure):
+    _fields_ = [("launches", C.c_uint64), ("captures", C.c_int), ("buckets", C.c_int), ("sequences", C.c_int),
+                ("items_capacity", C.c_int), ("merge_capacity", C.c_int), ("fused_rope", C.c_int),
+                ("metadata_bytes", C.c_size_t)]
+
+
 class ExecutorContract(C.Structure):
     _fields_ = [("executor_class", C.c_char_p), ("optimization_profile", C.c_char_p),
                 ("n_host_kernels", C.c_int), ("host_kernels", C.POINTER(C.c_char_p)),
@@ -120,6 +126,10 @@ SIGNATURES = [
     ("zr_graph_capture_staged", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, c_void_pp]),
     ("zr_graph_launch", C.c_int, [C.c_void_p, C.c_void_p]),
     ("zr_graph_destroy", None, [C.c_void_p]),
+    ("zr_step_graph_create", C.c_int, [C.c_void_p, c_void_pp]),
+    ("zr_step_graph_launch", C.c_int, [C.c_void_p, C.POINTER(Microbatch), C.c_void_p, C.c_void_p, C.c_void_p]),
+    ("zr_step_graph_info", C.c_int, [C.c_void_p, C.POINTER(StepGraphStats)]),
+    ("zr_step_graph_destroy", None, [C.c_void_p]),
     ("zr_pack", C.c_int, [C.c_void_p, C.POINTER(Microbatch), c_int_p, c_int_p, c_int_p, c_int_p, c_int_p]),
     ("zr_rope_kv_write", C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int]),
     ("zr_attention", C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]),
@@ -192,6 +202,11 @@ SIGNATURES = [
     ("zrh_fast_path_stage_prefill_positions", C.c_int, [C.POINTER(FastPathPlan), C.c_uint64, C.c_int, c_u32_p]),
     ("zrh_fast_path_validate_decode_contexts", C.c_int, [C.POINTER(FastPathPlan), C.POINTER(FastPathBackendContext),
                                                          C.c_int]),
+    ("zrh_decode_pipeline_create", C.c_int, [c_void_pp, C.c_int, c_u32_p, c_void_pp]),
+    ("zrh_decode_pipeline_step", C.c_int, [C.c_void_p, c_u32_p, c_int_p]),
+    ("zrh_decode_pipeline_finish", C.c_int, [C.c_void_p, c_u32_p]),
+    ("zrh_decode_pipeline_info", C.c_int, [C.c_void_p, C.POINTER(C.c_uint64), C.POINTER(StepGraphStats)]),
+    ("zrh_decode_pipeline_destroy", None, [C.c_void_p]),
     ("zrh_kv_reserve", C.c_int, [C.c_void_p, C.c_int]),
     ("zrh_retain_suffix", C.c_int, [C.c_void_p, C.c_int]),
 ]

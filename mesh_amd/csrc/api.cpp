@@ -148,7 +148,57 @@ static void free_ctx_buffers(zr_context* ctx) {
 // ----------------------------------------------------------------- staging
 static inline size_t align16(size_t x) { return (x + 15) & ~(size_t)15; }
 
-zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta* st) {
+// Offsets of one staged blob: the host-written inputs and records first, then
+// the arrays the pack stage derives on the device.
+struct BlobLayout {
+    size_t o_qlen, o_kvb, o_fpos, o_foff, o_bt, o_tok, o_arec, o_mrec, o_pblk, o_psplit, host_bytes;
+    size_t o_cuq, o_cuk, o_pos, o_slot, o_seq, o_last, o_rcs, total_bytes;
+};
+
+static BlobLayout blob_layout(int S, int stride, int total_q, int n_items, int n_merge, int n_pblocks, int head_dim) {
+    BlobLayout b;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off = align16(off + bytes);
+        return o;
+    };
+    b.o_qlen = take(4 * S);
+    b.o_kvb = take(4 * S);
+    b.o_fpos = take(4 * S);
+    b.o_foff = take(4 * S);
+    b.o_bt = take(4 * (size_t)S * stride);
+    b.o_tok = take(4 * (size_t)std::max(total_q, 1));
+    b.o_arec = take(48 * (size_t)std::max(n_items, 1));
+    b.o_mrec = take(16 * (size_t)std::max(n_merge, 1));
+    b.o_pblk = take(16 * (size_t)std::max(n_pblocks, 1));
+    b.o_psplit = take(16 * (size_t)std::max(n_pblocks, 1));
+    b.host_bytes = off;
+    b.o_cuq = take(4 * (S + 1));
+    b.o_cuk = take(4 * (S + 1));
+    b.o_pos = take(4 * (size_t)total_q);
+    b.o_slot = take(4 * (size_t)total_q);
+    b.o_seq = take(4 * (size_t)total_q);
+    b.o_last = take(4 * S);
+    b.o_rcs = take(8 * (size_t)total_q * (head_dim / 2));
+    b.total_bytes = off;
+    return b;
+}
+
+void stage_fixed_bytes(const zr_context* ctx, int S, int total_q, const StageFixed& f, size_t* host_bytes,
+                       size_t* dev_bytes) {
+    const BlobLayout b = blob_layout(S, f.stride, total_q, f.items_cap, f.merge_cap, 0, ctx->head_dim);
+    *host_bytes = b.host_bytes;
+    *dev_bytes = b.total_bytes;
+}
+
+zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta* st, const StageFixed* fixed,
+                           bool* fits) {
+    if (fits) *fits = true;
+    auto no_fit = [&](const char* why) {
+        if (fits) *fits = false;
+        return set_err(ctx, ZR_E_UNSUPPORTED, "microbatch does not fit the step graph's bucket: %s", why);
+    };
     if (!mb) return set_err(ctx, ZR_E_INVALID, "null microbatch");
     const int S = mb->num_seqs;
     if (S <= 0 || S > ctx->desc.max_seqs)
@@ -189,10 +239,12 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
                 return set_err(ctx, ZR_E_INVALID, "Token %u out of vocabulary bounds %d", mb->tokens[t],
                                ctx->desc.vocab);
 
+    if (fixed && stride > fixed->stride) return no_fit("block table stride");
+    const int blob_stride = fixed ? fixed->stride : stride;
     st->ctx = ctx;
     st->num_seqs = S;
     st->total_q = total_q;
-    st->stride = stride;
+    st->stride = blob_stride;
     st->max_kv = max_kv;
 
     // attention tiles / split items (the generic kernel of plain-layout pools
@@ -358,8 +410,20 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     for (int s = 0; s < S && st->pure_decode; ++s) st->pure_decode = mb->q_len[s] == 1;
     st->fuse_rope = st->pure_decode && pps >= 48;
     if (const char* env = getenv("ZR_ATTN_FUSE_ROPE")) st->fuse_rope = st->pure_decode && atoi(env) != 0;
+    st->grid_items = st->n_attn_items;
+    st->grid_merge = st->n_merge;
+    if (fixed) {
+        if (!st->pure_decode || st->n_pblocks > 0) return no_fit("not a decode step of one row per sequence");
+        if (fixed->plan_only) return ZR_OK;
+        if (st->n_attn_items > fixed->items_cap) return no_fit("attention items");
+        if (st->n_merge > fixed->merge_cap) return no_fit("split merges");
+        st->fuse_rope = fixed->fuse_rope;
+        st->grid_items = fixed->items_cap;
+        st->grid_merge = fixed->merge_cap;
+    }
 
     const size_t need_part = (size_t)st->n_part_items * ctx->local_kv_heads * 16 * (ctx->head_dim + 2);
+    if (fixed && need_part > ctx->attn_part_floats) return no_fit("attention partial workspace");
     if (need_part > ctx->attn_part_floats) {
         hipStreamSynchronize(ctx->stream);
         if (ctx->attn_part) hipFree(ctx->attn_part);
@@ -371,64 +435,73 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     }
 
     // one blob: inputs, derived arrays, attention items
-    size_t off = 0;
-    auto take = [&](size_t bytes) {
-        const size_t o = off;
-        off = align16(off + bytes);
-        return o;
-    };
-    const size_t o_qlen = take(4 * S), o_kvb = take(4 * S), o_fpos = take(4 * S), o_foff = take(4 * S);
-    const size_t o_bt = take(4 * (size_t)S * stride), o_tok = take(4 * (size_t)std::max(total_q, 1));
-    const size_t o_arec = take(48 * (size_t)std::max(st->n_attn_items, 1));
-    const size_t o_mrec = take(16 * (size_t)std::max(st->n_merge, 1));
-    const size_t o_pblk = take(16 * (size_t)std::max(st->n_pblocks, 1));
-    const size_t o_psplit = take(16 * (size_t)std::max(st->n_pblocks, 1));
-    const size_t host_bytes = off;
-    const size_t o_cuq = take(4 * (S + 1)), o_cuk = take(4 * (S + 1)), o_pos = take(4 * (size_t)total_q);
-    const size_t o_slot = take(4 * (size_t)total_q), o_seq = take(4 * (size_t)total_q), o_last = take(4 * S);
-    const size_t o_rcs = take(8 * (size_t)total_q * (ctx->head_dim / 2));
-    const size_t total_bytes = off;
-    if (total_bytes > st->cap_bytes) {
-        hipStreamSynchronize(ctx->stream);
-        if (st->dev) hipFree(st->dev);
-        st->dev = nullptr;
-        st->cap_bytes = 0;
-        ZR_HIP(ctx, hipMalloc(&st->dev, total_bytes));
-        st->cap_bytes = total_bytes;
+    const BlobLayout L = blob_layout(S, blob_stride, total_q, st->grid_items, st->grid_merge, st->n_pblocks,
+                                     ctx->head_dim);
+    const size_t host_bytes = L.host_bytes, total_bytes = L.total_bytes;
+    unsigned char* hb;
+    if (fixed) {
+        if (total_bytes > fixed->dev_cap || host_bytes > fixed->host_cap)
+            return set_err(ctx, ZR_E_INVARIANT, "step graph blob of %zu bytes holds %zu", fixed->dev_cap, total_bytes);
+        st->dev = fixed->dev;
+        st->cap_bytes = fixed->dev_cap;
+        st->owns = false;
+        hb = fixed->host;
+    } else {
+        if (total_bytes > st->cap_bytes) {
+            hipStreamSynchronize(ctx->stream);
+            if (st->dev) hipFree(st->dev);
+            st->dev = nullptr;
+            st->cap_bytes = 0;
+            ZR_HIP(ctx, hipMalloc(&st->dev, total_bytes));
+            st->cap_bytes = total_bytes;
+        }
+        st->h_blob.assign(host_bytes, 0);
+        hb = st->h_blob.data();
     }
     st->dev_bytes = total_bytes;
-    st->h_blob.assign(host_bytes, 0);
-    unsigned char* hb = st->h_blob.data();
-    memcpy(hb + o_qlen, mb->q_len, 4 * S);
-    memcpy(hb + o_kvb, mb->kv_before, 4 * S);
-    memcpy(hb + o_fpos, mb->first_pos, 4 * S);
-    memcpy(hb + o_foff, mb->first_offset, 4 * S);
-    memcpy(hb + o_bt, mb->block_tables, 4 * (size_t)S * stride);
-    if (mb->tokens) memcpy(hb + o_tok, mb->tokens, 4 * (size_t)total_q);
-    if (st->n_attn_items) memcpy(hb + o_arec, st->h_attn_rec.data(), 48 * (size_t)st->n_attn_items);
-    if (st->n_merge) memcpy(hb + o_mrec, st->h_merge_rec.data(), 16 * (size_t)st->n_merge);
-    if (st->n_pblocks) memcpy(hb + o_pblk, st->h_pblocks.data(), 16 * (size_t)st->n_pblocks);
-    if (st->n_pblocks) memcpy(hb + o_psplit, st->h_psplits.data(), 16 * (size_t)st->n_pblocks);
+    memcpy(hb + L.o_qlen, mb->q_len, 4 * S);
+    memcpy(hb + L.o_kvb, mb->kv_before, 4 * S);
+    memcpy(hb + L.o_fpos, mb->first_pos, 4 * S);
+    memcpy(hb + L.o_foff, mb->first_offset, 4 * S);
+    if (blob_stride == stride) {
+        memcpy(hb + L.o_bt, mb->block_tables, 4 * (size_t)S * stride);
+    } else {  // a bucket's wider table: each row's pages, the rest of the row zero (pool page 0)
+        int* bt = (int*)(hb + L.o_bt);
+        for (int s = 0; s < S; ++s) {
+            memcpy(bt + (size_t)s * blob_stride, mb->block_tables + (size_t)s * stride, 4 * (size_t)stride);
+            memset(bt + (size_t)s * blob_stride + stride, 0, 4 * (size_t)(blob_stride - stride));
+        }
+    }
+    if (mb->tokens) memcpy(hb + L.o_tok, mb->tokens, 4 * (size_t)total_q);
+    if (st->n_attn_items) memcpy(hb + L.o_arec, st->h_attn_rec.data(), 48 * (size_t)st->n_attn_items);
+    if (st->grid_items > st->n_attn_items)  // empty records (nq = 0): their workgroups return at once
+        memset(hb + L.o_arec + 48 * (size_t)st->n_attn_items, 0, 48 * (size_t)(st->grid_items - st->n_attn_items));
+    if (st->n_merge) memcpy(hb + L.o_mrec, st->h_merge_rec.data(), 16 * (size_t)st->n_merge);
+    if (st->grid_merge > st->n_merge)
+        memset(hb + L.o_mrec + 16 * (size_t)st->n_merge, 0, 16 * (size_t)(st->grid_merge - st->n_merge));
+    if (st->n_pblocks) memcpy(hb + L.o_pblk, st->h_pblocks.data(), 16 * (size_t)st->n_pblocks);
+    if (st->n_pblocks) memcpy(hb + L.o_psplit, st->h_psplits.data(), 16 * (size_t)st->n_pblocks);
     unsigned char* db = (unsigned char*)st->dev;
-    st->q_len = (int*)(db + o_qlen);
-    st->kv_before = (int*)(db + o_kvb);
-    st->first_pos = (int*)(db + o_fpos);
-    st->first_offset = (int*)(db + o_foff);
-    st->block_tables = (int*)(db + o_bt);
-    st->tokens = (uint32_t*)(db + o_tok);
-    st->attn_rec = (int4*)(db + o_arec);
-    st->merge_rec = (int4*)(db + o_mrec);
-    st->pblocks = (int4*)(db + o_pblk);
-    st->psplits = (int4*)(db + o_psplit);
-    st->cu_q = (int*)(db + o_cuq);
-    st->cu_k = (int*)(db + o_cuk);
-    st->positions = (int*)(db + o_pos);
-    st->slot_mapping = (int*)(db + o_slot);
-    st->seq_ids = (int*)(db + o_seq);
-    st->last_rows = (int*)(db + o_last);
-    st->rope_cs = (float2*)(db + o_rcs);
+    st->q_len = (int*)(db + L.o_qlen);
+    st->kv_before = (int*)(db + L.o_kvb);
+    st->first_pos = (int*)(db + L.o_fpos);
+    st->first_offset = (int*)(db + L.o_foff);
+    st->block_tables = (int*)(db + L.o_bt);
+    st->tokens = (uint32_t*)(db + L.o_tok);
+    st->attn_rec = (int4*)(db + L.o_arec);
+    st->merge_rec = (int4*)(db + L.o_mrec);
+    st->pblocks = (int4*)(db + L.o_pblk);
+    st->psplits = (int4*)(db + L.o_psplit);
+    st->cu_q = (int*)(db + L.o_cuq);
+    st->cu_k = (int*)(db + L.o_cuk);
+    st->positions = (int*)(db + L.o_pos);
+    st->slot_mapping = (int*)(db + L.o_slot);
+    st->seq_ids = (int*)(db + L.o_seq);
+    st->last_rows = (int*)(db + L.o_last);
+    st->rope_cs = (float2*)(db + L.o_rcs);
     st->h_q_len.assign(mb->q_len, mb->q_len + S);
     st->h_kv_before.assign(mb->kv_before, mb->kv_before + S);
+    if (fixed) return ZR_OK;  // the step graph copies the host blob and runs the pack stage
     ZR_HIP(ctx, hipMemcpyAsync(st->dev, hb, host_bytes, hipMemcpyHostToDevice, ctx->stream));
     return launch_pack(ctx, st);
 }
@@ -783,6 +856,8 @@ zr_status zr_stage(zr_context* ctx, const zr_microbatch* mb, zr_staged** out) {
         delete st;
         return rc;
     }
+    st->id = ctx->next_staged_id++;
+    ctx->live_staged.push_back(st->id);
     *out = (zr_staged*)st;
     return ZR_OK;
 }
@@ -790,7 +865,11 @@ zr_status zr_stage(zr_context* ctx, const zr_microbatch* mb, zr_staged** out) {
 void zr_staged_destroy(zr_staged* s) {
     StagedMeta* st = (StagedMeta*)s;
     if (!st) return;
-    if (st->ctx) hipStreamSynchronize(st->ctx->stream);
+    if (st->ctx) {
+        hipStreamSynchronize(st->ctx->stream);
+        auto& live = st->ctx->live_staged;
+        live.erase(std::remove(live.begin(), live.end(), st->id), live.end());
+    }
     if (st->dev) hipFree(st->dev);
     delete st;
 }
@@ -826,6 +905,7 @@ struct zr_graph {
     hipGraphExec_t exec = nullptr;
     bool token_check = false;  // the step copies the device id-check word to the host
     uint64_t buffer_epoch = 0; // the context's buffer epoch at capture
+    uint64_t staged_id = 0;    // the staged microbatch the graph replays
 };
 
 zr_status zr_graph_capture_staged(zr_context* ctx, zr_staged* s, const uint32_t* d_tokens, uint32_t* d_out_tokens,
@@ -862,6 +942,7 @@ zr_status zr_graph_capture_staged(zr_context* ctx, zr_staged* s, const uint32_t*
     g->exec = exec;
     g->token_check = d_tokens != nullptr;
     g->buffer_epoch = ctx->buffer_epoch;
+    g->staged_id = st->id;
     *out = g;
     return ZR_OK;
 }
@@ -872,6 +953,8 @@ zr_status zr_graph_launch(zr_context* ctx, zr_graph* g) {
     if (g->buffer_epoch != ctx->buffer_epoch)
         return set_err(ctx, ZR_E_INVALID,
                        "graph captured before a workspace, the KV pool or weights were reallocated: capture it again");
+    if (std::find(ctx->live_staged.begin(), ctx->live_staged.end(), g->staged_id) == ctx->live_staged.end())
+        return set_err(ctx, ZR_E_INVALID, "the graph's staged microbatch was destroyed: stage and capture again");
     ZR_HIP(ctx, hipGraphLaunch(g->exec, ctx->stream));
     if (g->token_check) ctx->token_check_pending = true;
     return ZR_OK;
@@ -882,6 +965,247 @@ void zr_graph_destroy(zr_graph* g) {
     if (g->ctx && g->ctx->stream) (void)hipStreamSynchronize(g->ctx->stream);
     if (g->exec) (void)hipGraphExecDestroy(g->exec);
     if (g->graph) (void)hipGraphDestroy(g->graph);
+    delete g;
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------ step graphs
+// One decode step captured per bucket and replayed for every later step that
+// fits the bucket, each launch with its own metadata.  Two blobs alternate:
+// step i stages into pinned host buffer i % 2 (after that buffer's previous
+// copy has finished), a copy stream moves it into device blob i % 2 once the
+// replay that last read the blob (step i - 2) has finished, and the replay of
+// step i waits for that copy.  The host staging of step i + 1 overlaps step i
+// on the device.
+struct zr_step_graph {
+    zr_context* ctx = nullptr;
+    hipStream_t copy = nullptr;
+    bool valid = false;          // a bucket is set up
+    int S = 0;                   // sequences of the bucket
+    uint64_t epoch = 0;          // the context's buffer epoch at set-up
+    StageFixed fixed[2];
+    size_t host_bytes = 0;       // host part of a blob (copied per step)
+    unsigned char* pinned[2] = {nullptr, nullptr};
+    void* dev[2] = {nullptr, nullptr};
+    size_t host_cap = 0, dev_cap = 0;
+    hipEvent_t copied[2] = {nullptr, nullptr};    // the copy into blob b has finished
+    hipEvent_t replayed[2] = {nullptr, nullptr};  // the replay that read blob b has finished
+    bool copy_pending[2] = {false, false}, replay_pending[2] = {false, false};
+    StagedMeta st[2];
+    struct Exec {
+        const uint32_t* in;
+        uint32_t* out;
+        int blob;
+        hipGraph_t graph;
+        hipGraphExec_t exec;
+    };
+    std::vector<Exec> execs;
+    uint64_t launches = 0;
+    int captures = 0, buckets = 0;
+};
+
+namespace {
+
+void step_graph_drop_execs(zr_step_graph* g) {
+    for (auto& e : g->execs) {
+        if (e.exec) (void)hipGraphExecDestroy(e.exec);
+        if (e.graph) (void)hipGraphDestroy(e.graph);
+    }
+    g->execs.clear();
+}
+
+zr_status step_graph_quiesce(zr_step_graph* g) {
+    zr_context* ctx = g->ctx;
+    ZR_HIP(ctx, hipStreamSynchronize(g->copy));
+    ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    for (int b = 0; b < 2; ++b) g->copy_pending[b] = g->replay_pending[b] = false;
+    return ZR_OK;
+}
+
+// Sizes a bucket for the sequence count and the counts of `mb` with room to
+// grow: records for 1.25x the step's attention items (+64) and merges (+16),
+// the context's widest block table, and the step's RoPE placement.
+zr_status step_graph_setup(zr_step_graph* g, const zr_microbatch* mb) {
+    zr_context* ctx = g->ctx;
+    StagedMeta probe;
+    StageFixed plan;
+    plan.plan_only = true;
+    plan.stride = ctx->desc.max_pages_per_seq;
+    bool fits = true;
+    zr_status rc = stage_microbatch(ctx, mb, &probe, &plan, &fits);
+    if (rc) return rc;  // not a decode step of one row per sequence, or invalid
+    if ((rc = step_graph_quiesce(g))) return rc;
+    step_graph_drop_execs(g);
+    g->valid = false;
+    StageFixed f;
+    f.stride = ctx->desc.max_pages_per_seq;
+    f.items_cap = (probe.n_attn_items + std::max(64, probe.n_attn_items / 4) + 7) / 8 * 8;
+    f.merge_cap = probe.n_merge + std::max(16, probe.n_merge / 4);
+    f.fuse_rope = probe.fuse_rope;
+    // partials of every item a step of the bucket can hold (decode items only)
+    const size_t need_part = (size_t)f.items_cap * ctx->local_kv_heads * 16 * (ctx->head_dim + 2);
+    if (need_part > ctx->attn_part_floats) {
+        if (ctx->attn_part) hipFree(ctx->attn_part);
+        ++ctx->buffer_epoch;
+        ctx->attn_part = nullptr;
+        ctx->attn_part_floats = 0;
+        ZR_HIP(ctx, hipMalloc(&ctx->attn_part, need_part * sizeof(float)));
+        ctx->attn_part_floats = need_part;
+    }
+    size_t hbytes = 0, dbytes = 0;
+    stage_fixed_bytes(ctx, mb->num_seqs, probe.total_q, f, &hbytes, &dbytes);
+    for (int b = 0; b < 2; ++b) {
+        if (hbytes > g->host_cap) {
+            if (g->pinned[b]) (void)hipHostFree(g->pinned[b]);
+            g->pinned[b] = nullptr;
+            ZR_HIP(ctx, hipHostMalloc((void**)&g->pinned[b], hbytes, hipHostMallocDefault));
+        }
+        if (dbytes > g->dev_cap) {
+            if (g->dev[b]) (void)hipFree(g->dev[b]);
+            g->dev[b] = nullptr;
+            ZR_HIP(ctx, hipMalloc(&g->dev[b], dbytes));
+        }
+    }
+    g->host_cap = std::max(g->host_cap, hbytes);
+    g->dev_cap = std::max(g->dev_cap, dbytes);
+    for (int b = 0; b < 2; ++b) {
+        g->fixed[b] = f;
+        g->fixed[b].host = g->pinned[b];
+        g->fixed[b].host_cap = g->host_cap;
+        g->fixed[b].dev = g->dev[b];
+        g->fixed[b].dev_cap = g->dev_cap;
+    }
+    g->host_bytes = hbytes;
+    g->S = mb->num_seqs;
+    g->epoch = ctx->buffer_epoch;
+    g->valid = true;
+    ++g->buckets;
+    return ZR_OK;
+}
+
+zr_status step_graph_capture(zr_step_graph* g, int b, const uint32_t* in, uint32_t* out, hipGraphExec_t* exec_out) {
+    zr_context* ctx = g->ctx;
+    for (auto& e : g->execs)
+        if (e.in == in && e.out == out && e.blob == b) {
+            *exec_out = e.exec;
+            return ZR_OK;
+        }
+    // a capture starts on an idle stream (once per bucket and token pair)
+    ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    const bool pending = ctx->token_check_pending;
+    ZR_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    zr_status rc = launch_pack(ctx, &g->st[b]);
+    if (!rc) rc = run_forward(ctx, &g->st[b], in, out, nullptr, nullptr);
+    hipGraph_t graph = nullptr;
+    const hipError_t e_end = hipStreamEndCapture(ctx->stream, &graph);
+    ctx->token_check_pending = pending;  // nothing ran yet
+    if (!rc && e_end != hipSuccess) rc = set_err(ctx, ZR_E_HIP, "step graph capture: %s", hipGetErrorString(e_end));
+    hipGraphExec_t exec = nullptr;
+    if (!rc) {
+        const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        if (e != hipSuccess) rc = set_err(ctx, ZR_E_HIP, "step graph instantiate: %s", hipGetErrorString(e));
+    }
+    if (rc) {
+        if (graph) (void)hipGraphDestroy(graph);
+        (void)hipGetLastError();
+        return rc;
+    }
+    g->execs.push_back({in, out, b, graph, exec});
+    ++g->captures;
+    *exec_out = exec;
+    return ZR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+zr_status zr_step_graph_create(zr_context* ctx, zr_step_graph** out) {
+    if (!ctx || !out) return set_global_err(ZR_E_INVALID, "null argument");
+    if (ctx->plain_kv) return set_err(ctx, ZR_E_UNSUPPORTED, "step graphs need the MFMA page layout");
+    ZR_HIP(ctx, hipSetDevice(ctx->device));
+    zr_step_graph* g = new zr_step_graph();
+    g->ctx = ctx;
+    hipError_t e = hipStreamCreateWithFlags(&g->copy, hipStreamNonBlocking);
+    for (int b = 0; b < 2 && e == hipSuccess; ++b) {
+        e = hipEventCreateWithFlags(&g->copied[b], hipEventDisableTiming);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&g->replayed[b], hipEventDisableTiming);
+    }
+    if (e != hipSuccess) {
+        zr_step_graph_destroy(g);
+        return set_err(ctx, ZR_E_HIP, "step graph: %s", hipGetErrorString(e));
+    }
+    *out = g;
+    return ZR_OK;
+}
+
+zr_status zr_step_graph_launch(zr_step_graph* g, const zr_microbatch* mb, const uint32_t* d_tokens,
+                               uint32_t* d_out_tokens, uint32_t* h_out_tokens) {
+    if (!g || !mb || !d_tokens || !d_out_tokens) return set_global_err(ZR_E_INVALID, "null argument");
+    zr_context* ctx = g->ctx;
+    zr_status rc = check_ready(ctx);
+    if (rc) return rc;
+    if (ctx->timing.enabled) return set_err(ctx, ZR_E_INVALID, "step graph launch with per-class timing on");
+    ZR_HIP(ctx, hipSetDevice(ctx->device));
+    if (!g->valid || g->epoch != ctx->buffer_epoch || g->S != mb->num_seqs)
+        if ((rc = step_graph_setup(g, mb))) return rc;
+    const int b = (int)(g->launches & 1);
+    if (g->copy_pending[b]) {  // pinned buffer b is free once its last copy has finished
+        ZR_HIP(ctx, hipEventSynchronize(g->copied[b]));
+        g->copy_pending[b] = false;
+    }
+    bool fits = true;
+    rc = stage_microbatch(ctx, mb, &g->st[b], &g->fixed[b], &fits);
+    if (rc && !fits) {  // a new bucket, sized for this step
+        if ((rc = step_graph_setup(g, mb))) return rc;
+        rc = stage_microbatch(ctx, mb, &g->st[b], &g->fixed[b], &fits);
+    }
+    if (rc) return rc;
+    if (g->replay_pending[b]) ZR_HIP(ctx, hipStreamWaitEvent(g->copy, g->replayed[b], 0));
+    ZR_HIP(ctx, hipMemcpyAsync(g->dev[b], g->pinned[b], g->host_bytes, hipMemcpyHostToDevice, g->copy));
+    ZR_HIP(ctx, hipEventRecord(g->copied[b], g->copy));
+    g->copy_pending[b] = true;
+    hipGraphExec_t exec = nullptr;
+    if ((rc = step_graph_capture(g, b, d_tokens, d_out_tokens, &exec))) return rc;
+    ZR_HIP(ctx, hipStreamWaitEvent(ctx->stream, g->copied[b], 0));
+    ZR_HIP(ctx, hipGraphLaunch(exec, ctx->stream));
+    ZR_HIP(ctx, hipEventRecord(g->replayed[b], ctx->stream));
+    g->replay_pending[b] = true;
+    ctx->token_check_pending = true;  // the replay copies the id-check word (device-fed ids)
+    if (h_out_tokens)
+        ZR_HIP(ctx, hipMemcpyAsync(h_out_tokens, d_out_tokens, 4 * (size_t)mb->num_seqs, hipMemcpyDeviceToHost,
+                                   ctx->stream));
+    ++g->launches;
+    return ZR_OK;
+}
+
+zr_status zr_step_graph_info(const zr_step_graph* g, zr_step_graph_stats* out) {
+    if (!g || !out) return set_global_err(ZR_E_INVALID, "null argument");
+    out->launches = g->launches;
+    out->captures = g->captures;
+    out->buckets = g->buckets;
+    out->sequences = g->S;
+    out->items_capacity = g->valid ? g->fixed[0].items_cap : 0;
+    out->merge_capacity = g->valid ? g->fixed[0].merge_cap : 0;
+    out->fused_rope = g->valid && g->fixed[0].fuse_rope;
+    out->metadata_bytes = g->host_bytes;
+    return ZR_OK;
+}
+
+void zr_step_graph_destroy(zr_step_graph* g) {
+    if (!g) return;
+    if (g->copy) (void)hipStreamSynchronize(g->copy);
+    if (g->ctx && g->ctx->stream) (void)hipStreamSynchronize(g->ctx->stream);
+    step_graph_drop_execs(g);
+    for (int b = 0; b < 2; ++b) {
+        if (g->pinned[b]) (void)hipHostFree(g->pinned[b]);
+        if (g->dev[b]) (void)hipFree(g->dev[b]);
+        if (g->copied[b]) (void)hipEventDestroy(g->copied[b]);
+        if (g->replayed[b]) (void)hipEventDestroy(g->replayed[b]);
+        g->st[b].dev = nullptr;  // the blob belongs to the step graph
+    }
+    if (g->copy) (void)hipStreamDestroy(g->copy);
     delete g;
 }
 

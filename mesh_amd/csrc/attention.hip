@@ -234,6 +234,7 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
     // everything the workgroup needs to start its loads, in one record
     const int4 r0 = a.rec[3 * rank], r1 = a.rec[3 * rank + 1], r2 = a.rec[3 * rank + 2];
     const int seq = r0.x, row0 = r0.y, nq = r0.z, page_b = r0.w, page_e = r1.x, foff = r1.z;
+    if (nq == 0) return;  // an empty record past a replayed bucket's items
     const unsigned meta = (unsigned)r1.w;
     const int item = (int)(meta & (kAttnSingle - 1));
     const int c = lane & 15, q4 = lane >> 4;
@@ -816,6 +817,7 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(const float* __res
     const int4 mr = merge_rec[blockIdx.x];
     const int kvh = blockIdx.y;
     const int first = mr.x, nparts = mr.y, row0 = mr.z, nq = mr.w;
+    if (nq <= 0) return;  // an empty record past a replayed bucket's merges
     const int ncols = min(nq, 16 / G) * G;
     const size_t pstride = (size_t)kv_heads * 16 * (D + 2);
     const float* base = part + ((size_t)first * kv_heads + kvh) * 16 * (D + 2);
@@ -975,7 +977,7 @@ static zr_status launch_attn_t(zr_context* ctx, StagedMeta* st, int layer, const
     a.block_tables = st->block_tables;
     a.stride = st->stride;
     a.rec = st->attn_rec;
-    a.n_items = st->n_attn_items;
+    a.n_items = st->grid_items;
     a.G = ctx->q_per_kv;
     a.kv_heads = ctx->local_kv_heads;
     a.scale_log2 = 1.4426950408889634f / sqrtf((float)D);
@@ -985,10 +987,10 @@ static zr_status launch_attn_t(zr_context* ctx, StagedMeta* st, int layer, const
     a.out_lo_offset = (ctx->desc.flags & ZR_FLAG_SPLIT_ACTIVATIONS) ? a_plane(st->total_q, ctx->q_cols) : 0;
     hipEvent_t ev;
     timing_mark_begin(ctx, kClassAttention, &ev);
-    if (st->n_attn_items > 0) {
+    if (st->grid_items > 0) {
         // bf16 pages: a 6-page ring, one wave per SIMD (measured: a 4-page ring
         // at two waves per SIMD spills and loses ~20%); f32 pages: 4 pages
-        const dim3 grid(((st->n_attn_items + 7) / 8) * 8 * ctx->local_kv_heads);
+        const dim3 grid(((st->grid_items + 7) / 8) * 8 * ctx->local_kv_heads);
         if (qkv)
             hipLaunchKernelGGL((paged_attention_kernel<KV, D, sizeof(KV) == 4 ? 4 : 6, true>), grid, dim3(64), 0,
                                ctx->stream, a);
@@ -1026,9 +1028,9 @@ static zr_status launch_attn_t(zr_context* ctx, StagedMeta* st, int layer, const
         }
     }
     timing_mark_end(ctx, kClassAttention, ev);
-    if (st->n_merge > 0) {
+    if (st->grid_merge > 0) {
         timing_mark_begin(ctx, kClassOther, &ev);
-        hipLaunchKernelGGL((attention_merge_kernel<D>), dim3(st->n_merge, ctx->local_kv_heads), dim3(256), 0,
+        hipLaunchKernelGGL((attention_merge_kernel<D>), dim3(st->grid_merge, ctx->local_kv_heads), dim3(256), 0,
                            ctx->stream, ctx->attn_part, st->merge_rec, ctx->q_per_kv, ctx->local_kv_heads,
                            ctx->q_cols, out, out_bf16, a.out_lo_offset);
         ZR_LAUNCH_CHECK(ctx);
@@ -1180,7 +1182,7 @@ zr_status launch_attention(zr_context* ctx, StagedMeta* st, int layer, const flo
                    ? launch_attn_generic<uint16_t>(ctx, st, layer, q, out, out_bf16)
                    : launch_attn_generic<float>(ctx, st, layer, q, out, out_bf16);
     }
-    if (st->n_attn_items == 0 && st->n_pblocks == 0) return ZR_OK;
+    if (st->grid_items == 0 && st->n_pblocks == 0) return ZR_OK;
     const size_t need = (size_t)st->n_part_items * ctx->local_kv_heads * 16 * (ctx->head_dim + 2);
     if (need > ctx->attn_part_floats)
         return set_err(ctx, ZR_E_OOM, "attention partial workspace too small: need %zu floats, have %zu",
@@ -1199,7 +1201,7 @@ zr_status launch_attention_rope(zr_context* ctx, StagedMeta* st, int layer, cons
                                 float* out, uint16_t* out_bf16) {
     if (!st->pure_decode)
         return set_err(ctx, ZR_E_UNSUPPORTED, "RoPE inside attention needs a microbatch of one-row decode sequences");
-    if (st->n_attn_items == 0) return ZR_OK;
+    if (st->grid_items == 0) return ZR_OK;
     const size_t need = (size_t)st->n_part_items * ctx->local_kv_heads * 16 * (ctx->head_dim + 2);
     if (need > ctx->attn_part_floats)
         return set_err(ctx, ZR_E_OOM, "attention partial workspace too small: need %zu floats, have %zu",

@@ -957,6 +957,123 @@ zr_status zrh_fast_path_stage_decode(const zrh_fast_path_plan* plan, zrh_backend
     return ZR_OK;
 }
 
+// ------------------------------------------------------ decode pipeline
+}  // extern "C"
+
+struct zrh_decode_pipeline {
+    std::vector<zrh_backend*> backends;
+    zr_context* ctx = nullptr;
+    zr_step_graph* graph = nullptr;
+    uint32_t* d_tok[2] = {nullptr, nullptr};  // ids in / out, alternating
+    uint32_t* h_tok[2] = {nullptr, nullptr};  // pinned copies of each step's ids
+    hipEvent_t done[2] = {nullptr, nullptr};  // the step's id copy has landed
+    uint64_t steps = 0;
+};
+
+extern "C" {
+
+zr_status zrh_decode_pipeline_create(zrh_backend* const* backends, int n, const uint32_t* first_tokens,
+                                     zrh_decode_pipeline** out) {
+    if (!backends || !first_tokens || !out || n <= 0 || !backends[0])
+        return set_global_err(ZR_E_INVALID, "Decode microbatch requires at least one backend and token");
+    zr_context* ctx = backends[0]->ctx;
+    if (!ctx) return set_global_err(ZR_E_INVALID, "bookkeeping-only pool has no device context");
+    for (int i = 0; i < n; ++i) {
+        if (!backends[i] || backends[i]->ctx != ctx) return set_err(ctx, ZR_E_INVALID, "microbatch mixes contexts");
+        for (int j = 0; j < i; ++j)
+            if (backends[j] == backends[i])
+                return set_err(ctx, ZR_E_INVALID, "session %d appears twice in one microbatch", i);
+    }
+    if (n > ctx->desc.max_seqs || n > ctx->desc.max_tokens)
+        return set_err(ctx, ZR_E_INVALID, "microbatch has %d sequences (capacity %d)", n,
+                       std::min(ctx->desc.max_seqs, ctx->desc.max_tokens));
+    for (int i = 0; i < n; ++i)
+        if (first_tokens[i] >= (uint32_t)ctx->desc.vocab)
+            return set_err(ctx, ZR_E_INVALID, "Token %u out of vocabulary bounds %d", first_tokens[i], ctx->desc.vocab);
+    ZR_HIP(ctx, hipSetDevice(ctx->device));
+    zrh_decode_pipeline* p = new zrh_decode_pipeline();
+    p->backends.assign(backends, backends + n);
+    p->ctx = ctx;
+    zr_status rc = zr_step_graph_create(ctx, &p->graph);
+    hipError_t e = hipSuccess;
+    for (int b = 0; b < 2 && !rc && e == hipSuccess; ++b) {
+        e = hipMalloc((void**)&p->d_tok[b], 4 * (size_t)n);
+        if (e == hipSuccess) e = hipHostMalloc((void**)&p->h_tok[b], 4 * (size_t)n, hipHostMallocDefault);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&p->done[b], hipEventDisableTiming);
+    }
+    if (!rc && e == hipSuccess)
+        e = hipMemcpy(p->d_tok[0], first_tokens, 4 * (size_t)n, hipMemcpyHostToDevice);
+    if (!rc && e != hipSuccess) rc = set_err(ctx, ZR_E_HIP, "decode pipeline: %s", hipGetErrorString(e));
+    if (rc) {
+        zrh_decode_pipeline_destroy(p);
+        return rc;
+    }
+    *out = p;
+    return ZR_OK;
+}
+
+zr_status zrh_decode_pipeline_step(zrh_decode_pipeline* p, uint32_t* prev_tokens, int* prev_ready) {
+    if (!p) return set_global_err(ZR_E_INVALID, "null argument");
+    zr_context* ctx = p->ctx;
+    const int n = (int)p->backends.size();
+    if (prev_ready) *prev_ready = 0;
+    const uint64_t i = p->steps;
+    zrh_backend* const* bs = p->backends.data();
+    // the decode rows of BackendMicrobatchExecutor::decode_step_batch:
+    // window trim and page reservation per session (attention_output 1446-1452)
+    PoolTxn txn(bs[0]->pool);
+    Assembled a;
+    Saved saved;
+    std::vector<int> ones(n, 1);
+    zr_status rc = assemble(bs, n, ones.data(), true, a, saved, txn);
+    if (rc) return rc;
+    zr_microbatch mb = as_microbatch(a, nullptr);
+    rc = zr_step_graph_launch(p->graph, &mb, p->d_tok[i & 1], p->d_tok[(i + 1) & 1], p->h_tok[i & 1]);
+    if (!rc) {
+        const hipError_t e = hipEventRecord(p->done[i & 1], ctx->stream);
+        if (e != hipSuccess) rc = set_err(ctx, ZR_E_HIP, "decode pipeline: %s", hipGetErrorString(e));
+    }
+    if (rc) {
+        saved.restore(bs, n, txn);
+        return rc;
+    }
+    for (int s = 0; s < n; ++s) bs[s]->position += 1;
+    p->steps = i + 1;
+    if (i > 0) {  // the previous step's ids: the host waits for that step only
+        ZR_HIP(ctx, hipEventSynchronize(p->done[(i - 1) & 1]));
+        if (prev_tokens) memcpy(prev_tokens, p->h_tok[(i - 1) & 1], 4 * (size_t)n);
+        if (prev_ready) *prev_ready = 1;
+    }
+    return ZR_OK;
+}
+
+zr_status zrh_decode_pipeline_finish(zrh_decode_pipeline* p, uint32_t* last_tokens) {
+    if (!p) return set_global_err(ZR_E_INVALID, "null argument");
+    if (p->steps == 0) return set_err(p->ctx, ZR_E_INVALID, "decode pipeline has run no step");
+    zr_status rc = zr_synchronize(p->ctx);  // also reports a device-fed id out of the vocabulary
+    if (rc) return rc;
+    if (last_tokens) memcpy(last_tokens, p->h_tok[(p->steps - 1) & 1], 4 * p->backends.size());
+    return ZR_OK;
+}
+
+zr_status zrh_decode_pipeline_info(const zrh_decode_pipeline* p, uint64_t* steps, zr_step_graph_stats* graph) {
+    if (!p) return set_global_err(ZR_E_INVALID, "null argument");
+    if (steps) *steps = p->steps;
+    return graph ? zr_step_graph_info(p->graph, graph) : ZR_OK;
+}
+
+void zrh_decode_pipeline_destroy(zrh_decode_pipeline* p) {
+    if (!p) return;
+    if (p->ctx && p->ctx->stream) (void)hipStreamSynchronize(p->ctx->stream);
+    if (p->graph) zr_step_graph_destroy(p->graph);
+    for (int b = 0; b < 2; ++b) {
+        if (p->d_tok[b]) (void)hipFree(p->d_tok[b]);
+        if (p->h_tok[b]) (void)hipHostFree(p->h_tok[b]);
+        if (p->done[b]) (void)hipEventDestroy(p->done[b]);
+    }
+    delete p;
+}
+
 zr_status zrh_kv_reserve(zrh_backend* b, int rows) {
     if (!b) return set_global_err(ZR_E_INVALID, "null backend");
     if (rows <= 0) return set_err(b->ctx, ZR_E_INVALID, "Device KV append received an empty key shape");

@@ -186,6 +186,10 @@ struct zr_context {
     // workspace regrown, the KV pool or weights replaced): graphs captured
     // before hold its old address and are refused at launch
     uint64_t buffer_epoch = 0;
+    // staged microbatches (zr_stage) not yet destroyed: a graph replays its
+    // staged blob, so it is refused once that blob is gone
+    std::vector<uint64_t> live_staged;
+    uint64_t next_staged_id = 1;
 
     zr::StagedMeta* scratch_stage = nullptr;  // reused by zr_forward
     float* kv_stage = nullptr;      // KV gather / scatter staging (rows + table)
@@ -244,6 +248,7 @@ void timing_mark_end(zr_context* ctx, int cls, hipEvent_t begin);
 // Staged microbatch metadata (device) ------------------------------------
 struct StagedMeta {
     zr_context* ctx = nullptr;
+    uint64_t id = 0;          // zr_stage handle id (zr_context::live_staged)
     int num_seqs = 0, total_q = 0, stride = 0;
     int max_kv = 0;           // max kv_after over sequences
     int n_attn_items = 0;     // attention work items (per kv head)
@@ -255,6 +260,9 @@ struct StagedMeta {
                               // inside the decode attention kernel
     bool fuse_rope = false;   // ... and the forward pass has them do so
     bool owns = true;
+    int grid_items = 0;       // decode attention records the launch covers (n_attn_items, or a bucket's
+                              // capacity whose records past n_attn_items are empty)
+    int grid_merge = 0;       // merge records the launch covers (likewise)
     // one device allocation holding every array below
     void* dev = nullptr;
     size_t dev_bytes = 0, cap_bytes = 0;
@@ -288,7 +296,29 @@ struct StagedMeta {
     std::vector<unsigned char> h_blob;
 };
 
-zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta* st);
+// A replayed step's bucket: the staged arrays sit at the same offsets of the
+// same device blob every step, sized for the bucket's capacities; records past
+// a step's counts are empty (nq = 0).  The host blob is written in place into
+// `host` (pinned); nothing is allocated, copied or launched.
+struct StageFixed {
+    int stride = 0;                  // block-table stride of the blob
+    int items_cap = 0;               // decode attention records
+    int merge_cap = 0;               // merge records
+    bool fuse_rope = false;          // RoPE + KV append inside attention (fixed per bucket)
+    unsigned char* host = nullptr;
+    size_t host_cap = 0;
+    void* dev = nullptr;
+    size_t dev_cap = 0;
+    bool plan_only = false;          // only the counts (items, merges, partials) for sizing a bucket
+};
+// Blob bytes of a fixed layout: host part (copied per step) and the whole.
+void stage_fixed_bytes(const zr_context* ctx, int S, int total_q, const StageFixed& f, size_t* host_bytes,
+                       size_t* dev_bytes);
+// Stages a microbatch.  With `fixed`, a microbatch that is not a pure decode
+// step or exceeds the bucket's capacities sets *fits = false and returns
+// ZR_E_UNSUPPORTED (the caller captures a new bucket).
+zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta* st, const StageFixed* fixed = nullptr,
+                           bool* fits = nullptr);
 // flags of a decode attention record's last field (above them: the item index)
 constexpr unsigned kAttnSingle = 1u << 30;  // the item's tile has one split: it writes the final output
 constexpr unsigned kAttnLast = 1u << 31;    // the item is its tile's last split (holds the newest rows)

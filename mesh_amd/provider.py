@@ -717,6 +717,54 @@ def _backend_array(backends):
     return C.cast(arr, C.POINTER(C.c_void_p)), arr
 
 
+class DecodePipeline:
+    """The serving loop of BackendMicrobatchExecutor.decode_step_batch over a
+    fixed set of sessions, pipelined (zrh_decode_pipeline): every step does its
+    host bookkeeping, stages its metadata and replays the bucket's captured
+    step graph; step() returns the previous step's greedy ids, so the host work
+    of step k + 1 overlaps step k on the device.  Ids stay on the device between
+    steps (step 0 reads `first_tokens`)."""
+
+    def __init__(self, backends: Sequence["RocmExecutionBackend"], first_tokens: Sequence[int]):
+        self.ctx = backends[0].ctx
+        self.lib = self.ctx.lib
+        self.n = len(backends)
+        self._ptrs, self._keep = _backend_array(backends)
+        toks = np.ascontiguousarray(first_tokens, np.uint32)
+        h = C.c_void_p()
+        self.ctx.check(self.lib.zrh_decode_pipeline_create(self._ptrs, self.n, _ptr(toks, C.c_uint32), C.byref(h)))
+        self.h = h.value
+        self._prev = np.zeros(self.n, np.uint32)
+        self._ready = C.c_int(0)
+
+    def step(self) -> Optional[np.ndarray]:
+        """Enqueues the next step; returns the previous step's ids (None on the first)."""
+        self.ctx.check(self.lib.zrh_decode_pipeline_step(self.h, _ptr(self._prev, C.c_uint32), C.byref(self._ready)))
+        return self._prev.copy() if self._ready.value else None
+
+    def finish(self) -> np.ndarray:
+        """Waits for the last enqueued step; its ids."""
+        out = np.zeros(self.n, np.uint32)
+        self.ctx.check(self.lib.zrh_decode_pipeline_finish(self.h, _ptr(out, C.c_uint32)))
+        return out
+
+    def info(self) -> dict:
+        steps = C.c_uint64()
+        st = _lib.StepGraphStats()
+        self.ctx.check(self.lib.zrh_decode_pipeline_info(self.h, C.byref(steps), C.byref(st)))
+        out = {name: getattr(st, name) for name, _ in _lib.StepGraphStats._fields_}
+        out["steps"] = steps.value
+        return out
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.zrh_decode_pipeline_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+
 class BackendMicrobatchExecutor:
     @staticmethod
     def decode_step_batch(requests: List[DecodeMicrobatchRequest], want_logits: bool = False,

@@ -158,3 +158,27 @@ def test_a_graph_is_refused_once_a_buffer_it_reads_was_reallocated(tiny):
             lib.zr_graph_destroy(g)
         for p in (d_logits, d_out, d_x, d_am):
             lib.zr_device_free(ctx.h, p)
+
+
+def test_a_graph_is_refused_once_its_staged_microbatch_was_destroyed(tiny):
+    """A graph replays its staged blob: after zr_staged_destroy the launch is
+    refused instead of replaying freed device addresses."""
+    from tests.gpu_util import stage_mixed
+
+    b = tiny
+    ctx, lib = b.ctx, b.ctx.lib
+    st = stage_mixed(ctx, b.backends, [1] * b.B)
+    g = C.c_void_p()
+    try:
+        ctx.check(lib.zr_graph_capture_staged(ctx.h, st, b.tok[0], b.tok[1], None, C.byref(g)))
+        lib.zr_staged_destroy(st)
+        st = None
+        rc = lib.zr_graph_launch(ctx.h, g)
+        assert rc == -1, rc
+        assert b"staged microbatch was destroyed" in lib.zr_last_error(ctx.h)
+        assert lib.zr_synchronize(ctx.h) == 0  # nothing was enqueued
+    finally:
+        if g.value:
+            lib.zr_graph_destroy(g)
+        if st is not None:
+            lib.zr_staged_destroy(st)
