@@ -277,12 +277,19 @@ zr_status zr_kv_upload_async(zr_context* ctx, const float* src_k, const float* s
  * n_rows must be the transfer's. */
 zr_status zr_kv_scatter_transfer(zr_context* ctx, zr_transfer* t, const int* block_table, int n_pages,
                                  int first_offset, int first_row, int n_rows);
+/* Only the pages the rows touch are copied with the transfer, so
+ * block_table may be the session's whole table (n_pages entries). */
 /* 1 when the transfer's host copy has finished, 0 while it runs, <0 on error. */
 int zr_transfer_done(const zr_transfer* t);
 zr_status zr_transfer_wait(zr_transfer* t);
 /* Waits for the copy and the last kernel on the buffer, keeps the buffer for
- * reuse.  Destroy every transfer before its context. */
+ * reuse (the 8 largest finished buffers are kept; a transfer that fits none
+ * frees the smaller ones, and all of them before one retry when device memory
+ * runs out).  Destroy every transfer before its context.  No reference
+ * counterpart: the reference copies synchronously (forward_pass.rs:1169-1242). */
 void zr_transfer_destroy(zr_transfer* t);
+/* Bytes of device memory the context keeps in finished transfers' buffers. */
+size_t zr_transfer_cached_bytes(const zr_context* ctx);
 /* KV snapshot wire format (KVCache::to_bytes, kv_cache.rs:880-887: ciborium
  * 0.2.2 CBOR of the cache DeviceKVCache::export_snapshot builds,
  * forward_pass.rs:1169-1204): gathers rows [first_row, first_row + n_rows)

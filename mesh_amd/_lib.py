@@ -126,6 +126,7 @@ SIGNATURES = [
     ("zr_graph_capture_staged", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, c_void_pp]),
     ("zr_graph_launch", C.c_int, [C.c_void_p, C.c_void_p]),
     ("zr_graph_destroy", None, [C.c_void_p]),
+    ("zr_transfer_cached_bytes", C.c_size_t, [C.c_void_p]),
     ("zr_step_graph_create", C.c_int, [C.c_void_p, c_void_pp]),
     ("zr_step_graph_launch", C.c_int, [C.c_void_p, C.POINTER(Microbatch), C.c_void_p, C.c_void_p, C.c_void_p]),
     ("zr_step_graph_info", C.c_int, [C.c_void_p, C.POINTER(StepGraphStats)]),

@@ -631,6 +631,26 @@ zr_status zr_context_create(const zr_model_desc* desc, int device, zr_context** 
         rc = set_err(ctx, ZR_E_UNSUPPORTED, "hidden %d / ffn %d must be multiples of 32", d.hidden, d.ffn_cols);
     if (!rc) rc = resolve_geometry(ctx);
     if (!rc) {
+        // The GEMM kernels address each operand with 32-bit buffer offsets
+        // (launch_gemm): every packed weight and every A operand at max_tokens
+        // rows (bf16 hi + lo planes) stays below 2 GiB, refused here rather
+        // than mid-step.
+        const int H = d.hidden, Q = ctx->q_cols, KVc = ctx->kv_cols, F = d.ffn_cols;
+        const struct {
+            const char* name;
+            int k, n;
+        } w[] = {{"w_qkv", H, Q + 2 * KVc}, {"w_o", Q, H}, {"w_gate_up", H, 2 * F}, {"w_down", F, H},
+                 {"lm_head", H, d.vocab}};
+        for (const auto& x : w)
+            if (!rc && 2 * packed_weight_elems(x.k, x.n) > 0x7fffffffull)
+                rc = set_err(ctx, ZR_E_UNSUPPORTED, "packed %s [%d, %d] exceeds the GEMM's 2 GiB operand limit", x.name,
+                             x.k, x.n);
+        const int widest_k = std::max(H, std::max(Q, F));
+        if (!rc && 2 * 2 * a_plane(d.max_tokens, widest_k) > 0x7fffffffull)
+            rc = set_err(ctx, ZR_E_UNSUPPORTED, "max_tokens %d x K %d activations exceed the GEMM's 2 GiB operand limit",
+                         d.max_tokens, widest_k);
+    }
+    if (!rc) {
         rc = zr_probe(device, nullptr);  // geometry errors are reported before device errors
         if (rc) ctx->err = g_err;
     }
@@ -1350,6 +1370,23 @@ struct zr_transfer {
 namespace zr {
 
 // a transfer with a buffer of >= floats: the smallest finished one that fits, else a new allocation
+// Finished transfers' buffers kept for reuse: at most this many (the
+// smallest beyond it are freed when a transfer is destroyed).
+constexpr size_t kXferKeep = 8;
+
+// Frees the kept buffers smaller than `floats` (all of them with floats = max).
+static void xfer_release_below(zr_context* ctx, size_t floats) {
+    auto& fl = ctx->xfer_free;
+    for (size_t i = 0; i < fl.size();) {
+        if (fl[i].second < floats) {
+            (void)hipFree(fl[i].first);
+            fl.erase(fl.begin() + i);
+        } else {
+            ++i;
+        }
+    }
+}
+
 static zr_status xfer_new(zr_context* ctx, size_t floats, zr_transfer** out) {
     zr_transfer* t = new zr_transfer();
     t->ctx = ctx;
@@ -1363,7 +1400,16 @@ static zr_status xfer_new(zr_context* ctx, size_t floats, zr_transfer** out) {
         t->floats = ctx->xfer_free[best].second;
         ctx->xfer_free.erase(ctx->xfer_free.begin() + best);
     } else {
+        // none fits: the kept buffers too small for this window go first, and
+        // when device memory is short every kept buffer before one retry
+        xfer_release_below(ctx, floats);
         e = hipMalloc(&t->buf, floats * sizeof(float));
+        if (e == hipErrorOutOfMemory) {
+            (void)hipGetLastError();
+            xfer_release_below(ctx, ~(size_t)0);
+            e = hipMalloc(&t->buf, floats * sizeof(float));
+        }
+        if (e != hipSuccess) t->buf = nullptr;
         t->floats = floats;
     }
     if (e == hipSuccess) e = hipEventCreateWithFlags(&t->copied, hipEventDisableTiming);
@@ -1454,18 +1500,26 @@ zr_status zr_kv_scatter_transfer(zr_context* ctx, zr_transfer* t, const int* blo
     if (zr_status rc = kv_copy_check(ctx, block_table, n_pages, first_offset, first_row, n_rows)) return rc;
     const int L = ctx->desc.num_layers;
     const size_t elems = (size_t)L * n_rows * ctx->kv_cols;
-    if (2 * elems + (size_t)n_pages > t->floats)
-        return set_err(ctx, ZR_E_INVALID, "page table of %d pages does not fit the KV transfer", n_pages);
+    // only the pages the rows touch travel with the transfer (at most
+    // n_rows / 16 + 2: the room every transfer keeps), addressed from the
+    // first of them
+    const int p0 = (first_offset + first_row) / kPageRows;
+    const int p1 = (first_offset + first_row + n_rows - 1) / kPageRows;
+    const int used_pages = p1 - p0 + 1;
+    if (2 * elems + (size_t)used_pages > t->floats)
+        return set_err(ctx, ZR_E_INVALID, "page table of %d pages does not fit the KV transfer", used_pages);
     ZR_HIP(ctx, hipSetDevice(ctx->device));
     float* d_k = t->buf;
     float* d_v = d_k + elems;
     int* d_table = (int*)(d_v + elems);
     // an upload is waited for; a gather's rows are on the device already (an
     // earlier launch on this stream), its copy-out only reads them
-    hipError_t e = hipMemcpyAsync(d_table, block_table, 4 * (size_t)n_pages, hipMemcpyHostToDevice, ctx->stream);
+    hipError_t e = hipMemcpyAsync(d_table, block_table + p0, 4 * (size_t)used_pages, hipMemcpyHostToDevice,
+                                  ctx->stream);
     if (e == hipSuccess && !t->to_host) e = hipStreamWaitEvent(ctx->stream, t->copied, 0);
     if (e != hipSuccess) return set_err(ctx, ZR_E_HIP, "kv transfer scatter: %s", hipGetErrorString(e));
-    if (zr_status rc = launch_kv_copy(ctx, 0, L, d_table, first_offset, first_row, n_rows, d_k, d_v, 1)) return rc;
+    const int sliced_offset = (first_offset + first_row) - p0 * kPageRows;
+    if (zr_status rc = launch_kv_copy(ctx, 0, L, d_table, sliced_offset, 0, n_rows, d_k, d_v, 1)) return rc;
     ZR_HIP(ctx, hipEventRecord(t->used, ctx->stream));
     return ZR_OK;
 }
@@ -1489,10 +1543,27 @@ void zr_transfer_destroy(zr_transfer* t) {
     // the buffer is reused once its host copy and its last kernel are done
     (void)hipEventSynchronize(t->copied);
     (void)hipEventSynchronize(t->used);
-    if (t->buf) t->ctx->xfer_free.emplace_back(t->buf, t->floats);
+    if (t->buf) {
+        auto& fl = t->ctx->xfer_free;
+        fl.emplace_back(t->buf, t->floats);
+        while (fl.size() > kXferKeep) {  // keep the largest
+            size_t smallest = 0;
+            for (size_t i = 1; i < fl.size(); ++i)
+                if (fl[i].second < fl[smallest].second) smallest = i;
+            (void)hipFree(fl[smallest].first);
+            fl.erase(fl.begin() + smallest);
+        }
+    }
     (void)hipEventDestroy(t->copied);
     (void)hipEventDestroy(t->used);
     delete t;
+}
+
+size_t zr_transfer_cached_bytes(const zr_context* ctx) {
+    if (!ctx) return 0;
+    size_t floats = 0;
+    for (const auto& fb : ctx->xfer_free) floats += fb.second;
+    return floats * sizeof(float);
 }
 
 zr_status zr_kv_gather(zr_context* ctx, const int* block_table, int n_pages, int first_offset, int first_row,

@@ -184,7 +184,8 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_kernel(
     // Copies are buffer loads into LDS: the lane's 16 B of a 1 KiB fragment
     // is a constant vector offset, the fragment's byte offset a scalar, so
     // the per-step address arithmetic stays in the scalar unit.  Offsets are
-    // 32-bit: packed operands stay below 4 GiB (launch_gemm checks).
+    // 32-bit: packed operands stay below 2 GiB (zr_context_create refuses
+    // geometries past it; launch_gemm checks again).
     const __amdgpu_buffer_rsrc_t rsrc_a = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, 0x7fffffff, 0x00020000);
     const __amdgpu_buffer_rsrc_t rsrc_w = __builtin_amdgcn_make_buffer_rsrc((void*)Wp, 0, 0x7fffffff, 0x00020000);
     const int voff = lane * 16;
@@ -664,7 +665,9 @@ zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_pack
     if (a_bytes > 0x7fffffffull || w_bytes > 0x7fffffffull)
         return set_err(ctx, ZR_E_UNSUPPORTED, "GEMM operands of %zu / %zu bytes exceed 2 GiB", a_bytes, w_bytes);
     const bool split_act = (ctx->desc.flags & ZR_FLAG_SPLIT_ACTIVATIONS) != 0;
-    if (swiglu_ksplit(m, n, k, epilogue) && c_bf16 && !c_f32 && !deferred) {
+    if (swiglu_ksplit(m, n, k, epilogue) && (!c_bf16 || c_f32 || deferred))
+        return set_err(ctx, ZR_E_INVARIANT, "K-split SwiGLU (M=%d) writes the bf16 operand only", m);
+    if (swiglu_ksplit(m, n, k, epilogue)) {
         const GemmPlan p = gemm_plan(m, n, k, epilogue);
         hipEvent_t ev;
         timing_mark_begin(ctx, kClassGemm, &ev);

@@ -66,6 +66,9 @@ def _desc(**kw):
     (dict(num_kv_heads=2), "Unsupported grouped-query attention geometry"),
     (dict(shard_start=384, shard_end=384), "Invalid shard range"),
     (dict(page_tokens=32), "page_tokens must be 16"),
+    # GEMM operands are addressed with 32-bit buffer offsets: refused up front
+    (dict(vocab=2_000_000), "packed lm_head [576, 2000000] exceeds the GEMM's 2 GiB operand limit"),
+    (dict(max_tokens=1_000_000), "max_tokens 1000000 x K 576 activations exceed the GEMM's 2 GiB operand limit"),
 ])
 def test_context_rejects_bad_geometry_with_reference_messages(kw, msg):
     # resolve_attention_shard_layout (forward_pass.rs:1257-1315) error texts

@@ -580,7 +580,7 @@ def test_gemm_matches_fp64(split, m, k, n):
                                    (32, 2048, 5632),     # the 32-session TinyLlama gate / up: K over 4 waves
                                    (1, 128, 64), (7, 256, 96),  # <= 32 rows, K over 4 waves of 1 / 2 steps
                                    (5, 96, 64),          # K = 3 steps: split-K slabs and the reduce
-                                   (100, 256, 512),      # 65-128 rows: fused, 8-wave 128 x 256 tiles
+                                   (100, 256, 512),      # 65-128 rows: fused, 64 x 256 tiles
                                    (130, 200, 96),       # fused, 128 x 256 tiles, K padded to 224
                                    (256, 4096, 14336),   # the Llama-3-8B gate / up product of the decode step
                                    (2108, 1024, 2048)])  # prefill-sized: fused 128 x 512 tiles

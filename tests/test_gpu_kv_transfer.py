@@ -92,3 +92,58 @@ def test_upload_then_import_equals_synchronous_import(kv_dtype):
     assert e.cache_seq_len() == 0
     up.close()
     ctx.close()
+
+
+def test_kept_transfer_buffers_stay_bounded():
+    """Finished transfers keep their device buffers for reuse: at most the 8
+    largest, and a window that fits none of them frees the smaller ones."""
+    ctx, geo = _ctx("f32")
+    rng = np.random.default_rng(13)
+    lib = ctx.lib
+    per_row = 2 * geo.num_layers * geo.kv_cols * 4  # K and V bytes of one row
+    for rows in range(10, 130, 8):  # 15 windows, each larger than every buffer before it
+        up = ctx.upload_kv_async(_snap(rng, geo, rows, rows, "f32"))
+        up.wait()
+        up.close()
+        cached = lib.zr_transfer_cached_bytes(ctx.h)
+        # the window's own buffer (plus its page-table room) is all that is kept
+        assert rows * per_row <= cached <= rows * per_row + 4 * 64, (rows, cached)
+    ups = [ctx.upload_kv_async(_snap(rng, geo, r, r, "f32")) for r in (5, 6, 7, 8, 9, 10, 11, 12, 13, 14)]
+    for up in ups:
+        up.wait()
+        up.close()
+    cached = lib.zr_transfer_cached_bytes(ctx.h)
+    assert cached <= 8 * (122 * per_row + 4 * 64), cached  # 8 buffers at most, the largest 122 rows
+    ctx.close()
+
+
+@pytest.mark.parametrize("first_row", [0, 37])
+def test_scatter_transfer_takes_a_whole_session_table(first_row):
+    """zr_kv_scatter_transfer with the session's full block table (spare pages
+    included) writes the same rows zr_kv_scatter does."""
+    import ctypes as C
+
+    ctx, geo = _ctx("f32")
+    rng = np.random.default_rng(14)
+    lib = ctx.lib
+    rows = 50
+    s = ctx.new_backend(4096)
+    s.kv_reserve(first_row + rows + 200)  # pages well past the window
+    table = s.block_table()
+    pages = np.ascontiguousarray([gp for _, _, _, gp in table], np.int32)
+    assert pages.size > (rows + 15) // 16 + 2
+    snap = _snap(rng, geo, rows, rows, "f32")
+    up = ctx.upload_kv_async(snap)
+    i32p = C.POINTER(C.c_int)
+    ctx.check(lib.zr_kv_scatter_transfer(ctx.h, up.h, pages.ctypes.data_as(i32p), int(pages.size), int(table[0][1]),
+                                         first_row, rows))
+    k = np.zeros((geo.num_layers, rows, geo.kv_cols), np.float32)
+    v = np.zeros_like(k)
+    f32p = C.POINTER(C.c_float)
+    ctx.check(lib.zr_kv_gather(ctx.h, pages.ctypes.data_as(i32p), int(pages.size), int(table[0][1]), first_row, rows,
+                               k.ctypes.data_as(f32p), v.ctypes.data_as(f32p)))
+    np.testing.assert_array_equal(k, snap.keys)
+    np.testing.assert_array_equal(v, snap.values)
+    up.close()
+    s.close()
+    ctx.close()
