@@ -416,53 +416,7 @@ def measure_kv_append(bench, kv_size=2, reps=5):
 
 
 # ------------------------------------------------------------- CPU baseline --
-def cpu_baseline(name):
-    """The oracle (C restatement of the CPU provider) on this host's cores: one
-    decode microbatch of the same sessions and contexts with 1 and with 2
-    layers; per-step time = T1 + (L - 1) * (T2 - T1)."""
-    import oracle as O
-
-    w = WORKLOADS[name]
-    geo = w["geo"]
-    B, ctxlens, max_seq = w["batch"], w["contexts"](), w["max_seq_len"]
-    H, V, F = geo["hidden"], geo["vocab"], geo["ffn"]
-    d = H // geo["num_heads"]
-    KV = geo["num_kv_heads"] * d
-    rng = np.random.default_rng(0)
-    block = (rng.standard_normal(1 << 20, dtype=np.float32) * 0.02)
-
-    def fill(shape):
-        return np.resize(block, shape).astype(np.float32)
-
-    def model(layers):
-        cfg = dict(hidden=H, num_heads=geo["num_heads"], num_kv_heads=geo["num_kv_heads"], num_layers=layers,
-                   vocab=V, ffn_cols=F, rms_norm_eps=1e-5, rope_base=geo["rope_base"])
-        lw = [dict(w_q=fill((H, H)), w_k=fill((H, KV)), w_v=fill((H, KV)), w_o=fill((H, H)), w_gate=fill((H, F)),
-                   w_up=fill((H, F)), w_down=fill((F, H)), attn_norm=np.ones(H, np.float32),
-                   mlp_norm=np.ones(H, np.float32)) for _ in range(layers)]
-        return O.Model(cfg, dict(embedding=fill((V, H)), final_norm=np.ones(H, np.float32), lm_head=fill((H, V)),
-                                 layers=lw))
-
-    kv_rows = np.resize(rng.standard_normal(1 << 20, dtype=np.float32), (int(ctxlens.max()), KV))
-    times = {}
-    for layers in (1, 2):
-        m = model(layers)
-        sess = []
-        for L in ctxlens:
-            s = O.Session(layers, KV, 16, max_seq)
-            s.append_all_layers(kv_rows[:L], kv_rows[:L])
-            s.position = int(L)
-            sess.append(s)
-        toks = rng.integers(0, V, B).astype(np.uint32)
-        # untimed: one session's step first, so that the thread pool start and the
-        # first touch of the weights (both once per model) stay out of T1 and T2
-        m.decode(sess[:1], toks[:1])
-        t0 = time.perf_counter()
-        m.decode(sess, toks)
-        times[layers] = time.perf_counter() - t0
-        del sess, m
-    per_layer = max(times[2] - times[1], 1e-9)
-    step_s = times[1] + (geo["num_layers"] - 1) * per_layer
+def _cpu_host():
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     model_name = "unknown"
     try:
@@ -470,12 +424,162 @@ def cpu_baseline(name):
             model_name = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), model_name)
     except OSError:
         pass
-    return dict(value=B / step_s, unit="tokens/s", cores=threads, kind="port", cpu_model=model_name,
-                affinity_cpus=len(os.sched_getaffinity(0)), nproc=os.cpu_count(),
-                sample=f"oracle decode microbatch of the same {B} sessions and contexts with 1 and 2 layers of "
-                       f"the model ({times[1]:.2f} s, {times[2]:.2f} s); step = T1 + {geo['num_layers'] - 1} x "
-                       f"(T2 - T1) = {step_s:.2f} s, each after an untimed one-session step on the same model; "
-                       f"f32 weights/KV as the reference CPU provider")
+    return dict(cores=threads, kind="port", cpu_model=model_name, affinity_cpus=len(os.sched_getaffinity(0)),
+                nproc=os.cpu_count())
+
+
+def _median_time(fn, reps, budget_s):
+    """Runs fn up to `reps` times, stopping early once `budget_s` is spent
+    (at least once); returns (median seconds, samples)."""
+    ts, spent = [], 0.0
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+        spent += ts[-1]
+        if spent >= budget_s:
+            break
+    return float(np.median(ts)), ts
+
+
+def _oracle_geometry(geo):
+    H, nh, nkv = geo["hidden"], geo["num_heads"], geo["num_kv_heads"]
+    d = H // nh
+    s0, s1 = geo.get("shard_start", 0), geo.get("shard_end", H)
+    Q = s1 - s0
+    KV = (Q // ((nh // nkv) * d)) * d
+    F = geo.get("ffn_cols", geo["ffn"])
+    cfg = dict(hidden=H, num_heads=nh, num_kv_heads=nkv, vocab=geo["vocab"], ffn_cols=F, shard_start=s0,
+               shard_end=s1, rms_norm_eps=1e-5, rope_base=geo["rope_base"])
+    return cfg, Q, KV, F
+
+
+def _oracle_model(O, geo, layers, rng):
+    """The oracle's model of the workload's shape with `layers` layers; every
+    layer references one set of f32 N(0, 0.02) matrices (the per-layer work is
+    the same, the host memory that of one layer)."""
+    cfg, Q, KV, F = _oracle_geometry(geo)
+    H, V = geo["hidden"], geo["vocab"]
+    block = rng.standard_normal(1 << 20, dtype=np.float32) * np.float32(0.02)
+
+    def fill(shape):
+        return np.resize(block, shape).astype(np.float32)
+
+    lw = dict(w_q=fill((H, Q)), w_k=fill((H, KV)), w_v=fill((H, KV)), w_o=fill((Q, H)), w_gate=fill((H, F)),
+              w_up=fill((H, F)), w_down=fill((F, H)), attn_norm=np.ones(H, np.float32), mlp_norm=np.ones(H, np.float32))
+    return O.Model(dict(cfg, num_layers=layers), dict(embedding=fill((V, H)), final_norm=np.ones(H, np.float32),
+                                                      lm_head=fill((H, V)), layers=[lw] * layers)), KV
+
+
+def cpu_baseline(name, reps=3, budget_s=10.0, full_depth=False):
+    """The oracle (C restatement of the CPU provider) on this host's cores: one
+    decode microbatch of the workload's sessions and contexts (f32 weights and
+    KV as the reference CPU provider).  full_depth: the whole model, median of
+    `reps` runs.  Otherwise (the oracle's f32 KV of every layer would not fit
+    in host memory at full depth) the same step with 1 and with 2 layers, each
+    the median of `reps` runs, and step = T1 + (L - 1) (T2 - T1)."""
+    import oracle as O
+
+    w = WORKLOADS[name]
+    geo = w["geo"]
+    B, ctxlens, max_seq = w["batch"], w["contexts"](), w["max_seq_len"]
+    rng = np.random.default_rng(0)
+    L = geo["num_layers"]
+    kv_rows = None
+
+    def step_time(layers):
+        nonlocal kv_rows
+        m, KV = _oracle_model(O, geo, layers, rng)
+        if kv_rows is None:
+            kv_rows = np.resize(rng.standard_normal(1 << 20, dtype=np.float32), (int(ctxlens.max()), KV))
+        sess = []
+        for n in ctxlens:
+            s = O.Session(layers, KV, 16, max_seq)
+            s.append_all_layers(kv_rows[:n], kv_rows[:n])
+            s.position = int(n)
+            sess.append(s)
+        toks = rng.integers(0, geo["vocab"], B).astype(np.uint32)
+        # untimed: one session's step first (thread pool start, first touch of the weights)
+        m.decode(sess[:1], toks[:1])
+        # every run appends its row and advances the sessions: contexts grow by one row a run
+        med, ts = _median_time(lambda: m.decode(sess, toks), reps, budget_s)
+        del sess, m
+        return med, ts
+
+    out = _cpu_host()
+    if full_depth:
+        step_s, ts = step_time(L)
+        sample = (f"oracle decode microbatch of the same {B} sessions and contexts through all {L} layers, median of "
+                  f"{len(ts)} runs ({', '.join(f'{t:.2f}' for t in ts)} s) after an untimed one-session step")
+    else:
+        t1, ts1 = step_time(1)
+        t2, ts2 = step_time(2)
+        step_s = t1 + (L - 1) * max(t2 - t1, 1e-9)
+        sample = (f"oracle decode microbatch of the same {B} sessions and contexts with 1 and 2 layers of the model, "
+                  f"medians of {len(ts1)} / {len(ts2)} runs (T1 {t1:.2f} s, T2 {t2:.2f} s); step = T1 + {L - 1} x "
+                  f"(T2 - T1) = {step_s:.2f} s, each after an untimed one-session step")
+    out.update(value=B / step_s, unit="tokens/s", ms_per_step=step_s * 1e3,
+               sample=sample + "; f32 weights / KV as the reference CPU provider")
+    return out
+
+
+def cpu_baseline_mixed(reps=3, budget_s=10.0):
+    """The oracle on the mixed microbatch's work as the reference CPU provider
+    does it (no ragged batching: each prefill chunk on its own, then the 60
+    decode rows as one microbatch), from a bounded sample: one 512-row chunk
+    (prefix 1000) and the 60 decode rows, each with 1 and with 2 layers
+    (medians of `reps` runs); per layer = T2 - T1, and the microbatch =
+    4 x (chunk T1 + 3 per-layer) + (decode T1 + 3 per-layer).  The chunks'
+    prefixes (0 to 1531) change only their attention, ~5% of a chunk's
+    per-layer work (the GEMMs of 512 rows are the rest)."""
+    import oracle as O
+
+    geo = MIXED_WORKLOAD["geo"]
+    rng = np.random.default_rng(0xC3)
+    dec = rng.integers(256, 4097, 60)
+    V = geo["vocab"]
+    chunk = rng.integers(0, V, 512).astype(np.uint32)
+    dtoks = rng.integers(0, V, 60).astype(np.uint32)
+    t = {}
+    for layers in (1, 2):
+        m, KV = _oracle_model(O, geo, layers, rng)
+        rows = np.resize(rng.standard_normal(1 << 20, dtype=np.float32), (int(dec.max()), KV))
+        warm = O.Session(layers, KV, 16, 8192)
+        warm.append_all_layers(rows[:16], rows[:16])
+        warm.position = 16
+        m.decode([warm], dtoks[:1])  # untimed warm-up (thread pool start, first touch of the weights)
+        tc, td = [], []
+        for _ in range(reps):  # fresh sessions every run, built outside the timing
+            s = O.Session(layers, KV, 16, 8192)
+            s.append_all_layers(rows[:1000], rows[:1000])
+            s.position = 1000
+            de = []
+            for n in dec:
+                d = O.Session(layers, KV, 16, 8192)
+                d.append_all_layers(rows[:n], rows[:n])
+                d.position = int(n)
+                de.append(d)
+            t0 = time.perf_counter()
+            m.prefill_chunk(s, chunk)
+            t1 = time.perf_counter()
+            m.decode(de, dtoks)
+            t2 = time.perf_counter()
+            tc.append(t1 - t0)
+            td.append(t2 - t1)
+            del s, de
+            if sum(tc) + sum(td) >= budget_s:
+                break
+        t[layers] = (float(np.median(tc)), float(np.median(td)), len(tc))
+        del m
+    (c1, d1, n1), (c2, d2, n2) = t[1], t[2]
+    total = 4 * (c1 + 3 * max(c2 - c1, 0.0)) + d1 + 3 * max(d2 - d1, 0.0)
+    out = _cpu_host()
+    out.update(value=2108 / total, unit="rows/s", ms_per_microbatch=total * 1e3,
+               sample=f"oracle, bounded sample: one 512-row prefill chunk (prefix 1000) and the 60 decode rows, with "
+                      f"1 and 2 layers, medians of {n1} / {n2} runs (chunk {c1:.2f} / {c2:.2f} s, decode {d1:.2f} / "
+                      f"{d2:.2f} s); microbatch = 4 chunks x 4 layers + the decode rows x 4 layers = {total:.2f} s; "
+                      f"f32 weights / KV as the reference CPU provider")
+    return out
 
 
 # pinned_windows: eviction buffers (2048-row windows, 0.54 GB each) pinned before the steps, about the
@@ -877,6 +981,14 @@ def main():
     sampling = None if a.skip_sampling else measure_sampling()
     mixed = None if a.skip_mixed else measure_mixed()
     cpu = None if a.skip_cpu else cpu_baseline(a.workload)
+    if not a.skip_cpu and a.workload == "llama3_8b_b256":
+        # the other configurations' CPU figures, beside their GPU legs
+        if bs32 is not None:
+            bs32["cpu_baseline"] = cpu_baseline("tinyllama_b32", full_depth=True)
+        if tp_shard is not None:
+            tp_shard["cpu_baseline"] = cpu_baseline("llama3_8b_tp2_b64")
+        if mixed is not None:
+            mixed["cpu_baseline"] = cpu_baseline_mixed()
     att = main_r["attention"]
     line = {
         "metric": METRIC, "value": main_r["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": a.steps,
