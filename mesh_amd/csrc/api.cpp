@@ -306,15 +306,19 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     }
     const int n_decode_tiles = (int)st->h_tiles.size();
     st->n_attn_items = (int)st->h_items.size();
-    // Prefill blocks split along their key tiles (32 keys each) so the causal
-    // triangle and unequal prefixes even out: about 512 workgroups (two
-    // resident per CU), at least 16 key tiles per split (at the 2108-row mixed
-    // microbatch, 16 to 48 tiles and no split at all measured within 3 %: the
-    // merge costs what the balance gains).  A block with several splits writes
-    // partials per 16-column group (16 / G rows x G heads, the decode tiles'
-    // layout), one item per (group, split) after the decode items, and its
-    // groups join the merge list as tiles.
+    // Prefill blocks split along their key tiles (32 keys each) when the
+    // blocks alone leave CUs idle: about 512 workgroups (two resident per CU),
+    // at least 16 key tiles per split.  Blocks that fill two workgroups per CU
+    // by themselves run unsplit (the 2108-row mixed microbatch, 64 blocks x 8
+    // kv heads: attention + merge 0.81 ms per microbatch against 1.00 with
+    // 16-tile splits, whose merge takes 0.27 ms; 8.13 against 8.26 ms per
+    // microbatch; running the prefill kernel on a second stream beside the
+    // decode rows' attention measured no faster either way).  A block with several splits writes partials per 16-column
+    // group (16 / G rows x G heads, the decode tiles' layout), one item per
+    // (group, split) after the decode items, and its groups join the merge
+    // list as tiles.
     int tps = (int)std::max<long>(16, (total_ktiles * ctx->local_kv_heads + 511) / 512);
+    if ((long)pblk.size() * ctx->local_kv_heads >= 512) tps = 1 << 30;
     if (const char* env = getenv("ZR_ATTN_PREFILL_TILES_PER_SPLIT")) tps = std::max(1, atoi(env));
     if (G > 16) tps = 1 << 30;  // a 16-column group must hold whole rows
     int next_item = st->n_attn_items;

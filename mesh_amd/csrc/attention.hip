@@ -630,15 +630,21 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attention_kernel(Prefill
     const int* bt = block_tables + (size_t)seq * a.stride;
     const size_t kv_tile = (size_t)kPageRows * D;
     const size_t v_block = (size_t)a.kv_heads * kv_tile;
-    // stage of key tile kt into ring slot `slot`: chunk group f = i NW + wave
-    // is (page pp, K or V, 1 KiB group) of the tile's two pages; a page past
-    // the window's end repeats the last page (its keys are masked)
-    auto issue = [&](int slot, int kt) {
+    // stage of a key tile into ring slot `slot` from the pool pages of its two
+    // pages (pg0, pg1): chunk group f = i NW + wave is (page pp, K or V, 1 KiB
+    // group); a page past the window's end repeats the last page (its keys are
+    // masked).  The page ids are read a tile ahead (tile_pages), so no scalar
+    // load waits in front of a stage's copies.
+    auto tile_pages = [&](int kt, int& pg0, int& pg1) {
+        pg0 = __builtin_amdgcn_readfirstlane(bt[min(2 * kt, npages - 1)]);
+        pg1 = __builtin_amdgcn_readfirstlane(bt[min(2 * kt + 1, npages - 1)]);
+    };
+    auto issue = [&](int slot, int pg0, int pg1) {
 #pragma unroll
         for (int i = 0; i < VM; ++i) {
             const int f = i * NW + wave;
             const int pp = f / (2 * VM), kv = (f / VM) & 1, grp = f % VM;
-            const int page = __builtin_amdgcn_readfirstlane(bt[min(2 * kt + pp, npages - 1)]);
+            const int page = pp ? pg1 : pg0;
             const uint16_t* src = pool + (size_t)page * a.page_elems + (kv ? v_block : 0) + (size_t)kvh * kv_tile +
                                   ((size_t)grp * 64 + lane) * 8;
             __builtin_amdgcn_global_load_lds(src, (lds_void*)&lds[slot][f * 64], 16, 0, 0);
@@ -657,9 +663,14 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attention_kernel(Prefill
     // block's first row's last visible key
     const int ntiles = kt1 - kt0;
     const int jfree = kvb + r0;  // keys <= jfree are visible to every row of the block
+    int npg0 = 0, npg1 = 0;  // pool pages of the next tile to stage
 #pragma unroll
     for (int s = 0; s < STAGES - 1; ++s)
-        if (s < ntiles) issue(s, kt0 + s);
+        if (s < ntiles) {
+            tile_pages(kt0 + s, npg0, npg1);
+            issue(s, npg0, npg1);
+        }
+    tile_pages(kt0 + STAGES - 1, npg0, npg1);
     // Q^T fragments (B operand): lane holds Q[col][16 ks + 8 h + j] * log2(e) / sqrt(d)
     // as hi + lo (scores come out in log2 units).  Loaded after the first
     // stages' copies are issued, so both latencies overlap.
@@ -684,19 +695,42 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attention_kernel(Prefill
         const int slot = t % STAGES;
         const int it = kt0 + t;
         ring_wait<VM, STAGES - 2>(min(STAGES - 2, ntiles - 1 - t));
-        if (t + STAGES - 1 < ntiles) issue((t + STAGES - 1) % STAGES, kt0 + t + STAGES - 1);
+        if (t + STAGES - 1 < ntiles) issue((t + STAGES - 1) % STAGES, npg0, npg1);
         const bf16x8* st = lds[slot];
+        // The tile's LDS fragments are read in two batches, each ahead of its
+        // consumers: K before the S = K Q^T MFMAs, V before the softmax (its
+        // reads return under the softmax's VALU work), instead of a read and a
+        // wait in front of every MFMA pair.
+        const int kbase = ((lane >> 4) & 1) * 2 * (2 * D) + (lane & 15);  // page pp = (l % 32) / 16, row l % 16
+        bf16x8 kf[D / 16];
+#pragma unroll
+        for (int ks = 0; ks < D / 16; ++ks) kf[ks] = st[kbase + (2 * ks + h) * 16];
+        __builtin_amdgcn_sched_barrier(0);  // the K reads stay ahead of the MFMAs
         // S = K Q^T over D
         f32x16 s;
 #pragma unroll
         for (int i = 0; i < 16; ++i) s[i] = 0.0f;
-        const int kbase = ((lane >> 4) & 1) * 2 * (2 * D) + (lane & 15);  // page pp = (l % 32) / 16, row l % 16
 #pragma unroll
         for (int ks = 0; ks < D / 16; ++ks) {
-            const bf16x8 kf = st[kbase + (2 * ks + h) * 16];
-            s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qh[ks], s, 0, 0, 0);
-            s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, ql[ks], s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], qh[ks], s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], ql[ks], s, 0, 0, 0);
         }
+        bf16x8 vfr[2][D / 32];
+        {
+            const bf16x4* sv = (const bf16x4*)st;
+#pragma unroll
+            for (int ks2 = 0; ks2 < 2; ++ks2) {
+                const int vbase = (2 * ks2 + 1) * 4 * D;  // 8-byte units of page ks2's V block
+#pragma unroll
+                for (int db = 0; db < D / 32; ++db) {
+                    // unit of (rows 4 q .. 4 q + 3, dim d): ((d / 32 * 4 + q) * 16 + d % 16) * 2 + d / 16 % 2
+                    const int u = ((db * 4 + h) * 16 + (lane & 15)) * 2 + ((lane >> 4) & 1);
+                    const bf16x4 v0 = sv[vbase + u], v1 = sv[vbase + u + 2 * 16 * 2];
+                    vfr[ks2][db] = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // the V reads go out before the softmax
         // online softmax step over the tile's 32 keys; the causal mask only on
         // tiles that can hold a key before the window or past the block's
         // first row (a uniform branch, kept out of the common path)
@@ -739,22 +773,22 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attention_kernel(Prefill
             lsum += pr[i];
         }
         // O += V^T P over the tile's two pages (k-steps ks2)
-        const bf16x4* sv = (const bf16x4*)st;
 #pragma unroll
         for (int ks2 = 0; ks2 < 2; ++ks2) {
             bf16x8 ph, pl;
             split_bf16x8(pr + 8 * ks2, ph, pl);
-            const int vbase = (2 * ks2 + 1) * 4 * D;  // 8-byte units of page ks2's V block
 #pragma unroll
             for (int db = 0; db < D / 32; ++db) {
-                // unit of (rows 4 q .. 4 q + 3, dim d): ((d / 32 * 4 + q) * 16 + d % 16) * 2 + d / 16 % 2
-                const int u = ((db * 4 + h) * 16 + (lane & 15)) * 2 + ((lane >> 4) & 1);
-                const bf16x4 v0 = sv[vbase + u], v1 = sv[vbase + u + 2 * 16 * 2];
-                const bf16x8 vf = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
-                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, ph, o[db], 0, 0, 0);
-                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pl, o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vfr[ks2][db], ph, o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vfr[ks2][db], pl, o[db], 0, 0, 0);
             }
         }
+        // the page ids of the tile after the one just staged, read once this
+        // tile's LDS reads have returned (scalar loads return out of order: one
+        // in flight would turn every LDS wait above into a full drain); the
+        // next ring barrier waits for them
+        __builtin_amdgcn_sched_barrier(0);
+        if (t + STAGES - 1 < ntiles) tile_pages(kt0 + t + STAGES, npg0, npg1);
     }
     lsum = pair_sum(lsum);
     if (!valid) return;
