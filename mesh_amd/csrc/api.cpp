@@ -310,10 +310,10 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     // blocks alone leave CUs idle: about 512 workgroups (two resident per CU),
     // at least 16 key tiles per split.  Blocks that fill two workgroups per CU
     // by themselves run unsplit (the 2108-row mixed microbatch, 64 blocks x 8
-    // kv heads: attention + merge 0.81 ms per microbatch against 1.00 with
-    // 16-tile splits, whose merge takes 0.27 ms; 8.13 against 8.26 ms per
-    // microbatch; running the prefill kernel on a second stream beside the
-    // decode rows' attention measured no faster either way).  A block with several splits writes partials per 16-column
+    // kv heads: 7.82-7.88 ms per microbatch against 7.97-8.02 with 33-tile
+    // splits, whose merge takes 0.19 of the 0.91 ms of attention + merge per 4
+    // layers; running the prefill kernel on a second stream beside the decode
+    // rows' attention measured no faster either way).  A block with several splits writes partials per 16-column
     // group (16 / G rows x G heads, the decode tiles' layout), one item per
     // (group, split) after the decode items, and its groups join the merge
     // list as tiles.
