@@ -466,6 +466,15 @@ U32_MAX = 0xFFFFFFFF
 PREFILL_BUCKET_TOKENS = (128, 512, 2048, 8192, 16384)        # fast_path.rs:17
 
 
+def fnv1a64(data):
+    """FNV-1a, 64-bit (Fowler, Noll, Vo; offset basis 0xcbf29ce484222325,
+    prime 0x100000001b3): the hash the library's layout hash uses."""
+    h = 0xcbf29ce484222325
+    for b in data:
+        h = ((h ^ b) * 0x100000001b3) & 0xFFFFFFFFFFFFFFFF
+    return h
+
+
 def fast_path_layout_hash(phase, batch_size_ceiling, token_ceiling, fields):
     """The layout hash of a bucket key (phase 0 decode / 1 prefill, provider
     rocm, profile rocm_fused, both ceilings) and its metadata fields, hashed
@@ -473,20 +482,14 @@ def fast_path_layout_hash(phase, batch_size_ceiling, token_ceiling, fields):
     reference's hasher (Rust's DefaultHasher) is process-local; the library
     uses FNV-1a 64 over the same items (integers as 8 little-endian bytes,
     names as their bytes then 0xff), restated here."""
-    h = 0xcbf29ce484222325
-
-    def byte(b):
-        nonlocal h
-        h = ((h ^ b) * 0x100000001b3) & 0xFFFFFFFFFFFFFFFF
+    out = bytearray()
 
     def u64(v):
-        for i in range(8):
-            byte((v >> (8 * i)) & 0xFF)
+        out.extend(int(v).to_bytes(8, "little"))
 
     def name(s):
-        for c in s.encode():
-            byte(c)
-        byte(0xFF)
+        out.extend(s.encode())
+        out.append(0xFF)
 
     u64(phase)
     name("rocm")
@@ -498,7 +501,7 @@ def fast_path_layout_hash(phase, batch_size_ceiling, token_ceiling, fields):
         u64(4)
         u64(count)
         u64(stride)
-    return h
+    return fnv1a64(bytes(out))
 
 
 def _fast_path_plan(phase, b, t, actual_batch, actual_tokens):

@@ -41,6 +41,18 @@ def test_oracle_staging_reproduces_the_reference_known_answers():
         O.fast_path_plan_decode(9, 10)
 
 
+def test_oracle_fnv1a64_matches_the_published_test_vectors():
+    # FNV-1a 64 vectors from the algorithm's published test suite (Noll's test_fnv.c)
+    assert O.fnv1a64(b"") == 0xcbf29ce484222325
+    assert O.fnv1a64(b"a") == 0xaf63dc4c8601ec8c
+    assert O.fnv1a64(b"foobar") == 0x85944171f73967e8
+    # the layout hash is FNV-1a over the key's items in order: one reordered item changes it
+    f = [("slot_sequence_lengths", 1, 4), ("slot_positions", 1, 4), ("slot_block_tables", 128, 512),
+         ("slot_mapping", 1, 4)]
+    assert O.fast_path_layout_hash(0, 1, 2048, f) != O.fast_path_layout_hash(0, 1, 2048, [f[1], f[0]] + f[2:])
+    assert O.fast_path_layout_hash(0, 1, 2048, f) != O.fast_path_layout_hash(1, 1, 2048, f)
+
+
 def test_oracle_prefill_plan_positions_and_validation_reproduce_the_reference_known_answers():
     # decode_plan_selects_smallest_supported_bucket (935-942): the fused profile replays
     assert O.fast_path_plan_decode(3, 5000)["capture_strategy"] == "replay_preferred"
