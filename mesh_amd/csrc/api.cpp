@@ -306,19 +306,32 @@ zr_status stage_microbatch(zr_context* ctx, const zr_microbatch* mb, StagedMeta*
     }
     const int n_decode_tiles = (int)st->h_tiles.size();
     st->n_attn_items = (int)st->h_items.size();
+    // A prefill workgroup takes its block's key tiles in steps of `kh`: with
+    // kh = 2 its 8 waves are two halves of 4, each half streaming every other
+    // tile for all of the block's columns, and the halves' (m, l, O) meet in
+    // LDS at the end (no partials, no merge launch).  That halves the longest
+    // block's chain of tiles at one 8-wave workgroup per CU instead of two
+    // 4-wave ones (the 2108-row mixed microbatch, Llama-3 layer: prefill
+    // kernel 89.2 against 96.9 us per layer with one half, rocprofv3 means).
+    // ZR_ATTN_PREFILL_KEY_HALVES=1 / 2 forces either form.
+    int kh = 2;
+    if (const char* env = getenv("ZR_ATTN_PREFILL_KEY_HALVES")) kh = atoi(env) == 1 ? 1 : 2;
+    st->prefill_kh = kh;
     // Prefill blocks split along their key tiles (32 keys each) when the
-    // blocks alone leave CUs idle: about 512 workgroups (two resident per CU),
-    // at least 16 key tiles per split.  Blocks that fill two workgroups per CU
-    // by themselves run unsplit (the 2108-row mixed microbatch, 64 blocks x 8
-    // kv heads: 7.82-7.88 ms per microbatch against 7.97-8.02 with 33-tile
-    // splits, whose merge takes 0.19 of the 0.91 ms of attention + merge per 4
-    // layers; running the prefill kernel on a second stream beside the decode
-    // rows' attention measured no faster either way).  A block with several splits writes partials per 16-column
-    // group (16 / G rows x G heads, the decode tiles' layout), one item per
-    // (group, split) after the decode items, and its groups join the merge
-    // list as tiles.
-    int tps = (int)std::max<long>(16, (total_ktiles * ctx->local_kv_heads + 511) / 512);
-    if ((long)pblk.size() * ctx->local_kv_heads >= 512) tps = 1 << 30;
+    // blocks alone leave CUs idle: about 512 / kh workgroups (the resident
+    // slots: 2 / kh per CU), at least 16 kh key tiles per split.  Blocks that
+    // fill the slots by themselves run unsplit (the 2108-row mixed
+    // microbatch, 64 blocks x 8 kv heads, with 4-wave workgroups: 7.82-7.88 ms
+    // per microbatch against 7.97-8.02 with 33-tile splits, whose merge takes
+    // 0.19 of the 0.91 ms of attention + merge per 4 layers; running the
+    // prefill kernel on a second stream beside the decode rows' attention
+    // measured no faster either way).  A block with several splits writes
+    // partials per 16-column group (16 / G rows x G heads, the decode tiles'
+    // layout), one item per (group, split) after the decode items, and its
+    // groups join the merge list as tiles.
+    const long slots = 512 / kh;
+    int tps = (int)std::max<long>(16 * kh, (total_ktiles * ctx->local_kv_heads + slots - 1) / slots);
+    if ((long)pblk.size() * ctx->local_kv_heads >= slots) tps = 1 << 30;
     if (const char* env = getenv("ZR_ATTN_PREFILL_TILES_PER_SPLIT")) tps = std::max(1, atoi(env));
     if (G > 16) tps = 1 << 30;  // a 16-column group must hold whole rows
     int next_item = st->n_attn_items;

@@ -596,17 +596,20 @@ __device__ inline float pair_sum(float x) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-template <int D, int STAGES>
-__global__ __launch_bounds__(256, 2) void paged_prefill_attention_kernel(PrefillArgs a,
-                                                                      const int* __restrict__ block_tables) {
-    constexpr int NW = 4;
-    constexpr int CHUNKS = 8 * D;   // 16 B chunks per stage: 2 pages x (K, V) x 16 rows x D bf16
+template <int D, int STAGES, int KH>
+__global__ __launch_bounds__(256 * KH, 2 / KH) void paged_prefill_attention_kernel(PrefillArgs a,
+                                                                               const int* __restrict__ block_tables) {
+    constexpr int NW = 4;            // column waves (32 columns each)
+    constexpr int CHUNKS = 8 * D;   // 16 B chunks per tile: 2 pages x (K, V) x 16 rows x D bf16
     constexpr int VM = D / 32;      // global_load_lds per wave per stage (1 KiB each)
     static_assert(CHUNKS == NW * VM * 64, "stage copy split");
-    __shared__ bf16x8 lds[STAGES][CHUNKS];
+    static_assert(KH == 1 || KH == 2, "key halves");
+    // a stage holds KH consecutive key tiles, tile h for the waves of half h
+    __shared__ bf16x8 lds[STAGES][KH][CHUNKS];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int half = wave / NW, wq = wave - half * NW;  // key half, column wave
     // block-uniform values in scalar registers
     const int rank = __builtin_amdgcn_readfirstlane(blockIdx.x / a.kv_heads);
     const int kvh = blockIdx.x - rank * a.kv_heads;
@@ -617,8 +620,8 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attention_kernel(Prefill
     const int kt0 = __builtin_amdgcn_readfirstlane(spl.x), kt1 = __builtin_amdgcn_readfirstlane(spl.y);
     const int h = lane >> 5;
     const int col = lane & 31;
-    const int rpw = 32 / a.G;  // query rows per wave
-    const int rloc = wave * rpw + col / a.G, g = col - (col / a.G) * a.G;
+    const int rpw = 32 / a.G;  // query rows per column wave
+    const int rloc = wq * rpw + col / a.G, g = col - (col / a.G) * a.G;
     const bool valid = rloc < nrows;
     const int kvb = __builtin_amdgcn_readfirstlane(a.kv_before[seq]);
     const int foff = __builtin_amdgcn_readfirstlane(a.first_offset[seq]);
@@ -630,24 +633,35 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attention_kernel(Prefill
     const int* bt = block_tables + (size_t)seq * a.stride;
     const size_t kv_tile = (size_t)kPageRows * D;
     const size_t v_block = (size_t)a.kv_heads * kv_tile;
-    // stage of a key tile into ring slot `slot` from the pool pages of its two
-    // pages (pg0, pg1): chunk group f = i NW + wave is (page pp, K or V, 1 KiB
-    // group); a page past the window's end repeats the last page (its keys are
-    // masked).  The page ids are read a tile ahead (tile_pages), so no scalar
-    // load waits in front of a stage's copies.
+    // Key tiles [kt0, kt1) go in steps of KH: step p holds tile kt0 + KH p + h
+    // for the waves of half h.  A half stages its own tile of each step into
+    // ring slot `slot` from the pool pages of the tile's two pages (pg0, pg1):
+    // chunk group f = i NW + wq is (page pp, K or V, 1 KiB group); a page past
+    // the window's end repeats the last page (its keys are masked, and a tile
+    // past kt1 is copied the same way and skipped), so every wave issues VM
+    // copies per stage.  The page ids are read a step ahead (tile_pages), so
+    // no scalar load waits in front of a stage's copies.
     auto tile_pages = [&](int kt, int& pg0, int& pg1) {
         pg0 = __builtin_amdgcn_readfirstlane(bt[min(2 * kt, npages - 1)]);
         pg1 = __builtin_amdgcn_readfirstlane(bt[min(2 * kt + 1, npages - 1)]);
     };
+    // Copies are buffer loads into LDS over one page: the page's base in the
+    // (scalar) buffer descriptor, the lane's 16 B as the vector offset, the
+    // K / V block, kv head and 1 KiB group as a scalar offset.
+    const uint32_t page_bytes = (uint32_t)(a.page_elems * 2);
+    const int voff = lane * 16;
     auto issue = [&](int slot, int pg0, int pg1) {
+        const __amdgpu_buffer_rsrc_t r0 =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(pool + (size_t)pg0 * a.page_elems), 0, page_bytes, 0x00020000);
+        const __amdgpu_buffer_rsrc_t r1 =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(pool + (size_t)pg1 * a.page_elems), 0, page_bytes, 0x00020000);
 #pragma unroll
         for (int i = 0; i < VM; ++i) {
-            const int f = i * NW + wave;
+            const int f = i * NW + wq;
             const int pp = f / (2 * VM), kv = (f / VM) & 1, grp = f % VM;
-            const int page = pp ? pg1 : pg0;
-            const uint16_t* src = pool + (size_t)page * a.page_elems + (kv ? v_block : 0) + (size_t)kvh * kv_tile +
-                                  ((size_t)grp * 64 + lane) * 8;
-            __builtin_amdgcn_global_load_lds(src, (lds_void*)&lds[slot][f * 64], 16, 0, 0);
+            const int soff = (int)(((kv ? v_block : 0) + (size_t)kvh * kv_tile) * 2) + grp * 1024;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(pp ? r1 : r0, (lds_void*)&lds[slot][half][f * 64], 16, voff, soff,
+                                                     0, 0);
         }
     };
 
@@ -658,19 +672,19 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attention_kernel(Prefill
         for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
     float m = -INFINITY, lsum = 0.0f;
 
-    // key tiles [kt0, kt1) of the block's window; a tile needs the causal mask
-    // only if it may hold a key before the window (first_offset) or after the
-    // block's first row's last visible key
+    // a tile needs the causal mask only if it may hold a key before the
+    // window (first_offset) or after the block's first row's last visible key
     const int ntiles = kt1 - kt0;
+    const int nsteps = (ntiles + KH - 1) / KH;
     const int jfree = kvb + r0;  // keys <= jfree are visible to every row of the block
-    int npg0 = 0, npg1 = 0;  // pool pages of the next tile to stage
+    int npg0 = 0, npg1 = 0;  // pool pages of this half's tile of the next step to stage
 #pragma unroll
     for (int s = 0; s < STAGES - 1; ++s)
-        if (s < ntiles) {
-            tile_pages(kt0 + s, npg0, npg1);
+        if (s < nsteps) {
+            tile_pages(kt0 + KH * s + half, npg0, npg1);
             issue(s, npg0, npg1);
         }
-    tile_pages(kt0 + STAGES - 1, npg0, npg1);
+    tile_pages(kt0 + KH * (STAGES - 1) + half, npg0, npg1);
     // Q^T fragments (B operand): lane holds Q[col][16 ks + 8 h + j] * log2(e) / sqrt(d)
     // as hi + lo (scores come out in log2 units).  Loaded after the first
     // stages' copies are issued, so both latencies overlap.
@@ -691,23 +705,35 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attention_kernel(Prefill
             ql[ks] = to_bf16x8(x, true);
         }
     }
-    for (int t = 0; t < ntiles; ++t) {
-        const int slot = t % STAGES;
-        const int it = kt0 + t;
-        ring_wait<VM, STAGES - 2>(min(STAGES - 2, ntiles - 1 - t));
-        if (t + STAGES - 1 < ntiles) issue((t + STAGES - 1) % STAGES, npg0, npg1);
-        const bf16x8* st = lds[slot];
-        // The tile's LDS fragments are read in two batches, each ahead of its
-        // consumers: K before the S = K Q^T MFMAs, V before the softmax (its
-        // reads return under the softmax's VALU work), instead of a read and a
-        // wait in front of every MFMA pair.
+    // One tile of a half in two parts.  phase_s: the tile's LDS fragments,
+    // read in two batches ahead of their consumers (K before the S = K Q^T
+    // MFMAs, V before the softmax, whose VALU work covers their return), and
+    // S.  phase_p: the causal mask where needed, the online softmax step and
+    // O += V^T P, on registers only.
+    f32x16 s;
+    bf16x8 vfr[2][D / 32];
+    int s_it = 0;        // key tile held in s / vfr
+    bool s_act = false;  // ... and whether it is one of the block's tiles
+    auto phase_s = [&](int t) {
+        s_it = kt0 + KH * t + half;
+        s_act = KH == 1 || s_it < kt1;
+        if (!s_act) {
+            // (s and vfr are written on every path, so the previous tile's
+            // values are not kept alive through this one)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[i] = 0.0f;
+#pragma unroll
+            for (int ks2 = 0; ks2 < 2; ++ks2)
+#pragma unroll
+                for (int db = 0; db < D / 32; ++db) vfr[ks2][db] = bf16x8{};
+            return;
+        }
+        const bf16x8* st = lds[t % STAGES][half];
         const int kbase = ((lane >> 4) & 1) * 2 * (2 * D) + (lane & 15);  // page pp = (l % 32) / 16, row l % 16
         bf16x8 kf[D / 16];
 #pragma unroll
         for (int ks = 0; ks < D / 16; ++ks) kf[ks] = st[kbase + (2 * ks + h) * 16];
         __builtin_amdgcn_sched_barrier(0);  // the K reads stay ahead of the MFMAs
-        // S = K Q^T over D
-        f32x16 s;
 #pragma unroll
         for (int i = 0; i < 16; ++i) s[i] = 0.0f;
 #pragma unroll
@@ -715,25 +741,26 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attention_kernel(Prefill
             s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], qh[ks], s, 0, 0, 0);
             s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], ql[ks], s, 0, 0, 0);
         }
-        bf16x8 vfr[2][D / 32];
-        {
-            const bf16x4* sv = (const bf16x4*)st;
+        const bf16x4* sv = (const bf16x4*)st;
 #pragma unroll
-            for (int ks2 = 0; ks2 < 2; ++ks2) {
-                const int vbase = (2 * ks2 + 1) * 4 * D;  // 8-byte units of page ks2's V block
+        for (int ks2 = 0; ks2 < 2; ++ks2) {
+            const int vbase = (2 * ks2 + 1) * 4 * D;  // 8-byte units of page ks2's V block
 #pragma unroll
-                for (int db = 0; db < D / 32; ++db) {
-                    // unit of (rows 4 q .. 4 q + 3, dim d): ((d / 32 * 4 + q) * 16 + d % 16) * 2 + d / 16 % 2
-                    const int u = ((db * 4 + h) * 16 + (lane & 15)) * 2 + ((lane >> 4) & 1);
-                    const bf16x4 v0 = sv[vbase + u], v1 = sv[vbase + u + 2 * 16 * 2];
-                    vfr[ks2][db] = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
-                }
+            for (int db = 0; db < D / 32; ++db) {
+                // unit of (rows 4 q .. 4 q + 3, dim d): ((d / 32 * 4 + q) * 16 + d % 16) * 2 + d / 16 % 2
+                const int u = ((db * 4 + h) * 16 + (lane & 15)) * 2 + ((lane >> 4) & 1);
+                const bf16x4 v0 = sv[vbase + u], v1 = sv[vbase + u + 2 * 16 * 2];
+                vfr[ks2][db] = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
             }
         }
         __builtin_amdgcn_sched_barrier(0);  // the V reads go out before the softmax
-        // online softmax step over the tile's 32 keys; the causal mask only on
-        // tiles that can hold a key before the window or past the block's
-        // first row (a uniform branch, kept out of the common path)
+    };
+    auto phase_p = [&]() {
+        if (!s_act) return;
+        const int it = s_it;
+        // the causal mask only on tiles that can hold a key before the window
+        // or past the block's first row (a uniform branch, kept out of the
+        // common path)
         if (it * 32 - foff < 0 || it * 32 + 31 - foff > jfree) {
             asm volatile("" ::: "memory");
             const int jbase = it * 32 + 4 * h - foff;
@@ -783,20 +810,102 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attention_kernel(Prefill
                 o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vfr[ks2][db], pl, o[db], 0, 0, 0);
             }
         }
-        // the page ids of the tile after the one just staged, read once this
-        // tile's LDS reads have returned (scalar loads return out of order: one
-        // in flight would turn every LDS wait above into a full drain); the
-        // next ring barrier waits for them
+    };
+    // the page ids of the step after the one just staged, read once this
+    // step's LDS reads have been issued and waited for (scalar loads return
+    // out of order: one in flight would turn every LDS wait into a full
+    // drain); the next ring barrier waits for them
+    auto prefetch_pages = [&](int t) {
         __builtin_amdgcn_sched_barrier(0);
-        if (t + STAGES - 1 < ntiles) tile_pages(kt0 + t + STAGES, npg0, npg1);
+        if (t + STAGES - 1 < nsteps) tile_pages(kt0 + KH * (t + STAGES) + half, npg0, npg1);
+    };
+    if constexpr (KH == 1) {
+        for (int t = 0; t < nsteps; ++t) {
+            ring_wait<VM, STAGES - 2>(min(STAGES - 2, nsteps - 1 - t));
+            if (t + STAGES - 1 < nsteps) issue((t + STAGES - 1) % STAGES, npg0, npg1);
+            phase_s(t);
+            phase_p();
+            prefetch_pages(t);
+        }
+    } else {
+        // Two halves in ping-pong: the ring barrier of step t and a second
+        // barrier halfway split it into phases A and B.  Half 0 runs phase_s
+        // of its tile in A and phase_p in B; half 1 runs phase_p of its
+        // previous tile in A and phase_s of this one in B (one extra A phase
+        // after the last step).  The two waves on a SIMD (one per half) then
+        // alternate MFMA-bound and VALU-bound work instead of issuing the same
+        // kind together.  phase_s of step t reads slot t % STAGES only before
+        // the ring barrier of step t + 1, which the copies into that slot
+        // (stage t + STAGES, issued at step t + 1) come after.
+        // Every wave passes two barriers per step (the ring barrier, then the
+        // halfway one), in two loops written out per half.
+        auto ring_step = [&](int t) {
+            ring_wait<VM, STAGES - 2>(min(STAGES - 2, nsteps - 1 - t));
+            if (t + STAGES - 1 < nsteps) issue((t + STAGES - 1) % STAGES, npg0, npg1);
+        };
+        auto half_barrier = [&]() {
+            __builtin_amdgcn_sched_barrier(0);
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        if (half == 0) {
+            for (int t = 0; t < nsteps; ++t) {
+                ring_step(t);
+                phase_s(t);
+                half_barrier();
+                phase_p();
+                prefetch_pages(t);
+            }
+        } else {
+            for (int t = 0; t < nsteps; ++t) {
+                ring_step(t);
+                if (t > 0) phase_p();
+                half_barrier();
+                phase_s(t);
+                prefetch_pages(t);
+            }
+            if (nsteps > 0) phase_p();
+        }
     }
     lsum = pair_sum(lsum);
+    if constexpr (KH == 2) {
+        // The halves' (m, l, O) of each column meet in LDS (the ring is free:
+        // every wave has passed its last ring wait and LDS read): half 1
+        // writes, half 0 rescales both to the larger m and adds.  A half with
+        // no visible key in its tiles (m = -inf, l = 0, O = 0) gets weight 0.
+        constexpr int CW = 2 + 16 * (D / 32);  // floats per column lane
+        static_assert((size_t)NW * CW * 64 * 4 <= sizeof(lds), "combine buffer");
+        float* cmb = (float*)&lds[0][0][0] + (size_t)wq * CW * 64 + lane;  // [wq][j][lane]
+        __syncthreads();
+        if (half == 1) {
+            cmb[0] = m;
+            cmb[64] = lsum;
+#pragma unroll
+            for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) cmb[(2 + db * 16 + i) * 64] = o[db][i];
+        }
+        __syncthreads();
+        if (half == 1) return;
+        const float m1 = cmb[0], l1 = cmb[64];
+        const float mm = fmaxf(m, m1);
+        const float a0 = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mm);
+        const float a1 = m1 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m1 - mm);
+        m = mm;
+        lsum = lsum * a0 + l1 * a1;
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[db][i] = o[db][i] * a0 + cmb[(2 + db * 16 + i) * 64] * a1;
+    }
     if (!valid) return;
     if (spl.w > 1) {
         // one split of several: (m, l, o) of this column into the item of its
         // 16-column group (16 / G rows x G heads, the decode tiles' layout);
         // attention_merge_kernel combines the splits
-        const int item = spl.z + ((wave * 32 + col) >> 4) * spl.w;
+        const int item = spl.z + ((wq * 32 + col) >> 4) * spl.w;
         float* out = a.part + (((size_t)item * a.kv_heads + kvh) * 16 + (col & 15)) * (D + 2);
         if (h == 0) {
             out[0] = m;
@@ -810,25 +919,42 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_attention_kernel(Prefill
     }
     const float inv = 1.0f / lsum;
     const int ocol0 = (kvh * a.G + g) * D;
+    if (a.out_bf16) {
+        // Lane (col, h) holds dims 32 db + 16 p + 4 h + [0, 4) (o[db][8 p + i])
+        // and 32 db + 16 p + 8 + 4 h + [0, 4) (o[db][8 p + 4 + i]) of its row;
+        // its partner lane (col, 1 - h) the other two quarters.  One
+        // permlane32 swap per float gives lane h the 8 consecutive dims
+        // 32 db + 16 p + 8 h + [0, 8), which are one 16-byte run of the
+        // fragment-packed operand (hi plane, then lo): one store each instead
+        // of eight 2-byte stores.  The partner has the same column, so the
+        // same `valid`.
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                float x[8];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(o[db][8 * p + i] * inv),
+                                                                     __float_as_uint(o[db][8 * p + 4 + i] * inv), false,
+                                                                     false);
+                    x[i] = __uint_as_float(sw[0]);
+                    x[4 + i] = __uint_as_float(sw[1]);
+                }
+                const size_t oi = a_pack_index(grow, ocol0 + db * 32 + 16 * p + 8 * h, a.q_cols);
+                *(bf16x8*)(a.out_bf16 + oi) = to_bf16x8(x, false);
+                if (a.out_lo_offset) *(bf16x8*)(a.out_bf16 + a.out_lo_offset + oi) = to_bf16x8(x, true);
+            }
+        return;
+    }
 #pragma unroll
     for (int db = 0; db < D / 32; ++db)
 #pragma unroll
         for (int i4 = 0; i4 < 4; ++i4) {
             const int d = db * 32 + 8 * i4 + 4 * h;
-            if (a.out_bf16) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    uint16_t hi, lo;
-                    split_bf16(o[db][4 * i4 + i] * inv, hi, lo);
-                    const size_t oi = a_pack_index(grow, ocol0 + d + i, a.q_cols);
-                    a.out_bf16[oi] = hi;
-                    if (a.out_lo_offset) a.out_bf16[a.out_lo_offset + oi] = lo;
-                }
-            } else {
-                const f32x4 v = {o[db][4 * i4] * inv, o[db][4 * i4 + 1] * inv, o[db][4 * i4 + 2] * inv,
-                                 o[db][4 * i4 + 3] * inv};
-                *(f32x4*)(a.out_f32 + (size_t)grow * a.q_cols + ocol0 + d) = v;
-            }
+            const f32x4 v = {o[db][4 * i4] * inv, o[db][4 * i4 + 1] * inv, o[db][4 * i4 + 2] * inv,
+                             o[db][4 * i4 + 3] * inv};
+            *(f32x4*)(a.out_f32 + (size_t)grow * a.q_cols + ocol0 + d) = v;
         }
 }
 
@@ -1056,8 +1182,12 @@ static zr_status launch_attn_t(zr_context* ctx, StagedMeta* st, int layer, const
             pa.out_lo_offset = a.out_lo_offset;
             // one workgroup per (block, kv head): kv head = block index mod kv_heads, so
             // with kv_heads dividing 8 a kv head's pages stay on the XCDs it maps to
-            hipLaunchKernelGGL((paged_prefill_attention_kernel<D, 4>), dim3(st->n_pblocks * ctx->local_kv_heads),
-                               dim3(256), 0, ctx->stream, pa, st->block_tables);
+            if (st->prefill_kh == 2)
+                hipLaunchKernelGGL((paged_prefill_attention_kernel<D, 4, 2>), dim3(st->n_pblocks * ctx->local_kv_heads),
+                                   dim3(512), 0, ctx->stream, pa, st->block_tables);
+            else
+                hipLaunchKernelGGL((paged_prefill_attention_kernel<D, 4, 1>), dim3(st->n_pblocks * ctx->local_kv_heads),
+                                   dim3(256), 0, ctx->stream, pa, st->block_tables);
             ZR_LAUNCH_CHECK(ctx);
         }
     }

@@ -566,6 +566,11 @@ static GemmCfg pick_cfg(int m, int n, int k, int epilogue = kEpiStore) {
         // sessions -4.7 / -4.2 %); at 256 rows they are slower (GEMMs 7.5
         // against 6.8 ms per step)
         if (m <= 128) return {2, 2, 1, 4, 3, false};
+        // 129-256 rows: the same 128 x 256 tiles in 16-wave blocks (32 x 64
+        // wave tiles, four waves per SIMD to cover the copies' latency):
+        // GEMM class 7.33-7.36 against 7.47-7.50 ms per 256-session step with
+        // 8 waves.  The store products measured slower in 16-wave blocks.
+        if (m <= 256) return {1, 2, 4, 4, 3, false};
         return {2, 2, 2, 4, 3, false};
     }
     // <= 32 rows: a 4-deep ring and one pass of splits over the CUs (TinyLlama
@@ -715,6 +720,7 @@ zr_status launch_gemm(zr_context* ctx, const uint16_t* a, const uint16_t* w_pack
     ZR_GEMM_FUSED_CASE(2, 4, 2, 4, 3)
     ZR_GEMM_FUSED_CASE(2, 2, 2, 4, 3)
     ZR_GEMM_FUSED_CASE(2, 2, 1, 4, 3)
+    ZR_GEMM_FUSED_CASE(1, 2, 4, 4, 3)
 #undef ZR_GEMM_FUSED_CASE
 #define ZR_GEMM_CASE(WMV, WNV, WAM, WAN, ST)                                                           \
     if (!fused && !launched && cfg.wm == WMV && cfg.wn == WNV && cfg.waves_m == WAM &&                 \

@@ -255,6 +255,7 @@ struct StagedMeta {
     int n_tiles = 0;          // attention query tiles (per kv head)
     int n_merge = 0;          // tiles with more than one split
     int n_pblocks = 0;        // prefill work units (block, key split) per kv head
+    int prefill_kh = 1;       // key halves per prefill workgroup (1: 4 waves, 2: 8 waves)
     int n_part_items = 0;     // partial items: decode items, then prefill (group, split) items
     bool pure_decode = false; // every sequence has one query row (MFMA page layout): RoPE + KV append can run
                               // inside the decode attention kernel

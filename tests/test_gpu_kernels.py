@@ -404,12 +404,17 @@ def test_chunked_prefill_attention_causal_with_prefix(kv_dtype):
     ctx.close()
 
 
-def test_prefill_blocks_llama3_heads_trimmed_windows_and_decode_rows():
+@pytest.mark.parametrize("key_halves", ["1", "2"])
+def test_prefill_blocks_llama3_heads_trimmed_windows_and_decode_rows(monkeypatch, key_halves):
     """Chunked-prefill attention at Llama-3 heads (32 q / 8 kv, head_dim 128,
     bf16 pool): chunks of 512, 100, 33 and 32 rows (whole and partial 32-row
     query blocks) against prefixes of 0, 1531, 700 and 40 rows, where the
     700-row window was trimmed by retain_suffix so its first page starts at
-    row 9; two decode rows (one also trimmed) share the microbatch."""
+    row 9; two decode rows (one also trimmed) share the microbatch.  Both
+    workgroup forms: 4 waves over every key tile, and 8 waves as two halves
+    over alternate tiles whose (m, l, O) meet in LDS (odd tile counts leave
+    the second half's last step empty)."""
+    monkeypatch.setenv("ZR_ATTN_PREFILL_KEY_HALVES", key_halves)
     geo = ModelGeometry(hidden=4096, num_heads=32, num_kv_heads=8, num_layers=1, vocab=64, ffn=64)
     ctx = DeviceContext(geo, kv_dtype="bf16", max_tokens=1024, max_seqs=8, max_pages_per_seq=160)
     ctx.create_kv_pool(1024)
@@ -455,16 +460,20 @@ def test_prefill_blocks_llama3_heads_trimmed_windows_and_decode_rows():
     ctx.close()
 
 
+@pytest.mark.parametrize("key_halves,tiles_per_split", [("1", "2"), ("2", "2"), ("2", "3")])
 @pytest.mark.parametrize("heads,kv_heads,D", [(8, 8, 64), (8, 4, 128), (32, 8, 128), (16, 2, 64)])
-def test_prefill_blocks_gqa_groups_with_forced_splits(monkeypatch, heads, kv_heads, D):
+def test_prefill_blocks_gqa_groups_with_forced_splits(monkeypatch, heads, kv_heads, D, key_halves, tiles_per_split):
     """The prefill kernel at G = 1, 2, 4 and 8 (blocks of 128, 64, 32 and 16
     rows; merge groups of 16, 8, 4 and 2 rows), with its key splits forced to
-    2 tiles (ZR_ATTN_PREFILL_TILES_PER_SPLIT) so every block of these chunks
-    goes through the partials and the merge.  The page-unaligned prefix puts
-    the causal edge inside waves: a split can start past some rows' last
-    visible key while the wave's other rows see keys in it (those columns
-    must keep a zero weight, not NaN)."""
-    monkeypatch.setenv("ZR_ATTN_PREFILL_TILES_PER_SPLIT", "2")
+    2 or 3 tiles (ZR_ATTN_PREFILL_TILES_PER_SPLIT) so every block of these
+    chunks goes through the partials and the merge, in both workgroup forms
+    (ZR_ATTN_PREFILL_KEY_HALVES; with two halves, splits of one or three tiles
+    leave the second half an empty step).  The page-unaligned prefix puts the
+    causal edge inside waves: a split can start past some rows' last visible
+    key while the wave's other rows see keys in it (those columns must keep a
+    zero weight, not NaN)."""
+    monkeypatch.setenv("ZR_ATTN_PREFILL_TILES_PER_SPLIT", tiles_per_split)
+    monkeypatch.setenv("ZR_ATTN_PREFILL_KEY_HALVES", key_halves)
     G = heads // kv_heads
     prows = 128 // G
     q_cols, kv_cols = heads * D, kv_heads * D
