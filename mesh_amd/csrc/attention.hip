@@ -514,22 +514,37 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
         // the tile has one split: normalise and write the final output here
         const int row = row0 + qi;
         const float inv = 1.0f / lsum;
+        if (a.out_bf16) {
+            // Lane (c, q4) holds dims 16 db + 4 q4 + [0, 4); lane (c, q4 ^ 1)
+            // the neighbouring 4.  One exchange per float gives the even-q4
+            // lane dims 16 db + 4 q4 + [0, 8) of an even block db and the odd
+            // one the same run of block db + 1: one 16-byte run of the
+            // fragment-packed operand per plane.  The partner has the same
+            // column, so the same col_valid.
+            static_assert(D % 32 == 0, "pairs of 16-dim blocks");
+            const bool odd = q4 & 1;
+#pragma unroll
+            for (int db = 0; db < D / 16; db += 2) {
+                float x[8];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float mine = (odd ? o[db + 1][i] : o[db][i]) * inv;
+                    const float theirs = shfl_xor((odd ? o[db][i] : o[db + 1][i]) * inv, 16);
+                    x[i] = odd ? theirs : mine;
+                    x[4 + i] = odd ? mine : theirs;
+                }
+                const int d0 = odd ? 16 * (db + 1) + 4 * (q4 - 1) : 16 * db + 4 * q4;
+                const size_t o_idx = a_pack_index(row, (kvh * a.G + g) * D + d0, a.q_cols);
+                *(bf16x8*)(a.out_bf16 + o_idx) = to_bf16x8(x, false);
+                if (a.out_lo_offset) *(bf16x8*)(a.out_bf16 + a.out_lo_offset + o_idx) = to_bf16x8(x, true);
+            }
+            return;
+        }
 #pragma unroll
         for (int db = 0; db < D / 16; ++db)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int col = (kvh * a.G + g) * D + db * 16 + q4 * 4 + i;
-                const float v = o[db][i] * inv;
-                if (a.out_bf16) {
-                    uint16_t hi, lo;
-                    split_bf16(v, hi, lo);
-                    const size_t o_idx = a_pack_index(row, col, a.q_cols);
-                    a.out_bf16[o_idx] = hi;
-                    if (a.out_lo_offset) a.out_bf16[a.out_lo_offset + o_idx] = lo;
-                } else {
-                    a.out_f32[(size_t)row * a.q_cols + col] = v;
-                }
-            }
+            for (int i = 0; i < 4; ++i)
+                a.out_f32[(size_t)row * a.q_cols + (kvh * a.G + g) * D + db * 16 + q4 * 4 + i] = o[db][i] * inv;
         return;
     }
     float* out = a.part + (((size_t)item * a.kv_heads + kvh) * 16 + c) * (D + 2);
@@ -1023,18 +1038,26 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(const float* __res
             }
         const int qi = c / G, g = c - qi * G;
         const int row = row0 + qi;
-#pragma unroll
-        for (int j = 0; j < DT; ++j) {
-            const int col = (kvh * G + g) * D + d0 + j;
-            if (out_bf16) {
-                uint16_t hi, lo;
-                split_bf16(acc[j], hi, lo);
-                const size_t o = a_pack_index(row, col, q_cols);
-                out_bf16[o] = hi;
-                if (lo_offset) out_bf16[lo_offset + o] = lo;
+        if (out_bf16) {
+            // the thread's DT consecutive dims (d0 a multiple of DT) are one
+            // contiguous run of the fragment-packed operand: one store per plane
+            static_assert(DT == 4 || DT == 8, "runs of 4 or 8 dims");
+            const size_t o = a_pack_index(row, (kvh * G + g) * D + d0, q_cols);
+            if constexpr (DT == 8) {
+                *(bf16x8*)(out_bf16 + o) = to_bf16x8(acc, false);
+                if (lo_offset) *(bf16x8*)(out_bf16 + lo_offset + o) = to_bf16x8(acc, true);
             } else {
-                out[(size_t)row * q_cols + col] = acc[j];
+                ushort4 hi, lo;
+                split_bf16(acc[0], hi.x, lo.x);
+                split_bf16(acc[1], hi.y, lo.y);
+                split_bf16(acc[2], hi.z, lo.z);
+                split_bf16(acc[3], hi.w, lo.w);
+                *(ushort4*)(out_bf16 + o) = hi;
+                if (lo_offset) *(ushort4*)(out_bf16 + lo_offset + o) = lo;
             }
+        } else {
+#pragma unroll
+            for (int j = 0; j < DT; ++j) out[(size_t)row * q_cols + (kvh * G + g) * D + d0 + j] = acc[j];
         }
         return;
     }
