@@ -77,17 +77,6 @@ template <int D> struct PageRegs<float, D> {
     }
 };
 
-__device__ inline bf16x8 to_bf16x8(const float* x, bool lo_part) {
-    bf16x8 r;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        uint16_t hi, lo;
-        split_bf16(x[j], hi, lo);
-        r[j] = __builtin_bit_cast(__bf16, lo_part ? lo : hi);
-    }
-    return r;
-}
-
 // x[0..7] as bf16 hi + lo fragments, two values per v_cvt_pk_bf16_f32 (the
 // same bits as split_bf16)
 __device__ inline void split_bf16x8(const float* x, bf16x8& hi, bf16x8& lo) {

@@ -275,24 +275,45 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm_kernel(
     }
 
     if constexpr (SWIGLU) {
+        // Each 32 x 32 tile of H (silu(g) * u of a gate / up tile pair) goes
+        // through a per-wave LDS tile (row pitch 33): written in the product's
+        // layout (lane = column), read back as 8 consecutive columns of a row
+        // per lane, which is one 16-byte run of the fragment-packed operand.
+        // One store per plane and 8 values instead of 8 2-byte stores
+        // (256-session decode step: the 2-byte stores cost 0.33 ms of GEMM).
+        // F = N / 2 is a multiple of 32 (the planner's SwiGLU requires N % 64
+        // == 0), so a run is either whole or past F.
+        constexpr int TP = 32 * 33;
+        static_assert((size_t)NW * TP * sizeof(float) <= sizeof(lds), "transpose tiles fit the ring");
         const int F = N / 2;
         const size_t plane = a_plane(M, F);
+        float* tp = (float*)&lds[0][0][0] + wave * TP;
+        __syncthreads();  // every wave is past its last ring read
 #pragma unroll
         for (int mt = 0; mt < WM; ++mt)
 #pragma unroll
             for (int p = 0; p < WN / 2; ++p) {
-                const int j = ((nt_blk + wn_idx * WN + 2 * p) >> 1) * 32 + (lane & 31);
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int m = m0 + (wm_idx * WM + mt) * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+                for (int i = 0; i < 16; ++i)
+                    tp[(8 * (i >> 2) + 4 * (lane >> 5) + (i & 3)) * 33 + (lane & 31)] =
+                        swiglu(acc[mt][2 * p][i], acc[mt][2 * p + 1][i]);
+                __syncthreads();
+                const int j0 = ((nt_blk + wn_idx * WN + 2 * p) >> 1) * 32;
+                const int mb = m0 + (wm_idx * WM + mt) * 32;
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const int r = (lane + 64 * t) >> 2, grp = lane & 3;
+                    const int m = mb + r, j = j0 + 8 * grp;
                     if (m < M && j < F) {
-                        uint16_t hi, lo;
-                        split_bf16(swiglu(acc[mt][2 * p][i], acc[mt][2 * p + 1][i]), hi, lo);
+                        float x[8];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) x[e] = tp[r * 33 + 8 * grp + e];
                         const size_t o = a_pack_index(m, j, F);
-                        H[o] = hi;
-                        if (h_lo) H[plane + o] = lo;
+                        *(bf16x8*)(H + o) = to_bf16x8(x, false);
+                        if (h_lo) *(bf16x8*)(H + plane + o) = to_bf16x8(x, true);
                     }
                 }
+                __syncthreads();  // the tile is read before the next one is written
             }
     } else {
         float* out = C + (size_t)split * split_stride;

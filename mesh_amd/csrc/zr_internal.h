@@ -39,6 +39,20 @@ __device__ inline void split_bf16(float x, uint16_t& hi, uint16_t& lo) {
     lo = __builtin_bit_cast(uint16_t, (__bf16)(x - (float)h));
 }
 
+// x[0..7] as the hi (lo_part false) or lo halves of split_bf16, one bf16x8
+// (8 consecutive columns of the fragment-packed operand below are one 16-byte
+// run)
+__device__ inline bf16x8 to_bf16x8(const float* x, bool lo_part) {
+    bf16x8 r;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        uint16_t hi, lo;
+        split_bf16(x[j], hi, lo);
+        r[j] = __builtin_bit_cast(__bf16, lo_part ? lo : hi);
+    }
+    return r;
+}
+
 // GEMM A operands (bf16 activations) are stored fragment-packed for the
 // 32x32x16 MFMA: the [rows, K] matrix (K a multiple of 32, rows padded to
 // 32) is a sequence of 1 KiB fragments (32-row tile mt, 16-column slice kt16)
