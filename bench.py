@@ -271,7 +271,8 @@ class GpuDecodeBench:
         try:
             for _ in range(warmup):
                 pipe.step()
-            pipe.finish()
+            if warmup:
+                pipe.finish()  # (a pipeline that has run no step has nothing to finish)
             t0 = time.perf_counter()
             for _ in range(count):
                 pipe.step()
