@@ -461,10 +461,11 @@ def test_prefill_blocks_llama3_heads_trimmed_windows_and_decode_rows(monkeypatch
 
 
 @pytest.mark.parametrize("key_halves,tiles_per_split", [("1", "2"), ("2", "2"), ("2", "3")])
-@pytest.mark.parametrize("heads,kv_heads,D", [(8, 8, 64), (8, 4, 128), (32, 8, 128), (16, 2, 64)])
+@pytest.mark.parametrize("heads,kv_heads,D", [(8, 8, 64), (8, 4, 128), (32, 8, 128), (16, 2, 64), (16, 1, 64),
+                                           (16, 1, 128)])
 def test_prefill_blocks_gqa_groups_with_forced_splits(monkeypatch, heads, kv_heads, D, key_halves, tiles_per_split):
-    """The prefill kernel at G = 1, 2, 4 and 8 (blocks of 128, 64, 32 and 16
-    rows; merge groups of 16, 8, 4 and 2 rows), with its key splits forced to
+    """The prefill kernel at G = 1, 2, 4, 8 and 16 (blocks of 128, 64, 32, 16
+    and 8 rows; merge groups of 16, 8, 4, 2 and 1 rows), with its key splits forced to
     2 or 3 tiles (ZR_ATTN_PREFILL_TILES_PER_SPLIT) so every block of these
     chunks goes through the partials and the merge, in both workgroup forms
     (ZR_ATTN_PREFILL_KEY_HALVES; with two halves, splits of one or three tiles
