@@ -339,6 +339,18 @@ def measure(name, steps, warmup, kv_dtype="bf16"):
     attn_bytes_per_launch = (kv_bytes + qo_bytes) / max(attn_launches, 1)
     attn_ms_per_launch = ms_t[0] / max(attn_launches, 1)
     attn_gbs = attn_bytes_per_launch / (attn_ms_per_launch * 1e-3) / 1e9
+    # the read ceiling of the same launch: a read-only copy of its page stream
+    # (zr_kv_read_probe) over one eager step's work list, every layer, 3
+    # launches each; its K/V bytes over its time against the kernel's
+    ctx, lib = bench.ctx, bench.ctx.lib
+    probe_ms = []
+    for layer in range(g.num_layers):
+        ms = C.c_double()
+        ctx.check(lib.zr_kv_read_probe(ctx.h, bench.staged[warmup], layer, 3, C.byref(ms)))
+        probe_ms.append(ms.value)
+    probe_kv_bytes = bench.kv_rows[warmup] * g.kv_cols * 2 * kv_size
+    probe_gbs = probe_kv_bytes / (np.mean(probe_ms) * 1e-3) / 1e9
+    attn_kv_gbs = (kv_bytes / max(attn_launches, 1)) / (attn_ms_per_launch * 1e-3) / 1e9
     sb = np.mean([step_bytes(g, B, r, kv_size) for r in timed_rows])
     nb = BREAKDOWN_STEPS
     gemm_tflops = gemm_flops(g, B) * nb / (ms_b[1] * 1e-3) / 1e12 if ms_b[1] > 0 else 0.0
@@ -352,7 +364,13 @@ def measure(name, steps, warmup, kv_dtype="bf16"):
         kernel_ms_per_step={"attention": ms_b[0] / nb, "gemm": ms_b[1] / nb, "norm_rope_kv": ms_b[2] / nb,
                             "other": ms_b[3] / nb},
         attention=dict(launches=attn_launches, bytes_per_launch=attn_bytes_per_launch,
-                       avg_ms=attn_ms_per_launch, achieved_gbs=attn_gbs, frac=attn_gbs / HBM_PEAK_GBS),
+                       avg_ms=attn_ms_per_launch, achieved_gbs=attn_gbs, frac=attn_gbs / HBM_PEAK_GBS,
+                       read_ceiling=dict(entry="zr_kv_read_probe", gbs=probe_gbs, ms_per_launch=float(np.mean(probe_ms)),
+                                         kv_bytes_per_launch=probe_kv_bytes, kernel_kv_gbs=attn_kv_gbs,
+                                         frac=attn_kv_gbs / probe_gbs,
+                                         note="K/V bytes per launch over the time of a read-only copy of the "
+                                              "attention launch's page stream (same grid, work records and "
+                                              "16-byte nontemporal page loads; no Q, softmax, MFMA or output)")),
         gemm=dict(launches=n_b[1] // nb, ms_per_step=ms_b[1] / nb, achieved_tflops=gemm_tflops,
                   frac=gemm_tflops / MFMA_BF16_PEAK_TFLOPS,
                   weight_gbs=(gemm_flops(g, B) / B) * nb / (ms_b[1] * 1e-3) / 1e9 if ms_b[1] > 0 else 0.0),
@@ -953,7 +971,8 @@ def main():
         r = measure("tinyllama_b32", a.steps, a.warmup)
         bs32 = dict(value=r["tokens_per_s"], unit="tokens/s", ms_per_step=r["ms_per_step"],
                     workload=r["workload"], step_roofline_frac=r["step_roofline_frac"],
-                    attention_gbs=r["attention"]["achieved_gbs"], kernel_ms_per_step=r["kernel_ms_per_step"],
+                    attention_gbs=r["attention"]["achieved_gbs"],
+                    attention_read_ceiling=r["attention"]["read_ceiling"], kernel_ms_per_step=r["kernel_ms_per_step"],
                     gemm_tflops=r["gemm"]["achieved_tflops"], gemm_weight_gbs=r["gemm"]["weight_gbs"],
                     host_path=r["host_path"], eager=r["eager"], pipeline=r["pipeline"])
     tp_shard = None
@@ -961,7 +980,8 @@ def main():
         r = measure("llama3_8b_tp2_b64", max(4, a.steps // 2), 2)
         tp_shard = dict(value=r["tokens_per_s"], unit="tokens/s (one shard's step)", ms_per_step=r["ms_per_step"],
                         workload=r["workload"], step_roofline_frac=r["step_roofline_frac"],
-                        attention_gbs=r["attention"]["achieved_gbs"], kernel_ms_per_step=r["kernel_ms_per_step"],
+                        attention_gbs=r["attention"]["achieved_gbs"],
+                    attention_read_ceiling=r["attention"]["read_ceiling"], kernel_ms_per_step=r["kernel_ms_per_step"],
                         gemm_tflops=r["gemm"]["achieved_tflops"], gemm_weight_gbs=r["gemm"]["weight_gbs"],
                         host_path=r["host_path"])
     f32_kv = None
@@ -976,7 +996,9 @@ def main():
                       roofline={"bound": "hbm", "kernel": "paged_attention_kernel<float>",
                                 "achieved": att32["achieved_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                 "frac": att32["frac"], "bytes_per_launch": att32["bytes_per_launch"],
-                                "avg_ms": att32["avg_ms"], "launches": att32["launches"], "sizeof_kv": 4})
+                                "avg_ms": att32["avg_ms"], "launches": att32["launches"], "sizeof_kv": 4,
+                                "read_ceiling_gbs": att32["read_ceiling"]["gbs"],
+                                "frac_of_read_ceiling": att32["read_ceiling"]["frac"]})
     soak = None if a.skip_soak else measure_soak(max(4, a.steps // 2), 2)
     kv_snapshot = None if a.skip_kv_snapshot else measure_kv_snapshot()
     sampling = None if a.skip_sampling else measure_sampling()
@@ -1008,7 +1030,8 @@ def main():
         "roofline": {"bound": "hbm", "kernel": "paged_attention_kernel", "achieved": att["achieved_gbs"],
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": att["frac"], "traffic": measured_traffic(),
                      "bytes_per_launch": att["bytes_per_launch"], "avg_ms": att["avg_ms"],
-                     "launches": att["launches"]},
+                     "launches": att["launches"], "read_ceiling_gbs": att["read_ceiling"]["gbs"],
+                     "frac_of_read_ceiling": att["read_ceiling"]["frac"]},
         "step_roofline": {"tokens_per_s": main_r["step_roofline_tokens_per_s"], "frac": main_r["step_roofline_frac"],
                           "bytes_per_step": main_r["step_bytes"]},
         "kernel_ms_per_step": main_r["kernel_ms_per_step"],

@@ -229,6 +229,17 @@ zr_status zr_rope_kv_write(zr_context* ctx, zr_staged* st, int layer, const floa
  * staged microbatch for `layer`: d_q device [sum q_len, q_cols] f32 (RoPE'd),
  * d_out device [sum q_len, q_cols] f32. */
 zr_status zr_attention(zr_context* ctx, zr_staged* st, int layer, const float* d_q, float* d_out);
+/* Diagnostic, no counterpart in the reference: the HBM rate the decode
+ * attention launch's access pattern can reach.  Launches `repeats` times
+ * (1..10000) a read-only copy of that launch's page stream for the staged
+ * microbatch at `layer` -- the same grid, work records, block tables and
+ * 16-byte nontemporal page loads in the same order, without Q, softmax, MFMA
+ * or output -- and returns the mean launch time in *mean_ms (HIP events on
+ * the context stream; synchronises).  Needs the MFMA page layout (head_dim 64
+ * or 128) and decode attention items in `st`.  For a bench or a profiler:
+ * dividing the launch's K/V bytes by it gives the ceiling that the attention
+ * kernel's own rate is measured against. */
+zr_status zr_kv_read_probe(zr_context* ctx, zr_staged* st, int layer, int repeats, double* mean_ms);
 /* The RopeKvWrite and Attention stages in one launch, for a staged
  * microbatch whose sequences each have one query row (decode; the MFMA page
  * layout): d_qkv as for zr_rope_kv_write, d_out as for zr_attention.  The

@@ -134,6 +134,7 @@ SIGNATURES = [
     ("zr_pack", C.c_int, [C.c_void_p, C.POINTER(Microbatch), c_int_p, c_int_p, c_int_p, c_int_p, c_int_p]),
     ("zr_rope_kv_write", C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int]),
     ("zr_attention", C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]),
+    ("zr_kv_read_probe", C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.POINTER(C.c_double)]),
     ("zr_rope_attention", C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int]),
     ("zr_kv_gather", C.c_int, [C.c_void_p, c_int_p, C.c_int, C.c_int, C.c_int, C.c_int, c_f32_p, c_f32_p]),
     ("zr_kv_scatter", C.c_int, [C.c_void_p, c_int_p, C.c_int, C.c_int, C.c_int, C.c_int, c_f32_p, c_f32_p]),

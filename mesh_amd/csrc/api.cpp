@@ -1311,6 +1311,15 @@ zr_status zr_attention(zr_context* ctx, zr_staged* s, int layer, const float* d_
     return rc;
 }
 
+zr_status zr_kv_read_probe(zr_context* ctx, zr_staged* s, int layer, int repeats, double* mean_ms) {
+    StagedMeta* st = (StagedMeta*)s;
+    if (!ctx || !st || !mean_ms) return set_global_err(ZR_E_INVALID, "null argument");
+    if (layer < 0 || layer >= ctx->desc.num_layers) return set_err(ctx, ZR_E_INVALID, "Invalid layer index: %d", layer);
+    if (repeats <= 0 || repeats > 10000) return set_err(ctx, ZR_E_INVALID, "repeats %d outside 1..10000", repeats);
+    if (!ctx->kv_pool) return set_err(ctx, ZR_E_INVALID, "KV pool not created");
+    return launch_kv_read_probe(ctx, st, layer, repeats, mean_ms);
+}
+
 // the page window of a gather / scatter lies inside the table and the pool
 static zr_status kv_copy_check(zr_context* ctx, const int* block_table, int n_pages, int first_offset, int first_row,
                                int n_rows) {

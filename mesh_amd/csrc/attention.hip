@@ -1349,6 +1349,129 @@ static zr_status launch_attn_generic(zr_context* ctx, StagedMeta* st, int layer,
     return ZR_OK;
 }
 
+// XOR of every 32-bit word a page set holds (keeps the probe's loads live)
+__device__ inline unsigned xor4(uint4 w) { return w.x ^ w.y ^ w.z ^ w.w; }
+template <int D>
+__device__ inline unsigned page_fold(const PageRegs<uint16_t, D>& r) {
+    unsigned x = 0;
+#pragma unroll
+    for (int b = 0; b < D / 32; ++b) x ^= xor4(__builtin_bit_cast(uint4, r.k[b])) ^ xor4(__builtin_bit_cast(uint4, r.v[b]));
+    return x;
+}
+template <int D>
+__device__ inline unsigned page_fold(const PageRegs<float, D>& r) {
+    unsigned x = 0;
+#pragma unroll
+    for (int b = 0; b < D / 32; ++b)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            x ^= xor4(__builtin_bit_cast(uint4, r.k[b][h])) ^ xor4(__builtin_bit_cast(uint4, r.v[b][h]));
+    return x;
+}
+
+// Read-only twin of paged_attention_kernel's page stream, for measuring the
+// HBM rate its access pattern can reach: the same grid and block -> (item,
+// kv head) mapping, the same work records and block tables, the same
+// nontemporal 16-byte loads of each page's K and V tiles through a ring of
+// RING page sets loaded in the same order (the first RING - 2 from the
+// record, then two ahead per pair), and no Q, softmax, MFMA or output: each
+// page set is folded into one XOR word, and each workgroup writes one.
+template <typename KV, int D, int RING>
+__global__ __launch_bounds__(64) void kv_read_probe_kernel(AttnArgs a, unsigned* out) {
+    const int lane = threadIdx.x;
+    const int per_grp = 8 * a.kv_heads;
+    const int rem = blockIdx.x % per_grp;
+    const int kvh = rem >> 3;
+    const int rank = (blockIdx.x / per_grp) * 8 + (rem & 7);
+    unsigned acc = 0;
+    if (rank < a.n_items) {
+        const int4 r0 = a.rec[3 * rank], r1 = a.rec[3 * rank + 1], r2 = a.rec[3 * rank + 2];
+        const int seq = r0.x, nq = r0.z, page_b = r0.w, page_e = r1.x;
+        if (nq > 0) {
+            const KV* pool = (const KV*)a.pool;
+            const int* bt = a.block_tables + (size_t)seq * a.stride;
+            const size_t kv_tile = (size_t)kPageRows * D;
+            const size_t v_block = (size_t)a.kv_heads * kv_tile;
+            PageRegs<KV, D> ring[RING];
+            auto load_page = [&](PageRegs<KV, D>& r, int pool_page) {
+                const KV* base = pool + (size_t)pool_page * a.page_elems + (size_t)kvh * kv_tile;
+                r.load(base, base + v_block, lane);
+            };
+            auto load_or_shared = [&](PageRegs<KV, D>& r, int p) {
+                const int pg = bt[min(p, page_e - 1)];
+                load_page(r, p < page_e ? pg : 0);
+            };
+            auto fold = [&](const PageRegs<KV, D>& r) { acc ^= page_fold(r); };
+            static_assert(RING - 2 <= 4, "the record holds the first 4 pages");
+            const int first_pages[4] = {r2.x, r2.y, r2.z, r2.w};
+#pragma unroll
+            for (int r = 0; r < RING - 2; ++r) load_page(ring[r], first_pages[r]);
+            for (int p = page_b; p < page_e; p += RING) {
+#pragma unroll
+                for (int r = 0; r < RING; r += 2) {
+                    const int pp = p + r;
+                    if (pp >= page_e) break;
+                    load_or_shared(ring[(r + RING - 2) % RING], pp + RING - 2);
+                    load_or_shared(ring[(r + RING - 1) % RING], pp + RING - 1);
+                    fold(ring[r]);
+                    if (pp + 1 < page_e) fold(ring[r + 1]);
+                }
+            }
+        }
+    }
+    if (lane == 0) out[blockIdx.x] = acc;
+}
+
+template <typename KV, int D>
+static zr_status launch_kv_read_probe_t(zr_context* ctx, StagedMeta* st, int layer, int repeats, double* mean_ms) {
+    AttnArgs a{};
+    a.page_elems = (size_t)2 * ctx->kv_cols * kPageRows;
+    a.pool = (const KV*)ctx->kv_pool + (size_t)layer * ctx->n_pages * a.page_elems;
+    a.block_tables = st->block_tables;
+    a.stride = st->stride;
+    a.rec = st->attn_rec;
+    a.n_items = st->grid_items;
+    a.kv_heads = ctx->local_kv_heads;
+    const dim3 grid(((st->grid_items + 7) / 8) * 8 * ctx->local_kv_heads);
+    // one word per workgroup, in the attention partials' workspace
+    if ((size_t)grid.x > ctx->attn_part_floats)
+        return set_err(ctx, ZR_E_OOM, "attention partial workspace too small for %u probe words", grid.x);
+    hipEvent_t e0, e1;
+    ZR_HIP(ctx, hipEventCreate(&e0));
+    hipError_t e = hipEventCreate(&e1);
+    if (e != hipSuccess) {
+        (void)hipEventDestroy(e0);
+        return set_err(ctx, ZR_E_HIP, "hipEventCreate: %s", hipGetErrorString(e));
+    }
+    e = hipEventRecord(e0, ctx->stream);
+    for (int i = 0; i < repeats && e == hipSuccess; ++i) {
+        hipLaunchKernelGGL((kv_read_probe_kernel<KV, D, sizeof(KV) == 4 ? 4 : 6>), grid, dim3(64), 0, ctx->stream, a,
+                           (unsigned*)ctx->attn_part);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipEventRecord(e1, ctx->stream);
+    if (e == hipSuccess) e = hipEventSynchronize(e1);
+    float ms = 0.0f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (e != hipSuccess) return set_err(ctx, ZR_E_HIP, "KV read probe: %s", hipGetErrorString(e));
+    *mean_ms = (double)ms / repeats;
+    return ZR_OK;
+}
+
+zr_status launch_kv_read_probe(zr_context* ctx, StagedMeta* st, int layer, int repeats, double* mean_ms) {
+    if (ctx->plain_kv || (ctx->head_dim != 64 && ctx->head_dim != 128))
+        return set_err(ctx, ZR_E_UNSUPPORTED, "the KV read probe follows the MFMA page layout (head_dim 64 or 128)");
+    if (st->grid_items == 0) return set_err(ctx, ZR_E_INVALID, "the staged microbatch has no decode attention items");
+    const bool bf = ctx->desc.kv_dtype == ZR_DTYPE_BF16;
+    if (ctx->head_dim == 64)
+        return bf ? launch_kv_read_probe_t<uint16_t, 64>(ctx, st, layer, repeats, mean_ms)
+                  : launch_kv_read_probe_t<float, 64>(ctx, st, layer, repeats, mean_ms);
+    return bf ? launch_kv_read_probe_t<uint16_t, 128>(ctx, st, layer, repeats, mean_ms)
+              : launch_kv_read_probe_t<float, 128>(ctx, st, layer, repeats, mean_ms);
+}
+
 zr_status launch_attention(zr_context* ctx, StagedMeta* st, int layer, const float* q, float* out,
                            uint16_t* out_bf16) {
     if (st->total_q == 0) return ZR_OK;

@@ -366,6 +366,9 @@ zr_status launch_attention(zr_context* ctx, StagedMeta* st, int layer, const flo
                            uint16_t* out_bf16);
 // Pure decode microbatches (st->pure_decode): RoPE + KV append and attention in
 // one launch, q and the new K / V rows read from the QKV product's slabs.
+// Times `repeats` launches of a read-only copy of the decode attention
+// launch's page stream for staged microbatch `st` at `layer` (mean ms).
+zr_status launch_kv_read_probe(zr_context* ctx, StagedMeta* st, int layer, int repeats, double* mean_ms);
 zr_status launch_attention_rope(zr_context* ctx, StagedMeta* st, int layer, const Slabs& qkv, int rope,
                                 float* out_f32, uint16_t* out_bf16);
 zr_status launch_kv_copy(zr_context* ctx, int layer_begin, int layer_end, const int* d_table,

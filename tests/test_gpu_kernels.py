@@ -286,6 +286,34 @@ def _snapshot(k, v):
 
 
 @pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
+def test_kv_read_probe_times_the_decode_page_stream(kv_dtype):
+    """zr_kv_read_probe (a diagnostic with no reference counterpart) launches
+    a read-only copy of the decode attention launch's page stream: it returns
+    a positive mean time, refuses out-of-range arguments, and leaves the pool
+    as it was."""
+    B, ctxlens, order, Q, K, V = c1_inputs()
+    ctx, geo = tiny_llama_attn_ctx(kv_dtype, 512, order)
+    backends = [ctx.new_backend() for _ in range(B)]
+    for b, L, k, v in zip(backends, ctxlens, K, V):
+        if L > 1:
+            b.import_kv_cache(_snapshot(k[:-1], v[:-1]))
+    st = stage_mixed(ctx, backends, [1] * B)  # (staging reserves each session's decode row)
+    before = [b.export_kv_cache() for b in backends]
+    ms = C.c_double()
+    ctx.check(ctx.lib.zr_kv_read_probe(ctx.h, st, 0, 5, C.byref(ms)))
+    assert 0.0 < ms.value < 100.0
+    assert ctx.lib.zr_kv_read_probe(ctx.h, st, 1, 5, C.byref(ms)) == _lib.ZR_E_INVALID  # one layer
+    assert ctx.lib.zr_kv_read_probe(ctx.h, st, 0, 0, C.byref(ms)) == _lib.ZR_E_INVALID
+    assert ctx.lib.zr_kv_read_probe(ctx.h, st, 0, 5, None) == _lib.ZR_E_INVALID
+    ctx.lib.zr_staged_destroy(st)
+    for b, snap in zip(backends, before):
+        after = b.export_kv_cache()
+        np.testing.assert_array_equal(after.keys, snap.keys)
+        np.testing.assert_array_equal(after.values, snap.values)
+    ctx.close()
+
+
+@pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
 def test_c1_paged_gqa_decode_attention_and_append(kv_dtype):
     ctx, backends, (B, ctxlens, order, Q, K, V), out = run_c1(kv_dtype)
     bf = kv_dtype == "bf16"
