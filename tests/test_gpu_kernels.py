@@ -371,6 +371,112 @@ def test_c1_decode_attention_merges_many_splits(monkeypatch, pages_per_split):
     ctx.close()
 
 
+def _attend(kv_dtype, prefixes, new_rows, q_len=None):
+    """TinyLlama attention shape (32 q heads, 4 kv heads, D 64): session s
+    imports prefixes[s] = (K, V) rows, stages q_len[s] rows (default 1) whose
+    q / K / V come from new_rows[s] ([q_len, 2048 + 512]), appends them
+    (rope off) and attends.  Returns the f32 output [rows, 2048]."""
+    B = len(prefixes)
+    q_len = [1] * B if q_len is None else q_len
+    ctx, _ = tiny_llama_attn_ctx(kv_dtype, 512)
+    backends = [ctx.new_backend() for _ in range(B)]
+    for b, (k, v) in zip(backends, prefixes):
+        if k.shape[0]:
+            b.import_kv_cache(_snapshot(k, v))
+    st = stage_mixed(ctx, backends, q_len)
+    qkv = np.ascontiguousarray(np.concatenate(new_rows, 0), np.float32)
+    d_qkv = DeviceBuffer.from_numpy(ctx, qkv)
+    d_q = DeviceBuffer(ctx, 4 * qkv.shape[0] * 2048)
+    d_o = DeviceBuffer(ctx, 4 * qkv.shape[0] * 2048)
+    ctx.check(ctx.lib.zr_rope_kv_write(ctx.h, st, 0, d_qkv.ptr, d_q.ptr, 0))
+    ctx.check(ctx.lib.zr_attention(ctx.h, st, 0, d_q.ptr, d_o.ptr))
+    out = d_o.download(np.float32, (qkv.shape[0], 2048))
+    ctx.lib.zr_staged_destroy(st)
+    ctx.close()
+    return out
+
+
+def _kv_as_stored(x, kv_dtype):
+    return O.round_bf16(x) if kv_dtype == "bf16" else x
+
+
+@pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
+def test_attention_single_key_returns_its_value(kv_dtype):
+    """Closed form: a query that sees one key gets that key's value row
+    (softmax weight 1).  Decode rows of sessions with no prefix, and with a
+    bf16 pool also the first row of a 16-row prefill chunk (the prefill
+    kernel: row 0 sees key 0 only).  bf16 pool: exact; f32 pool (V split into
+    bf16 hi + lo inside the MFMA): within 1e-5."""
+    rng = np.random.default_rng(0x51)
+    B = 6
+    rows = [rng.standard_normal((1, 2560), dtype=np.float32) for _ in range(B)]
+    empty = (np.zeros((0, 256), np.float32), np.zeros((0, 256), np.float32))
+    out = _attend(kv_dtype, [empty] * B, rows)
+    for s in range(B):
+        v = _kv_as_stored(rows[s][0, 2304:], kv_dtype)
+        want = np.concatenate([v[(h // 8) * 64:(h // 8 + 1) * 64] for h in range(32)])
+        if kv_dtype == "bf16":
+            np.testing.assert_array_equal(out[s], want)
+        else:
+            np.testing.assert_allclose(out[s], want, rtol=1e-5, atol=1e-6)
+    if kv_dtype == "bf16":
+        chunk = rng.standard_normal((16, 2560), dtype=np.float32)
+        out = _attend(kv_dtype, [empty], [chunk], q_len=[16])
+        v = _kv_as_stored(chunk[0, 2304:], kv_dtype)
+        want = np.concatenate([v[(h // 8) * 64:(h // 8 + 1) * 64] for h in range(32)])
+        np.testing.assert_array_equal(out[0], want)
+
+
+@pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
+def test_attention_identical_keys_average_the_values(kv_dtype):
+    """Closed form: when every visible key is the same vector, every score is
+    the same and the output is the plain mean of the visible values.  Windows
+    of 1..400 keys (one page to several splits, a partial last page)."""
+    rng = np.random.default_rng(0x52)
+    lens = [1, 15, 16, 17, 129, 400]
+    prefixes, rows, want = [], [], []
+    for L in lens:
+        k = rng.standard_normal(256, dtype=np.float32)
+        V = rng.standard_normal((L, 256), dtype=np.float32)
+        prefixes.append((np.tile(k, (L - 1, 1)), V[:-1]))
+        row = np.concatenate([rng.standard_normal(2048, dtype=np.float32), k, V[-1]])[None]
+        rows.append(row)
+        m = _kv_as_stored(V, kv_dtype).astype(np.float64).mean(0)
+        want.append(np.concatenate([m[(h // 8) * 64:(h // 8 + 1) * 64] for h in range(32)]))
+    out = _attend(kv_dtype, prefixes, rows)
+    for s, L in enumerate(lens):
+        np.testing.assert_allclose(out[s], want[s], rtol=1e-5, atol=1e-5, err_msg=f"L={L}")
+
+
+@pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
+def test_attention_dominant_key_selects_its_value(kv_dtype):
+    """Closed form at saturation: one key scores ~100 (natural log units)
+    above every other visible key, so its softmax weight is 1 to within
+    e^-90 and the output is its value row.  The dominant key sits at the
+    window's start, middle or end, across several splits."""
+    rng = np.random.default_rng(0x53)
+    L = 300
+    prefixes, rows, want = [], [], []
+    for pos in (0, 151, L - 1):
+        q = rng.standard_normal(2048, dtype=np.float32)
+        K = 0.1 * rng.standard_normal((L, 256), dtype=np.float32)
+        V = rng.standard_normal((L, 256), dtype=np.float32)
+        for kvh in range(4):  # key `pos` of kv head kvh: 100 sqrt(d) / |q_h|^2 q_h of its first q head
+            qh = q[kvh * 8 * 64:(kvh * 8 + 1) * 64]
+            K[pos, kvh * 64:(kvh + 1) * 64] = 100.0 * 8.0 * qh / float(qh @ qh)
+        q = q.copy()
+        for h in range(32):  # every q head of a kv head asks the same question
+            q[h * 64:(h + 1) * 64] = q[(h // 8) * 8 * 64:((h // 8) * 8 + 1) * 64]
+        prefixes.append((K[:-1], V[:-1]))
+        rows.append(np.concatenate([q, K[-1], V[-1]])[None])
+        v = _kv_as_stored(V[pos], kv_dtype)
+        want.append(np.concatenate([v[(h // 8) * 64:(h // 8 + 1) * 64] for h in range(32)]))
+    out = _attend(kv_dtype, prefixes, rows)
+    assert np.isfinite(out).all()
+    for s in range(3):
+        np.testing.assert_allclose(out[s], want[s], rtol=1e-5, atol=1e-6)
+
+
 def test_c1_raw_page_row_holds_appended_kv_in_pool_layout():
     ctx, backends, (B, ctxlens, order, Q, K, V), out = run_c1("f32")
     s = 3
