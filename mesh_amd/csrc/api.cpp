@@ -1284,9 +1284,17 @@ zr_status zr_pack(zr_context* ctx, const zr_microbatch* mb, int* cu_q, int* cu_k
     return ZR_OK;
 }
 
+// A staged microbatch's arrays index this context's pool and workspaces: one
+// staged by another context is refused before anything launches.
+static zr_status staged_for(zr_context* ctx, const StagedMeta* st) {
+    if (st->ctx != ctx) return set_err(ctx, ZR_E_INVALID, "staged microbatch of another context");
+    return ZR_OK;
+}
+
 zr_status zr_rope_kv_write(zr_context* ctx, zr_staged* s, int layer, const float* d_qkv, float* d_q_out, int rope) {
     StagedMeta* st = (StagedMeta*)s;
     if (!ctx || !st || !d_qkv || !d_q_out) return set_global_err(ZR_E_INVALID, "null argument");
+    if (zr_status rc = staged_for(ctx, st)) return rc;
     if (layer < 0 || layer >= ctx->desc.num_layers) return set_err(ctx, ZR_E_INVALID, "Invalid layer index: %d", layer);
     zr_status rc = launch_rope_kv_write(ctx, st, layer, d_qkv, d_q_out, rope);
     if (!rc) ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -1296,6 +1304,7 @@ zr_status zr_rope_kv_write(zr_context* ctx, zr_staged* s, int layer, const float
 zr_status zr_rope_attention(zr_context* ctx, zr_staged* s, int layer, const float* d_qkv, float* d_out, int rope) {
     StagedMeta* st = (StagedMeta*)s;
     if (!ctx || !st || !d_qkv || !d_out) return set_global_err(ZR_E_INVALID, "null argument");
+    if (zr_status rc = staged_for(ctx, st)) return rc;
     if (layer < 0 || layer >= ctx->desc.num_layers) return set_err(ctx, ZR_E_INVALID, "Invalid layer index: %d", layer);
     zr_status rc = launch_attention_rope(ctx, st, layer, Slabs(d_qkv), rope, d_out, nullptr);
     if (!rc) ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -1305,6 +1314,7 @@ zr_status zr_rope_attention(zr_context* ctx, zr_staged* s, int layer, const floa
 zr_status zr_attention(zr_context* ctx, zr_staged* s, int layer, const float* d_q, float* d_out) {
     StagedMeta* st = (StagedMeta*)s;
     if (!ctx || !st || !d_q || !d_out) return set_global_err(ZR_E_INVALID, "null argument");
+    if (zr_status rc = staged_for(ctx, st)) return rc;
     if (layer < 0 || layer >= ctx->desc.num_layers) return set_err(ctx, ZR_E_INVALID, "Invalid layer index: %d", layer);
     zr_status rc = launch_attention(ctx, st, layer, d_q, d_out, nullptr);
     if (!rc) ZR_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -1314,6 +1324,7 @@ zr_status zr_attention(zr_context* ctx, zr_staged* s, int layer, const float* d_
 zr_status zr_kv_read_probe(zr_context* ctx, zr_staged* s, int layer, int repeats, double* mean_ms) {
     StagedMeta* st = (StagedMeta*)s;
     if (!ctx || !st || !mean_ms) return set_global_err(ZR_E_INVALID, "null argument");
+    if (zr_status rc = staged_for(ctx, st)) return rc;
     if (layer < 0 || layer >= ctx->desc.num_layers) return set_err(ctx, ZR_E_INVALID, "Invalid layer index: %d", layer);
     if (repeats <= 0 || repeats > 10000) return set_err(ctx, ZR_E_INVALID, "repeats %d outside 1..10000", repeats);
     if (!ctx->kv_pool) return set_err(ctx, ZR_E_INVALID, "KV pool not created");

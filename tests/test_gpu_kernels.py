@@ -313,6 +313,28 @@ def test_kv_read_probe_times_the_decode_page_stream(kv_dtype):
     ctx.close()
 
 
+def test_op_entries_refuse_a_microbatch_staged_by_another_context():
+    """A staged microbatch indexes its own context's pool and workspaces: the
+    op-level entries refuse one staged by another context (ZR_E_INVALID)
+    before launching anything."""
+    B, ctxlens, order, Q, K, V = c1_inputs()
+    ctx_a, _ = tiny_llama_attn_ctx("bf16", 512, order)
+    ctx_b, _ = tiny_llama_attn_ctx("bf16", 512, order)
+    backends = [ctx_a.new_backend() for _ in range(2)]
+    st = stage_mixed(ctx_a, backends, [1, 1])
+    d_qkv = DeviceBuffer(ctx_b, 4 * 2 * 2560)
+    d_out = DeviceBuffer(ctx_b, 4 * 2 * 2048)
+    ms = C.c_double()
+    lib = ctx_b.lib
+    assert lib.zr_attention(ctx_b.h, st, 0, d_qkv.ptr, d_out.ptr) == _lib.ZR_E_INVALID
+    assert lib.zr_rope_kv_write(ctx_b.h, st, 0, d_qkv.ptr, d_out.ptr, 1) == _lib.ZR_E_INVALID
+    assert lib.zr_rope_attention(ctx_b.h, st, 0, d_qkv.ptr, d_out.ptr, 1) == _lib.ZR_E_INVALID
+    assert lib.zr_kv_read_probe(ctx_b.h, st, 0, 1, C.byref(ms)) == _lib.ZR_E_INVALID
+    ctx_a.lib.zr_staged_destroy(st)
+    ctx_b.close()
+    ctx_a.close()
+
+
 @pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
 def test_c1_paged_gqa_decode_attention_and_append(kv_dtype):
     ctx, backends, (B, ctxlens, order, Q, K, V), out = run_c1(kv_dtype)
