@@ -58,21 +58,24 @@ template <int D> struct PageRegs<uint16_t, D> {
     }
 };
 
+// f32 pool (page_order): the same 8 values per lane and 32 dims, as two
+// 16 B halves that each come from one contiguous 1 KiB wave run (K: dims
+// 8 g + [0, 4) then + [4, 8); V: dim d then d + 16, 4 tokens each).
 template <int D> struct PageRegs<float, D> {
     f32x4 k[D / 32][2];
     f32x4 v[D / 32][2];
     __device__ inline void load(const float* kp, const float* vp, int lane) {
 #pragma unroll
         for (int kb = 0; kb < D / 32; ++kb) {
-            const f32x4* src = (const f32x4*)(kp + ((size_t)kb * kWave + lane) * 8);
+            const f32x4* src = (const f32x4*)(kp + (size_t)kb * kWave * 8) + lane;
             k[kb][0] = __builtin_nontemporal_load(src);
-            k[kb][1] = __builtin_nontemporal_load(src + 1);
+            k[kb][1] = __builtin_nontemporal_load(src + kWave);
         }
 #pragma unroll
         for (int vb = 0; vb < D / 32; ++vb) {
-            const f32x4* src = (const f32x4*)(vp + ((size_t)vb * kWave + lane) * 8);
+            const f32x4* src = (const f32x4*)(vp + (size_t)vb * kWave * 8) + lane;
             v[vb][0] = __builtin_nontemporal_load(src);
-            v[vb][1] = __builtin_nontemporal_load(src + 1);
+            v[vb][1] = __builtin_nontemporal_load(src + kWave);
         }
     }
 };
@@ -457,10 +460,10 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
             for (int i = 0; i < NE; ++i) {
                 const int e = lane + 64 * i;
                 if (e < D / 2) {
-                    store_elem(kt + k_off(r, e), av[i][0]);
-                    store_elem(kt + k_off(r, e + D / 2), av[i][1]);
+                    store_elem(kt + page_order<KV>(k_off(r, e)), av[i][0]);
+                    store_elem(kt + page_order<KV>(k_off(r, e + D / 2)), av[i][1]);
                 } else if (e < D / 2 + D) {
-                    store_elem(vt + v_off(r, e - D / 2), av[i][0]);
+                    store_elem(vt + page_order<KV>(v_off(r, e - D / 2)), av[i][0]);
                 }
             }
             ring_barrier<0>();  // the row is written before its page is read

@@ -1,6 +1,7 @@
 // Ragged-batch packing, fused RoPE + paged-KV append, and the KV handoff
-// gather/scatter kernels.  The KV pool's page layouts (MFMA fragment and
-// plain) are k_off / v_off / k_off_of / v_off_of in zr_internal.h.
+// gather/scatter kernels.  The KV pool's page layouts (MFMA fragment, with
+// f32 pools' page_order, and plain) are k_off / v_off / page_order /
+// k_off_of / v_off_of in zr_internal.h.
 #include "zr_internal.h"
 
 namespace zr {
@@ -159,8 +160,8 @@ __global__ __launch_bounds__(256) void rope_kv_write_kernel(
                 q_out[(size_t)t * q_cols + head * D + i + half] = b;
             } else {
                 KV* kt = kpage + (size_t)head * kPageRows * D;
-                store_elem(kt + k_off_of(r, i, D, plain), a);
-                store_elem(kt + k_off_of(r, i + half, D, plain), b);
+                store_elem(kt + k_off_of<KV>(r, i, D, plain), a);
+                store_elem(kt + k_off_of<KV>(r, i + half, D, plain), b);
             }
         } else {
             const int c = j - nq - nk;
@@ -176,7 +177,7 @@ __global__ __launch_bounds__(256) void rope_kv_write_kernel(
             for (int sl = 1; sl < kSlabsAhead; ++sl)
                 if (sl < qkv_n) vv += lv[sl];
             for (int sl = kSlabsAhead; sl < qkv_n; ++sl) vv += src[sl * qkv_slab];
-            store_elem(vt + v_off_of(r, d, D, plain), vv);
+            store_elem(vt + v_off_of<KV>(r, d, D, plain), vv);
         }
     }
 }
@@ -263,8 +264,8 @@ __global__ __launch_bounds__(64) void rope_kv_write_vec_kernel(
             KV* kt = kpage + (size_t)hh * kPageRows * D;
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                store_elem(kt + k_off_of(r, i0 + u, D, plain), a[u]);
-                store_elem(kt + k_off_of(r, half + i0 + u, D, plain), b[u]);
+                store_elem(kt + k_off_of<KV>(r, i0 + u, D, plain), a[u]);
+                store_elem(kt + k_off_of<KV>(r, half + i0 + u, D, plain), b[u]);
             }
         }
     } else {
@@ -284,7 +285,7 @@ __global__ __launch_bounds__(64) void rope_kv_write_vec_kernel(
         }
         const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
 #pragma unroll
-        for (int u = 0; u < 4; ++u) store_elem(vt + v_off_of(r, d + u, D, plain), vv[u]);
+        for (int u = 0; u < 4; ++u) store_elem(vt + v_off_of<KV>(r, d + u, D, plain), vv[u]);
     }
 }
 
@@ -364,6 +365,40 @@ struct alignas(8 * sizeof(KV)) Group8 {
     KV x[8];
 };
 
+// Group g of a K or V block: its elements 8 g .. 8 g + 7 in the bf16 order
+// (k_off / v_off), which f32 pools hold as two runs of 4, 256 elements apart
+// (page_order).
+template <typename KV>
+__device__ inline Group8<KV> get_group(const KV* blk, size_t g) {
+    if constexpr (sizeof(KV) == 2) {
+        return ((const Group8<KV>*)blk)[g];
+    } else {
+        const KV* p = blk + page_order<KV>(8 * g);
+        const f32x4 a = *(const f32x4*)p, b = *(const f32x4*)(p + 256);
+        Group8<KV> r;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            r.x[i] = a[i];
+            r.x[4 + i] = b[i];
+        }
+        return r;
+    }
+}
+template <typename KV>
+__device__ inline void put_group(KV* blk, size_t g, const Group8<KV>& x) {
+    if constexpr (sizeof(KV) == 2) {
+        ((Group8<KV>*)blk)[g] = x;
+    } else {
+        KV* p = blk + page_order<KV>(8 * g);
+        *(f32x4*)p = f32x4{x.x[0], x.x[1], x.x[2], x.x[3]};
+        *(f32x4*)(p + 256) = f32x4{x.x[4], x.x[5], x.x[6], x.x[7]};
+    }
+}
+template <typename KV>
+__device__ inline KV* group_elem(KV* blk, size_t g, int i) {
+    return blk + page_order<KV>(8 * g + i);
+}
+
 template <typename KV>
 __device__ inline void store4(KV* p, f32x4 x);
 template <>
@@ -434,7 +469,6 @@ __global__ __launch_bounds__(256) void kv_copy_kernel(KV* __restrict__ pool, siz
     }
     for (int which = 0; which < 2; ++which) {
         KV* blk = kblk + (size_t)which * kv_cols * kPageRows;
-        Group8<KV>* gp0 = (Group8<KV>*)blk;
         // row r of the page is row rbase + r >= 0 of layer l's f32 rows (r_lo <= r < r_hi)
         float* rows = (which ? v : k) + (size_t)l * n_rows * kv_cols;
         if (which) __syncthreads();  // the K block's LDS reads are done
@@ -451,9 +485,9 @@ __global__ __launch_bounds__(256) void kv_copy_kernel(KV* __restrict__ pool, siz
                 const int g = cg >> 4, r = cg & 15;  // K group cg = g * 16 + r
                 KV* t = tile + r * pitch + h * D + 8 * g;
                 if (to_pool) {
-                    if (r >= r_lo && r < r_hi) gp0[gi] = *(const Group8<KV>*)t;
+                    if (r >= r_lo && r < r_hi) put_group(blk, gi, *(const Group8<KV>*)t);
                 } else {
-                    *(Group8<KV>*)t = gp0[gi];
+                    *(Group8<KV>*)t = get_group(blk, gi);
                 }
             }
         } else {
@@ -462,12 +496,12 @@ __global__ __launch_bounds__(256) void kv_copy_kernel(KV* __restrict__ pool, siz
                 const int h = qi / (D / 2), cg0 = (qi - h * (D / 2)) * 4;
                 const int q = (cg0 >> 4) & 3, d0 = (cg0 >> 6) * 32 + (cg0 & 15);
                 const int r0 = 4 * q;
-                Group8<KV>* gp = gp0 + (size_t)h * tile8 + cg0;
+                const size_t g0 = (size_t)h * tile8 + cg0;  // groups g0 .. g0 + 3
                 KV* t = tile + r0 * pitch + h * D + d0;
                 if (!to_pool) {
                     Group8<KV> gr[4];
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) gr[j] = gp[j];
+                    for (int j = 0; j < 4; ++j) gr[j] = get_group(blk, g0 + j);
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -485,13 +519,13 @@ __global__ __launch_bounds__(256) void kv_copy_kernel(KV* __restrict__ pool, siz
                             gr[j].x[4 + i] = t[i * pitch + 16 + j];
                         }
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) gp[j] = gr[j];
+                    for (int j = 0; j < 4; ++j) put_group(blk, g0 + j, gr[j]);
                 } else if (r0 + 3 >= r_lo && r0 < r_hi) {
                     for (int j = 0; j < 4; ++j)
                         for (int i = 0; i < 4; ++i) {
                             if (r0 + i < r_lo || r0 + i >= r_hi) continue;
-                            gp[j].x[i] = t[i * pitch + j];
-                            gp[j].x[4 + i] = t[i * pitch + 16 + j];
+                            *group_elem(blk, g0 + j, i) = t[i * pitch + j];
+                            *group_elem(blk, g0 + j, 4 + i) = t[i * pitch + 16 + j];
                         }
                 }
             }

@@ -114,14 +114,36 @@ struct StagedMeta;  // device copy of one microbatch's metadata
 //           one P.V MFMA operand lane; dims d and d + 16 sit side by side, so a
 //           lane loads both with one 16 B (bf16) load and a wave reads 1 KiB
 //           contiguous per 32 dims.
+// (f32 pools then reorder each 512-element block: page_order below.)
 // Plain layout (pools whose head_dim the MFMA kernels do not take): both tiles
 // row-major [16 rows][head_dim].
 __device__ inline size_t k_off(int t, int d) { return ((size_t)(d >> 3) * kPageRows + t) * 8 + (d & 7); }
 __device__ inline size_t v_off(int t, int d) {
     return (((((size_t)(d >> 5) * 4 + (t >> 2)) * 16 + (d & 15)) * 2 + ((d >> 4) & 1)) * 4) + (t & 3);
 }
-__device__ inline size_t k_off_of(int t, int d, int D, int plain) { return plain ? (size_t)t * D + d : k_off(t, d); }
-__device__ inline size_t v_off_of(int t, int d, int D, int plain) { return plain ? (size_t)t * D + d : v_off(t, d); }
+// f32 pools keep those offsets' 512-element blocks (one 64-lane x 8-element
+// wave fragment each: 32 dims of K, or of V, of one kv head's page) but hold
+// each lane's 8 elements as two runs of 4, half-major: lane l's elements 0-3
+// at 4 l, 4-7 at 256 + 4 l.  Each 16-byte lane load of a wave is then one
+// contiguous 1 KiB run, as in a bf16 page (with lane-contiguous 32-byte
+// groups every f32 load spanned 2 KiB for 1 KiB of data).
+template <typename KV>
+__device__ inline size_t page_order(size_t e) {
+    if constexpr (sizeof(KV) == 2) {
+        return e;
+    } else {
+        const size_t w = e & 511;
+        return (e & ~(size_t)511) | ((w & 4) << 6) | ((w >> 3) << 2) | (w & 3);
+    }
+}
+template <typename KV>
+__device__ inline size_t k_off_of(int t, int d, int D, int plain) {
+    return plain ? (size_t)t * D + d : page_order<KV>(k_off(t, d));
+}
+template <typename KV>
+__device__ inline size_t v_off_of(int t, int d, int D, int plain) {
+    return plain ? (size_t)t * D + d : page_order<KV>(v_off(t, d));
+}
 template <typename T> __device__ inline void store_elem(T* p, float x);
 template <> __device__ inline void store_elem<float>(float* p, float x) { *p = x; }
 template <> __device__ inline void store_elem<uint16_t>(uint16_t* p, float x) { *p = f32_to_bf16_bits(x); }

@@ -499,21 +499,39 @@ def test_attention_dominant_key_selects_its_value(kv_dtype):
         np.testing.assert_allclose(out[s], want[s], rtol=1e-5, atol=1e-6)
 
 
-def test_c1_raw_page_row_holds_appended_kv_in_pool_layout():
-    ctx, backends, (B, ctxlens, order, Q, K, V), out = run_c1("f32")
+def _f32_page_order(e):
+    """f32 pools: each 512-element block (64 lanes x 8) holds lane l's
+    elements 0-3 at 4 l and 4-7 at 256 + 4 l."""
+    w = e & 511
+    return (e & ~511) | ((w & 4) << 6) | ((w >> 3) << 2) | (w & 3)
+
+
+@pytest.mark.parametrize("kv_dtype", ["f32", "bf16"])
+def test_c1_raw_page_row_holds_appended_kv_in_pool_layout(kv_dtype):
+    """The appended row sits in its page at the documented offsets: K element
+    (t, d) at ((d/8)·16 + t)·8 + d%8, V element at ((((d/32)·4 + t/4)·16 +
+    d%16)·2 + (d/16)%2)·4 + t%4 of its kv head's tile, f32 pools with each
+    512-element block in the half-major order of _f32_page_order."""
+    ctx, backends, (B, ctxlens, order, Q, K, V), out = run_c1(kv_dtype)
     s = 3
     table = backends[s].block_table()
     last = table[-1]
     row = (last[1] + last[2] - 1)  # row of the newest token inside its page
-    page = np.zeros(2 * 256 * 16, np.float32)
+    f32 = kv_dtype == "f32"
+    page = np.zeros(2 * 256 * 16, np.float32 if f32 else np.uint16)
     pages = np.array([last[3]], np.int32)
     ctx.check(ctx.lib.zr_kv_read_pages(ctx.h, 0, i32p(pages), 1, page.ctypes.data))
+    if not f32:  # bf16 bits -> f32
+        page = (page.astype(np.uint32) << 16).view(np.float32)
+    order_of = _f32_page_order if f32 else (lambda e: e)
+    want_k = K[s][-1] if f32 else O.round_bf16(K[s][-1])
+    want_v = V[s][-1] if f32 else O.round_bf16(V[s][-1])
     kblk, vblk = page[:4096].reshape(4, 16 * 64), page[4096:].reshape(4, 16 * 64)
     for h in range(4):
         for d in range(64):
-            assert kblk[h][((d // 8) * 16 + row) * 8 + d % 8] == K[s][-1][h * 64 + d]
+            assert kblk[h][order_of(((d // 8) * 16 + row) * 8 + d % 8)] == want_k[h * 64 + d]
             v_off = ((((d // 32) * 4 + row // 4) * 16 + d % 16) * 2 + (d // 16) % 2) * 4 + row % 4
-            assert vblk[h][v_off] == V[s][-1][h * 64 + d]
+            assert vblk[h][order_of(v_off)] == want_v[h * 64 + d]
     ctx.close()
 
 
