@@ -526,9 +526,12 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
                     x[4 + i] = odd ? mine : theirs;
                 }
                 const int d0 = odd ? 16 * (db + 1) + 4 * (q4 - 1) : 16 * db + 4 * q4;
+                // nontemporal: the lines need not stay in L2 beside the page
+                // stream (256-session step: launch 276.5-277.8 -> 271.1-271.7 us)
                 const size_t o_idx = a_pack_index(row, (kvh * a.G + g) * D + d0, a.q_cols);
-                *(bf16x8*)(a.out_bf16 + o_idx) = to_bf16x8(x, false);
-                if (a.out_lo_offset) *(bf16x8*)(a.out_bf16 + a.out_lo_offset + o_idx) = to_bf16x8(x, true);
+                __builtin_nontemporal_store(to_bf16x8(x, false), (bf16x8*)(a.out_bf16 + o_idx));
+                if (a.out_lo_offset)
+                    __builtin_nontemporal_store(to_bf16x8(x, true), (bf16x8*)(a.out_bf16 + a.out_lo_offset + o_idx));
             }
             return;
         }
