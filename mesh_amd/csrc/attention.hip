@@ -326,7 +326,9 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
         const int row = row0;
         const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
         // Every column reads a q head of the row (g < G), so the loads need
-        // no guard: columns past the tile are zeroed after the sums.
+        // no guard: columns past the tile are zeroed after the sums.  The
+        // slabs are read nontemporal, like the pages (256-session step:
+        // launch 275.4-277.9 -> 272.8-273.5 us).
         const float* qp = a.qkv + (size_t)row * a.qkv_stride + (size_t)(kvh * a.G + g) * D + q4 * 8;
         // (cos, sin) of the lane's dims 32 kb + 8 q4 + j for kb < D / 64 (the
         // rotate-half partner of block kb is kb + D / 64), fetched together
@@ -347,8 +349,8 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
         }
 #pragma unroll
         for (int kb = 0; kb < D / 32; ++kb) {
-            qx[kb][0] = *(const f32x4*)(qp + kb * 32);
-            qx[kb][1] = *(const f32x4*)(qp + kb * 32 + 4);
+            qx[kb][0] = __builtin_nontemporal_load((const f32x4*)(qp + kb * 32));
+            qx[kb][1] = __builtin_nontemporal_load((const f32x4*)(qp + kb * 32 + 4));
         }
         constexpr int CH = D == 64 ? 8 : 4;  // slabs per batch of loads
         // The tile's last split appends the new row.  Lane e (and e + 64 ...)
@@ -388,9 +390,9 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(AttnArgs a) {
                 for (int kb = 0; kb < D / 32; ++kb)
 #pragma unroll
                     for (int h = 0; h < 2; ++h)
-                        t[u][kb][h] = s0 + u < a.qkv_n
-                                          ? *(const f32x4*)(qp + (size_t)(s0 + u) * a.qkv_slab + kb * 32 + 4 * h)
-                                          : zero;
+                        t[u][kb][h] = s0 + u < a.qkv_n ? __builtin_nontemporal_load((const f32x4*)(
+                                                              qp + (size_t)(s0 + u) * a.qkv_slab + kb * 32 + 4 * h))
+                                                        : zero;
 #pragma unroll
             for (int u = 0; u < CH; ++u)
                 if (s0 + u < a.qkv_n)
