@@ -147,7 +147,9 @@ typedef struct {
 zr_status zr_forward(zr_context* ctx, const zr_microbatch* mb, uint32_t* out_tokens,
                      float* out_logits, float* out_partials);
 
-/* Device-resident variant: metadata staged once into device memory. */
+/* Device-resident variant: metadata staged once into device memory.  Every
+ * entry below that takes a zr_staged returns ZR_E_INVALID ("staged
+ * microbatch of another context") for one staged by another context. */
 typedef struct zr_staged zr_staged;
 zr_status zr_stage(zr_context* ctx, const zr_microbatch* mb, zr_staged** out);
 void zr_staged_destroy(zr_staged* st);
