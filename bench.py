@@ -395,8 +395,11 @@ def measure(name, steps, warmup, kv_dtype="bf16"):
     result["host_path"] = dict(
         entry="zrh_decode_step_batch", steps=steps, ms_per_step=dt_host / steps * 1e3,
         tokens_per_s=B * steps / dt_host,
-        includes="host page tables and window trim, zr_stage (metadata H2D), pack_kernel, the forward pass, "
-                 "greedy token D2H and the stream synchronisation, per step")
+        includes="host page tables and window trim, metadata staged and copied up with the ids, pack_kernel + "
+                 "rope_table_kernel and the forward pass (replayed from the context's step graph from the third "
+                 "step of the same sequence count; the warm-up steps run eagerly and capture it), greedy token "
+                 "D2H and the stream synchronisation, per step",
+        replays=bench.ctx.forward_replay_info()["launches"])
     bench.close()
     return result
 

@@ -143,7 +143,12 @@ typedef struct {
  * arrays, each nullable: out_tokens [num_seqs] greedy ids (first index on
  * ties), out_logits [num_seqs, vocab] f32, out_partials
  * [num_layers][2][sum q_len][hidden] f32 = per-layer pre-all-reduce
- * (o_partial, down_partial) (forward_pass.rs:2265, 2290). */
+ * (o_partial, down_partial) (forward_pass.rs:2265, 2290).  A decode
+ * microbatch (one row per sequence, MFMA page layout) asking for out_tokens
+ * only is replayed from the context's step graph once its sequence count has
+ * run three calls in a row: the same kernels on the same metadata as the
+ * eager pass, so the same ids bit for bit, without its per-kernel launches
+ * (zr_forward_replay_info). */
 zr_status zr_forward(zr_context* ctx, const zr_microbatch* mb, uint32_t* out_tokens,
                      float* out_logits, float* out_partials);
 
@@ -215,6 +220,12 @@ zr_status zr_step_graph_launch(zr_step_graph* g, const zr_microbatch* mb, const 
                                uint32_t* d_out_tokens, uint32_t* h_out_tokens);
 zr_status zr_step_graph_info(const zr_step_graph* g, zr_step_graph_stats* out);
 void zr_step_graph_destroy(zr_step_graph* g);
+/* Diagnostic, no counterpart in the reference: the step graph that
+ * zr_forward replays decode steps from (one row per sequence, MFMA page
+ * layout, greedy ids only -- no logits or partials -- once the same sequence
+ * count has run three calls in a row; ZR_FORWARD_REPLAY=0 keeps zr_forward
+ * eager).  Zeros before the first replay. */
+zr_status zr_forward_replay_info(const zr_context* ctx, zr_step_graph_stats* out);
 
 /* ------------------------------------------------------ op-level entries --- */
 /* Ragged packing on the GPU: device outputs cu_q/cu_k [num_seqs+1],

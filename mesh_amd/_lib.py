@@ -130,6 +130,7 @@ SIGNATURES = [
     ("zr_step_graph_create", C.c_int, [C.c_void_p, c_void_pp]),
     ("zr_step_graph_launch", C.c_int, [C.c_void_p, C.POINTER(Microbatch), C.c_void_p, C.c_void_p, C.c_void_p]),
     ("zr_step_graph_info", C.c_int, [C.c_void_p, C.POINTER(StepGraphStats)]),
+    ("zr_forward_replay_info", C.c_int, [C.c_void_p, C.POINTER(StepGraphStats)]),
     ("zr_step_graph_destroy", None, [C.c_void_p]),
     ("zr_pack", C.c_int, [C.c_void_p, C.POINTER(Microbatch), c_int_p, c_int_p, c_int_p, c_int_p, c_int_p]),
     ("zr_rope_kv_write", C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int]),

@@ -760,6 +760,9 @@ void zr_context_destroy(zr_context* ctx) {
     hipSetDevice(ctx->device);
     for (hipStream_t st : {ctx->stream, ctx->d2h_stream, ctx->h2d_stream})
         if (st) hipStreamSynchronize(st);
+    if (ctx->fwd_graph) zr_step_graph_destroy(ctx->fwd_graph);
+    if (ctx->fwd_ids) (void)hipFree(ctx->fwd_ids);
+    if (ctx->fwd_h_ids) (void)hipHostFree(ctx->fwd_h_ids);
     for (auto& fb : ctx->xfer_free) (void)hipFree(fb.first);
     ctx->xfer_free.clear();
     if (ctx->scratch_stage) {
@@ -1246,11 +1249,68 @@ void zr_step_graph_destroy(zr_step_graph* g) {
     delete g;
 }
 
+// A decode step of one row per sequence whose caller wants only the greedy
+// ids, replayed from the context's step graph (the kernels and metadata of
+// the eager forward pass, captured once per bucket): the ids go up, the graph
+// replays, the ids come back.  Taken once the same sequence count has run
+// kForwardReplayAfter times in a row, so that a steady decode loop replays
+// and batches that change every step (sessions joining and leaving) do not
+// capture a graph per step.  ZR_FORWARD_REPLAY=0 keeps every step eager.
+constexpr int kForwardReplayAfter = 3;
+
+static bool forward_replay_fits(const zr_context* ctx, const zr_microbatch* mb) {
+    if (ctx->plain_kv || ctx->timing.enabled || mb->num_seqs < 1 || mb->num_seqs > ctx->desc.max_seqs) return false;
+    for (int s = 0; s < mb->num_seqs; ++s)
+        if (mb->q_len[s] != 1) return false;
+    static const bool off = [] {
+        const char* e = getenv("ZR_FORWARD_REPLAY");
+        return e && atoi(e) == 0;
+    }();
+    return !off;
+}
+
+static zr_status forward_replayed(zr_context* ctx, const zr_microbatch* mb, uint32_t* out_tokens) {
+    const int S = mb->num_seqs, cap = ctx->desc.max_seqs;
+    zr_status rc = ZR_OK;
+    if (!ctx->fwd_graph && (rc = zr_step_graph_create(ctx, &ctx->fwd_graph))) return rc;
+    if (!ctx->fwd_ids) ZR_HIP(ctx, hipMalloc((void**)&ctx->fwd_ids, 8 * (size_t)cap));
+    if (!ctx->fwd_h_ids) ZR_HIP(ctx, hipHostMalloc((void**)&ctx->fwd_h_ids, 8 * (size_t)cap, hipHostMallocDefault));
+    // (the previous call synchronised, so the pinned ids are free)
+    memcpy(ctx->fwd_h_ids, mb->tokens, 4 * (size_t)S);
+    ZR_HIP(ctx, hipMemcpyAsync(ctx->fwd_ids, ctx->fwd_h_ids, 4 * (size_t)S, hipMemcpyHostToDevice, ctx->stream));
+    rc = zr_step_graph_launch(ctx->fwd_graph, mb, ctx->fwd_ids, ctx->fwd_ids + cap, ctx->fwd_h_ids + cap);
+    if (rc) {
+        (void)hipStreamSynchronize(ctx->stream);
+        return rc;
+    }
+    if ((rc = zr_synchronize(ctx))) return rc;
+    memcpy(out_tokens, ctx->fwd_h_ids + cap, 4 * (size_t)S);
+    return ZR_OK;
+}
+
+zr_status zr_forward_replay_info(const zr_context* ctx, zr_step_graph_stats* out) {
+    if (!ctx || !out) return set_global_err(ZR_E_INVALID, "null argument");
+    if (!ctx->fwd_graph) {
+        *out = zr_step_graph_stats{};
+        return ZR_OK;
+    }
+    return zr_step_graph_info(ctx->fwd_graph, out);
+}
+
 zr_status zr_forward(zr_context* ctx, const zr_microbatch* mb, uint32_t* out_tokens, float* out_logits,
                      float* out_partials) {
     if (!ctx || !mb) return set_global_err(ZR_E_INVALID, "null argument");
     if (!mb->tokens) return set_err(ctx, ZR_E_INVALID, "zr_forward needs host token ids");
     ZR_HIP(ctx, hipSetDevice(ctx->device));
+    if (mb->num_seqs == ctx->fwd_seqs) {
+        ++ctx->fwd_repeats;
+    } else {
+        ctx->fwd_seqs = mb->num_seqs;
+        ctx->fwd_repeats = 1;
+    }
+    if (out_tokens && !out_logits && !out_partials && ctx->fwd_repeats >= kForwardReplayAfter &&
+        forward_replay_fits(ctx, mb))
+        return forward_replayed(ctx, mb, out_tokens);
     StagedMeta* st = ctx->scratch_stage;
     zr_status rc = stage_microbatch(ctx, mb, st);
     if (!rc) rc = run_forward(ctx, st, nullptr, ctx->tokens_out, nullptr, out_partials);

@@ -228,6 +228,13 @@ struct zr_context {
     uint64_t next_staged_id = 1;
 
     zr::StagedMeta* scratch_stage = nullptr;  // reused by zr_forward
+    // zr_forward's decode steps replayed from a step graph once a sequence
+    // count repeats: the graph, ids in / out (device [2][max_seqs]; pinned
+    // host [2][max_seqs]) and the run of calls with the current count
+    zr_step_graph* fwd_graph = nullptr;
+    uint32_t* fwd_ids = nullptr;
+    uint32_t* fwd_h_ids = nullptr;
+    int fwd_seqs = 0, fwd_repeats = 0;
     float* kv_stage = nullptr;      // KV gather / scatter staging (rows + table)
     size_t kv_stage_floats = 0;
     // KV window copies between HBM and host memory that overlap the compute

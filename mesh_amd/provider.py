@@ -327,6 +327,13 @@ class DeviceContext:
         self._pinned = weakref.WeakSet()
         self._transfers = weakref.WeakSet()
 
+    def forward_replay_info(self) -> dict:
+        """The step graph that zr_forward replays greedy decode steps from
+        (zr_forward_replay_info; zeros before the first replay)."""
+        st = _lib.StepGraphStats()
+        self.check(self.lib.zr_forward_replay_info(self.h, C.byref(st)))
+        return {name: getattr(st, name) for name, _ in _lib.StepGraphStats._fields_}
+
     def close(self):
         for b in list(getattr(self, "_backends", ())):
             b.close()

@@ -35,11 +35,14 @@ def _twin_sessions(ctx, rng, lens, max_seqs, kv_cols, layers):
     return a, b
 
 
-def _sync_steps(sessions, first, steps):
+def _sync_steps(sessions, first, steps, want_logits=False):
+    """Synchronous batched steps.  With want_logits every step runs eagerly
+    (kernel by kernel); greedy-only steps replay zr_forward's step graph from
+    the third call of the same sequence count."""
     toks, out = list(map(int, first)), []
     for _ in range(steps):
         reqs = [DecodeMicrobatchRequest(str(i), t, s) for i, (t, s) in enumerate(zip(toks, sessions))]
-        toks = [o.sampled_token for o in BackendMicrobatchExecutor.decode_step_batch(reqs)]
+        toks = [o.sampled_token for o in BackendMicrobatchExecutor.decode_step_batch(reqs, want_logits=want_logits)]
         out.append(np.asarray(toks, np.uint32))
     return out
 
@@ -82,7 +85,7 @@ def test_pipeline_equals_the_synchronous_step_bit_for_bit(kv_dtype):
     a, b = _twin_sessions(ctx, rng, lens, max_seqs, geo["kv_cols"], cfg["num_layers"])
     first = rng.integers(0, cfg["vocab"], len(lens))
     steps = 40
-    want = _sync_steps(a, first, steps)
+    want = _sync_steps(a, first, steps, want_logits=True)
     got, info = _pipeline_steps(b, first, steps)
     assert len(got) == steps
     for k in range(steps):
@@ -106,7 +109,7 @@ def test_pipeline_takes_a_new_bucket_when_the_work_list_outgrows_it(monkeypatch)
     # the bucket has room for ~70
     want, got = [], []
     monkeypatch.setenv("ZR_ATTN_PAGES_PER_SPLIT", "64")
-    want += _sync_steps(a, first, 3)
+    want += _sync_steps(a, first, 3, want_logits=True)
     pipe = DecodePipeline(b, first)
     try:
         for _ in range(3):
@@ -114,7 +117,7 @@ def test_pipeline_takes_a_new_bucket_when_the_work_list_outgrows_it(monkeypatch)
             if prev is not None:
                 got.append(prev)
         monkeypatch.setenv("ZR_ATTN_PAGES_PER_SPLIT", "1")
-        want += _sync_steps(a, want[-1], 3)
+        want += _sync_steps(a, want[-1], 3, want_logits=True)
         for _ in range(3):
             got.append(pipe.step())
         got.append(pipe.finish())
@@ -160,7 +163,7 @@ def test_pipeline_equals_the_synchronous_step_at_the_tinyllama_b32_workload():
             t.import_kv_cache(s.export_kv_cache())
             twins.append(t)
         first = np.random.default_rng(9).integers(0, bb.geo.vocab, bb.B)
-        want = _sync_steps(bb.backends, first, 6)
+        want = _sync_steps(bb.backends, first, 6, want_logits=True)
         got, info = _pipeline_steps(twins, first, 6)
         for k in range(6):
             np.testing.assert_array_equal(got[k], want[k], err_msg=f"step {k}")
@@ -173,3 +176,39 @@ def test_pipeline_equals_the_synchronous_step_at_the_tinyllama_b32_workload():
             t.close()
     finally:
         bb.close()
+
+
+@pytest.mark.parametrize("kv_dtype", ["bf16", "f32"])
+def test_synchronous_greedy_steps_replay_and_equal_the_eager_steps(kv_dtype):
+    """zr_forward replays greedy-only decode steps from the context's step
+    graph once a sequence count has run three calls in a row.  On twin
+    sessions, greedy-only steps (two eager calls, then replays; a new count
+    starts over and sets up a new bucket) equal steps that also fetch the
+    logits (always eager) bit for bit: the ids of every step, the positions
+    and every appended K / V row."""
+    cfg = SMALL
+    geo = geometry(cfg)
+    weights = random_weights(cfg, geo, seed=37, std=0.05)
+    ctx, _ = make(cfg, geo, weights, kv_dtype, True, max_tokens=16, max_seqs=16, pages=1024, pps=64)
+    rng = np.random.default_rng(0xF0)
+    lens = [3, 15, 16, 33, 40, 100, 180, 61]
+    max_seqs = [4096, 4096, 4096, 4096, 48, 4096, 4096, 70]
+    a, b = _twin_sessions(ctx, rng, lens, max_seqs, geo["kv_cols"], cfg["num_layers"])
+    first = rng.integers(0, cfg["vocab"], len(lens))
+    assert ctx.forward_replay_info()["launches"] == 0
+    got = _sync_steps(b, first, 8)
+    info = ctx.forward_replay_info()
+    assert (info["launches"], info["sequences"], info["buckets"]) == (6, 8, 1), info
+    want = _sync_steps(a, first, 8, want_logits=True)
+    assert ctx.forward_replay_info()["launches"] == 6  # steps that fetch logits stay eager
+    for k in range(8):
+        np.testing.assert_array_equal(got[k], want[k], err_msg=f"step {k}")
+    # five of the sessions: a new sequence count
+    got = _sync_steps(b[:5], got[-1][:5], 8)
+    info = ctx.forward_replay_info()
+    assert (info["launches"], info["sequences"], info["buckets"]) == (12, 5, 2), info
+    want = _sync_steps(a[:5], want[-1][:5], 8, want_logits=True)
+    for k in range(8):
+        np.testing.assert_array_equal(got[k], want[k], err_msg=f"five sessions, step {k}")
+    _same_sessions(a, b)
+    ctx.close()
